@@ -1,0 +1,148 @@
+/*
+ * qmoe.h -- C ABI of the MI355X-native MoE FFN layer (libqmoe.so).
+ *
+ * Drop-in for the reference's MoE layer module (rye-001/Qwenium):
+ *   MoELayer::Hparams          src/layers/moe.h:34-39
+ *   MoELayer::MoELayer(...)    src/layers/moe.h:44-53, src/layers/moe.cpp:27-53
+ *   MoELayer::build(...)       src/layers/moe.h:58-63, src/layers/moe.cpp:55-177
+ *   build_rms_norm(...)        src/layers/norm.h:10-15, src/layers/norm.cpp:15-26
+ * Weight roles/shapes follow TransformerBlock's MoE slots,
+ * src/core/model.h:110-119, in GGUF block layout (ggml ne/nb conventions).
+ *
+ * Conventions
+ *   - All tensor data and activation pointers are DEVICE pointers.
+ *   - Every call returns QMOE_OK (0) or a QMOE_ERR_* code; the message of the
+ *     last failure on the calling thread is qmoe_last_error().  Messages name
+ *     the slot/parameter, the expected value and the actual value, in that
+ *     order (the reference's fail-loud contract, src/qinf_error.h:1-29).
+ *   - Work is enqueued on the caller's HIP stream; no host synchronisation
+ *     happens inside qmoe_layer_forward.
+ *   - A layer (and a workspace) is not thread-safe; calls that share a
+ *     workspace must be ordered on one stream.
+ */
+#ifndef QMOE_H
+#define QMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids, as stored in GGUF (read at gguf_loader.cpp:490). */
+enum qmoe_type {
+    QMOE_TYPE_F32  = 0,
+    QMOE_TYPE_Q4_0 = 2,
+    QMOE_TYPE_Q8_0 = 8
+};
+
+enum qmoe_status {
+    QMOE_OK           = 0,
+    QMOE_ERR_NULL     = 1,  /* required pointer was NULL */
+    QMOE_ERR_SHAPE    = 2,  /* ne/nb/dimension mismatch */
+    QMOE_ERR_TYPE     = 3,  /* unsupported or mismatched ggml type */
+    QMOE_ERR_VALUE    = 4,  /* bad hparam / argument value */
+    QMOE_ERR_CAPACITY = 5,  /* n_tokens above the workspace capacity */
+    QMOE_ERR_HIP      = 6   /* a HIP runtime call failed */
+};
+
+/* A borrowed ggml tensor view: device data + ggml type + ne/nb (ne[0] contiguous).
+ * Replaces the ggml_tensor* slots of MoELayer::MoELayer (moe.h:44-53). */
+typedef struct qmoe_tensor {
+    const void* data;
+    int32_t     type;      /* enum qmoe_type */
+    int32_t     n_dims;    /* 1..3 */
+    int64_t     ne[4];
+    uint64_t    nb[4];     /* byte strides */
+} qmoe_tensor;
+
+/* Mirrors MoELayer::Hparams (moe.h:34-39). */
+typedef struct qmoe_hparams {
+    int32_t n_experts;
+    int32_t top_k;
+    int32_t ffn_dim;
+    int32_t has_shared_expert;
+} qmoe_hparams;
+
+/* Optional device-side copies of the intermediates that the reference names
+ * moe_logits / moe_idx / moe_weights (moe.cpp:73,83,95) plus the per-expert
+ * row lists that ggml_mul_mat_id builds internally.  Any pointer may be NULL. */
+typedef struct qmoe_debug {
+    float*   logits;    /* [T][n_experts] router logits */
+    int32_t* topk_idx;  /* [T][top_k] expert ids, descending logit, ties -> lowest id */
+    float*   topk_w;    /* [T][top_k] softmax over the selected logits */
+    float*   sh_gate;   /* [T] sigmoid(w_sh_norm . x); only with a shared expert */
+    int32_t* offsets;   /* [n_experts+1] exclusive prefix of per-expert counts */
+    int32_t* rows;      /* [T*top_k] assignment t*top_k+j, grouped by expert,
+                           ascending (token, slot) inside each group */
+} qmoe_debug;
+
+typedef struct qmoe_layer qmoe_layer;
+typedef struct qmoe_workspace qmoe_workspace;
+
+/* Thread-local text of the last failure ("" if none). */
+const char* qmoe_last_error(void);
+
+/* Replaces MoELayer::MoELayer (moe.h:44-53, moe.cpp:27-53).  Slots in the
+ * reference's order.  w_router [n_embd, n_experts] F32; w_exp_gate/up
+ * [n_embd, ffn_dim, n_experts] and w_exp_down [ffn_dim, n_embd, n_experts]
+ * Q4_0 or Q8_0; w_sh_gate/up [n_embd, ffn_dim], w_sh_down [ffn_dim, n_embd]
+ * (same types as the routed gate/up and down); w_sh_norm [n_embd] F32.
+ * w_sh_* must be non-NULL iff hp->has_shared_expert.  Weights are borrowed:
+ * they must outlive the layer.  The layer is bound to the current device. */
+int qmoe_layer_create(const qmoe_tensor* w_router,
+                      const qmoe_tensor* w_exp_gate,
+                      const qmoe_tensor* w_exp_up,
+                      const qmoe_tensor* w_exp_down,
+                      const qmoe_tensor* w_sh_gate,
+                      const qmoe_tensor* w_sh_up,
+                      const qmoe_tensor* w_sh_down,
+                      const qmoe_tensor* w_sh_norm,
+                      const qmoe_hparams* hp,
+                      qmoe_layer** out);
+int qmoe_layer_destroy(qmoe_layer* layer);
+/* n_embd of a created layer (ne[0] of w_router). */
+int qmoe_layer_n_embd(const qmoe_layer* layer);
+
+/* Scratch for routing tables, quantized activations and per-row outputs,
+ * sized for up to max_tokens tokens of layers no larger than `like`.  One
+ * workspace may serve every layer of a model on one stream. */
+int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_workspace** out);
+int qmoe_workspace_destroy(qmoe_workspace* ws);
+int32_t qmoe_workspace_capacity(const qmoe_workspace* ws);
+
+/* Replaces MoELayer::build (moe.h:58-63, moe.cpp:55-177):
+ *   y[T][n_embd] = MoE(x[T][n_embd])  (+ residual[T][n_embd] when non-NULL,
+ *   the caller's ggml_add(cur, ffn_inp) of qwen36.cpp:304).
+ * x, y, residual: device f32, token-major (ggml [n_embd, n_tokens]).  y may
+ * alias residual but not x.  ws == NULL uses a workspace owned by the layer,
+ * allocated (synchronously) on first use and grown when n_tokens exceeds it.
+ * n_tokens == 0 is a no-op.  dbg may be NULL. */
+int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
+                       const float* x, int32_t n_tokens, float* y,
+                       const float* residual, const qmoe_debug* dbg,
+                       void* hip_stream);
+
+/* Replaces build_rms_norm (norm.cpp:15-26): y = x / sqrt(mean(x^2) + eps) * w,
+ * per token (ggml_rms_norm followed by ggml_mul).  w may be NULL (no scale). */
+int qmoe_rms_norm(const float* x, const float* w, int32_t n_tokens, int32_t n_embd,
+                  float eps, float* y, void* hip_stream);
+
+/* Seeded synthetic data for tests and benchmarks, generated on the device.
+ * Value i of a stream is N(mean, sigma) from a counter-based hash of
+ * (seed, stream, i) and a Box-Muller transform made of fixed IEEE operations,
+ * so the bytes equal those of a CPU implementation of the same recipe.
+ *   qmoe_synth_f32:   dst[i] = (float)(mean + sigma * z_i), i < n
+ *   qmoe_synth_quant: n_rows rows of row_len values (value index row*row_len+col)
+ *                     quantized to `type` with ggml's reference quantizers
+ *                     (quantize_row_q4_0_ref / quantize_row_q8_0_ref). */
+int qmoe_synth_f32(float* dst, int64_t n, uint64_t seed, uint64_t stream,
+                   double mean, double sigma, void* hip_stream);
+int qmoe_synth_quant(void* dst, int32_t type, int64_t n_rows, int64_t row_len,
+                     uint64_t seed, uint64_t stream, double sigma, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMOE_H */

@@ -1,0 +1,126 @@
+// misc_kernels.hip -- RMSNorm (the MoE layer's pre-norm caller slice) and the
+// seeded synthetic-data generators used by tests and benchmarks.
+#include "qmoe_device.h"
+#include "qmoe_internal.h"
+
+namespace qmoe {
+
+// ---------------------------------------------------------------------------
+// RMSNorm, restating ggml_rms_norm + ggml_mul as used by build_rms_norm
+// (src/layers/norm.cpp:15-26): sum of f32 squares accumulated in f64,
+// mean rounded to f32, scale = 1/sqrtf(mean + eps), y = (x*scale)*w.
+// One block per token.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rms_norm(const float* x, const float* w, int H, float eps, float* y) {
+#pragma clang fp contract(off)
+    __shared__ double s_part[4];
+    const int t = blockIdx.x;
+    const float* xr = x + (uint64_t)t * H;
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < H; i += 256) {
+        const float v = xr[i];
+        acc += (double)(v * v);
+    }
+    acc = group_sum_f64<64>(acc);
+    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const double sum = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    const float mean = (float)(sum / (double)H);
+    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
+    for (int i = threadIdx.x; i < H; i += 256) {
+        const float v = xr[i] * scale;
+        y[(uint64_t)t * H + i] = w ? v * w[i] : v;
+    }
+}
+
+hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream) {
+    hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic data: N(mean, sigma) from (seed, stream, index); quantized rows
+// use ggml's reference quantizers (quantize_row_q4_0_ref / _q8_0_ref).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_synth_f32(float* dst, int64_t n, uint64_t key, double mean, double sigma) {
+#pragma clang fp contract(off)
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        dst[i] = (float)(mean + sigma * normal_det(key, (uint64_t)i));
+}
+
+template <int WT>
+__global__ __launch_bounds__(256) void k_synth_quant(uint8_t* dst, int64_t n_rows, int64_t row_len, uint64_t key,
+                                                      double sigma) {
+#pragma clang fp contract(off)
+    const int64_t nb = row_len / 32;
+    const int64_t total = n_rows * nb;
+    constexpr int BS = BlockTraits<WT>::kBytes;
+    for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < total; g += (int64_t)gridDim.x * 256) {
+        const int64_t row = g / nb, b = g % nb;
+        const uint64_t i0 = (uint64_t)(row * row_len + 32 * b);
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = (float)(0.0 + sigma * normal_det(key, i0 + j));
+        uint16_t* out = (uint16_t*)(dst + row * nb * BS + b * BS);
+        if (WT == kTypeQ4_0) {
+            float amax = 0.0f, vmax = 0.0f;
+            for (int j = 0; j < 32; ++j) {
+                if (amax < __builtin_fabsf(v[j])) { amax = __builtin_fabsf(v[j]); vmax = v[j]; }
+            }
+            const float d = vmax / -8.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            out[0] = (uint16_t)f32_to_fp16(d);
+#pragma unroll
+            for (int j = 0; j < 16; j += 2) {
+                uint32_t pair = 0;
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const float x0 = v[j + jj] * id;
+                    const float x1 = v[16 + j + jj] * id;
+                    const int xi0 = min(15, (int)(x0 + 8.5f));
+                    const int xi1 = min(15, (int)(x1 + 8.5f));
+                    pair |= (uint32_t)(xi0 | (xi1 << 4)) << (8 * jj);
+                }
+                out[1 + j / 2] = (uint16_t)pair;
+            }
+        } else {
+            float amax = 0.0f;
+            for (int j = 0; j < 32; ++j) amax = fmaxf(amax, __builtin_fabsf(v[j]));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            out[0] = (uint16_t)f32_to_fp16(d);
+#pragma unroll
+            for (int j = 0; j < 32; j += 2) {
+                const int q0 = (int)__builtin_roundf(v[j] * id);
+                const int q1 = (int)__builtin_roundf(v[j + 1] * id);
+                out[1 + j / 2] = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+            }
+        }
+    }
+}
+
+hipError_t launch_synth_f32(float* dst, int64_t n, uint64_t seed, uint64_t stream_id, double mean, double sigma,
+                            hipStream_t stream) {
+    const int64_t blocks = n <= 0 ? 1 : (n + 255) / 256;
+    const int grid = (int)(blocks < 65536 ? blocks : 65536);
+    hipLaunchKernelGGL(k_synth_f32, dim3(grid), dim3(256), 0, stream, dst, n, stream_key(seed, stream_id), mean,
+                       sigma);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth_quant(void* dst, int type, int64_t n_rows, int64_t row_len, uint64_t seed,
+                              uint64_t stream_id, double sigma, hipStream_t stream) {
+    const int64_t total = n_rows * (row_len / 32);
+    const int64_t blocks = total <= 0 ? 1 : (total + 255) / 256;
+    const int grid = (int)(blocks < 65536 ? blocks : 65536);
+    const uint64_t key = stream_key(seed, stream_id);
+    if (type == kTypeQ4_0)
+        hipLaunchKernelGGL((k_synth_quant<kTypeQ4_0>), dim3(grid), dim3(256), 0, stream, (uint8_t*)dst, n_rows,
+                           row_len, key, sigma);
+    else
+        hipLaunchKernelGGL((k_synth_quant<kTypeQ8_0>), dim3(grid), dim3(256), 0, stream, (uint8_t*)dst, n_rows,
+                           row_len, key, sigma);
+    return hipGetLastError();
+}
+
+}  // namespace qmoe

@@ -1,0 +1,397 @@
+// qmoe_api.cpp -- the C ABI of include/qmoe.h: argument validation, workspace
+// management and the per-layer launch sequence.
+//
+// Validation mirrors the reference's fail-loud contract (src/qinf_error.h:1-29:
+// "<slot> expected <value>, got <value>") and the one check MoELayer's
+// constructor performs (src/layers/moe.cpp:47-52).  Everything is checked on
+// the host before any launch; kernels never see a shape they do not support.
+#include "qmoe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "qmoe_internal.h"
+
+using qmoe::LayerDesc;
+using qmoe::Workspace;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+std::string slot_error(const char* slot, const std::string& expected, const std::string& got) {
+    return std::string("qmoe: slot \"") + slot + "\" expected " + expected + ", got " + got;
+}
+
+const char* type_name(int t) {
+    switch (t) {
+        case QMOE_TYPE_F32: return "F32";
+        case QMOE_TYPE_Q4_0: return "Q4_0";
+        case QMOE_TYPE_Q8_0: return "Q8_0";
+        default: return "unsupported";
+    }
+}
+
+std::string type_str(int t) { return std::string(type_name(t)) + " (ggml type " + std::to_string(t) + ")"; }
+
+std::string shape_str(const qmoe_tensor* t) {
+    std::string s = "[";
+    for (int i = 0; i < t->n_dims; ++i) {
+        if (i) s += ",";
+        s += std::to_string(t->ne[i]);
+    }
+    return s + "]";
+}
+
+uint64_t block_bytes(int type) {
+    switch (type) {
+        case QMOE_TYPE_Q4_0: return 18;
+        case QMOE_TYPE_Q8_0: return 34;
+        case QMOE_TYPE_F32: return 4;
+        default: return 0;
+    }
+}
+
+// Checks type, rank, ne (ne_expect[i] < 0 means "any"), contiguous rows and
+// 4-byte aligned data/strides.  Returns 0 or an error code (message set).
+int check_tensor(const char* slot, const qmoe_tensor* t, int n_dims, const int64_t* ne_expect,
+                 bool quantized) {
+    if (!t) return fail(QMOE_ERR_NULL, slot_error(slot, "a tensor", "null"));
+    if (!t->data) return fail(QMOE_ERR_NULL, slot_error(slot, "device data", "null data pointer"));
+    if (quantized) {
+        if (t->type != QMOE_TYPE_Q4_0 && t->type != QMOE_TYPE_Q8_0)
+            return fail(QMOE_ERR_TYPE, slot_error(slot, "type Q4_0 or Q8_0", type_str(t->type)));
+    } else if (t->type != QMOE_TYPE_F32) {
+        return fail(QMOE_ERR_TYPE, slot_error(slot, "type F32", type_str(t->type)));
+    }
+    if (t->n_dims != n_dims) {
+        return fail(QMOE_ERR_SHAPE, slot_error(slot, std::to_string(n_dims) + " dims",
+                                               std::to_string(t->n_dims) + " dims " + shape_str(t)));
+    }
+    for (int i = 0; i < n_dims; ++i) {
+        if (ne_expect[i] >= 0 && t->ne[i] != ne_expect[i]) {
+            std::string exp = "ne[" + std::to_string(i) + "]=" + std::to_string(ne_expect[i]);
+            return fail(QMOE_ERR_SHAPE, slot_error(slot, exp, "shape " + shape_str(t)));
+        }
+    }
+    const uint64_t bb = block_bytes(t->type);
+    const uint64_t row = quantized ? (uint64_t)(t->ne[0] / 32) * bb : (uint64_t)t->ne[0] * 4;
+    if (t->nb[0] != bb)
+        return fail(QMOE_ERR_SHAPE, slot_error(slot, "nb[0]=" + std::to_string(bb), "nb[0]=" + std::to_string(t->nb[0])));
+    if (n_dims >= 2 && t->nb[1] < row)
+        return fail(QMOE_ERR_SHAPE, slot_error(slot, "nb[1]>=" + std::to_string(row), "nb[1]=" + std::to_string(t->nb[1])));
+    if (n_dims >= 3 && t->nb[2] < t->nb[1] * (uint64_t)t->ne[1])
+        return fail(QMOE_ERR_SHAPE, slot_error(slot, "nb[2]>=" + std::to_string(t->nb[1] * (uint64_t)t->ne[1]),
+                                               "nb[2]=" + std::to_string(t->nb[2])));
+    if (((uintptr_t)t->data & 3u) != 0)
+        return fail(QMOE_ERR_SHAPE, slot_error(slot, "4-byte aligned data", "misaligned pointer"));
+    for (int i = 1; i < n_dims; ++i)
+        if (t->nb[i] & 3u)
+            return fail(QMOE_ERR_SHAPE, slot_error(slot, "nb[" + std::to_string(i) + "] multiple of 4",
+                                                   "nb[" + std::to_string(i) + "]=" + std::to_string(t->nb[i])));
+    return QMOE_OK;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+    return fail(QMOE_ERR_HIP, std::string("qmoe: ") + what + " failed: " + hipGetErrorString(err));
+}
+
+}  // namespace
+
+namespace qmoe {
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves the workspace buffers out of `base` (when non-null) and returns the byte size.
+size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* base) {
+    const size_t A = (size_t)T * K;
+    const size_t R = A + (size_t)T;  // room for a shared expert
+    const int nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
+    const int max_tiles = (int)((A + kMfmaTileM - 1) / kMfmaTileM) + std::min<int>(E, (int)A) +
+                          (T + kMfmaTileM - 1) / kMfmaTileM + 1;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes, 256);
+        return base ? (void*)((char*)base + o) : nullptr;
+    };
+    Workspace tmp;
+    Workspace& ws = w ? *w : tmp;
+    ws.xq_qs = (int8_t*)take((size_t)T * H);
+    ws.xq_ds = (float2*)take((size_t)T * (H / 32) * sizeof(float2));
+    ws.logits = (float*)take((size_t)T * (E + 1) * sizeof(float));
+    ws.topk_idx = (int32_t*)take(A * sizeof(int32_t));
+    ws.topk_w = (float*)take(A * sizeof(float));
+    ws.sh_gate = (float*)take((size_t)T * sizeof(float));
+    ws.local_rank = (int32_t*)take(A * sizeof(int32_t));
+    ws.hist = (int32_t*)take((size_t)nblk * E * sizeof(int32_t));
+    ws.offsets = (int32_t*)take((size_t)(E + 2) * sizeof(int32_t));
+    ws.rows = (int32_t*)take(R * sizeof(int32_t));
+    ws.row_token = (int32_t*)take(R * sizeof(int32_t));
+    ws.pos = (int32_t*)take(A * sizeof(int32_t));
+    ws.active = (int32_t*)take((size_t)(E + 1) * sizeof(int32_t));
+    ws.counters = (int32_t*)take(16 * sizeof(int32_t));
+    ws.tiles = (int4*)take((size_t)max_tiles * sizeof(int4));
+    ws.hq_qs = (int8_t*)take(R * F);
+    ws.hq_ds = (float2*)take(R * (F / 32) * sizeof(float2));
+    ws.ybuf = (float*)take(R * H * sizeof(float));
+    ws.max_tiles = max_tiles;
+    ws.cap_T = T; ws.H = H; ws.E = E; ws.K = K; ws.F = F;
+    ws.base = base;
+    ws.bytes = off;
+    return off;
+}
+
+}  // namespace qmoe
+
+struct qmoe_layer {
+    LayerDesc d;
+    int device = 0;
+    qmoe_workspace* own_ws = nullptr;
+};
+
+struct qmoe_workspace {
+    Workspace w;
+    int device = 0;
+};
+
+extern "C" {
+
+const char* qmoe_last_error(void) { return g_last_error.c_str(); }
+
+int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate, const qmoe_tensor* w_exp_up,
+                      const qmoe_tensor* w_exp_down, const qmoe_tensor* w_sh_gate, const qmoe_tensor* w_sh_up,
+                      const qmoe_tensor* w_sh_down, const qmoe_tensor* w_sh_norm, const qmoe_hparams* hp,
+                      qmoe_layer** out) {
+    g_last_error.clear();
+    if (!out) return fail(QMOE_ERR_NULL, "qmoe: out expected a non-null qmoe_layer**, got null");
+    *out = nullptr;
+    if (!hp) return fail(QMOE_ERR_NULL, "qmoe: hp expected non-null hparams, got null");
+    // moe.cpp:47-52: the shared expert matrices are required when has_shared_expert
+    if (hp->has_shared_expert && (!w_sh_gate || !w_sh_up || !w_sh_down))
+        return fail(QMOE_ERR_NULL, "moe_layer: has_shared_expert=true but shared expert weights are null");
+    if (hp->n_experts < 1 || hp->n_experts > 1024)
+        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"n_experts\" expected 1..1024, got " + std::to_string(hp->n_experts));
+    if (hp->top_k < 1 || hp->top_k > hp->n_experts || hp->top_k > 64)
+        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"top_k\" expected 1..min(n_experts, 64) (n_experts=" +
+                                        std::to_string(hp->n_experts) + "), got " + std::to_string(hp->top_k));
+    if (hp->ffn_dim < 64 || hp->ffn_dim % 64 != 0)
+        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"ffn_dim\" expected a positive multiple of 64, got " +
+                                        std::to_string(hp->ffn_dim));
+    if (!w_router) return fail(QMOE_ERR_NULL, slot_error("w_router", "a tensor", "null"));
+    const int64_t H = w_router->ne[0];
+    if (H < 64 || H % 64 != 0)
+        return fail(QMOE_ERR_SHAPE, slot_error("w_router", "ne[0]=n_embd a positive multiple of 64",
+                                               "ne[0]=" + std::to_string(H)));
+    const int64_t E = hp->n_experts, F = hp->ffn_dim;
+    int rc;
+    {
+        const int64_t ne[2] = {H, E};
+        if ((rc = check_tensor("w_router", w_router, 2, ne, false))) return rc;
+    }
+    {
+        const int64_t ne[3] = {H, F, E};
+        if ((rc = check_tensor("w_exp_gate", w_exp_gate, 3, ne, true))) return rc;
+        if ((rc = check_tensor("w_exp_up", w_exp_up, 3, ne, true))) return rc;
+        if (w_exp_up->type != w_exp_gate->type)
+            return fail(QMOE_ERR_TYPE, slot_error("w_exp_up", "type " + type_str(w_exp_gate->type) + " (as w_exp_gate)",
+                                                  type_str(w_exp_up->type)));
+    }
+    {
+        const int64_t ne[3] = {F, H, E};
+        if ((rc = check_tensor("w_exp_down", w_exp_down, 3, ne, true))) return rc;
+    }
+    if (hp->has_shared_expert) {
+        const int64_t ne_gu[2] = {H, F};
+        const int64_t ne_d[2] = {F, H};
+        const int64_t ne_n[1] = {H};
+        if ((rc = check_tensor("w_sh_gate", w_sh_gate, 2, ne_gu, true))) return rc;
+        if ((rc = check_tensor("w_sh_up", w_sh_up, 2, ne_gu, true))) return rc;
+        if ((rc = check_tensor("w_sh_down", w_sh_down, 2, ne_d, true))) return rc;
+        if ((rc = check_tensor("w_sh_norm", w_sh_norm, 1, ne_n, false))) return rc;
+        if (w_sh_gate->type != w_exp_gate->type)
+            return fail(QMOE_ERR_TYPE, slot_error("w_sh_gate", "type " + type_str(w_exp_gate->type) + " (as w_exp_gate)",
+                                                  type_str(w_sh_gate->type)));
+        if (w_sh_up->type != w_exp_gate->type)
+            return fail(QMOE_ERR_TYPE, slot_error("w_sh_up", "type " + type_str(w_exp_gate->type) + " (as w_exp_gate)",
+                                                  type_str(w_sh_up->type)));
+        if (w_sh_down->type != w_exp_down->type)
+            return fail(QMOE_ERR_TYPE, slot_error("w_sh_down", "type " + type_str(w_exp_down->type) + " (as w_exp_down)",
+                                                  type_str(w_sh_down->type)));
+    }
+    qmoe_layer* L = new (std::nothrow) qmoe_layer();
+    if (!L) return fail(QMOE_ERR_VALUE, "qmoe: host allocation failed");
+    LayerDesc& d = L->d;
+    d.H = (int)H; d.E = (int)E; d.K = hp->top_k; d.F = (int)F; d.S = hp->has_shared_expert ? 1 : 0;
+    d.gu_type = w_exp_gate->type;
+    d.dn_type = w_exp_down->type;
+    d.w_router = (const float*)w_router->data;
+    d.router_ld = w_router->nb[1] / 4;
+    d.w_gate = (const uint8_t*)w_exp_gate->data; d.gate_nb1 = w_exp_gate->nb[1]; d.gate_nb2 = w_exp_gate->nb[2];
+    d.w_up = (const uint8_t*)w_exp_up->data; d.up_nb1 = w_exp_up->nb[1]; d.up_nb2 = w_exp_up->nb[2];
+    d.w_down = (const uint8_t*)w_exp_down->data; d.down_nb1 = w_exp_down->nb[1]; d.down_nb2 = w_exp_down->nb[2];
+    if (d.S) {
+        d.w_sh_gate = (const uint8_t*)w_sh_gate->data; d.sh_gate_nb1 = w_sh_gate->nb[1];
+        d.w_sh_up = (const uint8_t*)w_sh_up->data; d.sh_up_nb1 = w_sh_up->nb[1];
+        d.w_sh_down = (const uint8_t*)w_sh_down->data; d.sh_down_nb1 = w_sh_down->nb[1];
+        d.w_sh_norm = (const float*)w_sh_norm->data;
+    }
+    (void)hipGetDevice(&L->device);
+    *out = L;
+    return QMOE_OK;
+}
+
+int qmoe_layer_destroy(qmoe_layer* layer) {
+    if (!layer) return QMOE_OK;
+    if (layer->own_ws) qmoe_workspace_destroy(layer->own_ws);
+    delete layer;
+    return QMOE_OK;
+}
+
+int qmoe_layer_n_embd(const qmoe_layer* layer) { return layer ? layer->d.H : 0; }
+
+int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_workspace** out) {
+    g_last_error.clear();
+    if (!out) return fail(QMOE_ERR_NULL, "qmoe: out expected a non-null qmoe_workspace**, got null");
+    *out = nullptr;
+    if (!like) return fail(QMOE_ERR_NULL, "qmoe: like expected a layer, got null");
+    if (max_tokens < 1 || max_tokens > (1 << 20))
+        return fail(QMOE_ERR_VALUE, "qmoe: max_tokens expected 1..1048576, got " + std::to_string(max_tokens));
+    const LayerDesc& d = like->d;
+    qmoe_workspace* ws = new (std::nothrow) qmoe_workspace();
+    if (!ws) return fail(QMOE_ERR_VALUE, "qmoe: host allocation failed");
+    const size_t bytes = qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, nullptr, nullptr);
+    void* base = nullptr;
+    hipError_t err = hipMalloc(&base, bytes);
+    if (err != hipSuccess) {
+        delete ws;
+        return hip_fail(err, "hipMalloc(workspace)");
+    }
+    qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, &ws->w, base);
+    (void)hipGetDevice(&ws->device);
+    *out = ws;
+    return QMOE_OK;
+}
+
+int qmoe_workspace_destroy(qmoe_workspace* ws) {
+    if (!ws) return QMOE_OK;
+    if (ws->w.base) (void)hipFree(ws->w.base);
+    delete ws;
+    return QMOE_OK;
+}
+
+int32_t qmoe_workspace_capacity(const qmoe_workspace* ws) { return ws ? ws->w.cap_T : 0; }
+
+int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, int32_t n_tokens, float* y,
+                       const float* residual, const qmoe_debug* dbg, void* hip_stream) {
+    g_last_error.clear();
+    if (!layer) return fail(QMOE_ERR_NULL, "qmoe: layer expected non-null, got null");
+    if (n_tokens < 0)
+        return fail(QMOE_ERR_VALUE, "qmoe: n_tokens expected >= 0, got " + std::to_string(n_tokens));
+    if (n_tokens == 0) return QMOE_OK;
+    if (!x) return fail(QMOE_ERR_NULL, "qmoe: x expected a device pointer, got null");
+    if (!y) return fail(QMOE_ERR_NULL, "qmoe: y expected a device pointer, got null");
+    if (x == y) return fail(QMOE_ERR_VALUE, "qmoe: y expected a buffer distinct from x, got x");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)residual & 15u))
+        return fail(QMOE_ERR_VALUE, "qmoe: x/y/residual expected 16-byte aligned device pointers, got a misaligned one");
+    const LayerDesc& d = layer->d;
+    if (!ws) {
+        if (!layer->own_ws || layer->own_ws->w.cap_T < n_tokens) {
+            if (layer->own_ws) {
+                (void)hipDeviceSynchronize();
+                qmoe_workspace_destroy(layer->own_ws);
+                layer->own_ws = nullptr;
+            }
+            int rc = qmoe_workspace_create(layer, n_tokens, &layer->own_ws);
+            if (rc) return rc;
+        }
+        ws = layer->own_ws;
+    }
+    const Workspace& w = ws->w;
+    if (n_tokens > w.cap_T)
+        return fail(QMOE_ERR_CAPACITY, "qmoe: n_tokens expected <= workspace capacity " + std::to_string(w.cap_T) +
+                                           ", got " + std::to_string(n_tokens));
+    if (w.H < d.H || w.E < d.E || w.K < d.K || w.F < d.F)
+        return fail(QMOE_ERR_SHAPE, "qmoe: workspace expected dims >= layer (H,E,K,F)=(" + std::to_string(d.H) + "," +
+                                        std::to_string(d.E) + "," + std::to_string(d.K) + "," + std::to_string(d.F) +
+                                        "), got (" + std::to_string(w.H) + "," + std::to_string(w.E) + "," +
+                                        std::to_string(w.K) + "," + std::to_string(w.F) + ")");
+    // buffers are sized for the workspace's (larger or equal) dims; kernels index with the layer's
+    const Workspace& v = w;
+    hipStream_t stream = (hipStream_t)hip_stream;
+    hipError_t err = qmoe::launch_route(d, v, x, n_tokens, stream);
+    if (err != hipSuccess) return hip_fail(err, "route kernels");
+    err = qmoe::launch_experts_gemv(d, v, n_tokens, stream);
+    if (err != hipSuccess) return hip_fail(err, "expert kernels");
+    err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream);
+    if (err != hipSuccess) return hip_fail(err, "combine kernel");
+    if (dbg) {
+        const size_t T = (size_t)n_tokens;
+        if (dbg->logits) {
+            err = hipMemcpy2DAsync(dbg->logits, d.E * sizeof(float), v.logits, (d.E + 1) * sizeof(float),
+                                   d.E * sizeof(float), T, hipMemcpyDeviceToDevice, stream);
+            if (err != hipSuccess) return hip_fail(err, "debug copy (logits)");
+        }
+        struct { void* dst; const void* src; size_t bytes; const char* what; } cp[] = {
+            {dbg->topk_idx, v.topk_idx, T * d.K * 4, "topk_idx"},
+            {dbg->topk_w, v.topk_w, T * d.K * 4, "topk_w"},
+            {d.S ? dbg->sh_gate : nullptr, v.sh_gate, T * 4, "sh_gate"},
+            {dbg->offsets, v.offsets, (size_t)(d.E + 1) * 4, "offsets"},
+            {dbg->rows, v.rows, T * d.K * 4, "rows"},
+        };
+        for (auto& c : cp) {
+            if (!c.dst) continue;
+            err = hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice, stream);
+            if (err != hipSuccess) return hip_fail(err, c.what);
+        }
+    }
+    return QMOE_OK;
+}
+
+int qmoe_rms_norm(const float* x, const float* w, int32_t n_tokens, int32_t n_embd, float eps, float* y,
+                  void* hip_stream) {
+    g_last_error.clear();
+    if (n_tokens < 0) return fail(QMOE_ERR_VALUE, "qmoe: n_tokens expected >= 0, got " + std::to_string(n_tokens));
+    if (n_tokens == 0) return QMOE_OK;
+    if (!x || !y) return fail(QMOE_ERR_NULL, "qmoe: x/y expected device pointers, got null");
+    if (n_embd < 1) return fail(QMOE_ERR_VALUE, "qmoe: n_embd expected >= 1, got " + std::to_string(n_embd));
+    hipError_t err = qmoe::launch_rms_norm(x, w, n_tokens, n_embd, eps, y, (hipStream_t)hip_stream);
+    return err == hipSuccess ? QMOE_OK : hip_fail(err, "rms_norm kernel");
+}
+
+int qmoe_synth_f32(float* dst, int64_t n, uint64_t seed, uint64_t stream, double mean, double sigma,
+                   void* hip_stream) {
+    g_last_error.clear();
+    if (n < 0) return fail(QMOE_ERR_VALUE, "qmoe: n expected >= 0, got " + std::to_string(n));
+    if (n == 0) return QMOE_OK;
+    if (!dst) return fail(QMOE_ERR_NULL, "qmoe: dst expected a device pointer, got null");
+    hipError_t err = qmoe::launch_synth_f32(dst, n, seed, stream, mean, sigma, (hipStream_t)hip_stream);
+    return err == hipSuccess ? QMOE_OK : hip_fail(err, "synth_f32 kernel");
+}
+
+int qmoe_synth_quant(void* dst, int32_t type, int64_t n_rows, int64_t row_len, uint64_t seed, uint64_t stream,
+                     double sigma, void* hip_stream) {
+    g_last_error.clear();
+    if (type != QMOE_TYPE_Q4_0 && type != QMOE_TYPE_Q8_0)
+        return fail(QMOE_ERR_TYPE, "qmoe: type expected Q4_0 or Q8_0, got " + type_str(type));
+    if (n_rows < 0 || row_len < 0 || row_len % 32 != 0)
+        return fail(QMOE_ERR_VALUE, "qmoe: rows x row_len expected n_rows >= 0 and row_len a multiple of 32, got " +
+                                        std::to_string(n_rows) + " x " + std::to_string(row_len));
+    if (n_rows == 0 || row_len == 0) return QMOE_OK;
+    if (!dst) return fail(QMOE_ERR_NULL, "qmoe: dst expected a device pointer, got null");
+    if ((uintptr_t)dst & 1u) return fail(QMOE_ERR_VALUE, "qmoe: dst expected 2-byte alignment, got odd address");
+    hipError_t err = qmoe::launch_synth_quant(dst, type, n_rows, row_len, seed, stream, sigma, (hipStream_t)hip_stream);
+    return err == hipSuccess ? QMOE_OK : hip_fail(err, "synth_quant kernel");
+}
+
+}  // extern "C"

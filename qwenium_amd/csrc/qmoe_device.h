@@ -1,0 +1,295 @@
+// qmoe_device.h -- device helpers shared by the qmoe HIP kernels (gfx950).
+//
+// Numeric contract (matches the CPU restatement in oracle/ exactly):
+//   * exp_det / log_det / cospi2_det are fixed sequences of separately
+//     rounded IEEE f64 operations (contraction disabled), so they return the
+//     same bits as any IEEE CPU running the same sequence.
+//   * Quantized block dots accumulate d_w*d_x*isum in f64.  Each term is
+//     exact in f64 (22-bit scale product x <= 19-bit integer) and the row sum
+//     stays exact for the scale ranges of these layers, so the result does
+//     not depend on summation order (lane split, butterfly, MFMA tiling).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmoe {
+
+constexpr int kTypeF32 = 0;
+constexpr int kTypeQ4_0 = 2;
+constexpr int kTypeQ8_0 = 8;
+
+template <int WT> struct BlockTraits;
+template <> struct BlockTraits<kTypeQ4_0> { static constexpr int kBytes = 18; static constexpr int kPairDwords = 9; };
+template <> struct BlockTraits<kTypeQ8_0> { static constexpr int kBytes = 34; static constexpr int kPairDwords = 17; };
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// fp16 <-> fp32 (IEEE binary16, round to nearest even)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float fp16_to_f32(uint32_t h16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h16 & 0xffffu));
+}
+__device__ __forceinline__ uint32_t f32_to_fp16(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic f64 elementary functions
+// ---------------------------------------------------------------------------
+constexpr double kLn2Hi = 6.93147180369123816490e-01;  // 32 significant bits
+constexpr double kLn2Lo = 1.90821492927058770002e-10;
+constexpr double kLog2e = 1.44269504088896338700e+00;
+
+__device__ __forceinline__ double exp_det(double x) {
+#pragma clang fp contract(off)
+    if (x != x) return x;
+    if (x > 709.78) return __builtin_huge_val();
+    if (x < -745.2) return 0.0;
+    const double k = __builtin_rint(x * kLog2e);
+    double r = x - k * kLn2Hi;
+    r = r - k * kLn2Lo;
+    // Taylor series of exp(r), |r| <= 0.347, degree 13
+    double p = 1.0 / 6227020800.0;
+    p = p * r + 1.0 / 479001600.0;
+    p = p * r + 1.0 / 39916800.0;
+    p = p * r + 1.0 / 3628800.0;
+    p = p * r + 1.0 / 362880.0;
+    p = p * r + 1.0 / 40320.0;
+    p = p * r + 1.0 / 5040.0;
+    p = p * r + 1.0 / 720.0;
+    p = p * r + 1.0 / 120.0;
+    p = p * r + 1.0 / 24.0;
+    p = p * r + 1.0 / 6.0;
+    p = p * r + 0.5;
+    p = p * r + 1.0;
+    p = p * r + 1.0;
+    return __builtin_ldexp(p, (int)k);
+}
+
+__device__ __forceinline__ double log_det(double x) {
+#pragma clang fp contract(off)
+    int e;
+    double m = __builtin_frexp(x, &e);
+    if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
+    const double s = (m - 1.0) / (m + 1.0);
+    const double s2 = s * s;
+    double p = 1.0 / 23.0;
+    p = p * s2 + 1.0 / 21.0;
+    p = p * s2 + 1.0 / 19.0;
+    p = p * s2 + 1.0 / 17.0;
+    p = p * s2 + 1.0 / 15.0;
+    p = p * s2 + 1.0 / 13.0;
+    p = p * s2 + 1.0 / 11.0;
+    p = p * s2 + 1.0 / 9.0;
+    p = p * s2 + 1.0 / 7.0;
+    p = p * s2 + 1.0 / 5.0;
+    p = p * s2 + 1.0 / 3.0;
+    p = p * s2 + 1.0;
+    const double de = (double)e;
+    return de * kLn2Hi + (de * kLn2Lo + 2.0 * s * p);
+}
+
+__device__ __forceinline__ double cospi2_det(double u) {
+#pragma clang fp contract(off)
+    const double t = u * 4.0;
+    double q = __builtin_floor(t);
+    double f = t - q;
+    if (f > 0.5) { f = f - 1.0; q = q + 1.0; }
+    const double a = f * 1.57079632679489661923;
+    const double a2 = a * a;
+    double c = 1.0 / 20922789888000.0;
+    c = c * a2 - 1.0 / 87178291200.0;
+    c = c * a2 + 1.0 / 479001600.0;
+    c = c * a2 - 1.0 / 3628800.0;
+    c = c * a2 + 1.0 / 40320.0;
+    c = c * a2 - 1.0 / 720.0;
+    c = c * a2 + 1.0 / 24.0;
+    c = c * a2 - 0.5;
+    c = c * a2 + 1.0;
+    double s = 1.0 / 355687428096000.0;
+    s = s * a2 - 1.0 / 1307674368000.0;
+    s = s * a2 + 1.0 / 6227020800.0;
+    s = s * a2 - 1.0 / 39916800.0;
+    s = s * a2 + 1.0 / 362880.0;
+    s = s * a2 - 1.0 / 5040.0;
+    s = s * a2 + 1.0 / 120.0;
+    s = s * a2 - 1.0 / 6.0;
+    s = s * a2 + 1.0;
+    s = s * a;
+    switch (((int)q) & 3) {
+        case 0: return c;
+        case 1: return -s;
+        case 2: return -c;
+        default: return s;
+    }
+}
+
+// h = silu(g) * u, evaluated in f64 and rounded once to f32.
+__device__ __forceinline__ float silu_mul_det(float g, float u) {
+#pragma clang fp contract(off)
+    const double gd = (double)g;
+    const double s = gd / (1.0 + exp_det(-gd));
+    return (float)(s * (double)u);
+}
+
+__device__ __forceinline__ float sigmoid_det(float g) {
+#pragma clang fp contract(off)
+    return (float)(1.0 / (1.0 + exp_det(-(double)g)));
+}
+
+// ---------------------------------------------------------------------------
+// Counter-based normal generator (splitmix64 finalizer + Box-Muller)
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__host__ __device__ __forceinline__ uint64_t stream_key(uint64_t seed, uint64_t stream) {
+    return mix64(seed ^ mix64(stream + 0x632BE59BD9B4E019ull));
+}
+__device__ __forceinline__ double normal_det(uint64_t key, uint64_t idx) {
+#pragma clang fp contract(off)
+    const uint64_t h1 = mix64(key ^ (2 * idx));
+    const uint64_t h2 = mix64(key ^ (2 * idx + 1));
+    const double u1 = (double)((h1 >> 11) + 1) * (1.0 / 9007199254740992.0);
+    const double u2 = (double)(h2 >> 11) * (1.0 / 9007199254740992.0);
+    const double r = __builtin_sqrt(-2.0 * log_det(u1));
+    return r * cospi2_det(u2);
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level reductions (wave64; WIDTH lanes per independent group)
+// ---------------------------------------------------------------------------
+template <int WIDTH>
+__device__ __forceinline__ double group_sum_f64(double v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ int group_sum_i32(int v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ float group_max_f32(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Quantized weight pair loaders.  A "pair" is two consecutive 32-value blocks
+// of one row: 36 bytes (Q4_0) or 68 bytes (Q8_0), starting 4-byte aligned
+// when the row starts 4-byte aligned.  Loads are dword-aligned dwordx4.
+// ---------------------------------------------------------------------------
+template <int WT> struct WPair;
+
+template <> struct WPair<kTypeQ4_0> {
+    uint32_t w[9];
+    __device__ __forceinline__ void load(const uint8_t* row, int pair) {
+        const uint32_t* b = (const uint32_t*)(row + 36 * pair);
+        const u32x4a4 a0 = *(const u32x4a4*)(b);
+        const u32x4a4 a1 = *(const u32x4a4*)(b + 4);
+        w[0] = a0.x; w[1] = a0.y; w[2] = a0.z; w[3] = a0.w;
+        w[4] = a1.x; w[5] = a1.y; w[6] = a1.z; w[7] = a1.w;
+        w[8] = b[8];
+    }
+    // scales (as f32) of block A and block B
+    __device__ __forceinline__ float dA() const { return fp16_to_f32(w[0]); }
+    __device__ __forceinline__ float dB() const { return fp16_to_f32(w[4] >> 16); }
+    // integer dot of block A / B against 32 int8 activations xs[0..7] (dwords);
+    // returns sum_j (q_j - 8) * x_j given xsum = sum_j x_j
+    __device__ __forceinline__ int dotA(const uint32_t* xs, int xsum) const {
+        int acc = -8 * xsum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+            acc = __builtin_amdgcn_sdot4((int)(q & 0x0f0f0f0fu), (int)xs[i], acc, false);
+            acc = __builtin_amdgcn_sdot4((int)((q >> 4) & 0x0f0f0f0fu), (int)xs[4 + i], acc, false);
+        }
+        return acc;
+    }
+    __device__ __forceinline__ int dotB(const uint32_t* xs, int xsum) const {
+        int acc = -8 * xsum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = w[5 + i];
+            acc = __builtin_amdgcn_sdot4((int)(q & 0x0f0f0f0fu), (int)xs[i], acc, false);
+            acc = __builtin_amdgcn_sdot4((int)((q >> 4) & 0x0f0f0f0fu), (int)xs[4 + i], acc, false);
+        }
+        return acc;
+    }
+};
+
+template <> struct WPair<kTypeQ8_0> {
+    uint32_t w[17];
+    __device__ __forceinline__ void load(const uint8_t* row, int pair) {
+        const uint32_t* b = (const uint32_t*)(row + 68 * pair);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4a4 a = *(const u32x4a4*)(b + 4 * i);
+            w[4 * i + 0] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
+        }
+        w[16] = b[16];
+    }
+    __device__ __forceinline__ float dA() const { return fp16_to_f32(w[0]); }
+    __device__ __forceinline__ float dB() const { return fp16_to_f32(w[8] >> 16); }
+    __device__ __forceinline__ int dotA(const uint32_t* xs, int /*xsum*/) const {
+        int acc = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t q = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+            acc = __builtin_amdgcn_sdot4((int)q, (int)xs[i], acc, false);
+        }
+        return acc;
+    }
+    __device__ __forceinline__ int dotB(const uint32_t* xs, int /*xsum*/) const {
+        int acc = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = __builtin_amdgcn_sdot4((int)w[9 + i], (int)xs[i], acc, false);
+        return acc;
+    }
+};
+
+// Activation pair in the workspace layout: qs[64] int8 + {dA, sumA, dB, sumB}.
+struct XPair {
+    uint32_t xs[16];
+    float dA, dB;
+    int sA, sB;
+    __device__ __forceinline__ void load(const int8_t* qs_row, const float2* ds_row, int pair) {
+        const u32x4* q = (const u32x4*)(qs_row + 64 * pair);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 v = q[i];
+            xs[4 * i + 0] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
+        }
+        // {dA, sumA, dB, sumB}: loaded as integers and bit-cast as scalars (a
+        // bit_cast of an ext-vector element reads element 0 in this compiler)
+        const u32x4 d = *(const u32x4*)(ds_row + 2 * pair);
+        const uint32_t da = d.x, sa = d.y, db = d.z, sb = d.w;
+        dA = __builtin_bit_cast(float, da);
+        sA = (int)sa;
+        dB = __builtin_bit_cast(float, db);
+        sB = (int)sb;
+    }
+};
+
+// Exact contribution of one weight pair against one activation pair (f64).
+template <int WT>
+__device__ __forceinline__ double pair_dot(const WPair<WT>& w, const XPair& x) {
+    const int ia = w.dotA(x.xs, x.sA);
+    const int ib = w.dotB(x.xs + 8, x.sB);
+    const float ca = w.dA() * x.dA;  // exact: two 11-bit significands
+    const float cb = w.dB() * x.dB;
+    return __builtin_fma((double)ca, (double)ia, (double)cb * (double)ib);
+}
+
+}  // namespace qmoe

@@ -1,0 +1,73 @@
+// qmoe_internal.h -- host-side layer/workspace structures and kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmoe {
+
+// Tokens handled by one top-k block; the per-block histogram granularity of
+// the stable counting sort.
+constexpr int kTopkTokensPerBlock = 16;
+// Row tile of the prefill grouped GEMM (rows of one expert per tile).
+constexpr int kMfmaTileM = 64;
+
+struct LayerDesc {
+    int H = 0, E = 0, K = 0, F = 0, S = 0;  // n_embd, n_experts, top_k, ffn_dim, shared (0/1)
+    int gu_type = 0, dn_type = 0;           // gate/up type, down type (Q4_0 or Q8_0)
+    const float* w_router = nullptr;
+    uint64_t router_ld = 0;                 // row stride in floats
+    const uint8_t* w_gate = nullptr;
+    const uint8_t* w_up = nullptr;
+    uint64_t gate_nb1 = 0, gate_nb2 = 0, up_nb1 = 0, up_nb2 = 0;
+    const uint8_t* w_down = nullptr;
+    uint64_t down_nb1 = 0, down_nb2 = 0;
+    const uint8_t* w_sh_gate = nullptr;
+    const uint8_t* w_sh_up = nullptr;
+    const uint8_t* w_sh_down = nullptr;
+    uint64_t sh_gate_nb1 = 0, sh_up_nb1 = 0, sh_down_nb1 = 0;
+    const float* w_sh_norm = nullptr;
+};
+
+// Device scratch.  R = T*K + S*T rows: routed assignments sorted by expert,
+// then the shared expert's rows in token order.
+struct Workspace {
+    int cap_T = 0, H = 0, E = 0, K = 0, F = 0;
+    void* base = nullptr;
+    size_t bytes = 0;
+    int8_t* xq_qs = nullptr;      // [T][H]   Q8_0 activation quants
+    float2* xq_ds = nullptr;      // [T][H/32] {d, bitcast(sum q)}
+    float* logits = nullptr;      // [T][E+1] (column E: shared gate logit)
+    int32_t* topk_idx = nullptr;  // [T][K]
+    float* topk_w = nullptr;      // [T][K]
+    float* sh_gate = nullptr;     // [T]
+    int32_t* local_rank = nullptr;  // [T*K]
+    int32_t* hist = nullptr;      // [nblk][E] per top-k block counts -> bases
+    int32_t* offsets = nullptr;   // [E+2]
+    int32_t* rows = nullptr;      // [R] assignment id (t*K+j); shared rows: -1
+    int32_t* row_token = nullptr; // [R]
+    int32_t* pos = nullptr;       // [T*K] position of assignment
+    int32_t* active = nullptr;    // [E+1] active experts (ascending), shared (=E) last
+    int32_t* counters = nullptr;  // [16] n_active, n_tiles, ...
+    int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
+    int8_t* hq_qs = nullptr;      // [R][F]
+    float2* hq_ds = nullptr;      // [R][F/32]
+    float* ybuf = nullptr;        // [R][H] down outputs (unweighted)
+    int max_tiles = 0;
+};
+
+size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* carve, void* base);
+
+// --- launchers (each enqueues on `stream`, returns hipError_t of the launch) ---
+hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, hipStream_t stream);
+hipError_t launch_experts_gemv(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+hipError_t launch_experts_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+hipError_t launch_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
+                          hipStream_t stream);
+hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream);
+hipError_t launch_synth_f32(float* dst, int64_t n, uint64_t seed, uint64_t stream_id, double mean, double sigma,
+                            hipStream_t stream);
+hipError_t launch_synth_quant(void* dst, int type, int64_t n_rows, int64_t row_len, uint64_t seed,
+                              uint64_t stream_id, double sigma, hipStream_t stream);
+
+}  // namespace qmoe

@@ -1,0 +1,173 @@
+"""Python mirror of the reference's MoE layer module over libqmoe's C ABI.
+
+Reference interface (rye-001/Qwenium):
+  MoELayer::Hparams           src/layers/moe.h:34-39
+  MoELayer::MoELayer(8 slots) src/layers/moe.h:44-53, src/layers/moe.cpp:27-53
+  MoELayer::build(...)        src/layers/moe.h:58-63  -> MoELayer.forward here
+  build_rms_norm(...)         src/layers/norm.cpp:15-26 -> rms_norm here
+
+torch supplies device memory and the current HIP stream only; every
+computation runs in libqmoe's HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, QmoeDebug, QmoeHparams, check, lib, make_tensor, row_bytes
+
+
+class Phase:
+    """layer.h:19-22; accepted by forward() for interface symmetry and ignored."""
+    Prefill = 0
+    Decode = 1
+
+
+@dataclasses.dataclass
+class Hparams:
+    n_experts: int
+    top_k: int
+    ffn_dim: int
+    has_shared_expert: bool
+
+
+@dataclasses.dataclass
+class GGMLTensor:
+    """A device tensor in ggml/GGUF layout: raw bytes (uint8) or f32 data plus
+    the ggml type id and ne (ne[0] contiguous)."""
+    data: torch.Tensor
+    type: int
+    ne: tuple
+
+    def desc(self) -> _lib.QmoeTensor:
+        if not self.data.is_contiguous():
+            raise ValueError("GGMLTensor.data must be contiguous")
+        return make_tensor(self.data.data_ptr(), self.type, tuple(self.ne))
+
+
+def _stream_ptr(stream) -> Optional[int]:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+class Workspace:
+    """Scratch for up to max_tokens tokens of layers no larger than `like`."""
+
+    def __init__(self, like: "MoELayer", max_tokens: int):
+        h = ctypes.c_void_p()
+        check(lib().qmoe_workspace_create(like._handle, int(max_tokens), ctypes.byref(h)))
+        self._handle = h
+
+    @property
+    def capacity(self) -> int:
+        return int(lib().qmoe_workspace_capacity(self._handle))
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            lib().qmoe_workspace_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MoELayer:
+    """Same slot order and hparams as the reference's MoELayer constructor."""
+
+    def __init__(self, w_router: GGMLTensor, w_exp_gate: GGMLTensor, w_exp_up: GGMLTensor,
+                 w_exp_down: GGMLTensor, w_sh_gate: Optional[GGMLTensor], w_sh_up: Optional[GGMLTensor],
+                 w_sh_down: Optional[GGMLTensor], w_sh_norm: Optional[GGMLTensor], hp: Hparams):
+        self.hp = hp
+        # keep the borrowed weights alive for the layer's lifetime
+        self._weights = (w_router, w_exp_gate, w_exp_up, w_exp_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_norm)
+        descs = [w.desc() if w is not None else None for w in self._weights]
+        ptrs = [ctypes.byref(d) if d is not None else None for d in descs]
+        c_hp = QmoeHparams(int(hp.n_experts), int(hp.top_k), int(hp.ffn_dim), 1 if hp.has_shared_expert else 0)
+        h = ctypes.c_void_p()
+        check(lib().qmoe_layer_create(*ptrs, ctypes.byref(c_hp), ctypes.byref(h)))
+        self._handle = h
+        self.n_embd = int(lib().qmoe_layer_n_embd(h))
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            lib().qmoe_layer_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, x: torch.Tensor, phase: int = Phase.Prefill, il: int = 0, *,
+                residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                workspace: Optional[Workspace] = None, debug: bool = False, stream=None):
+        """y[T][n_embd] = MoE(x) (+ residual).  With debug=True also returns the
+        routing intermediates (logits, topk_idx, topk_w, sh_gate, offsets, rows)."""
+        del phase, il  # MoE has one topology (moe.h:55-57); il only names tensors in ggml
+        if x.dim() != 2 or x.shape[1] != self.n_embd or x.dtype != torch.float32 or not x.is_cuda:
+            raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got "
+                             f"{tuple(x.shape)} {x.dtype} on {x.device}")
+        x = x.contiguous()
+        T = x.shape[0]
+        y = out if out is not None else torch.empty_like(x)
+        dbg = None
+        dbg_tensors = None
+        if debug:
+            E, k = self.hp.n_experts, self.hp.top_k
+            dev = x.device
+            dbg_tensors = {
+                "logits": torch.empty((T, E), dtype=torch.float32, device=dev),
+                "topk_idx": torch.empty((T, k), dtype=torch.int32, device=dev),
+                "topk_w": torch.empty((T, k), dtype=torch.float32, device=dev),
+                "sh_gate": torch.empty((T,), dtype=torch.float32, device=dev),
+                "offsets": torch.empty((E + 1,), dtype=torch.int32, device=dev),
+                "rows": torch.empty((T * k,), dtype=torch.int32, device=dev),
+            }
+            dbg = QmoeDebug(*(dbg_tensors[n].data_ptr() for n in
+                              ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows")))
+        check(lib().qmoe_layer_forward(
+            self._handle, workspace._handle if workspace is not None else None,
+            x.data_ptr(), int(T), y.data_ptr(),
+            residual.contiguous().data_ptr() if residual is not None else None,
+            ctypes.byref(dbg) if dbg is not None else None, _stream_ptr(stream)))
+        if debug:
+            return y, dbg_tensors
+        return y
+
+    __call__ = forward
+
+
+def rms_norm(x: torch.Tensor, w: Optional[torch.Tensor], eps: float, out: Optional[torch.Tensor] = None,
+             stream=None) -> torch.Tensor:
+    """build_rms_norm (norm.cpp:15-26): x / sqrt(mean(x^2) + eps) * w, per token."""
+    x = x.contiguous()
+    y = out if out is not None else torch.empty_like(x)
+    check(lib().qmoe_rms_norm(x.data_ptr(), w.data_ptr() if w is not None else None, int(x.shape[0]),
+                              int(x.shape[1]), float(eps), y.data_ptr(), _stream_ptr(stream)))
+    return y
+
+
+def synth_f32(n: int, seed: int, stream_id: int, mean: float = 0.0, sigma: float = 1.0,
+              device="cuda", out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    y = out if out is not None else torch.empty((n,), dtype=torch.float32, device=device)
+    check(lib().qmoe_synth_f32(y.data_ptr(), int(n), int(seed), int(stream_id), float(mean), float(sigma),
+                               _stream_ptr(stream)))
+    return y
+
+
+def synth_quant(type_id: int, n_rows: int, row_len: int, seed: int, stream_id: int, sigma: float,
+                device="cuda", out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    nbytes = n_rows * row_bytes(type_id, row_len)
+    y = out if out is not None else torch.empty((nbytes,), dtype=torch.uint8, device=device)
+    check(lib().qmoe_synth_quant(y.data_ptr(), int(type_id), int(n_rows), int(row_len), int(seed),
+                                 int(stream_id), float(sigma), _stream_ptr(stream)))
+    return y
