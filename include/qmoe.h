@@ -124,6 +124,15 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
                        const float* residual, const qmoe_debug* dbg,
                        void* hip_stream);
 
+/* Optional per-phase timing for benchmarks and profilers.  events points to
+ * QMOE_N_PHASE_EVENTS hipEvent_t created by the caller (or is NULL to disable).
+ * While set, each qmoe_layer_forward records them on its stream: [0] before
+ * routing, [1] after routing, [2] after the gate/up expert kernel, [3] after
+ * the down expert kernel, [4] after the combine.  No counterpart in the
+ * reference (ggml schedules the graph itself). */
+#define QMOE_N_PHASE_EVENTS 5
+int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events);
+
 /* Replaces build_rms_norm (norm.cpp:15-26): y = x / sqrt(mean(x^2) + eps) * w,
  * per token (ggml_rms_norm followed by ggml_mul).  w may be NULL (no scale). */
 int qmoe_rms_norm(const float* x, const float* w, int32_t n_tokens, int32_t n_embd,

@@ -33,6 +33,7 @@ EXPORTED = (
     "qmoe_workspace_destroy",
     "qmoe_workspace_capacity",
     "qmoe_layer_forward",
+    "qmoe_layer_set_phase_events",
     "qmoe_rms_norm",
     "qmoe_synth_f32",
     "qmoe_synth_quant",
@@ -106,6 +107,8 @@ def lib() -> ctypes.CDLL:
     L.qmoe_workspace_capacity.argtypes = [vp]
     L.qmoe_layer_forward.restype = ctypes.c_int
     L.qmoe_layer_forward.argtypes = [vp, vp, vp, ctypes.c_int32, vp, vp, P(QmoeDebug), vp]
+    L.qmoe_layer_set_phase_events.restype = ctypes.c_int
+    L.qmoe_layer_set_phase_events.argtypes = [vp, P(vp)]
     L.qmoe_rms_norm.restype = ctypes.c_int
     L.qmoe_rms_norm.argtypes = [vp, vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, vp, vp]
     L.qmoe_synth_f32.restype = ctypes.c_int

@@ -13,6 +13,8 @@
 #include "qmoe_device.h"
 #include "qmoe_internal.h"
 
+#include <algorithm>
+
 namespace qmoe {
 
 struct ExpertArgs {
@@ -21,211 +23,260 @@ struct ExpertArgs {
     const uint8_t* w_down; uint64_t down_nb1, down_nb2;
     const uint8_t* w_sh_gate; const uint8_t* w_sh_up; const uint8_t* w_sh_down;
     uint64_t sh_gate_nb1, sh_up_nb1, sh_down_nb1;
-    const int32_t* active;     // [E+1]
     const int32_t* counters;   // [0] n_active
+    const int4* slot_info;     // [E+1] {expert, first row, rows, token of first row}
     const int32_t* offsets;    // [E+2]
     const int32_t* row_token;  // [R]
     const int8_t* xq_qs; const float2* xq_ds;  // [T][H], [T][H/32]
-    int8_t* hq_qs; float2* hq_ds;              // [R][F], [R][F/32]
-    float* ybuf;                               // [R][H]
+    float2* gubuf;                             // [R][F] (gate, up) projections (f32)
+    int8_t* hq_qs; float2* hq_ds;              // [R][F], [R][F/32] Q8_0 of hbuf
+    float* ybuf;                               // [R][H] down outputs (unweighted)
 };
 
-// ---------------------------------------------------------------------------
-// G1: gate + up + SwiGLU + Q8_0 quantization of h.
-// Block = 4 waves = 32 consecutive ffn rows of one active expert (one Q8_0
-// block of h).  Wave w owns rows f0+8w .. f0+8w+7 of gate and of up.
-// LPR lanes cover one H row (LPR = min(64, H/64) pairs); RPI = 64/LPR rows
-// are loaded per instruction.
-// ---------------------------------------------------------------------------
-constexpr int kGuRowsPerWave = 8;
-constexpr int kGuTokChunk = 2;
+// Loads the slot table into LDS (all E+1 entries; those past n_active are
+// never read) and returns n_active.  One latency at kernel start.
+__device__ __forceinline__ int stage_slots(const ExpertArgs& a, int4* s_slots, int* s_nact) {
+    for (int i = threadIdx.x; i <= a.E; i += blockDim.x) s_slots[i] = a.slot_info[i];
+    if (threadIdx.x == 0) *s_nact = a.counters[0];
+    __syncthreads();
+    return *s_nact;
+}
 
-template <int WT, int LPR>
-__global__ __launch_bounds__(256) void k_gateup_gemv(ExpertArgs a) {
+// ---------------------------------------------------------------------------
+// G1: gate + up projections -> gubuf (f32 pairs), persistent streaming.
+// Work item = (active slot, group of RPW consecutive ffn rows of gate and up).
+// Items are strided over all waves (consecutive waves take consecutive row
+// groups of one expert); each wave prefetches the next item's weights and
+// first-token activations while it computes the current item.  LPR lanes
+// cover one H row (lane lp owns 64-value pair lp); RPI = 64/LPR rows per load
+// instruction, NI = RPW/RPI loads per matrix.
+// ---------------------------------------------------------------------------
+template <int WT, int LPR, int RPW>
+struct GuItem {
+    static constexpr int RPI = 64 / LPR;
+    static constexpr int NI = RPW / RPI;
+    WPair<WT> wg[NI], wu[NI];
+    XPair x;
+    int e, p0, nrows, f0;
+};
+
+template <int WT, int LPR, int RPW>
+__device__ __forceinline__ void gu_load(const ExpertArgs& a, const int4* s_slots, int item, int ips, int sub, int lp,
+                                        GuItem<WT, LPR, RPW>& it) {
     constexpr int RPI = 64 / LPR;
-    constexpr int NI = kGuRowsPerWave / RPI;   // loads per matrix per wave
-    const int slot = blockIdx.x;
-    if (slot >= a.counters[0]) return;
-    const int e = a.active[slot];
-    const int f0 = blockIdx.y * 32;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int sub = lane / LPR;       // row inside an instruction
-    const int lp = lane % LPR;        // lane inside the row
-    const int npairs = a.H >> 6;
-
-    const uint8_t* gbase; const uint8_t* ubase; uint64_t gnb1, unb1;
-    if (e < a.E) {
-        gbase = a.w_gate + (uint64_t)e * a.gate_nb2; gnb1 = a.gate_nb1;
-        ubase = a.w_up + (uint64_t)e * a.up_nb2; unb1 = a.up_nb1;
-    } else {
-        gbase = a.w_sh_gate; gnb1 = a.sh_gate_nb1;
-        ubase = a.w_sh_up; unb1 = a.sh_up_nb1;
+    constexpr int NI = RPW / RPI;
+    const int4 si = s_slots[item / ips];
+    it.e = si.x; it.p0 = si.y; it.nrows = si.z;
+    it.f0 = (item % ips) * RPW;
+    const int tok = si.w;
+    const bool sh = it.e >= a.E;
+    const uint8_t* gb = sh ? a.w_sh_gate : a.w_gate + (uint64_t)it.e * a.gate_nb2;
+    const uint8_t* ub = sh ? a.w_sh_up : a.w_up + (uint64_t)it.e * a.up_nb2;
+    const uint64_t gnb1 = sh ? a.sh_gate_nb1 : a.gate_nb1;
+    const uint64_t unb1 = sh ? a.sh_up_nb1 : a.up_nb1;
+    const int pair = min(lp, (a.H >> 6) - 1);  // lanes past the row re-read the last pair; their sums are dropped
+#pragma unroll
+    for (int m = 0; m < NI; ++m) {
+        const int f = it.f0 + m * RPI + sub;
+        it.wg[m].load(gb + (uint64_t)f * gnb1, pair);
+        it.wu[m].load(ub + (uint64_t)f * unb1, pair);
     }
-    const int p0 = a.offsets[e];
-    const int nrows = a.offsets[e + 1] - p0;
+    it.x.load(a.xq_qs + (uint64_t)tok * a.H, a.xq_ds + (uint64_t)tok * (a.H >> 5), pair);
+}
 
-    __shared__ float s_h[kGuTokChunk][32];
-
-    // rows of this wave: f = f0 + 8*wave + m*RPI + sub, m < NI
-    const int npass = (npairs + LPR - 1) / LPR;  // pair groups per lane (1 for H <= 64*LPR)
-
-    for (int c0 = 0; c0 < nrows; c0 += kGuTokChunk) {
-        const int nc = min(kGuTokChunk, nrows - c0);
-        double acc_g[NI][kGuTokChunk];
-        double acc_u[NI][kGuTokChunk];
-#pragma unroll
-        for (int m = 0; m < NI; ++m)
-#pragma unroll
-            for (int c = 0; c < kGuTokChunk; ++c) { acc_g[m][c] = 0.0; acc_u[m][c] = 0.0; }
-
-        for (int ps = 0; ps < npass; ++ps) {
-            const int pair = lp + ps * LPR;
-            if (pair < npairs) {
-                WPair<WT> wg[NI], wu[NI];
-#pragma unroll
-                for (int m = 0; m < NI; ++m) {
-                    const int f = f0 + kGuRowsPerWave * wave + m * RPI + sub;
-                    wg[m].load(gbase + (uint64_t)f * gnb1, pair);
-                    wu[m].load(ubase + (uint64_t)f * unb1, pair);
-                }
-#pragma unroll
-                for (int c = 0; c < kGuTokChunk; ++c) {
-                    if (c < nc) {
-                        const int t = a.row_token[p0 + c0 + c];
-                        XPair xp;
-                        xp.load(a.xq_qs + (uint64_t)t * a.H, a.xq_ds + (uint64_t)t * (a.H >> 5), pair);
-#pragma unroll
-                        for (int m = 0; m < NI; ++m) {
-                            acc_g[m][c] += pair_dot<WT>(wg[m], xp);
-                            acc_u[m][c] += pair_dot<WT>(wu[m], xp);
-                        }
-                    }
-                }
-            }
+template <int WT, int LPR, int RPW>
+__device__ __forceinline__ void gu_compute(const ExpertArgs& a, const GuItem<WT, LPR, RPW>& it, int sub, int lp) {
+    constexpr int RPI = 64 / LPR;
+    constexpr int NI = RPW / RPI;
+    const bool live = lp < (a.H >> 6);
+    XPair x = it.x;
+    for (int c = 0; c < it.nrows; ++c) {
+        if (c > 0) {
+            const int tok = it.e >= a.E ? c : a.row_token[it.p0 + c];
+            x.load(a.xq_qs + (uint64_t)tok * a.H, a.xq_ds + (uint64_t)tok * (a.H >> 5), min(lp, (a.H >> 6) - 1));
         }
-        // reduce over the LPR lanes of each row; SwiGLU into LDS
 #pragma unroll
-        for (int c = 0; c < kGuTokChunk; ++c) {
-#pragma unroll
-            for (int m = 0; m < NI; ++m) {
-                const double g = group_sum_f64<LPR>(acc_g[m][c]);
-                const double u = group_sum_f64<LPR>(acc_u[m][c]);
-                if (lp == 0 && c < nc) {
-                    const int fl = kGuRowsPerWave * wave + m * RPI + sub;
-                    s_h[c][fl] = silu_mul_det((float)g, (float)u);
-                }
-            }
+        for (int m = 0; m < NI; ++m) {
+            const double g = dpp_sum_f64<LPR>(live ? pair_dot<WT>(it.wg[m], x) : 0.0);
+            const double u = dpp_sum_f64<LPR>(live ? pair_dot<WT>(it.wu[m], x) : 0.0);
+            if (lp == LPR - 1) a.gubuf[(uint64_t)(it.p0 + c) * a.F + it.f0 + m * RPI + sub] = make_float2((float)g, (float)u);
         }
-        __syncthreads();
-        // Q8_0 quantization of each h row block (wave c handles token c)
-        if (wave < nc) {
-            const int c = wave;
-            const float v = lane < 32 ? s_h[c][lane] : 0.0f;
-            const float amax = group_max_f32<32>(__builtin_fabsf(v));
-            const float d = amax / 127.0f;
-            const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-            const int q = (int)__builtin_rintf(v * id);
-            const int sum = group_sum_i32<32>(q);
-            const int p = p0 + c0 + c;
-            if (lane < 32) a.hq_qs[(uint64_t)p * a.F + f0 + lane] = (int8_t)q;
-            if (lane == 0)
-                a.hq_ds[(uint64_t)p * (a.F >> 5) + blockIdx.y] =
-                    make_float2(fp16_to_f32(f32_to_fp16(d)), __builtin_bit_cast(float, sum));
-        }
-        __syncthreads();
+    }
+}
+
+template <int WT, int LPR, int RPW>
+__global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    __shared__ int s_nact;
+    int4* s_slots = (int4*)s_dyn;
+    const int n_act = stage_slots(a, s_slots, &s_nact);
+    const int ips = a.F / RPW;
+    const int n_items = n_act * ips;
+    const int lane = threadIdx.x & 63;
+    const int sub = lane / LPR, lp = lane % LPR;
+    const int tw = gridDim.x * (blockDim.x >> 6);
+    int item = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (item >= n_items) return;
+    // ping-pong: while one buffer is computed the other one's loads are in flight
+    GuItem<WT, LPR, RPW> b0, b1;
+    gu_load(a, s_slots, item, ips, sub, lp, b0);
+    for (;;) {
+        int nitem = item + tw;
+        if (nitem < n_items) gu_load(a, s_slots, nitem, ips, sub, lp, b1);
+        gu_compute(a, b0, sub, lp);
+        if (nitem >= n_items) break;
+        item = nitem;
+        nitem = item + tw;
+        if (nitem < n_items) gu_load(a, s_slots, nitem, ips, sub, lp, b0);
+        gu_compute(a, b1, sub, lp);
+        if (nitem >= n_items) break;
+        item = nitem;
     }
 }
 
 // ---------------------------------------------------------------------------
-// G2: down projection for every row of an active expert.  Block = 4 waves =
-// 64 consecutive output rows n; each wave owns 16 of them.  LPR lanes cover one
-// F row.  Writes ybuf[p][n] (unweighted expert output).
+// Q: SwiGLU h = silu(g)*u of each (row, ffn index), then Q8_0 quantization of
+// the h rows (the activation quantization ggml applies to src1 of the down
+// mul_mat_id).  One 32-lane group per block of 32 values.
 // ---------------------------------------------------------------------------
-constexpr int kDnRowsPerWave = 16;
-constexpr int kDnTokChunk = 4;
+__global__ __launch_bounds__(256) void k_quant_h(ExpertArgs a) {
+    const int nrows = a.offsets[a.E + 1];
+    const int nblk = a.F >> 5;
+    const int g = blockIdx.x * 8 + (threadIdx.x >> 5);
+    if (g >= nrows * nblk) return;
+    const int p = g / nblk, b = g % nblk, l32 = threadIdx.x & 31;
+    const float2 gu = a.gubuf[(uint64_t)p * a.F + 32 * b + l32];
+    const float v = silu_mul_det(gu.x, gu.y);  // h = silu(g) * u
+    const float amax = group_max_f32<32>(__builtin_fabsf(v));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const int q = (int)__builtin_rintf(v * id);
+    const int sum = group_sum_i32<32>(q);
+    a.hq_qs[(uint64_t)p * a.F + 32 * b + l32] = (int8_t)q;
+    if (l32 == 0) a.hq_ds[(uint64_t)p * nblk + b] = make_float2(fp16_to_f32(f32_to_fp16(d)), __builtin_bit_cast(float, sum));
+}
 
-template <int WT, int LPR>
-__global__ __launch_bounds__(256) void k_down_gemv(ExpertArgs a) {
+// ---------------------------------------------------------------------------
+// G2: down projection, persistent streaming.  Work item = (active slot, group
+// of RPW consecutive output rows n).  LPR lanes per F row.  Writes ybuf[p][n].
+// ---------------------------------------------------------------------------
+template <int WT, int LPR, int RPW>
+struct DnItem {
+    static constexpr int RPI = 64 / LPR;
+    static constexpr int NI = RPW / RPI;
+    WPair<WT> w[NI];
+    XPair x;
+    int e, p0, nrows, n0;
+};
+
+template <int WT, int LPR, int RPW>
+__device__ __forceinline__ void dn_load(const ExpertArgs& a, const int4* s_slots, int item, int ips, int sub, int lp,
+                                        DnItem<WT, LPR, RPW>& it) {
     constexpr int RPI = 64 / LPR;
-    constexpr int NI = kDnRowsPerWave / RPI;
-    const int slot = blockIdx.x;
-    if (slot >= a.counters[0]) return;
-    const int e = a.active[slot];
-    const int n0 = blockIdx.y * 64;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int sub = lane / LPR;
-    const int lp = lane % LPR;
-    const int npairs = a.F >> 6;
-    const int npass = (npairs + LPR - 1) / LPR;
+    constexpr int NI = RPW / RPI;
+    const int4 si = s_slots[item / ips];
+    it.e = si.x; it.p0 = si.y; it.nrows = si.z;
+    it.n0 = (item % ips) * RPW;
+    const bool sh = it.e >= a.E;
+    const uint8_t* db = sh ? a.w_sh_down : a.w_down + (uint64_t)it.e * a.down_nb2;
+    const uint64_t dnb1 = sh ? a.sh_down_nb1 : a.down_nb1;
+    const int pair = min(lp, (a.F >> 6) - 1);
+#pragma unroll
+    for (int m = 0; m < NI; ++m) it.w[m].load(db + (uint64_t)(it.n0 + m * RPI + sub) * dnb1, pair);
+    it.x.load(a.hq_qs + (uint64_t)it.p0 * a.F, a.hq_ds + (uint64_t)it.p0 * (a.F >> 5), pair);
+}
 
-    const uint8_t* dbase; uint64_t dnb1;
-    if (e < a.E) { dbase = a.w_down + (uint64_t)e * a.down_nb2; dnb1 = a.down_nb1; }
-    else { dbase = a.w_sh_down; dnb1 = a.sh_down_nb1; }
-    const int p0 = a.offsets[e];
-    const int nrows = a.offsets[e + 1] - p0;
-
-    for (int c0 = 0; c0 < nrows; c0 += kDnTokChunk) {
-        const int nc = min(kDnTokChunk, nrows - c0);
-        double acc[NI][kDnTokChunk];
+template <int WT, int LPR, int RPW>
+__device__ __forceinline__ void dn_compute(const ExpertArgs& a, const DnItem<WT, LPR, RPW>& it, int sub, int lp) {
+    constexpr int RPI = 64 / LPR;
+    constexpr int NI = RPW / RPI;
+    const bool live = lp < (a.F >> 6);
+    XPair x = it.x;
+    for (int c = 0; c < it.nrows; ++c) {
+        const int p = it.p0 + c;
+        if (c > 0) x.load(a.hq_qs + (uint64_t)p * a.F, a.hq_ds + (uint64_t)p * (a.F >> 5), min(lp, (a.F >> 6) - 1));
 #pragma unroll
-        for (int m = 0; m < NI; ++m)
-#pragma unroll
-            for (int c = 0; c < kDnTokChunk; ++c) acc[m][c] = 0.0;
-        for (int ps = 0; ps < npass; ++ps) {
-            const int pair = lp + ps * LPR;
-            if (pair < npairs) {
-                WPair<WT> wd[NI];
-#pragma unroll
-                for (int m = 0; m < NI; ++m) {
-                    const int n = n0 + kDnRowsPerWave * wave + m * RPI + sub;
-                    wd[m].load(dbase + (uint64_t)n * dnb1, pair);
-                }
-#pragma unroll
-                for (int c = 0; c < kDnTokChunk; ++c) {
-                    if (c < nc) {
-                        const int p = p0 + c0 + c;
-                        XPair xp;
-                        xp.load(a.hq_qs + (uint64_t)p * a.F, a.hq_ds + (uint64_t)p * (a.F >> 5), pair);
-#pragma unroll
-                        for (int m = 0; m < NI; ++m) acc[m][c] += pair_dot<WT>(wd[m], xp);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < kDnTokChunk; ++c) {
-#pragma unroll
-            for (int m = 0; m < NI; ++m) {
-                const double y = group_sum_f64<LPR>(acc[m][c]);
-                if (lp == 0 && c < nc) {
-                    const int n = n0 + kDnRowsPerWave * wave + m * RPI + sub;
-                    a.ybuf[(uint64_t)(p0 + c0 + c) * a.H + n] = (float)y;
-                }
-            }
+        for (int m = 0; m < NI; ++m) {
+            const double y = dpp_sum_f64<LPR>(live ? pair_dot<WT>(it.w[m], x) : 0.0);
+            if (lp == LPR - 1) a.ybuf[(uint64_t)p * a.H + it.n0 + m * RPI + sub] = (float)y;
         }
     }
+}
+
+template <int WT, int LPR, int RPW>
+__global__ __launch_bounds__(256) void k_down_stream(ExpertArgs a) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    __shared__ int s_nact;
+    int4* s_slots = (int4*)s_dyn;
+    const int n_act = stage_slots(a, s_slots, &s_nact);
+    const int ips = a.H / RPW;
+    const int n_items = n_act * ips;
+    const int lane = threadIdx.x & 63;
+    const int sub = lane / LPR, lp = lane % LPR;
+    const int tw = gridDim.x * (blockDim.x >> 6);
+    int item = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (item >= n_items) return;
+    DnItem<WT, LPR, RPW> b0, b1;
+    dn_load(a, s_slots, item, ips, sub, lp, b0);
+    for (;;) {
+        int nitem = item + tw;
+        if (nitem < n_items) dn_load(a, s_slots, nitem, ips, sub, lp, b1);
+        dn_compute(a, b0, sub, lp);
+        if (nitem >= n_items) break;
+        item = nitem;
+        nitem = item + tw;
+        if (nitem < n_items) dn_load(a, s_slots, nitem, ips, sub, lp, b0);
+        dn_compute(a, b1, sub, lp);
+        if (nitem >= n_items) break;
+        item = nitem;
+    }
+}
+
+// Persistent grid: every block resident at once (blocks per CU from the
+// occupancy calculator), never more waves than items.
+template <typename KernelT>
+static int stream_blocks(KernelT kernel, size_t lds, int n_items_max, int n_cu) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    const int want = (n_items_max + 3) / 4;
+    return std::max(1, std::min(want, n_cu * per_cu));
+}
+
+template <int WT, int LPR, int RPW>
+static hipError_t launch_gateup_v(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
+    const size_t lds = (size_t)(a.E + 1) * sizeof(int4);
+    auto kern = k_gateup_stream<WT, LPR, RPW>;
+    const int g = stream_blocks(kern, lds, max_slots * (a.F / RPW), n_cu);
+    hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+    return hipGetLastError();
 }
 
 template <int WT>
-static hipError_t launch_gateup(const ExpertArgs& a, int max_slots, hipStream_t stream) {
-    const dim3 grid(max_slots, a.F / 32), block(256);
+static hipError_t launch_gateup(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
     const int npairs = a.H / 64;
-    if (npairs >= 32) hipLaunchKernelGGL((k_gateup_gemv<WT, 32>), grid, block, 0, stream, a);
-    else if (npairs >= 16) hipLaunchKernelGGL((k_gateup_gemv<WT, 16>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((k_gateup_gemv<WT, 8>), grid, block, 0, stream, a);
+    if (npairs <= 16) return launch_gateup_v<WT, 16, 4>(a, max_slots, n_cu, stream);
+    if (npairs <= 32) return launch_gateup_v<WT, 32, 2>(a, max_slots, n_cu, stream);
+    return launch_gateup_v<WT, 64, 2>(a, max_slots, n_cu, stream);
+}
+
+template <int WT, int LPR>
+static hipError_t launch_down_v(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
+    constexpr int RPW = 2 * (64 / LPR);  // two load instructions per item
+    const size_t lds = (size_t)(a.E + 1) * sizeof(int4);
+    auto kern = k_down_stream<WT, LPR, RPW>;
+    const int g = stream_blocks(kern, lds, max_slots * (a.H / RPW), n_cu);
+    hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
 template <int WT>
-static hipError_t launch_down(const ExpertArgs& a, int max_slots, hipStream_t stream) {
-    const dim3 grid(max_slots, a.H / 64), block(256);
+static hipError_t launch_down(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
     const int npairs = a.F / 64;
-    if (npairs >= 16) hipLaunchKernelGGL((k_down_gemv<WT, 16>), grid, block, 0, stream, a);
-    else if (npairs >= 8) hipLaunchKernelGGL((k_down_gemv<WT, 8>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((k_down_gemv<WT, 4>), grid, block, 0, stream, a);
-    return hipGetLastError();
+    if (npairs <= 4) return launch_down_v<WT, 4>(a, max_slots, n_cu, stream);
+    if (npairs <= 8) return launch_down_v<WT, 8>(a, max_slots, n_cu, stream);
+    if (npairs <= 16) return launch_down_v<WT, 16>(a, max_slots, n_cu, stream);
+    if (npairs <= 32) return launch_down_v<WT, 32>(a, max_slots, n_cu, stream);
+    return launch_down_v<WT, 64>(a, max_slots, n_cu, stream);
 }
 
 static ExpertArgs make_expert_args(const LayerDesc& L, const Workspace& ws, int T) {
@@ -236,19 +287,29 @@ static ExpertArgs make_expert_args(const LayerDesc& L, const Workspace& ws, int 
     a.w_down = L.w_down; a.down_nb1 = L.down_nb1; a.down_nb2 = L.down_nb2;
     a.w_sh_gate = L.w_sh_gate; a.w_sh_up = L.w_sh_up; a.w_sh_down = L.w_sh_down;
     a.sh_gate_nb1 = L.sh_gate_nb1; a.sh_up_nb1 = L.sh_up_nb1; a.sh_down_nb1 = L.sh_down_nb1;
-    a.active = ws.active; a.counters = ws.counters; a.offsets = ws.offsets; a.row_token = ws.row_token;
-    a.xq_qs = ws.xq_qs; a.xq_ds = ws.xq_ds; a.hq_qs = ws.hq_qs; a.hq_ds = ws.hq_ds; a.ybuf = ws.ybuf;
+    a.counters = ws.counters; a.slot_info = ws.slot_info; a.offsets = ws.offsets; a.row_token = ws.row_token;
+    a.xq_qs = ws.xq_qs; a.xq_ds = ws.xq_ds; a.gubuf = ws.gubuf; a.hq_qs = ws.hq_qs; a.hq_ds = ws.hq_ds;
+    a.ybuf = ws.ybuf;
     return a;
 }
 
-hipError_t launch_experts_gemv(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
+hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
     const ExpertArgs a = make_expert_args(L, ws, T);
     const int max_slots = min(L.E, T * L.K) + L.S;
-    hipError_t err = (L.gu_type == kTypeQ4_0) ? launch_gateup<kTypeQ4_0>(a, max_slots, stream)
-                                              : launch_gateup<kTypeQ8_0>(a, max_slots, stream);
+    return (L.gu_type == kTypeQ4_0) ? launch_gateup<kTypeQ4_0>(a, max_slots, L.n_cu, stream)
+                                    : launch_gateup<kTypeQ8_0>(a, max_slots, L.n_cu, stream);
+}
+
+hipError_t launch_experts_down(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
+    const ExpertArgs a = make_expert_args(L, ws, T);
+    const int max_slots = min(L.E, T * L.K) + L.S;
+    const int max_rows = T * L.K + L.S * T;
+    const int qblocks = (max_rows * (L.F / 32) + 7) / 8;
+    hipLaunchKernelGGL(k_quant_h, dim3(qblocks), dim3(256), 0, stream, a);
+    hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    return (L.dn_type == kTypeQ4_0) ? launch_down<kTypeQ4_0>(a, max_slots, stream)
-                                    : launch_down<kTypeQ8_0>(a, max_slots, stream);
+    return (L.dn_type == kTypeQ4_0) ? launch_down<kTypeQ4_0>(a, max_slots, L.n_cu, stream)
+                                    : launch_down<kTypeQ8_0>(a, max_slots, L.n_cu, stream);
 }
 
 // ---------------------------------------------------------------------------

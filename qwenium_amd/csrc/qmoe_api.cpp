@@ -140,8 +140,10 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.row_token = (int32_t*)take(R * sizeof(int32_t));
     ws.pos = (int32_t*)take(A * sizeof(int32_t));
     ws.active = (int32_t*)take((size_t)(E + 1) * sizeof(int32_t));
+    ws.slot_info = (int4*)take((size_t)(E + 1) * sizeof(int4));
     ws.counters = (int32_t*)take(16 * sizeof(int32_t));
     ws.tiles = (int4*)take((size_t)max_tiles * sizeof(int4));
+    ws.gubuf = (float2*)take(R * F * sizeof(float2));
     ws.hq_qs = (int8_t*)take(R * F);
     ws.hq_ds = (float2*)take(R * (F / 32) * sizeof(float2));
     ws.ybuf = (float*)take(R * H * sizeof(float));
@@ -158,6 +160,8 @@ struct qmoe_layer {
     LayerDesc d;
     int device = 0;
     qmoe_workspace* own_ws = nullptr;
+    hipEvent_t phase_events[QMOE_N_PHASE_EVENTS] = {};
+    bool record_phases = false;
 };
 
 struct qmoe_workspace {
@@ -185,13 +189,13 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
     if (hp->top_k < 1 || hp->top_k > hp->n_experts || hp->top_k > 64)
         return fail(QMOE_ERR_VALUE, "qmoe: hparam \"top_k\" expected 1..min(n_experts, 64) (n_experts=" +
                                         std::to_string(hp->n_experts) + "), got " + std::to_string(hp->top_k));
-    if (hp->ffn_dim < 64 || hp->ffn_dim % 64 != 0)
-        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"ffn_dim\" expected a positive multiple of 64, got " +
+    if (hp->ffn_dim < 64 || hp->ffn_dim > 4096 || hp->ffn_dim % 64 != 0)
+        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"ffn_dim\" expected a multiple of 64 in [64, 4096], got " +
                                         std::to_string(hp->ffn_dim));
     if (!w_router) return fail(QMOE_ERR_NULL, slot_error("w_router", "a tensor", "null"));
     const int64_t H = w_router->ne[0];
-    if (H < 64 || H % 64 != 0)
-        return fail(QMOE_ERR_SHAPE, slot_error("w_router", "ne[0]=n_embd a positive multiple of 64",
+    if (H < 256 || H > 4096 || H % 256 != 0)
+        return fail(QMOE_ERR_SHAPE, slot_error("w_router", "ne[0]=n_embd a multiple of 256 in [256, 4096]",
                                                "ne[0]=" + std::to_string(H)));
     const int64_t E = hp->n_experts, F = hp->ffn_dim;
     int rc;
@@ -247,6 +251,9 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
         d.w_sh_norm = (const float*)w_sh_norm->data;
     }
     (void)hipGetDevice(&L->device);
+    int n_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, L->device) == hipSuccess && n_cu > 0)
+        d.n_cu = n_cu;
     *out = L;
     return QMOE_OK;
 }
@@ -329,12 +336,23 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
     // buffers are sized for the workspace's (larger or equal) dims; kernels index with the layer's
     const Workspace& v = w;
     hipStream_t stream = (hipStream_t)hip_stream;
-    hipError_t err = qmoe::launch_route(d, v, x, n_tokens, stream);
+    auto mark = [&](int i) -> hipError_t {
+        return layer->record_phases ? hipEventRecord(layer->phase_events[i], stream) : hipSuccess;
+    };
+    hipError_t err = mark(0);
+    if (err == hipSuccess) err = qmoe::launch_route(d, v, x, n_tokens, stream);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
-    err = qmoe::launch_experts_gemv(d, v, n_tokens, stream);
-    if (err != hipSuccess) return hip_fail(err, "expert kernels");
-    err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream);
+    err = mark(1);
+    if (err == hipSuccess) err = qmoe::launch_experts_gateup(d, v, n_tokens, stream);
+    if (err != hipSuccess) return hip_fail(err, "gate/up expert kernel");
+    err = mark(2);
+    if (err == hipSuccess) err = qmoe::launch_experts_down(d, v, n_tokens, stream);
+    if (err != hipSuccess) return hip_fail(err, "down expert kernel");
+    err = mark(3);
+    if (err == hipSuccess) err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream);
     if (err != hipSuccess) return hip_fail(err, "combine kernel");
+    err = mark(4);
+    if (err != hipSuccess) return hip_fail(err, "phase event record");
     if (dbg) {
         const size_t T = (size_t)n_tokens;
         if (dbg->logits) {
@@ -355,6 +373,22 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
             if (err != hipSuccess) return hip_fail(err, c.what);
         }
     }
+    return QMOE_OK;
+}
+
+int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events) {
+    g_last_error.clear();
+    if (!layer) return fail(QMOE_ERR_NULL, "qmoe: layer expected non-null, got null");
+    if (!events) {
+        layer->record_phases = false;
+        return QMOE_OK;
+    }
+    for (int i = 0; i < QMOE_N_PHASE_EVENTS; ++i) {
+        if (!events[i])
+            return fail(QMOE_ERR_NULL, "qmoe: events[" + std::to_string(i) + "] expected a hipEvent_t, got null");
+        layer->phase_events[i] = (hipEvent_t)events[i];
+    }
+    layer->record_phases = true;
     return QMOE_OK;
 }
 

@@ -164,7 +164,77 @@ __device__ __forceinline__ double normal_det(uint64_t key, uint64_t idx) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave-level reductions (wave64; WIDTH lanes per independent group)
+// DPP reductions (wave64).  Groups of WIDTH aligned lanes (WIDTH = 2..64);
+// the group result lands in the group's LAST lane (lane WIDTH-1 of the group).
+// Steps: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror, row_bcast:15 (rows 1,3), row_bcast:31 (rows 2,3).  All VALU; no
+// LDS round trip.
+// ---------------------------------------------------------------------------
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_f64_or_zero(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+template <int WIDTH>
+__device__ __forceinline__ double dpp_sum_f64(double v) {
+    static_assert(WIDTH == 2 || WIDTH == 4 || WIDTH == 8 || WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "width");
+    v += dpp_f64_or_zero<kDppQuadXor1, 0xF>(v);
+    if (WIDTH >= 4) v += dpp_f64_or_zero<kDppQuadXor2, 0xF>(v);
+    if (WIDTH >= 8) v += dpp_f64_or_zero<kDppRowHalfMirror, 0xF>(v);
+    if (WIDTH >= 16) v += dpp_f64_or_zero<kDppRowMirror, 0xF>(v);
+    if (WIDTH >= 32) v += dpp_f64_or_zero<kDppRowBcast15, 0xA>(v);
+    if (WIDTH >= 64) v += dpp_f64_or_zero<kDppRowBcast31, 0xC>(v);
+    return v;
+}
+
+// (value, index) arg-max step: keep the better of own and the DPP source
+// (larger value; ties to the lower index).  Masked rows keep their own pair.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void dpp_argmax_step(float& bv, int& bi) {
+    const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, bv),
+                                                                           __builtin_bit_cast(int, bv), CTRL,
+                                                                           ROW_MASK, 0xF, false));
+    const int oi = __builtin_amdgcn_update_dpp(bi, bi, CTRL, ROW_MASK, 0xF, false);
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+// Whole-wave inclusive prefix sum of an int (row_shr 1,2,4,8 then row
+// broadcasts); lane i receives sum of lanes 0..i.
+__device__ __forceinline__ int wave_incl_scan_i32(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast15, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast31, 0xC, 0xF, false);
+    return v;
+}
+
+// Whole-wave arg-max; the winner is returned to every lane.
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+    dpp_argmax_step<kDppQuadXor1, 0xF>(bv, bi);
+    dpp_argmax_step<kDppQuadXor2, 0xF>(bv, bi);
+    dpp_argmax_step<kDppRowHalfMirror, 0xF>(bv, bi);
+    dpp_argmax_step<kDppRowMirror, 0xF>(bv, bi);
+    dpp_argmax_step<kDppRowBcast15, 0xA>(bv, bi);
+    dpp_argmax_step<kDppRowBcast31, 0xC>(bv, bi);
+    bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bv), 63));
+    bi = __builtin_amdgcn_readlane(bi, 63);
+}
+
+// ---------------------------------------------------------------------------
+// Shuffle-based reductions (wave64; WIDTH lanes per independent group; result
+// in every lane of the group)
 // ---------------------------------------------------------------------------
 template <int WIDTH>
 __device__ __forceinline__ double group_sum_f64(double v) {

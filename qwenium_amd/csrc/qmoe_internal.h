@@ -27,6 +27,7 @@ struct LayerDesc {
     const uint8_t* w_sh_down = nullptr;
     uint64_t sh_gate_nb1 = 0, sh_up_nb1 = 0, sh_down_nb1 = 0;
     const float* w_sh_norm = nullptr;
+    int n_cu = 256;                         // compute units of the layer's device
 };
 
 // Device scratch.  R = T*K + S*T rows: routed assignments sorted by expert,
@@ -48,10 +49,12 @@ struct Workspace {
     int32_t* row_token = nullptr; // [R]
     int32_t* pos = nullptr;       // [T*K] position of assignment
     int32_t* active = nullptr;    // [E+1] active experts (ascending), shared (=E) last
+    int4* slot_info = nullptr;    // [E+1] per active slot {expert, first row, rows, 0}
     int32_t* counters = nullptr;  // [16] n_active, n_tiles, ...
     int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
-    int8_t* hq_qs = nullptr;      // [R][F]
-    float2* hq_ds = nullptr;      // [R][F/32]
+    float2* gubuf = nullptr;      // [R][F] (gate, up) projections
+    int8_t* hq_qs = nullptr;      // [R][F]   Q8_0 quants of h = silu(g)*u
+    float2* hq_ds = nullptr;      // [R][F/32] {d, bitcast(sum q)}
     float* ybuf = nullptr;        // [R][H] down outputs (unweighted)
     int max_tiles = 0;
 };
@@ -60,7 +63,8 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* carve, void
 
 // --- launchers (each enqueues on `stream`, returns hipError_t of the launch) ---
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, hipStream_t stream);
-hipError_t launch_experts_gemv(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+hipError_t launch_experts_down(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_experts_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
                           hipStream_t stream);

@@ -26,39 +26,70 @@ struct RouterArgs {
     float2* xq_ds;          // [T][H/32]
 };
 
-constexpr int kRouterMaxChunks = 64;  // H <= 4096 keeps the router row in registers
+// Router GEMV for small token counts: one 256-thread block per router row
+// (row E is the shared-expert gate vector).  Wave w owns float4 chunks
+// c = w + 4i of the row (chunk = 64 float4 = 256 values); every load is
+// unconditional (clamped index, zeroed weight) so a token chunk's loads issue
+// back to back.  Products are exact in f64; the sum is exact-order-free f64.
+constexpr int kRouterTokChunk = 8;
 
+template <int NCH>
+__device__ __forceinline__ void router_row(const RouterArgs& a, int e, float* s_part) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const float* wrow = (e < a.E) ? a.w_router + (uint64_t)e * a.router_ld : a.w_sh_norm;
+    const int nchunks = a.H >> 8;
+    f32x4 w[NCH];
+    int off[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const int c = wave + 4 * i;
+        const int cc = c < nchunks ? c : nchunks - 1;
+        off[i] = (cc * 64 + lane) * 4;
+        const f32x4 v = *(const f32x4*)(wrow + off[i]);
+        w[i] = c < nchunks ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    for (int t0 = 0; t0 < a.T; t0 += kRouterTokChunk) {
+        f32x4 xv[kRouterTokChunk][NCH];
+#pragma unroll
+        for (int c = 0; c < kRouterTokChunk; ++c) {
+            const int t = min(t0 + c, a.T - 1);
+            const float* xr = a.x + (uint64_t)t * a.H;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) xv[c][i] = *(const f32x4*)(xr + off[i]);
+        }
+#pragma unroll
+        for (int c = 0; c < kRouterTokChunk; ++c) {
+            double acc = 0.0;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                acc = __builtin_fma((double)w[i].x, (double)xv[c][i].x, acc);
+                acc = __builtin_fma((double)w[i].y, (double)xv[c][i].y, acc);
+                acc = __builtin_fma((double)w[i].z, (double)xv[c][i].z, acc);
+                acc = __builtin_fma((double)w[i].w, (double)xv[c][i].w, acc);
+            }
+            acc = group_sum_f64<64>(acc);
+            if (lane == 0) ((double*)s_part)[wave * kRouterTokChunk + c] = acc;
+        }
+        __syncthreads();
+        if (threadIdx.x < kRouterTokChunk && t0 + (int)threadIdx.x < a.T) {
+            const double* p = (const double*)s_part;
+            const int c = threadIdx.x;
+            const double sum = (p[0 * kRouterTokChunk + c] + p[1 * kRouterTokChunk + c]) +
+                               (p[2 * kRouterTokChunk + c] + p[3 * kRouterTokChunk + c]);
+            a.logits[(uint64_t)(t0 + c) * (a.E + 1) + e] = (float)sum;
+        }
+        __syncthreads();
+    }
+}
+
+template <int NCH>
 __global__ __launch_bounds__(256) void k_router_quant(RouterArgs a) {
+    __shared__ double s_part[4 * kRouterTokChunk];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     if ((int)blockIdx.x < a.n_router_blocks) {
-        const int e = blockIdx.x * 4 + wave;
-        if (e >= a.E + a.S) return;
-        const float* wrow = (e < a.E) ? a.w_router + (uint64_t)e * a.router_ld : a.w_sh_norm;
-        const int nch = a.H >> 6;  // values per lane
-        if (nch <= kRouterMaxChunks) {
-            float w[kRouterMaxChunks];
-#pragma unroll
-            for (int i = 0; i < kRouterMaxChunks; ++i)
-                if (i < nch) w[i] = wrow[i * 64 + lane];
-            for (int t = 0; t < a.T; ++t) {
-                const float* xr = a.x + (uint64_t)t * a.H;
-                double acc = 0.0;
-#pragma unroll
-                for (int i = 0; i < kRouterMaxChunks; ++i)
-                    if (i < nch) acc = __builtin_fma((double)w[i], (double)xr[i * 64 + lane], acc);
-                acc = group_sum_f64<64>(acc);
-                if (lane == 0) a.logits[(uint64_t)t * (a.E + 1) + e] = (float)acc;
-            }
-        } else {
-            for (int t = 0; t < a.T; ++t) {
-                const float* xr = a.x + (uint64_t)t * a.H;
-                double acc = 0.0;
-                for (int i = lane; i < a.H; i += 64) acc = __builtin_fma((double)wrow[i], (double)xr[i], acc);
-                acc = group_sum_f64<64>(acc);
-                if (lane == 0) a.logits[(uint64_t)t * (a.E + 1) + e] = (float)acc;
-            }
-        }
+        router_row<NCH>(a, blockIdx.x, (float*)s_part);
         return;
     }
     // activation quantization: one wave per token, one 32-value block per lane step
@@ -117,6 +148,7 @@ struct TopkArgs {
     int32_t* row_token;   // [R]
     int32_t* pos;         // [T*K]
     int32_t* active;      // [E+1]
+    int4* slot_info;      // [E+1] {expert, first row, rows, 0}
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
@@ -131,54 +163,91 @@ __device__ __forceinline__ bool better(float v, int i, float v2, int i2) {
     return v > v2 || (v == v2 && i < i2);
 }
 
-__device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_idx_row, float* s_val_row) {
+template <int EPL>
+__device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_idx_row, float* s_val_row,
+                               double* s_ex_row) {
     const float* l = a.logits + (uint64_t)t * (a.E + 1);
-    float v[kMaxExpertsPerLane];
-    const int per_lane = (a.E + 63) >> 6;
+    // this lane's candidates e = i*64 + lane, sorted by (logit desc, id asc)
+    float v[EPL];
+    int id[EPL];
 #pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+    for (int i = 0; i < EPL; ++i) {
         const int e = i * 64 + lane;
-        v[i] = (i < per_lane && e < a.E) ? l[e] : -__builtin_huge_valf();
+        const float lv = l[min(e, a.E - 1)];  // unconditional load, masked below
+        v[i] = e < a.E ? lv : -__builtin_huge_valf();
+        id[i] = e < a.E ? e : 0x7fffffff;
     }
-    uint32_t taken = 0;
+#pragma unroll
+    for (int i = 1; i < EPL; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j) {
+            if (better(v[j], id[j], v[j - 1], id[j - 1])) {
+                const float tv = v[j]; v[j] = v[j - 1]; v[j - 1] = tv;
+                const int ti = id[j]; id[j] = id[j - 1]; id[j - 1] = ti;
+            }
+        }
     for (int j = 0; j < a.K; ++j) {
-        float bv = -__builtin_huge_valf();
-        int bi = 0x7fffffff;
+        float bv = v[0];
+        int bi = id[0];
+        wave_argmax(bv, bi);
+        if (id[0] == bi) {  // the winning lane pops its head
 #pragma unroll
-        for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-            const int e = i * 64 + lane;
-            if (i < per_lane && e < a.E && !((taken >> i) & 1u) && better(v[i], e, bv, bi)) { bv = v[i]; bi = e; }
+            for (int i = 0; i + 1 < EPL; ++i) { v[i] = v[i + 1]; id[i] = id[i + 1]; }
+            v[EPL - 1] = -__builtin_huge_valf();
+            id[EPL - 1] = 0x7fffffff;
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
         if (lane == 0) {
             s_idx_row[j] = bi;
             s_val_row[j] = bv;
             a.topk_idx[(uint64_t)t * a.K + j] = bi;
         }
     }
-    if (lane == 0) {
+    // lanes below read what lane 0 wrote to LDS: order the wave's LDS accesses
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // softmax over the selected logits (slot 0 holds the maximum): exps in
+    // parallel lanes, the sum in slot order, the divisions in parallel lanes
+    {
 #pragma clang fp contract(off)
-        // softmax over the selected logits; slot 0 holds the maximum
         const double m = (double)s_val_row[0];
+        double ex = 0.0;
+        if (lane < a.K) {
+            ex = exp_det((double)s_val_row[lane] - m);
+            s_ex_row[lane] = ex;
+        }
+        if (lane == a.K && a.S) a.sh_gate[t] = sigmoid_det(l[a.E]);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
         double sum = 0.0;
-        for (int j = 0; j < a.K; ++j) sum = sum + exp_det((double)s_val_row[j] - m);
-        for (int j = 0; j < a.K; ++j)
-            a.topk_w[(uint64_t)t * a.K + j] = (float)(exp_det((double)s_val_row[j] - m) / sum);
-        if (a.S) a.sh_gate[t] = sigmoid_det(l[a.E]);
+        if (lane == 0) {
+            for (int j = 0; j < a.K; ++j) sum = sum + s_ex_row[j];
+            s_ex_row[kMaxTopK] = sum;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        sum = s_ex_row[kMaxTopK];
+        if (lane < a.K) a.topk_w[(uint64_t)t * a.K + lane] = (float)(ex / sum);
     }
 }
 
-// Scan of per-block histograms, expert offsets, active list, MFMA tile list and
-// the stable scatter.  Runs in ONE block (any blockDim multiple of 64).
-__device__ void scan_and_scatter(const TopkArgs& a, int32_t* s_scan /* >= E+1 ints */) {
+__device__ __forceinline__ void topk_dispatch(const TopkArgs& a, int t, int lane, int32_t* s_idx_row,
+                                              float* s_val_row, double* s_ex_row) {
+    const int epl = (a.E + 63) >> 6;
+    if (epl <= 1) topk_one_token<1>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+    else if (epl <= 2) topk_one_token<2>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+    else if (epl <= 4) topk_one_token<4>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+    else if (epl <= 8) topk_one_token<8>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+    else topk_one_token<16>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+}
+
+// Scan of per-block histograms, expert offsets, active list, slot table, MFMA
+// tile list and the stable scatter.  Runs in ONE block (blockDim a multiple of
+// 64, at least 256).
+__device__ void scan_and_scatter(const TopkArgs& a, int32_t* s_scan /* >= E+1 ints */, int32_t* s_misc /* >= 64 */) {
     const int tid = threadIdx.x;
     const int nthr = blockDim.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int nwaves = nthr >> 6;
     // 1. per-expert exclusive base per top-k block (in place) and totals
     for (int e = tid; e < a.E; e += nthr) {
         int run = 0;
@@ -190,51 +259,50 @@ __device__ void scan_and_scatter(const TopkArgs& a, int32_t* s_scan /* >= E+1 in
         s_scan[e] = run;
     }
     __syncthreads();
-    // 2. serial-in-wave exclusive scans (E <= 1024; done by wave 0)
-    if (tid < 64) {
-        int carry = 0;
-        int carry_act = 0;
-        int carry_tiles = 0;
-        for (int base = 0; base < a.E; base += 64) {
-            const int e = base + tid;
-            const int c = e < a.E ? s_scan[e] : 0;
-            const int act = c > 0 ? 1 : 0;
-            const int nt = (c + kMfmaTileM - 1) / kMfmaTileM;
-            int inc = c, inc_act = act, inc_t = nt;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int u = __shfl_up(inc, o, 64);
-                const int ua = __shfl_up(inc_act, o, 64);
-                const int ut = __shfl_up(inc_t, o, 64);
-                if (tid >= o) { inc += u; inc_act += ua; inc_t += ut; }
+    // 2. exclusive scans over experts: rows, active flags, MFMA tiles.  Chunks of
+    //    64 experts are scanned by separate waves, then chunk totals are combined.
+    const int nchunk = (a.E + 63) >> 6;  // <= 16
+    int c_rows = 0, c_act = 0, c_tiles = 0, inc = 0, inc_act = 0, inc_t = 0, e = 0;
+    if (wave < nchunk) {
+        e = wave * 64 + lane;
+        c_rows = e < a.E ? s_scan[e] : 0;
+        c_act = c_rows > 0 ? 1 : 0;
+        c_tiles = (c_rows + kMfmaTileM - 1) / kMfmaTileM;
+        inc = wave_incl_scan_i32(c_rows);
+        inc_act = wave_incl_scan_i32(c_act);
+        inc_t = wave_incl_scan_i32(c_tiles);
+        if (lane == 63) { s_misc[3 * wave] = inc; s_misc[3 * wave + 1] = inc_act; s_misc[3 * wave + 2] = inc_t; }
+    }
+    __syncthreads();
+    if (wave < nchunk) {
+        int base = 0, base_act = 0, base_t = 0;
+        for (int w = 0; w < wave; ++w) { base += s_misc[3 * w]; base_act += s_misc[3 * w + 1]; base_t += s_misc[3 * w + 2]; }
+        if (e < a.E) {
+            const int off = base + inc - c_rows;
+            a.offsets[e] = off;
+            s_scan[e] = off;  // offsets kept in LDS for the scatter
+            if (c_act) {
+                const int slot = base_act + inc_act - 1;
+                a.active[slot] = e;
+                a.slot_info[slot] = make_int4(e, off, c_rows, 0);
             }
-            if (e < a.E) {
-                const int off = carry + inc - c;
-                a.offsets[e] = off;
-                if (act) a.active[carry_act + inc_act - 1] = e;
-                int t0 = carry_tiles + inc_t - nt;
-                for (int i = 0; i < nt && t0 + i < a.max_tiles; ++i) {
-                    const int r0 = off + i * kMfmaTileM;
-                    const int nr = min(kMfmaTileM, c - i * kMfmaTileM);
-                    a.tiles[t0 + i] = make_int4(e, r0, nr, 0);
-                }
-            }
-            carry += __shfl(inc, 63, 64);
-            carry_act += __shfl(inc_act, 63, 64);
-            carry_tiles += __shfl(inc_t, 63, 64);
+            const int t0 = base_t + inc_t - c_tiles;
+            for (int i = 0; i < c_tiles && t0 + i < a.max_tiles; ++i)
+                a.tiles[t0 + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, c_rows - i * kMfmaTileM), 0);
         }
-        const int A = a.T * a.K;
-        if (tid == 0) {
+        if (wave == nchunk - 1 && lane == 63) {
+            const int A = a.T * a.K;
+            int n_act = base_act + inc_act;
+            int n_tiles = base_t + inc_t;
             a.offsets[a.E] = A;
             a.offsets[a.E + 1] = A + a.S * a.T;
-            int n_act = carry_act;
-            int n_tiles = carry_tiles;
             if (a.S) {
-                a.active[n_act++] = a.E;
+                a.active[n_act] = a.E;
+                a.slot_info[n_act] = make_int4(a.E, A, a.T, 0);
+                n_act++;
                 const int nt = (a.T + kMfmaTileM - 1) / kMfmaTileM;
-                for (int i = 0; i < nt && n_tiles < a.max_tiles; ++i) {
+                for (int i = 0; i < nt && n_tiles < a.max_tiles; ++i)
                     a.tiles[n_tiles++] = make_int4(a.E, A + i * kMfmaTileM, min(kMfmaTileM, a.T - i * kMfmaTileM), 0);
-                }
             }
             a.counters[0] = n_act;
             a.counters[1] = n_tiles;
@@ -245,9 +313,9 @@ __device__ void scan_and_scatter(const TopkArgs& a, int32_t* s_scan /* >= E+1 in
     const int A = a.T * a.K;
     for (int asg = tid; asg < A; asg += nthr) {
         const int t = asg / a.K;
-        const int e = a.topk_idx[asg];
+        const int ex = a.topk_idx[asg];
         const int blk = t / kTopkTokensPerBlock;
-        const int p = a.offsets[e] + a.hist[(uint64_t)blk * a.E + e] + a.local_rank[asg];
+        const int p = s_scan[ex] + a.hist[(uint64_t)blk * a.E + ex] + a.local_rank[asg];
         a.rows[p] = asg;
         a.row_token[p] = t;
         a.pos[asg] = p;
@@ -258,42 +326,134 @@ __device__ void scan_and_scatter(const TopkArgs& a, int32_t* s_scan /* >= E+1 in
             a.row_token[A + t] = t;
         }
     }
+    __syncthreads();
+    // 4. token of each slot's first row (lets the expert kernels fetch it without a lookup)
+    const int n_act = a.counters[0];
+    for (int i = tid; i < n_act; i += nthr) {
+        int4 si = a.slot_info[i];
+        si.w = a.row_token[si.y];
+        a.slot_info[i] = si;
+    }
 }
 
-// blockDim = 256 (4 waves), kTopkTokensPerBlock tokens per block.
-__global__ __launch_bounds__(256) void k_topk(TopkArgs a, int fused_scan) {
+// blockDim = 64 * kTopkTokensPerBlock: one wave per token.
+__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, int fused_scan) {
     __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
     __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
+    __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
+    __shared__ uint32_t s_mask[1024];  // per expert: bit ti set if block token ti chose it
     __shared__ int32_t s_cnt[1024 + 1];
+    __shared__ int32_t s_misc[64];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kTopkTokensPerBlock;
     const int ntok = min(kTopkTokensPerBlock, a.T - t0);
-    for (int i = wave; i < ntok; i += 4) topk_one_token(a, t0 + i, lane, s_idx[i], s_val[i]);
-    for (int e = threadIdx.x; e < a.E; e += blockDim.x) s_cnt[e] = 0;
+    for (int e = threadIdx.x; e < a.E; e += blockDim.x) s_mask[e] = 0;
     __syncthreads();
-    // local ranks (stable by token inside the block) and block histogram
+    if (wave < ntok) {
+        topk_dispatch(a, t0 + wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
+        if (lane < a.K) atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
+    }
+    __syncthreads();
+    // local rank of (token ti, slot j) = earlier block tokens that chose the same expert
     for (int asg = threadIdx.x; asg < ntok * a.K; asg += blockDim.x) {
         const int ti = asg / a.K;
         const int j = asg % a.K;
-        const int e = s_idx[ti][j];
-        int rank = 0;
-        for (int tp = 0; tp < ti; ++tp)
-            for (int jj = 0; jj < a.K; ++jj) rank += (s_idx[tp][jj] == e) ? 1 : 0;
-        a.local_rank[(uint64_t)(t0 + ti) * a.K + j] = rank;
-        atomicAdd(&s_cnt[e], 1);
+        const int ex = s_idx[ti][j];
+        a.local_rank[(uint64_t)(t0 + ti) * a.K + j] = __builtin_popcount(s_mask[ex] & ((1u << ti) - 1u));
     }
-    __syncthreads();
-    for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.hist[(uint64_t)blockIdx.x * a.E + e] = s_cnt[e];
+    for (int e = threadIdx.x; e < a.E; e += blockDim.x)
+        a.hist[(uint64_t)blockIdx.x * a.E + e] = __builtin_popcount(s_mask[e]);
     if (fused_scan) {
         __syncthreads();
-        scan_and_scatter(a, s_cnt);
+        scan_and_scatter(a, s_cnt, s_misc);
+    }
+}
+
+// Whole routing for T <= kTopkTokensPerBlock in ONE block, everything in LDS:
+// top-k per token (one wave each), per-expert token masks, counts, offsets,
+// active slots (with the token of each slot's first row = lowest mask bit),
+// stable scatter (rank = earlier tokens in the expert's mask) and tiles.
+__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_route_small(TopkArgs a) {
+    __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
+    __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
+    __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
+    __shared__ uint32_t s_mask[1024];
+    __shared__ int32_t s_off[1024];
+    __shared__ int32_t s_misc[64];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int A = a.T * a.K;
+    for (int e = tid; e < a.E; e += blockDim.x) s_mask[e] = 0;
+    __syncthreads();
+    if (wave < a.T) {
+        topk_dispatch(a, wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
+        if (lane < a.K) atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
+    }
+    __syncthreads();
+    const int nchunk = (a.E + 63) >> 6;
+    int cnt = 0, act = 0, nt = 0, inc = 0, inc_act = 0, inc_t = 0, e = 0;
+    if (wave < nchunk) {
+        e = wave * 64 + lane;
+        cnt = e < a.E ? __builtin_popcount(s_mask[e]) : 0;
+        act = cnt > 0 ? 1 : 0;
+        nt = (cnt + kMfmaTileM - 1) / kMfmaTileM;
+        inc = wave_incl_scan_i32(cnt);
+        inc_act = wave_incl_scan_i32(act);
+        inc_t = wave_incl_scan_i32(nt);
+        if (lane == 63) { s_misc[3 * wave] = inc; s_misc[3 * wave + 1] = inc_act; s_misc[3 * wave + 2] = inc_t; }
+    }
+    __syncthreads();
+    if (wave < nchunk) {
+        int base = 0, base_act = 0, base_t = 0;
+        for (int w = 0; w < wave; ++w) { base += s_misc[3 * w]; base_act += s_misc[3 * w + 1]; base_t += s_misc[3 * w + 2]; }
+        if (e < a.E) {
+            const int off = base + inc - cnt;
+            a.offsets[e] = off;
+            s_off[e] = off;
+            if (act) {
+                const int slot = base_act + inc_act - 1;
+                a.active[slot] = e;
+                a.slot_info[slot] = make_int4(e, off, cnt, __builtin_ctz(s_mask[e]));
+            }
+            if (nt) {
+                const int t0 = base_t + inc_t - nt;
+                if (t0 < a.max_tiles) a.tiles[t0] = make_int4(e, off, cnt, 0);  // cnt <= T <= 16 < tile rows
+            }
+        }
+        if (wave == nchunk - 1 && lane == 63) {
+            int n_act = base_act + inc_act;
+            int n_tiles = base_t + inc_t;
+            a.offsets[a.E] = A;
+            a.offsets[a.E + 1] = A + a.S * a.T;
+            if (a.S) {
+                a.active[n_act] = a.E;
+                a.slot_info[n_act] = make_int4(a.E, A, a.T, 0);
+                n_act++;
+                if (n_tiles < a.max_tiles) a.tiles[n_tiles++] = make_int4(a.E, A, a.T, 0);
+            }
+            a.counters[0] = n_act;
+            a.counters[1] = n_tiles;
+        }
+    }
+    __syncthreads();
+    for (int asg = tid; asg < A; asg += blockDim.x) {
+        const int t = asg / a.K, j = asg % a.K;
+        const int ex = s_idx[t][j];
+        const int p = s_off[ex] + __builtin_popcount(s_mask[ex] & ((1u << t) - 1u));
+        a.rows[p] = asg;
+        a.row_token[p] = t;
+        a.pos[asg] = p;
+    }
+    if (a.S && tid < a.T) {
+        a.rows[A + tid] = -1;
+        a.row_token[A + tid] = tid;
     }
 }
 
 __global__ __launch_bounds__(1024) void k_scan_scatter(TopkArgs a) {
     __shared__ int32_t s_cnt[1024 + 1];
-    scan_and_scatter(a, s_cnt);
+    __shared__ int32_t s_misc[64];
+    scan_and_scatter(a, s_cnt, s_misc);
 }
 
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, hipStream_t stream) {
@@ -303,12 +463,17 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     ra.router_ld = L.router_ld;
     ra.w_sh_norm = L.w_sh_norm;
     ra.T = T; ra.H = L.H; ra.E = L.E; ra.S = L.S;
-    ra.n_router_blocks = (L.E + L.S + 3) / 4;
     ra.logits = ws.logits;
     ra.xq_qs = ws.xq_qs;
     ra.xq_ds = ws.xq_ds;
     const int nq = (T + 3) / 4;
-    hipLaunchKernelGGL(k_router_quant, dim3(ra.n_router_blocks + nq), dim3(256), 0, stream, ra);
+    ra.n_router_blocks = L.E + L.S;
+    const dim3 grid(ra.n_router_blocks + nq);
+    const int nch_per_wave = (L.H / 256 + 3) / 4;  // float4 chunks of 256 values per wave
+    if (nch_per_wave <= 1) hipLaunchKernelGGL((k_router_quant<1>), grid, dim3(256), 0, stream, ra);
+    else if (nch_per_wave <= 2) hipLaunchKernelGGL((k_router_quant<2>), grid, dim3(256), 0, stream, ra);
+    else if (nch_per_wave <= 4) hipLaunchKernelGGL((k_router_quant<4>), grid, dim3(256), 0, stream, ra);
+    else hipLaunchKernelGGL((k_router_quant<8>), grid, dim3(256), 0, stream, ra);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
 
@@ -325,14 +490,18 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     ta.row_token = ws.row_token;
     ta.pos = ws.pos;
     ta.active = ws.active;
+    ta.slot_info = ws.slot_info;
     ta.counters = ws.counters;
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
     ta.nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
-    const int fused = ta.nblk == 1 ? 1 : 0;
-    hipLaunchKernelGGL(k_topk, dim3(ta.nblk), dim3(256), 0, stream, ta, fused);
+    if (ta.nblk == 1) {
+        hipLaunchKernelGGL(k_route_small, dim3(1), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(k_topk, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta, 0);
     err = hipGetLastError();
-    if (err != hipSuccess || fused) return err;
+    if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_scan_scatter, dim3(1), dim3(1024), 0, stream, ta);
     return hipGetLastError();
 }
