@@ -469,12 +469,12 @@ int qo_moe_forward(const qo_layer* L, const float* x, int T, float* y,
 
     /* 3. down mul_mat_id (moe.cpp:127), expert-major */
 #pragma omp parallel for schedule(dynamic, 1)
-    for (int64_t en = 0; en < (int64_t)E * (H / 64); ++en) {
-        const int e = (int)(en / (H / 64));
-        const int n0 = (int)(en % (H / 64)) * 64;
+    for (int64_t en = 0; en < (int64_t)E * (H / 32); ++en) {
+        const int e = (int)(en / (H / 32));
+        const int n0 = (int)(en % (H / 32)) * 32;
         for (int p = offsets[e]; p < offsets[e + 1]; ++p) {
             const int64_t a = rows[p];
-            for (int n = n0; n < n0 + 64; ++n) {
+            for (int n = n0; n < n0 + 32; ++n) {
                 const uint8_t* wd = (const uint8_t*)L->w_down + ((size_t)e * H + n) * wrow_f;
                 yd[a * H + n] = qo_vec_dot(wt, wd, hq + hq_row * a, F);
             }

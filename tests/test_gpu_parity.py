@@ -156,3 +156,83 @@ def test_rms_norm_matches_oracle(gpu):
     y = rms_norm(x, w, 1e-6).cpu().numpy()
     ref = po.rms_norm(x.cpu().numpy(), w.cpu().numpy(), 1e-6)
     np.testing.assert_allclose(y, ref, rtol=2e-7, atol=0)
+
+
+def test_config1_matches_committed_golden(gpu):
+    """GPU path vs tests/golden/config1_seed0.npz (written by the CPU oracle)."""
+    import os
+    ref = np.load(os.path.join(os.path.dirname(__file__), "golden", "config1_seed0.npz"), allow_pickle=False)
+    spec = synthetic.CONFIG1
+    layer = synthetic.make_layer(spec, 0)
+    x = synthetic.make_x(spec, 32, 0)
+    y, dbg = layer.forward(x, debug=True)
+    got = {k: v.cpu().numpy() for k, v in dbg.items()}
+    d_ref = {k: ref[k] for k in ("topk_idx", "offsets", "rows", "logits", "topk_w")}
+    assert_parity(y.cpu().numpy(), got, ref["y"], d_ref, spec, min_identical=1.0)
+
+
+def test_constant_weights_closed_form(gpu):
+    """All experts identical (the constant fills of tests/unit/test_moe.cpp:93-101):
+    routing cannot matter and y has a closed form in the quantized constants."""
+    import math
+    H, E, K, F, T = 256, 8, 2, 64, 3
+    wt = TYPE_Q8_0
+    dev = "cuda"
+    from qwenium_amd.moe import GGMLTensor, Hparams, MoELayer
+
+    def qconst(v, n):
+        return torch.from_numpy(po.quantize(wt, np.full(n, v, np.float32))).to(dev)
+
+    t = {
+        "router": GGMLTensor(torch.full((E * H,), 0.1, device=dev), 0, (H, E)),
+        "gate": GGMLTensor(qconst(0.05, E * F * H), wt, (H, F, E)),
+        "up": GGMLTensor(qconst(0.05, E * F * H), wt, (H, F, E)),
+        "down": GGMLTensor(qconst(0.05, E * H * F), wt, (F, H, E)),
+        "sh_gate": GGMLTensor(qconst(0.02, F * H), wt, (H, F)),
+        "sh_up": GGMLTensor(qconst(0.02, F * H), wt, (H, F)),
+        "sh_down": GGMLTensor(qconst(0.02, H * F), wt, (F, H)),
+        "sh_norm": GGMLTensor(torch.full((H,), 0.5, device=dev), 0, (H,)),
+    }
+    layer = MoELayer(t["router"], t["gate"], t["up"], t["down"], t["sh_gate"], t["sh_up"], t["sh_down"],
+                     t["sh_norm"], Hparams(E, K, F, True))
+    y, dbg = layer.forward(torch.full((T, H), 0.5, device=dev), debug=True)
+    idx = dbg["topk_idx"].cpu().numpy()
+    assert idx.tolist() == [[0, 1]] * T  # all logits tie: lowest ids win
+
+    def q8(v):
+        return float(po.dequantize(po.TYPE_Q8_0, po.quantize(po.TYPE_Q8_0, np.full(32, v, np.float32)), 32)[0])
+
+    xq = q8(0.5)
+    g = H * q8(0.05) * xq
+    routed = F * q8(0.05) * q8(g / (1 + math.exp(-g)) * g)
+    gs = H * q8(0.02) * xq
+    ys = F * q8(0.02) * q8(gs / (1 + math.exp(-gs)) * gs)
+    expect = routed + ys / (1 + math.exp(-(H * 0.5 * 0.5)))
+    np.testing.assert_allclose(y.cpu().numpy(), expect, rtol=2e-6)
+
+
+def test_graph_replay_matches_eager(gpu):
+    """The forward captured in a HIP graph: every replay (with eager work and
+    synchronizations between replays) equals the eager result bit for bit."""
+    from qwenium_amd import Workspace
+    spec = synthetic.QWEN35B
+    layers = [synthetic.make_layer(spec, 40 + i) for i in range(2)]
+    xs = [synthetic.make_x(spec, 10, 40, batch=b) for b in range(2)]
+    ws = Workspace(layers[0], 10)
+    eager = [layers[i].forward(xs[i], workspace=ws).clone() for i in range(2)]
+    outs = [torch.empty_like(xs[0]) for _ in range(2)]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(2):
+            layers[i].forward(xs[i], out=outs[i], workspace=ws)
+    for rep in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            np.testing.assert_array_equal(outs[i].cpu().numpy().view(np.int32), eager[i].cpu().numpy().view(np.int32))
+        layers[1].forward(xs[0], workspace=ws)  # eager work between replays
+        torch.cuda.synchronize()
