@@ -1,0 +1,81 @@
+// qmoe_layer.hpp -- header-only C++ drop-in over the C ABI of qmoe.h.
+//
+// Mirrors the reference's layer module (rye-001/Qwenium src/layers/moe.h:32-75):
+// the same Hparams fields, the same constructor slot order and the same
+// exception behaviour (std::runtime_error from the constructor when the shared
+// expert is requested without its weights, moe.cpp:47-52).  build() appended
+// ggml nodes; forward() here enqueues the layer on a HIP stream instead.
+#pragma once
+
+#include <stdexcept>
+#include <string>
+
+#include "qmoe.h"
+
+namespace qmoe {
+
+// layer.h:19-22; accepted by forward() for interface symmetry (no effect,
+// as in the reference, moe.h:55-57).
+enum class Phase { Prefill, Decode };
+
+inline void check(int rc) {
+    if (rc != QMOE_OK) throw std::runtime_error(qmoe_last_error());
+}
+
+class MoELayer {
+public:
+    struct Hparams {
+        int n_experts;
+        int top_k;
+        int ffn_dim;
+        bool has_shared_expert;
+    };
+
+    // All tensors are borrowed device views in GGUF block layout; the w_sh_*
+    // slots may be nullptr when !hp.has_shared_expert.
+    MoELayer(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate, const qmoe_tensor* w_exp_up,
+             const qmoe_tensor* w_exp_down, const qmoe_tensor* w_sh_gate, const qmoe_tensor* w_sh_up,
+             const qmoe_tensor* w_sh_down, const qmoe_tensor* w_sh_norm, const Hparams& hp)
+        : hp_(hp) {
+        const qmoe_hparams c{hp.n_experts, hp.top_k, hp.ffn_dim, hp.has_shared_expert ? 1 : 0};
+        check(qmoe_layer_create(w_router, w_exp_gate, w_exp_up, w_exp_down, w_sh_gate, w_sh_up, w_sh_down,
+                                w_sh_norm, &c, &layer_));
+    }
+    ~MoELayer() { qmoe_layer_destroy(layer_); }
+    MoELayer(const MoELayer&) = delete;
+    MoELayer& operator=(const MoELayer&) = delete;
+
+    int n_embd() const { return qmoe_layer_n_embd(layer_); }
+    const Hparams& hparams() const { return hp_; }
+    qmoe_layer* handle() const { return layer_; }
+
+    // y[n_tokens][n_embd] = MoE(x) (+ residual).  Device pointers; work is
+    // enqueued on `stream` (a hipStream_t, nullptr = default stream).
+    void forward(const float* x, int n_tokens, float* y, Phase /*phase*/ = Phase::Prefill, int /*il*/ = 0,
+                 void* stream = nullptr, qmoe_workspace* ws = nullptr, const float* residual = nullptr,
+                 const qmoe_debug* dbg = nullptr) {
+        check(qmoe_layer_forward(layer_, ws, x, n_tokens, y, residual, dbg, stream));
+    }
+
+private:
+    Hparams hp_;
+    qmoe_layer* layer_ = nullptr;
+};
+
+// A contiguous ggml-style view (ne[0] fastest) of device data.
+inline qmoe_tensor make_tensor(const void* data, int type, int n_dims, long long ne0, long long ne1 = 1,
+                               long long ne2 = 1) {
+    qmoe_tensor t{};
+    t.data = data;
+    t.type = type;
+    t.n_dims = n_dims;
+    t.ne[0] = ne0; t.ne[1] = ne1; t.ne[2] = ne2; t.ne[3] = 1;
+    const unsigned long long bb = type == QMOE_TYPE_Q4_0 ? 18 : type == QMOE_TYPE_Q8_0 ? 34 : 4;
+    t.nb[0] = bb;
+    t.nb[1] = type == QMOE_TYPE_F32 ? 4ull * ne0 : bb * (unsigned long long)(ne0 / 32);
+    t.nb[2] = t.nb[1] * ne1;
+    t.nb[3] = t.nb[2] * ne2;
+    return t;
+}
+
+}  // namespace qmoe

@@ -77,7 +77,25 @@ def build(verbose: bool = False, jobs: int = 5) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    build_cpp_tests(verbose)
     return LIB_PATH
+
+
+CPP_TEST_SRC = os.path.join(REPO_DIR, "tests", "cpp", "test_moe_layer.cpp")
+CPP_TEST_BIN = os.path.join(REPO_DIR, "tests", "cpp", "test_moe_layer")
+
+
+def build_cpp_tests(verbose: bool = False) -> str:
+    """The C++ drop-in test (tests/cpp/test_moe_layer.cpp) linked against libqmoe.so."""
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-I", os.path.join(REPO_DIR, "include"),
+           CPP_TEST_SRC, "-o", CPP_TEST_BIN, "-L", PKG_DIR, "-lqmoe",
+           "-Wl,-rpath,$ORIGIN/../../qwenium_amd"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"C++ test build failed:\n{res.stdout}{res.stderr}")
+    return CPP_TEST_BIN
 
 
 if __name__ == "__main__":

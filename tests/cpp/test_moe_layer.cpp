@@ -1,0 +1,213 @@
+// test_moe_layer.cpp -- the reference's MoE unit tests (tests/unit/test_moe.cpp)
+// re-run through the C++ drop-in (include/qmoe_layer.hpp) on the HIP path.
+//
+// Same cases and constant fills as the reference (router 0.1, experts 0.05,
+// shared 0.02, shared gate 0.5, input 0.5), at the smallest shapes the
+// quantized kernels take (n_embd 256, ffn 64, 8 experts, top-2, 2 tokens),
+// with Q8_0 expert weights.  TopKGatingCorrectness feeds the reference's KAT
+// logits {1,3,0.5,2,-1,0,4,1.5} through the real router (one-hot input, so
+// logits equal the router column exactly) and checks ids [6,1] and weights
+// 0.7310586 / 0.2689414.
+//
+// Usage: test_moe_layer [--host-only]   (--host-only: checks that need no GPU)
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "qmoe_layer.hpp"
+
+static int g_failures = 0;
+#define EXPECT(cond, msg)                                                       \
+    do {                                                                        \
+        if (!(cond)) {                                                          \
+            std::printf("    FAILED: %s (%s:%d)\n", msg, __FILE__, __LINE__);   \
+            ++g_failures;                                                       \
+        }                                                                       \
+    } while (0)
+#define HIP_OK(x)                                                                            \
+    do {                                                                                     \
+        hipError_t e_ = (x);                                                                 \
+        if (e_ != hipSuccess) {                                                              \
+            std::printf("HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); \
+            std::exit(2);                                                                    \
+        }                                                                                    \
+    } while (0)
+
+constexpr int N_EMBD = 256, N_EXPERTS = 8, TOP_K = 2, FFN_DIM = 64, N_TOKENS = 2;
+
+// Q8_0 bytes of n values all equal to v (quantize_row_q8_0_ref of a constant block).
+static std::vector<uint8_t> q8_const(float v, size_t n) {
+    const float amax = std::fabs(v);
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const _Float16 dh = (_Float16)d;
+    const int8_t q = (int8_t)std::roundf(v * id);
+    std::vector<uint8_t> out(n / 32 * 34);
+    for (size_t b = 0; b < n / 32; ++b) {
+        std::memcpy(&out[b * 34], &dh, 2);
+        std::memset(&out[b * 34 + 2], (uint8_t)q, 32);
+    }
+    return out;
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    explicit DevBuf(size_t bytes) { HIP_OK(hipMalloc(&p, bytes)); }
+    template <typename T>
+    DevBuf(const std::vector<T>& h) {
+        HIP_OK(hipMalloc(&p, h.size() * sizeof(T)));
+        HIP_OK(hipMemcpy(p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
+    }
+    ~DevBuf() { (void)hipFree(p); }
+};
+
+struct Fixture {
+    DevBuf router, gate, up, down, sh_gate, sh_up, sh_down, sh_norm;
+    qmoe_tensor t_router, t_gate, t_up, t_down, t_sh_gate, t_sh_up, t_sh_down, t_sh_norm;
+    Fixture(const std::vector<float>& router_vals, float expert_v)
+        : router(router_vals),
+          gate(q8_const(expert_v, (size_t)N_EXPERTS * FFN_DIM * N_EMBD)),
+          up(q8_const(expert_v, (size_t)N_EXPERTS * FFN_DIM * N_EMBD)),
+          down(q8_const(expert_v, (size_t)N_EXPERTS * N_EMBD * FFN_DIM)),
+          sh_gate(q8_const(0.02f, (size_t)FFN_DIM * N_EMBD)),
+          sh_up(q8_const(0.02f, (size_t)FFN_DIM * N_EMBD)),
+          sh_down(q8_const(0.02f, (size_t)N_EMBD * FFN_DIM)),
+          sh_norm(std::vector<float>(N_EMBD, 0.5f)) {
+        t_router = qmoe::make_tensor(router.p, QMOE_TYPE_F32, 2, N_EMBD, N_EXPERTS);
+        t_gate = qmoe::make_tensor(gate.p, QMOE_TYPE_Q8_0, 3, N_EMBD, FFN_DIM, N_EXPERTS);
+        t_up = qmoe::make_tensor(up.p, QMOE_TYPE_Q8_0, 3, N_EMBD, FFN_DIM, N_EXPERTS);
+        t_down = qmoe::make_tensor(down.p, QMOE_TYPE_Q8_0, 3, FFN_DIM, N_EMBD, N_EXPERTS);
+        t_sh_gate = qmoe::make_tensor(sh_gate.p, QMOE_TYPE_Q8_0, 2, N_EMBD, FFN_DIM);
+        t_sh_up = qmoe::make_tensor(sh_up.p, QMOE_TYPE_Q8_0, 2, N_EMBD, FFN_DIM);
+        t_sh_down = qmoe::make_tensor(sh_down.p, QMOE_TYPE_Q8_0, 2, FFN_DIM, N_EMBD);
+        t_sh_norm = qmoe::make_tensor(sh_norm.p, QMOE_TYPE_F32, 1, N_EMBD);
+    }
+};
+
+static qmoe::MoELayer::Hparams hparams(bool shared) { return {N_EXPERTS, TOP_K, FFN_DIM, shared}; }
+
+static std::vector<float> run_forward(bool use_shared, int n_tokens = N_TOKENS, float x_val = 0.5f) {
+    Fixture f(std::vector<float>((size_t)N_EMBD * N_EXPERTS, 0.1f), 0.05f);
+    qmoe::MoELayer layer(&f.t_router, &f.t_gate, &f.t_up, &f.t_down, use_shared ? &f.t_sh_gate : nullptr,
+                         use_shared ? &f.t_sh_up : nullptr, use_shared ? &f.t_sh_down : nullptr,
+                         use_shared ? &f.t_sh_norm : nullptr, hparams(use_shared));
+    DevBuf x(std::vector<float>((size_t)n_tokens * N_EMBD, x_val));
+    DevBuf y((size_t)n_tokens * N_EMBD * sizeof(float));
+    layer.forward((const float*)x.p, n_tokens, (float*)y.p, qmoe::Phase::Prefill, 0);
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<float> out((size_t)n_tokens * N_EMBD);
+    HIP_OK(hipMemcpy(out.data(), y.p, out.size() * sizeof(float), hipMemcpyDeviceToHost));
+    return out;
+}
+
+static void BuildSucceedsNoSharedExpert() { EXPECT(run_forward(false).size() == (size_t)N_EMBD * N_TOKENS, "size"); }
+static void BuildSucceedsWithSharedExpert() { EXPECT(run_forward(true).size() == (size_t)N_EMBD * N_TOKENS, "size"); }
+
+static void OutputIsFinite() {
+    for (float v : run_forward(false)) EXPECT(std::isfinite(v), "finite");
+}
+static void OutputIsFiniteWithSharedExpert() {
+    for (float v : run_forward(true)) EXPECT(std::isfinite(v), "finite");
+}
+
+static void TopKGatingCorrectness() {
+    const float kat[N_EXPERTS] = {1.0f, 3.0f, 0.5f, 2.0f, -1.0f, 0.0f, 4.0f, 1.5f};
+    std::vector<float> router((size_t)N_EMBD * N_EXPERTS, 0.0f);
+    for (int e = 0; e < N_EXPERTS; ++e) router[(size_t)e * N_EMBD] = kat[e];  // row e = [kat[e], 0, ...]
+    Fixture f(router, 0.05f);
+    qmoe::MoELayer layer(&f.t_router, &f.t_gate, &f.t_up, &f.t_down, nullptr, nullptr, nullptr, nullptr,
+                         hparams(false));
+    std::vector<float> xh(N_EMBD, 0.0f);
+    xh[0] = 1.0f;  // one-hot: logits == kat exactly
+    DevBuf x(xh);
+    DevBuf y(N_EMBD * sizeof(float));
+    DevBuf logits(N_EXPERTS * sizeof(float)), idx(TOP_K * sizeof(int32_t)), w(TOP_K * sizeof(float));
+    qmoe_debug dbg{};
+    dbg.logits = (float*)logits.p;
+    dbg.topk_idx = (int32_t*)idx.p;
+    dbg.topk_w = (float*)w.p;
+    layer.forward((const float*)x.p, 1, (float*)y.p, qmoe::Phase::Decode, 0, nullptr, nullptr, nullptr, &dbg);
+    HIP_OK(hipDeviceSynchronize());
+    int32_t ih[TOP_K];
+    float wh[TOP_K], lh[N_EXPERTS];
+    HIP_OK(hipMemcpy(ih, idx.p, sizeof(ih), hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(wh, w.p, sizeof(wh), hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(lh, logits.p, sizeof(lh), hipMemcpyDeviceToHost));
+    for (int e = 0; e < N_EXPERTS; ++e) EXPECT(lh[e] == kat[e], "router logits equal the KAT logits");
+    EXPECT(ih[0] == 6 && ih[1] == 1, "top-2 ids [6, 1]");
+    const float e6 = std::exp(4.0f), e1 = std::exp(3.0f);
+    EXPECT(std::fabs(wh[0] - e6 / (e6 + e1)) < 1e-5f, "weight 0");
+    EXPECT(std::fabs(wh[1] - e1 / (e6 + e1)) < 1e-5f, "weight 1");
+    EXPECT(std::fabs(wh[0] - 0.7310586f) < 1e-6f && std::fabs(wh[1] - 0.2689414f) < 1e-6f, "KAT weights");
+}
+
+static void SharedExpertChangesOutput() {
+    const std::vector<float> a = run_forward(false), b = run_forward(true);
+    bool any = false;
+    for (size_t i = 0; i < a.size(); ++i) any |= std::fabs(a[i] - b[i]) > 1e-6f;
+    EXPECT(any, "shared expert had no effect on output");
+}
+
+static void OutputShapeMatchesInput() {
+    Fixture f(std::vector<float>((size_t)N_EMBD * N_EXPERTS, 0.1f), 0.01f);
+    qmoe::MoELayer layer(&f.t_router, &f.t_gate, &f.t_up, &f.t_down, nullptr, nullptr, nullptr, nullptr,
+                         hparams(false));
+    EXPECT(layer.n_embd() == N_EMBD, "n_embd");
+    const int n_tok = 5;
+    DevBuf x(std::vector<float>((size_t)n_tok * N_EMBD, 0.5f));
+    DevBuf y((size_t)n_tok * N_EMBD * sizeof(float));
+    layer.forward((const float*)x.p, n_tok, (float*)y.p);
+    HIP_OK(hipDeviceSynchronize());
+}
+
+// Host-only: the constructor's fail-loud contract (moe.cpp:47-52), fake pointers.
+static void ConstructorThrowsWithoutSharedWeights() {
+    const void* fake = (const void*)0x10000000;
+    qmoe_tensor r = qmoe::make_tensor(fake, QMOE_TYPE_F32, 2, N_EMBD, N_EXPERTS);
+    qmoe_tensor g = qmoe::make_tensor(fake, QMOE_TYPE_Q8_0, 3, N_EMBD, FFN_DIM, N_EXPERTS);
+    qmoe_tensor d = qmoe::make_tensor(fake, QMOE_TYPE_Q8_0, 3, FFN_DIM, N_EMBD, N_EXPERTS);
+    std::string msg;
+    try {
+        qmoe::MoELayer layer(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hparams(true));
+    } catch (const std::runtime_error& e) {
+        msg = e.what();
+    }
+    EXPECT(msg == "moe_layer: has_shared_expert=true but shared expert weights are null", "reference message");
+    bool threw = false;
+    try {
+        qmoe::MoELayer ok(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hparams(false));
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    EXPECT(!threw, "valid layer constructs");
+}
+
+int main(int argc, char** argv) {
+    const bool host_only = argc > 1 && std::string(argv[1]) == "--host-only";
+    struct Case { const char* name; void (*fn)(); bool gpu; } cases[] = {
+        {"ConstructorThrowsWithoutSharedWeights", ConstructorThrowsWithoutSharedWeights, false},
+        {"BuildSucceedsNoSharedExpert", BuildSucceedsNoSharedExpert, true},
+        {"BuildSucceedsWithSharedExpert", BuildSucceedsWithSharedExpert, true},
+        {"OutputIsFinite", OutputIsFinite, true},
+        {"OutputIsFiniteWithSharedExpert", OutputIsFiniteWithSharedExpert, true},
+        {"TopKGatingCorrectness", TopKGatingCorrectness, true},
+        {"SharedExpertChangesOutput", SharedExpertChangesOutput, true},
+        {"OutputShapeMatchesInput", OutputShapeMatchesInput, true},
+    };
+    int run = 0;
+    for (const auto& c : cases) {
+        if (host_only && c.gpu) continue;
+        const int before = g_failures;
+        std::printf("[ RUN      ] MoELayerTest.%s\n", c.name);
+        std::fflush(stdout);
+        c.fn();
+        std::printf("[ %s ] MoELayerTest.%s\n", g_failures == before ? "      OK" : " FAILED ", c.name);
+        ++run;
+    }
+    std::printf("%d tests, %d failures\n", run, g_failures);
+    return g_failures ? 1 : 0;
+}
