@@ -300,14 +300,17 @@ hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T,
                                     : launch_gateup<kTypeQ8_0>(a, max_slots, L.n_cu, stream);
 }
 
-hipError_t launch_experts_down(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
+hipError_t launch_quant_h(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
     const ExpertArgs a = make_expert_args(L, ws, T);
-    const int max_slots = min(L.E, T * L.K) + L.S;
     const int max_rows = T * L.K + L.S * T;
     const int qblocks = (max_rows * (L.F / 32) + 7) / 8;
     hipLaunchKernelGGL(k_quant_h, dim3(qblocks), dim3(256), 0, stream, a);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
+    return hipGetLastError();
+}
+
+hipError_t launch_experts_down(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
+    const ExpertArgs a = make_expert_args(L, ws, T);
+    const int max_slots = min(L.E, T * L.K) + L.S;
     return (L.dn_type == kTypeQ4_0) ? launch_down<kTypeQ4_0>(a, max_slots, L.n_cu, stream)
                                     : launch_down<kTypeQ8_0>(a, max_slots, L.n_cu, stream);
 }

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -254,6 +255,11 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, L->device) == hipSuccess && n_cu > 0)
         d.n_cu = n_cu;
+    // token count from which the grouped int8-MFMA GEMMs replace the streaming GEMVs
+    if (const char* env = std::getenv("QMOE_MFMA_MIN_TOKENS")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v >= 1) d.mfma_min_tokens = (int)std::min<long>(v, 1 << 30);
+    }
     *out = L;
     return QMOE_OK;
 }
@@ -342,11 +348,15 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
     hipError_t err = mark(0);
     if (err == hipSuccess) err = qmoe::launch_route(d, v, x, n_tokens, stream);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
+    const bool mfma = n_tokens >= d.mfma_min_tokens;
     err = mark(1);
-    if (err == hipSuccess) err = qmoe::launch_experts_gateup(d, v, n_tokens, stream);
+    if (err == hipSuccess)
+        err = mfma ? qmoe::launch_gateup_mfma(d, v, n_tokens, stream) : qmoe::launch_experts_gateup(d, v, n_tokens, stream);
     if (err != hipSuccess) return hip_fail(err, "gate/up expert kernel");
     err = mark(2);
-    if (err == hipSuccess) err = qmoe::launch_experts_down(d, v, n_tokens, stream);
+    if (err == hipSuccess) err = qmoe::launch_quant_h(d, v, n_tokens, stream);
+    if (err == hipSuccess)
+        err = mfma ? qmoe::launch_down_mfma(d, v, n_tokens, stream) : qmoe::launch_experts_down(d, v, n_tokens, stream);
     if (err != hipSuccess) return hip_fail(err, "down expert kernel");
     err = mark(3);
     if (err == hipSuccess) err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream);

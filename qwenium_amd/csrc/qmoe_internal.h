@@ -28,6 +28,7 @@ struct LayerDesc {
     uint64_t sh_gate_nb1 = 0, sh_up_nb1 = 0, sh_down_nb1 = 0;
     const float* w_sh_norm = nullptr;
     int n_cu = 256;                         // compute units of the layer's device
+    int mfma_min_tokens = 128;              // token count from which the int8-MFMA path runs
 };
 
 // Device scratch.  R = T*K + S*T rows: routed assignments sorted by expert,
@@ -65,7 +66,9 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* carve, void
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, hipStream_t stream);
 hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_experts_down(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
-hipError_t launch_experts_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+hipError_t launch_quant_h(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+hipError_t launch_down_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
                           hipStream_t stream);
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream);

@@ -236,3 +236,55 @@ def test_graph_replay_matches_eager(gpu):
             np.testing.assert_array_equal(outs[i].cpu().numpy().view(np.int32), eager[i].cpu().numpy().view(np.int32))
         layers[1].forward(xs[0], workspace=ws)  # eager work between replays
         torch.cuda.synchronize()
+
+
+# ---- int8-MFMA grouped GEMM path (prefill) -------------------------------------------------
+@pytest.mark.parametrize("wtype", [TYPE_Q4_0, TYPE_Q8_0])
+@pytest.mark.parametrize("T", [1, 17, 64, 65, 130])
+def test_mfma_path_small_layer(gpu, monkeypatch, wtype, T):
+    """Forced MFMA path (QMOE_MFMA_MIN_TOKENS=1) on small shapes: tile edges at 64 rows."""
+    monkeypatch.setenv("QMOE_MFMA_MIN_TOKENS", "1")
+    spec = LayerSpec(256, 16, 4, 128, True, wtype)
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=200 + T)
+    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+
+
+def test_mfma_config1_forced(gpu, monkeypatch):
+    monkeypatch.setenv("QMOE_MFMA_MIN_TOKENS", "1")
+    spec = synthetic.CONFIG1
+    y, got, y_ref, d_ref, *_ = run_pair(spec, 32, seed=0)
+    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+
+
+def test_mfma_35b_q4_0_t256(gpu):
+    spec = synthetic.QWEN35B
+    y, got, y_ref, d_ref, *_ = run_pair(spec, 256, seed=9)
+    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+
+
+def test_prefill_35b_q4_0_t4096(gpu):
+    """The 4096-token prefill workload: routing checked for every token, outputs on
+    a sample of tokens (a token's output depends on that token only)."""
+    spec = synthetic.QWEN35B
+    T = 4096
+    tensors = synthetic.make_layer_tensors(spec, 3)
+    layer = synthetic.make_layer(spec, 3, tensors=tensors)
+    x = synthetic.make_x(spec, T, 3)
+    y, dbg = layer.forward(x, debug=True)
+    torch.cuda.synchronize()
+    ref = host_layer(spec, tensors)
+    xh = x.cpu().numpy()
+    logits = po.router_logits(ref.t["router"], xh)
+    idx, w = po.topk_softmax(logits, spec.top_k)
+    off, rows, _ = po.sort_assignments(idx, spec.n_experts)
+    np.testing.assert_array_equal(dbg["topk_idx"].cpu().numpy(), idx)
+    np.testing.assert_array_equal(dbg["offsets"].cpu().numpy(), off)
+    np.testing.assert_array_equal(dbg["rows"].cpu().numpy(), rows)
+    counts = np.diff(off)
+    assert counts.sum() == T * spec.top_k and counts.max() < 4 * T * spec.top_k / spec.n_experts
+    sample = np.random.default_rng(0).choice(T, 48, replace=False)
+    y_ref = ref.forward(xh[sample])
+    yg = y.cpu().numpy()[sample]
+    rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
+    assert np.max(np.abs(yg - y_ref)) <= TOL * rms
+    assert np.mean(yg.view(np.int32) == y_ref.view(np.int32)) >= 0.999
