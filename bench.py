@@ -1,22 +1,24 @@
 #!/usr/bin/env python3
 """MoE-layer throughput on one MI355X (gfx950).
 
-Workload (default, `--workload decode`): the Qwen3.6-35B-A3B-shaped MoE layer
-(hidden 2048, 256 experts, top-8 + 1 shared expert, ffn 512, SwiGLU, Q4_0
-expert weights from N(0,0.02), f32 router N(0,0.02)) at decode batch 10
-(10 tokens, f32 activations N(0,1)).  A step is one layer forward over one
-batch.  Steps rotate over `--layers` distinct synthetic layers (8 x 0.87 GB by
-default, far above the 256 MB Infinity Cache, so weights stream from HBM) and
-`--batches` distinct input batches, so expert sets change from step to step.
+Workloads (Qwen3.6-35B-A3B MoE layer shape: hidden 2048, 256 experts, top-8 +
+1 shared expert, ffn 512, SwiGLU; synthetic seeded weights N(0,0.02) in GGUF
+block layout, f32 router N(0,0.02), f32 activations N(0,1)):
 
-Output: ONE JSON line with value = tokens/s of the layer, the HBM roofline of
-the dominant kernel (gate/up expert GEMV; per-launch duration from HIP events
-recorded by the library on its own stream) and the CPU oracle timed on the
-host cores over a bounded sample.
+  decode  (default)  10 tokens, Q4_0 experts.  HBM-bound.  Steps rotate over
+                     --layers distinct layers (8 x 0.87 GB by default, far above
+                     the 256 MB Infinity Cache) and --batches input batches.
+  prefill            4096 tokens, Q4_0 experts.  int8-MFMA-bound.
+
+A step is one layer forward over one batch.  Output: ONE JSON line with value
+= tokens/s of the layer, the roofline of the dominant kernel (per-launch
+duration from HIP events the library records on its own stream) and the CPU
+oracle timed on the host cores over a bounded sample.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -28,6 +30,12 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_I8_PEAK_TOPS = 5000.0
+
+WORKLOADS = {
+    # name: (tokens, weight type name, default layers, default batches, default steps, warmup)
+    "decode": (10, "Q4_0", 8, 16, 2000, 64),
+    "prefill": (4096, "Q4_0", 4, 2, 64, 8),
+}
 
 
 def log(msg: str) -> None:
@@ -48,19 +56,56 @@ def cpu_model() -> str:
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--workload", default="decode", choices=["decode"])
-    ap.add_argument("--tokens", type=int, default=10)
-    ap.add_argument("--layers", type=int, default=8)
-    ap.add_argument("--batches", type=int, default=16)
+    ap.add_argument("--workload", default="decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--tokens", type=int, default=None)
+    ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--batches", type=int, default=None)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of HIP graph replays")
-    ap.add_argument("--profile-steps", type=int, default=256)
+    ap.add_argument("--profile-steps", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, os.cpu_count())")
     ap.add_argument("--no-cpu", action="store_true")
     return ap.parse_args()
+
+
+class PhaseEvents:
+    """Per-step HIP events recorded by the library around its phases."""
+
+    N = 5
+
+    def __init__(self, n_steps: int):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.evs = []
+        for _ in range(n_steps * self.N):
+            e = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            self.evs.append(e)
+
+    def arr(self, step: int):
+        return (ctypes.c_void_p * self.N)(*[self.evs[step * self.N + j].value for j in range(self.N)])
+
+    def phases_us(self, n_steps: int):
+        import numpy as np
+        out = np.zeros((n_steps, self.N - 1))
+        ms = ctypes.c_float()
+        for i in range(n_steps):
+            for j in range(self.N - 1):
+                if self.hip.hipEventElapsedTime(ctypes.byref(ms), self.evs[i * self.N + j],
+                                                self.evs[i * self.N + j + 1]) != 0:
+                    raise RuntimeError("hipEventElapsedTime failed")
+                out[i, j] = ms.value * 1e3
+        return out
+
+    def close(self):
+        for e in self.evs:
+            self.hip.hipEventDestroy(e)
 
 
 def main() -> int:
@@ -77,25 +122,28 @@ def main() -> int:
     from qwenium_amd import Workspace, lib, synthetic
     from qwenium_amd._lib import check, row_bytes
 
+    T0, wname, L0, B0, S0, W0 = WORKLOADS[args.workload]
+    T = args.tokens or T0
+    L = args.layers or L0
+    B = args.batches or B0
+    steps_req = args.steps or S0
+    warmup = args.warmup if args.warmup is not None else W0
     spec = synthetic.QWEN35B
-    T = args.tokens
     H, E, K, F = spec.n_embd, spec.n_experts, spec.top_k, spec.ffn_dim
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
-    log(f"generating {args.layers} layers ({spec.wtype=}) and {args.batches} input batches on the GPU")
+    log(f"workload {args.workload}: T={T}, generating {L} layers ({wname}) and {B} input batches on the GPU")
     layers, tensors = [], []
-    for l in range(args.layers):
+    for l in range(L):
         t = synthetic.make_layer_tensors(spec, args.seed, layer=l, device=dev)
         tensors.append(t)
         layers.append(synthetic.make_layer(spec, args.seed, layer=l, tensors=t))
-    xs = [synthetic.make_x(spec, T, args.seed, batch=b, device=dev) for b in range(args.batches)]
+    xs = [synthetic.make_x(spec, T, args.seed, batch=b, device=dev) for b in range(B)]
     ws = Workspace(layers[0], T)
     y = torch.empty((T, H), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
-    # schedule: step s uses layer s % L and batch s % B; a graph holds one period
-    L, B = args.layers, args.batches
     period = int(np.lcm(L, B))
     sched = [(s % L, s % B) for s in range(period)]
 
@@ -109,24 +157,24 @@ def main() -> int:
 
     rb_h = row_bytes(spec.wtype, H)
     rb_f = row_bytes(spec.wtype, F)
-    expert_bytes = 2 * F * rb_h + H * rb_f                # gate + up + down of one expert
-    shared_bytes = expert_bytes if spec.shared else 0
-    router_bytes = E * H * 4 + (H * 4 if spec.shared else 0)
-    act_bytes = 2 * T * H * 4                             # x in, y out (f32)
-    layer_bytes = D_mean * expert_bytes + shared_bytes + router_bytes + act_bytes
-    R = T * K + (T if spec.shared else 0)
-    gu_bytes = (D_mean + (1 if spec.shared else 0)) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * (F + F // 32 * 8)
+    expert_bytes = 2 * F * rb_h + H * rb_f
+    router_bytes = E * H * 4 + H * 4
+    R = T * K + T
+    layer_bytes = D_mean * expert_bytes + expert_bytes + router_bytes + 2 * T * H * 4
+    ops_gu = 2.0 * R * 2 * F * H      # int8 multiply-adds x2, gate + up
+    ops_dn = 2.0 * R * H * F
+    layer_ops = ops_gu + ops_dn
 
     def run_step(i):
         l, b = sched[i % period]
         layers[l].forward(xs[b], out=y, workspace=ws)
 
-    log(f"warmup {args.warmup} steps")
-    for i in range(args.warmup):
+    log(f"warmup {warmup} steps")
+    for i in range(warmup):
         run_step(i)
     torch.cuda.synchronize()
 
-    steps = args.steps
+    steps = steps_req
     graph = None
     if not args.eager:
         stream = torch.cuda.Stream()
@@ -137,7 +185,7 @@ def main() -> int:
         for _ in range(2):
             graph.replay()
         torch.cuda.synchronize()
-        steps = max(period, (steps // period) * period)
+        steps = max(period, (steps_req // period) * period)
 
     log(f"timing {steps} steps ({'eager' if args.eager else f'graph of {period} steps'})")
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -161,43 +209,51 @@ def main() -> int:
 
     # per-phase timing on the library's stream: eager steps queued behind a
     # bounded sleep kernel so host launch latency never shows up as GPU time
-    log(f"profiling {args.profile_steps} steps with phase events")
-    n_ev = 5
-    import ctypes
-    hip = ctypes.CDLL("libamdhip64.so")
-    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
-    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
-    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
-    evs = []
-    for _ in range(args.profile_steps * n_ev):
-        e = ctypes.c_void_p()
-        if hip.hipEventCreate(ctypes.byref(e)) != 0:
-            raise RuntimeError("hipEventCreate failed")
-        evs.append(e)
+    n_prof = args.profile_steps or (256 if T <= 64 else 16)
+    log(f"profiling {n_prof} steps with phase events")
+    pe = PhaseEvents(n_prof)
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2.4e9 * 0.05))  # ~50 ms at 2.4 GHz
-    for i in range(args.profile_steps):
+    for i in range(n_prof):
         l, b = sched[i % period]
-        arr = (ctypes.c_void_p * n_ev)(*[evs[i * n_ev + j].value for j in range(n_ev)])
-        check(lib().qmoe_layer_set_phase_events(layers[l]._handle, arr))
+        check(lib().qmoe_layer_set_phase_events(layers[l]._handle, pe.arr(i)))
         layers[l].forward(xs[b], out=y, workspace=ws)
         check(lib().qmoe_layer_set_phase_events(layers[l]._handle, None))
     torch.cuda.synchronize()
-    phase = np.zeros((args.profile_steps, n_ev - 1))
-    ms = ctypes.c_float()
-    for i in range(args.profile_steps):
-        for j in range(n_ev - 1):
-            if hip.hipEventElapsedTime(ctypes.byref(ms), evs[i * n_ev + j], evs[i * n_ev + j + 1]) != 0:
-                raise RuntimeError("hipEventElapsedTime failed")
-            phase[i, j] = ms.value * 1e3
-    for e in evs:
-        hip.hipEventDestroy(e)
+    phase = pe.phases_us(n_prof)
+    pe.close()
     phase_us = phase.mean(axis=0)
-    D_prof = float(np.mean([distinct[sched[i % period]] for i in range(args.profile_steps)]))
-    gu_bytes_prof = (D_prof + 1) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * (F + F // 32 * 8)
+    log("phase us: route %.2f gate/up %.2f h-quant+down %.2f combine %.2f" % tuple(phase_us))
+    D_prof = float(np.mean([distinct[sched[i % period]] for i in range(n_prof)]))
     gu_us = float(phase_us[1])
-    achieved = gu_bytes_prof / (gu_us * 1e-6) / 1e9
-    log("phase us: route %.2f gate/up %.2f down %.2f combine %.2f" % tuple(phase_us))
+
+    if args.workload == "decode":
+        gu_bytes = (D_prof + 1) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * F * 8
+        achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+        roofline = {
+            "bound": "hbm", "kernel": "k_gateup_stream (gate+up expert GEMV, prefetching persistent waves)",
+            "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None, "bytes_per_launch": gu_bytes, "avg_launch_us": gu_us,
+        }
+        layer_rate = {
+            "distinct_experts_mean": D_mean, "algorithmic_bytes_per_step": layer_bytes,
+            "achieved_GBs": layer_bytes / (ms_per_step * 1e-3) / 1e9,
+            "frac_of_hbm_peak": layer_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        }
+        metric = "MoE-layer tokens/s at 35B-A3B shape (decode batch 10, Q4_0)"
+    else:
+        achieved = ops_gu / (gu_us * 1e-6) / 1e12
+        roofline = {
+            "bound": "mfma", "kernel": "k_expert_mfma<gate/up> (int8 MFMA grouped GEMM, f64-exact block epilogue)",
+            "achieved": achieved, "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s", "frac": achieved / MFMA_I8_PEAK_TOPS,
+            "traffic": None, "ops_per_launch": ops_gu, "avg_launch_us": gu_us,
+        }
+        layer_rate = {
+            "distinct_experts_mean": D_mean, "int8_ops_per_step": layer_ops,
+            "achieved_TOPs": layer_ops / (ms_per_step * 1e-3) / 1e12,
+            "frac_of_int8_mfma_peak": layer_ops / (ms_per_step * 1e-3) / 1e12 / MFMA_I8_PEAK_TOPS,
+        }
+        metric = f"MoE-layer tokens/s at 35B-A3B shape (prefill {T} tokens, Q4_0)"
 
     # parity of one step against the CPU oracle, and the CPU baseline
     result_parity = None
@@ -209,42 +265,42 @@ def main() -> int:
         host["router"] = host["router"].reshape(E, H)
         ref = po.Layer(H, E, K, F, spec.shared, spec.wtype, host)
         x0 = xs[0].cpu().numpy()
+        n_chk = min(T, 32)
         y_gpu, dbg = layers[0].forward(xs[0], workspace=ws, debug=True)
         torch.cuda.synchronize()
-        y_ref, d_ref = ref.forward(x0, debug=True)
-        y_gpu = y_gpu.cpu().numpy()
+        y_ref, d_ref = ref.forward(x0[:n_chk], debug=True)
+        y_gpu = y_gpu.cpu().numpy()[:n_chk]
         rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
         result_parity = {
-            "routing_bit_exact": bool(np.array_equal(dbg["topk_idx"].cpu().numpy(), d_ref["topk_idx"])
-                                      and np.array_equal(dbg["rows"].cpu().numpy(), d_ref["rows"])),
+            "tokens_checked": n_chk,
+            "routing_bit_exact": bool(np.array_equal(dbg["topk_idx"].cpu().numpy()[:n_chk], d_ref["topk_idx"])),
             "max_abs_err_over_rms": float(np.max(np.abs(y_gpu - y_ref)) / rms),
             "bit_identical_frac": float(np.mean(y_gpu.view(np.int32) == y_ref.view(np.int32))),
         }
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        ref.forward(x0, nthreads=threads)  # warm
+        n_cpu_tok = min(T, 10 if args.workload == "decode" else 256)
+        xc = x0[:n_cpu_tok]
+        ref.forward(xc, nthreads=threads)  # warm
         iters, t_cpu = 0, 0.0
         t_start = time.perf_counter()
         while t_cpu < args.cpu_seconds:
-            ref.forward(x0, nthreads=threads)
+            ref.forward(xc, nthreads=threads)
             iters += 1
             t_cpu = time.perf_counter() - t_start
         cpu = {
-            "value": iters * T / t_cpu,
-            "unit": "tokens/s",
-            "cores": threads,
-            "kind": "port",
-            "sample": f"{iters} forwards of layer 0 on decode batch 0 ({T} tokens) in {t_cpu:.1f}s; "
+            "value": iters * n_cpu_tok / t_cpu, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{iters} forwards of layer 0 on {n_cpu_tok} tokens of batch 0 in {t_cpu:.1f}s; "
                       f"ggml-semantics CPU restatement (oracle/liboracle.so, OpenMP) on {cpu_model()}",
         }
         log(f"cpu baseline {cpu['value']:.4g} tok/s on {threads} threads")
 
     out = {
-        "metric": "MoE-layer tokens/s at 35B-A3B shape (decode batch 10, Q4_0)",
+        "metric": metric,
         "value": tok_per_s,
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -252,30 +308,16 @@ def main() -> int:
         "dtype": "q4_0 x q8_0 int8 dot, f64-exact accumulation, f32 activations",
         "data": "synthetic (seeded, generated on device; random-init weights of the 35B-A3B MoE layer shape)",
         "config": {
-            "workload": f"Qwen3.6-35B-A3B MoE layer, decode batch {T}: hidden {H}, {E} experts, top-{K} + shared, "
-                        f"ffn {F}, Q4_0",
+            "workload": f"Qwen3.6-35B-A3B MoE layer, {args.workload} {T} tokens: hidden {H}, {E} experts, "
+                        f"top-{K} + shared, ffn {F}, {wname}",
             "tokens": T, "hidden": H, "experts": E, "top_k": K, "ffn": F, "shared_expert": spec.shared,
-            "weight_type": "Q4_0", "distinct_layers": L, "distinct_batches": B, "timing": "eager" if args.eager
-            else f"hip graph of {period} steps",
+            "weight_type": wname, "distinct_layers": L, "distinct_batches": B,
+            "timing": "eager" if args.eager else f"hip graph of {period} steps",
         },
-        "layer_hbm": {
-            "distinct_experts_mean": D_mean,
-            "algorithmic_bytes_per_step": layer_bytes,
-            "achieved_GBs": layer_bytes / (ms_per_step * 1e-3) / 1e9,
-            "frac_of_peak": layer_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        },
-        "phase_us": {"route": phase_us[0], "gate_up": phase_us[1], "down": phase_us[2], "combine": phase_us[3]},
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "k_gateup_gemv (gate+up expert GEMV, SwiGLU, Q8_0 epilogue)",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
-            "bytes_per_launch": gu_bytes_prof,
-            "avg_launch_us": gu_us,
-        },
+        "layer": layer_rate,
+        "phase_us": {"route": phase_us[0], "gate_up": phase_us[1], "hquant_down": phase_us[2],
+                     "combine": phase_us[3]},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "parity": result_parity,
     }
