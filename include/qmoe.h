@@ -76,6 +76,12 @@ typedef struct qmoe_debug {
     int32_t* offsets;   /* [n_experts+1] exclusive prefix of per-expert counts */
     int32_t* rows;      /* [T*top_k] assignment t*top_k+j, grouped by expert,
                            ascending (token, slot) inside each group */
+    /* Batched-router internals, written only when the forward routed through
+     * the bf16-MFMA router (large token counts): its approximate logits and a
+     * bound with |router_approx - logits| <= router_bound elementwise.  No
+     * counterpart in the reference. */
+    float*   router_approx; /* [T][n_experts] */
+    float*   router_bound;  /* [T][n_experts] */
 } qmoe_debug;
 
 typedef struct qmoe_layer qmoe_layer;

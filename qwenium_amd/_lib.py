@@ -67,6 +67,8 @@ class QmoeDebug(ctypes.Structure):
         ("sh_gate", ctypes.c_void_p),
         ("offsets", ctypes.c_void_p),
         ("rows", ctypes.c_void_p),
+        ("router_approx", ctypes.c_void_p),
+        ("router_bound", ctypes.c_void_p),
     ]
 
 

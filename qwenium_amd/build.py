@@ -42,6 +42,8 @@ def common_flags() -> list[str]:
         "-fPIC",
         # packed FP32 VALU ops stay off (see the design notes on numerics)
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA results in VGPRs (no accumulator-register copies in the epilogues)
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-I", os.path.join(REPO_DIR, "include"),
         "-I", CSRC,
         "-Wall",

@@ -8,15 +8,22 @@
 // equal the GEMV path and the CPU restatement bit for bit.
 //
 // Tiles come from the routing kernels: tiles[i] = {expert, first row, rows <= 64}.
-// Block = 4 waves: wave (ms, ns) owns the 32x32 sub-tile of rows
-// 32*ms..+32 of the row tile and outputs ns*32..+32 of the block's 64 outputs.
-//   gate/up mode: ns = 0 -> 32 gate rows, ns = 1 -> the same 32 up rows;
-//                 results go to gubuf[p][f] as (g, u).
-//   down mode:    64 consecutive W_down rows; results go to ybuf[p][n].
-// Activation rows (int8 Q8_0 + f64 scales) are staged in LDS (row stride padded
-// to 272 bytes: conflict-free 16-byte fragment reads); weights are read per
-// lane straight from GGUF block layout (dword-aligned block pairs) and
-// unpacked to int8 in registers.
+// A block computes 64 rows x 64 output columns of one tile with 4 waves; wave
+// (ms, ws) owns rows 32*ms..+32 and two 32-column MFMA tiles:
+//   gate/up mode: the gate rows and the up rows of the same 32 ffn indices
+//                 f (block columns 32*ws..+32), written to gubuf[p][f] as (g, u);
+//   down mode:    64 consecutive W_down rows (block columns 64*ws..+64 of 128).
+// The two column tiles share the wave's activation fragment and its per-row
+// activation scales.  Activation rows (int8 Q8_0 + f64 scales) are staged in
+// LDS (row stride padded to 272 bytes: conflict-free 16-byte fragment reads),
+// the next chunk is prefetched through registers while the current one is
+// consumed; weights are read per lane straight from GGUF block layout
+// (dword-aligned block pairs, one pair ahead) and unpacked in registers.
+//
+// Block order: logical block g = (tile, y) with y fastest; the blocks of each
+// XCD (hardware deals workgroups round-robin over the 8 XCDs) take one
+// contiguous range of g, so the tiles of an expert and their column chunks
+// share one L2.
 #include "qmoe_device.h"
 #include "qmoe_internal.h"
 
@@ -45,6 +52,7 @@ struct MfmaArgs {
     float2* gubuf;                               // gate/up output [R][F]
     float* ybuf;                                 // down output [R][H]
     int n_out;                                   // outputs per row (F or H)
+    int n_y;                                     // column chunks per tile
 };
 
 // 16 int8 weights of block `blk` (0 = first of the pair, 1 = second), k-half kh,
@@ -79,94 +87,133 @@ __device__ __forceinline__ v4i weight_frag<kTypeQ8_0>(const WPair<kTypeQ8_0>& w,
 }
 
 template <int WT, bool GATEUP>
-__global__ __launch_bounds__(256) void k_expert_mfma(MfmaArgs a) {
+__global__ __launch_bounds__(256, 2) void k_expert_mfma(MfmaArgs a) {
     __shared__ __align__(16) int8_t s_x[kTileM * kRowStride];
     __shared__ __align__(16) double s_d[(kKC / 32) * kTileM];  // [block][row]
-    const int tile_id = blockIdx.x;
-    if (tile_id >= a.counters[1]) return;
+    // XCD-aware logical block (see the file comment); the grid has >= 8 spare blocks
+    const int total = a.counters[1] * a.n_y;
+    const int share = (total + 7) >> 3;
+    const int jb = (int)(blockIdx.x >> 3);
+    if (jb >= share) return;
+    const int g = (int)(blockIdx.x & 7) * share + jb;
+    if (g >= total) return;
+    const int tile_id = g / a.n_y, y = g - tile_id * a.n_y;
     const int4 tile = a.tiles[tile_id];
     const int e = tile.x, p0 = tile.y, nr = tile.z;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int ms = wave & 1, ns = wave >> 1;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int ms = wave & 1, ws = wave >> 1;
     const int col = lane & 31, kh = lane >> 5;
-    const int out0 = blockIdx.y * 64;
+    const bool sh = e >= a.E;
 
-    // weight row of this lane's output column
-    const uint8_t* wrow;
-    int out_idx;
+    // weight rows of this lane's two output columns
+    const uint8_t* wrow[2];
+    int out_idx[2];
     if (GATEUP) {
-        const bool sh = e >= a.E;
-        const uint8_t* base = ns == 0 ? (sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2)
-                                      : (sh ? a.sh1 : a.w1 + (uint64_t)e * a.w1_nb2);
-        const uint64_t nb1 = ns == 0 ? (sh ? a.sh0_nb1 : a.w0_nb1) : (sh ? a.sh1_nb1 : a.w1_nb1);
-        out_idx = blockIdx.y * 32 + col;  // ffn index f
-        wrow = base + (uint64_t)out_idx * nb1;
+        const int f = y * 64 + ws * 32 + col;
+        const uint8_t* g0 = sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2;
+        const uint8_t* u0 = sh ? a.sh1 : a.w1 + (uint64_t)e * a.w1_nb2;
+        wrow[0] = g0 + (uint64_t)f * (sh ? a.sh0_nb1 : a.w0_nb1);
+        wrow[1] = u0 + (uint64_t)f * (sh ? a.sh1_nb1 : a.w1_nb1);
+        out_idx[0] = out_idx[1] = f;
     } else {
-        const bool sh = e >= a.E;
         const uint8_t* base = sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2;
         const uint64_t nb1 = sh ? a.sh0_nb1 : a.w0_nb1;
-        out_idx = out0 + ns * 32 + col;  // output row n
-        wrow = base + (uint64_t)out_idx * nb1;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            out_idx[c] = y * 128 + ws * 64 + c * 32 + col;
+            wrow[c] = base + (uint64_t)out_idx[c] * nb1;
+        }
     }
 
-    double acc[16];
+    // staging assignment: 16-byte chunk (m = tid/16 + 16q, c16 = tid%16), q < 4;
+    // scales (m = tid%64, block tid/64 + 4q), q < 2
+    const int8_t* xsrc[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0;
-
+    for (int q = 0; q < 4; ++q) {
+        const int m = (tid >> 4) + 16 * q;
+        const int pr = p0 + min(m, nr - 1);
+        xsrc[q] = m < nr ? a.a_qs + (uint64_t)(GATEUP ? a.row_token[pr] : pr) * a.K + 16 * (tid & 15) : nullptr;
+    }
     const int nblk_k = a.K >> 5;
+    const float2* dsrc;
+    {
+        const int m = tid & 63;
+        const int pr = p0 + min(m, nr - 1);
+        dsrc = m < nr ? a.a_ds + (uint64_t)(GATEUP ? a.row_token[pr] : pr) * nblk_k : nullptr;
+    }
+    u32x4 px[4];
+    double pd[2];
+    auto stage_load = [&](int kc) {
+        const int kcn = min(kKC, a.K - kc);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            px[q] = (xsrc[q] && 16 * (tid & 15) < kcn) ? *(const u32x4*)(xsrc[q] + kc) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int bb = (tid >> 6) + 4 * q;
+            pd[q] = (dsrc && 32 * bb < kcn) ? (double)dsrc[(kc >> 5) + bb].x : 0.0;
+        }
+    };
+    stage_load(0);
+
+    double acc[2][16];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][r] = 0.0;
+
+    const bool active = 32 * ms < nr;  // wave-uniform: rows 32*ms.. of the tile exist
+    const int npairs = a.K >> 6;
+    WPair<WT> wc[2], wn[2];
+    if (active) {
+        wc[0].load(wrow[0], 0);
+        wc[1].load(wrow[1], 0);
+    }
+    int pidx = 0;
     for (int kc = 0; kc < a.K; kc += kKC) {
         const int kcn = min(kKC, a.K - kc);  // multiple of 64
+        __syncthreads();  // the previous chunk's LDS reads are done
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *(u32x4*)(s_x + ((tid >> 4) + 16 * q) * kRowStride + 16 * (tid & 15)) = px[q];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) s_d[((tid >> 6) + 4 * q) * kTileM + (tid & 63)] = pd[q];
         __syncthreads();
-        // stage A rows: kTileM rows x kcn bytes (16-byte chunks) + per-block scales
-        const int chunks = kcn / 16;
-        for (int i = threadIdx.x; i < kTileM * chunks; i += 256) {
-            const int m = i / chunks, c = i % chunks;
-            u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if (m < nr) {
-                const int p = p0 + m;
-                const int arow = GATEUP ? a.row_token[p] : p;
-                v = *(const u32x4*)(a.a_qs + (uint64_t)arow * a.K + kc + 16 * c);
-            }
-            *(u32x4*)(s_x + m * kRowStride + 16 * c) = v;
-        }
-        const int nbk = kcn / 32;
-        for (int i = threadIdx.x; i < kTileM * nbk; i += 256) {
-            const int m = i % kTileM, b = i / kTileM;
-            double d = 0.0;
-            if (m < nr) {
-                const int p = p0 + m;
-                const int arow = GATEUP ? a.row_token[p] : p;
-                d = (double)a.a_ds[(uint64_t)arow * nblk_k + (kc >> 5) + b].x;
-            }
-            s_d[b * kTileM + m] = d;
-        }
-        __syncthreads();
+        if (kc + kKC < a.K) stage_load(kc + kKC);
+        if (!active) continue;
         const int8_t* xrow = s_x + (32 * ms + col) * kRowStride + 16 * kh;
-        for (int bp = 0; bp < nbk; bp += 2) {
-            WPair<WT> w;
-            w.load(wrow, ((kc >> 5) + bp) >> 1);
+        for (int bp = 0; bp < kcn / 32; bp += 2, ++pidx) {
+            if (pidx + 1 < npairs) {
+                wn[0].load(wrow[0], pidx + 1);
+                wn[1].load(wrow[1], pidx + 1);
+            }
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub) {
                 const int b = bp + sub;
-                const v4i bf = weight_frag<WT>(w, sub, kh);
                 const v4i af = *(const v4i*)(xrow + 32 * b);
                 const v16i z = {};
-                const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, z, 0, 0, 0);
-                const double dw = (double)(sub == 0 ? w.dA() : w.dB());
+                const v16i is0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, weight_frag<WT>(wc[0], sub, kh), z, 0, 0, 0);
+                const v16i is1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, weight_frag<WT>(wc[1], sub, kh), z, 0, 0, 0);
                 const double* drow = s_d + b * kTileM + 32 * ms + 4 * kh;
+                double dx[16];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int r = 4 * i + j;
-                        // fp32(d_w)*fp32(d_x) is exact in f32 and in f64
-                        acc[r] = __builtin_fma(dw * drow[8 * i + j], (double)isum[r], acc[r]);
-                    }
-                }
+                    for (int j = 0; j < 4; ++j) dx[4 * i + j] = drow[8 * i + j];
+                const double dw0 = (double)(sub == 0 ? wc[0].dA() : wc[0].dB());
+                const double dw1 = (double)(sub == 0 ? wc[1].dA() : wc[1].dB());
+                // fp32(d_w)*fp32(d_x) is exact in f64; the block term and the sum are exact
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[0][r] = __builtin_fma(dw0 * dx[r], (double)is0[r], acc[0][r]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[1][r] = __builtin_fma(dw1 * dx[r], (double)is1[r], acc[1][r]);
             }
+            wc[0] = wn[0];
+            wc[1] = wn[1];
         }
     }
-    // output tile: lane holds column `col`, rows 8i + 4kh + j of the sub-tile
+    if (!active) return;
+    // output: lane holds column `col` of each MFMA tile, rows 8i + 4kh + j of the wave's 32
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -174,12 +221,12 @@ __global__ __launch_bounds__(256) void k_expert_mfma(MfmaArgs a) {
             const int m = 32 * ms + 8 * i + 4 * kh + j;
             if (m < nr) {
                 const int p = p0 + m;
-                const float v = (float)acc[4 * i + j];
+                const int r = 4 * i + j;
                 if (GATEUP) {
-                    float* dst = (float*)(a.gubuf + (uint64_t)p * a.n_out + out_idx);
-                    dst[ns] = v;
+                    a.gubuf[(uint64_t)p * a.n_out + out_idx[0]] = make_float2((float)acc[0][r], (float)acc[1][r]);
                 } else {
-                    a.ybuf[(uint64_t)p * a.n_out + out_idx] = v;
+                    a.ybuf[(uint64_t)p * a.n_out + out_idx[0]] = (float)acc[0][r];
+                    a.ybuf[(uint64_t)p * a.n_out + out_idx[1]] = (float)acc[1][r];
                 }
             }
         }
@@ -197,6 +244,11 @@ static MfmaArgs base_args(const LayerDesc& L, const Workspace& ws) {
     return a;
 }
 
+static int mfma_max_tiles(const LayerDesc& L, const Workspace& ws, int T) {
+    return min(ws.max_tiles, (T * L.K + kTileM - 1) / kTileM + min(L.E, T * L.K) +
+                                 (L.S ? (T + kTileM - 1) / kTileM : 0));
+}
+
 hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
     MfmaArgs a = base_args(L, ws);
     a.w0 = L.w_gate; a.w0_nb1 = L.gate_nb1; a.w0_nb2 = L.gate_nb2;
@@ -206,9 +258,8 @@ hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hi
     a.a_qs = ws.xq_qs; a.a_ds = ws.xq_ds;
     a.K = L.H;
     a.n_out = L.F;
-    const int max_tiles = min(ws.max_tiles, (T * L.K + kTileM - 1) / kTileM + min(L.E, T * L.K) +
-                                                (L.S ? (T + kTileM - 1) / kTileM : 0));
-    const dim3 grid(max_tiles, L.F / 32);
+    a.n_y = L.F / 64;
+    const dim3 grid(mfma_max_tiles(L, ws, T) * a.n_y + 8);
     if (L.gu_type == kTypeQ4_0) hipLaunchKernelGGL((k_expert_mfma<kTypeQ4_0, true>), grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((k_expert_mfma<kTypeQ8_0, true>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
@@ -221,9 +272,8 @@ hipError_t launch_down_mfma(const LayerDesc& L, const Workspace& ws, int T, hipS
     a.a_qs = ws.hq_qs; a.a_ds = ws.hq_ds;
     a.K = L.F;
     a.n_out = L.H;
-    const int max_tiles = min(ws.max_tiles, (T * L.K + kTileM - 1) / kTileM + min(L.E, T * L.K) +
-                                                (L.S ? (T + kTileM - 1) / kTileM : 0));
-    const dim3 grid(max_tiles, L.H / 64);
+    a.n_y = L.H / 128;
+    const dim3 grid(mfma_max_tiles(L, ws, T) * a.n_y + 8);
     if (L.dn_type == kTypeQ4_0) hipLaunchKernelGGL((k_expert_mfma<kTypeQ4_0, false>), grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((k_expert_mfma<kTypeQ8_0, false>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();

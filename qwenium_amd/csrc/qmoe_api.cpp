@@ -131,6 +131,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.xq_qs = (int8_t*)take((size_t)T * H);
     ws.xq_ds = (float2*)take((size_t)T * (H / 32) * sizeof(float2));
     ws.logits = (float*)take((size_t)T * (E + 1) * sizeof(float));
+    ws.logit_bound = (float*)take((size_t)T * E * sizeof(float));
     ws.topk_idx = (int32_t*)take(A * sizeof(int32_t));
     ws.topk_w = (float*)take(A * sizeof(float));
     ws.sh_gate = (float*)take((size_t)T * sizeof(float));
@@ -141,6 +142,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.row_token = (int32_t*)take(R * sizeof(int32_t));
     ws.pos = (int32_t*)take(A * sizeof(int32_t));
     ws.active = (int32_t*)take((size_t)(E + 1) * sizeof(int32_t));
+    ws.expert_slot = (int32_t*)take((size_t)E * sizeof(int32_t));
     ws.slot_info = (int4*)take((size_t)(E + 1) * sizeof(int4));
     ws.counters = (int32_t*)take(16 * sizeof(int32_t));
     ws.tiles = (int4*)take((size_t)max_tiles * sizeof(int4));
@@ -260,6 +262,11 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 1) d.mfma_min_tokens = (int)std::min<long>(v, 1 << 30);
     }
+    // token count from which routing runs the batched bf16-MFMA router
+    if (const char* env = std::getenv("QMOE_BIG_ROUTER_MIN_TOKENS")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v >= 1) d.big_router_min_tokens = (int)std::min<long>(v, 1 << 30);
+    }
     *out = L;
     return QMOE_OK;
 }
@@ -346,7 +353,13 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
         return layer->record_phases ? hipEventRecord(layer->phase_events[i], stream) : hipSuccess;
     };
     hipError_t err = mark(0);
-    if (err == hipSuccess) err = qmoe::launch_route(d, v, x, n_tokens, stream);
+    qmoe::RouteDebug rdbg;
+    if (dbg) {
+        rdbg.exact_logits = dbg->logits != nullptr;
+        rdbg.approx = dbg->router_approx;
+        rdbg.bound = dbg->router_bound;
+    }
+    if (err == hipSuccess) err = qmoe::launch_route(d, v, x, n_tokens, rdbg, stream);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
     const bool mfma = n_tokens >= d.mfma_min_tokens;
     err = mark(1);

@@ -29,6 +29,7 @@ struct LayerDesc {
     const float* w_sh_norm = nullptr;
     int n_cu = 256;                         // compute units of the layer's device
     int mfma_min_tokens = 128;              // token count from which the int8-MFMA path runs
+    int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs
 };
 
 // Device scratch.  R = T*K + S*T rows: routed assignments sorted by expert,
@@ -40,6 +41,7 @@ struct Workspace {
     int8_t* xq_qs = nullptr;      // [T][H]   Q8_0 activation quants
     float2* xq_ds = nullptr;      // [T][H/32] {d, bitcast(sum q)}
     float* logits = nullptr;      // [T][E+1] (column E: shared gate logit)
+    float* logit_bound = nullptr; // [T][E] error bound of the approximate (MFMA) logits
     int32_t* topk_idx = nullptr;  // [T][K]
     float* topk_w = nullptr;      // [T][K]
     float* sh_gate = nullptr;     // [T]
@@ -50,6 +52,7 @@ struct Workspace {
     int32_t* row_token = nullptr; // [R]
     int32_t* pos = nullptr;       // [T*K] position of assignment
     int32_t* active = nullptr;    // [E+1] active experts (ascending), shared (=E) last
+    int32_t* expert_slot = nullptr; // [E] slot of each active expert
     int4* slot_info = nullptr;    // [E+1] per active slot {expert, first row, rows, 0}
     int32_t* counters = nullptr;  // [16] n_active, n_tiles, ...
     int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
@@ -63,7 +66,17 @@ struct Workspace {
 size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* carve, void* base);
 
 // --- launchers (each enqueues on `stream`, returns hipError_t of the launch) ---
-hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, hipStream_t stream);
+// Routing: logits, top-k + softmax + shared gate, counting sort.  Large T
+// routes through the bf16-MFMA router with exact refinement; exact_logits
+// additionally leaves the exact logits of every expert in ws.logits.
+struct RouteDebug {
+    bool exact_logits = false;      // leave exact logits of all experts in ws.logits
+    float* approx = nullptr;        // [T][E] MFMA-router approximate logits (MFMA router only)
+    float* bound = nullptr;         // [T][E] their error bounds
+};
+bool route_uses_mfma(const LayerDesc& L, int T);
+hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, const RouteDebug& dbg,
+                        hipStream_t stream);
 hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_experts_down(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_quant_h(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);

@@ -83,20 +83,13 @@ __device__ __forceinline__ void router_row(const RouterArgs& a, int e, float* s_
     }
 }
 
-template <int NCH>
-__global__ __launch_bounds__(256) void k_router_quant(RouterArgs a) {
-    __shared__ double s_part[4 * kRouterTokChunk];
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    if ((int)blockIdx.x < a.n_router_blocks) {
-        router_row<NCH>(a, blockIdx.x, (float*)s_part);
-        return;
-    }
-    // activation quantization: one wave per token, one 32-value block per lane step
-    const int t = (blockIdx.x - a.n_router_blocks) * 4 + wave;
-    if (t >= a.T) return;
-    const float* xr = a.x + (uint64_t)t * a.H;
-    const int nb = a.H >> 5;
+// Q8_0 quantization of one token row (one wave; lane b handles 32-value
+// blocks b, b+64, ...): d = fp16(amax/127), q = rint(x * 127/amax), and the
+// block's quant sum for the Q4_0 offset term.
+__device__ __forceinline__ void quant_token_row(const float* x, int H, int t, int lane, int8_t* xq_qs,
+                                                float2* xq_ds) {
+    const float* xr = x + (uint64_t)t * H;
+    const int nb = H >> 5;
     for (int b = lane; b < nb; b += 64) {
         const f32x4* src = (const f32x4*)(xr + 32 * b);
         float v[32];
@@ -124,10 +117,171 @@ __global__ __launch_bounds__(256) void k_router_quant(RouterArgs a) {
             }
             packed[i] = word;
         }
-        u32x4* dst = (u32x4*)(a.xq_qs + (uint64_t)t * a.H + 32 * b);
+        u32x4* dst = (u32x4*)(xq_qs + (uint64_t)t * H + 32 * b);
         dst[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
         dst[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
-        a.xq_ds[(uint64_t)t * nb + b] = make_float2(df, __builtin_bit_cast(float, sum));
+        xq_ds[(uint64_t)t * nb + b] = make_float2(df, __builtin_bit_cast(float, sum));
+    }
+}
+
+// Blocks [0, n_router_blocks) compute router rows; any further blocks
+// quantize x, four tokens per block.
+template <int NCH>
+__global__ __launch_bounds__(256) void k_router_quant(RouterArgs a) {
+    __shared__ double s_part[4 * kRouterTokChunk];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    if ((int)blockIdx.x < a.n_router_blocks) {
+        router_row<NCH>(a, blockIdx.x, (float*)s_part);
+        return;
+    }
+    const int t = (blockIdx.x - a.n_router_blocks) * 4 + wave;
+    if (t < a.T) quant_token_row(a.x, a.H, t, lane, a.xq_qs, a.xq_ds);
+}
+
+// ---------------------------------------------------------------------------
+// R1': batched router for large token counts: approximate logits from bf16
+// MFMAs with a rigorous per-logit error bound; the top-k then recomputes
+// exactly every expert the bound cannot rule out.
+//
+// x = xh + xl + rx and w = wh + wl + rw with xh = bf16(x), xl = bf16(x - xh)
+// (round to nearest, 8-bit significands): |rx| <= 2^-16 |x|.  The MFMAs sum
+// xh*wh + xh*wl + xl*wh; the dropped terms are <= 3.05 * 2^-16 |x||w| per
+// product.  Each 64-wide k step accumulates its 192 products in a fresh f32
+// accumulator (error <= 191 * 2^-23 * sum|p|, valid for any summation order
+// and rounding no worse than truncation) and is then added in f64.  Summing
+// both over k and using sum |x||w| <= |x|_2 |w|_2:
+//     |approx - exact| <= 7.2e-5 * |x_t|_2 * |w_e|_2,
+// charged as kRouterBoundRel (8e-5, which also covers the f32 norms) plus
+// 2^-21 |approx| for the f32 roundings of the logits and of approx +- bound.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kRtTile = 64;          // tokens and experts per router tile
+constexpr int kRtK = 64;             // k step
+constexpr int kRtLd = kRtK + 8;      // LDS row stride in bf16: conflict-free 16-byte reads
+constexpr float kRouterBoundRel = 8.0e-5f;
+
+struct RouterMfmaArgs {
+    const float* x;         // [T][H]
+    const float* w;         // [E][ld]
+    uint64_t ld;
+    int T, H, E;
+    int n_etiles, n_tiles;  // router tiles; blocks beyond n_tiles quantize x
+    float* logits;          // [T][E+1] approximate logits (column E untouched)
+    float* bound;           // [T][E]
+    int8_t* xq_qs;
+    float2* xq_ds;
+};
+
+__device__ __forceinline__ void split_store(const f32x4 v, __bf16* hi_dst, __bf16* lo_dst) {
+    const bf16x4 h = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+    const bf16x4 l = {(__bf16)(v.x - (float)h.x), (__bf16)(v.y - (float)h.y), (__bf16)(v.z - (float)h.z),
+                      (__bf16)(v.w - (float)h.w)};
+    *(bf16x4*)hi_dst = h;
+    *(bf16x4*)lo_dst = l;
+}
+
+__global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
+    __shared__ __attribute__((aligned(16))) __bf16 s_xh[kRtTile * kRtLd];
+    __shared__ __attribute__((aligned(16))) __bf16 s_xl[kRtTile * kRtLd];
+    __shared__ __attribute__((aligned(16))) __bf16 s_wh[kRtTile * kRtLd];
+    __shared__ __attribute__((aligned(16))) __bf16 s_wl[kRtTile * kRtLd];
+    __shared__ float s_nx[kRtTile], s_nw[kRtTile];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if ((int)blockIdx.x >= a.n_tiles) {
+        const int t = ((int)blockIdx.x - a.n_tiles) * 4 + wave;
+        if (t < a.T) quant_token_row(a.x, a.H, t, lane, a.xq_qs, a.xq_ds);
+        return;
+    }
+    // XCD-aware order: blocks are dealt round-robin to the 8 XCDs, so block b
+    // takes logical tile (b % 8) * (n/8) + b / 8 and the expert tiles of one
+    // token tile run on one XCD and share its L2.
+    const int b = blockIdx.x;
+    const int g = (a.n_tiles & 7) == 0 ? (b & 7) * (a.n_tiles >> 3) + (b >> 3) : b;
+    const int t0 = (g / a.n_etiles) * kRtTile;
+    const int e0 = (g % a.n_etiles) * kRtTile;
+    // loader: float4 f = tid + 256 i -> tile row (tid >> 4) + 16 i, k (tid & 15) * 4
+    const int lrow = tid >> 4, lk = (tid & 15) * 4;
+    const float* xp[4];
+    const float* wp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        xp[i] = a.x + (uint64_t)min(t0 + lrow + 16 * i, a.T - 1) * a.H + lk;
+        wp[i] = a.w + (uint64_t)min(e0 + lrow + 16 * i, a.E - 1) * a.ld + lk;
+    }
+    f32x4 xv[4], wv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { xv[i] = *(const f32x4*)xp[i]; wv[i] = *(const f32x4*)wp[i]; }
+    float sqx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sqw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    double acc64[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc64[r] = 0.0;
+    const int ms = wave & 1, ns = wave >> 1;
+    const int arow = (ms * 32 + (lane & 31)) * kRtLd + (lane >> 5) * 8;
+    const int brow = (ns * 32 + (lane & 31)) * kRtLd + (lane >> 5) * 8;
+    for (int k0 = 0; k0 < a.H; k0 += kRtK) {
+        __syncthreads();  // the previous step's operand reads are done
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sqx[i] += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
+            sqw[i] += wv[i].x * wv[i].x + wv[i].y * wv[i].y + wv[i].z * wv[i].z + wv[i].w * wv[i].w;
+            const int o = (lrow + 16 * i) * kRtLd + lk;
+            split_store(xv[i], s_xh + o, s_xl + o);
+            split_store(wv[i], s_wh + o, s_wl + o);
+        }
+        __syncthreads();
+        if (k0 + kRtK < a.H) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xv[i] = *(const f32x4*)(xp[i] + k0 + kRtK);
+                wv[i] = *(const f32x4*)(wp[i] + k0 + kRtK);
+            }
+        }
+        f32x16 acc = {};
+#pragma unroll
+        for (int s = 0; s < kRtK / 16; ++s) {
+            const bf16x8 ah = *(const bf16x8*)(s_xh + arow + 16 * s);
+            const bf16x8 al = *(const bf16x8*)(s_xl + arow + 16 * s);
+            const bf16x8 bh = *(const bf16x8*)(s_wh + brow + 16 * s);
+            const bf16x8 bl = *(const bf16x8*)(s_wl + brow + 16 * s);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc64[r] += (double)acc[r];
+    }
+    // row norms: the 16 lanes of a loader row hold its partial sums
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float sx = sqx[i], sw = sqw[i];
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+            sx += __shfl_xor(sx, o, 64);
+            sw += __shfl_xor(sw, o, 64);
+        }
+        if ((tid & 15) == 0) {
+            s_nx[lrow + 16 * i] = __builtin_sqrtf(sx);
+            s_nw[lrow + 16 * i] = __builtin_sqrtf(sw);
+        }
+    }
+    __syncthreads();
+    // D[row][col]: row = 8 (r / 4) + 4 (lane / 32) + r % 4, col = lane % 32
+    const int col = ns * 32 + (lane & 31);
+    const int e = e0 + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = ms * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int t = t0 + row;
+        if (t < a.T && e < a.E) {
+            const float L = (float)acc64[r];
+            const float d = kRouterBoundRel * s_nx[row] * s_nw[col] + 0x1p-21f * __builtin_fabsf(L) + 1e-30f;
+            a.logits[(uint64_t)t * (a.E + 1) + e] = L;
+            a.bound[(uint64_t)t * a.E + e] = d;
+        }
     }
 }
 
@@ -136,8 +290,13 @@ __global__ __launch_bounds__(256) void k_router_quant(RouterArgs a) {
 // then (single block, or a second launch) scan + stable scatter.
 // ---------------------------------------------------------------------------
 struct TopkArgs {
-    const float* logits;  // [T][E+1]
-    int T, E, K, S;
+    const float* logits;       // [T][E+1] (approximate on the refined path)
+    const float* logit_bound;  // [T][E]   refined path only
+    const float* x;            // [T][H]   refined path only
+    const float* w_router;     // [E][router_ld]
+    uint64_t router_ld;
+    const float* w_sh_norm;    // [H] or null
+    int T, E, K, S, H;
     int32_t* topk_idx;    // [T][K]
     float* topk_w;        // [T][K]
     float* sh_gate;       // [T]
@@ -148,7 +307,8 @@ struct TopkArgs {
     int32_t* row_token;   // [R]
     int32_t* pos;         // [T*K]
     int32_t* active;      // [E+1]
-    int4* slot_info;      // [E+1] {expert, first row, rows, 0}
+    int32_t* expert_slot; // [E]
+    int4* slot_info;      // [E+1] {expert, first row, rows, token of first row}
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
@@ -163,20 +323,75 @@ __device__ __forceinline__ bool better(float v, int i, float v2, int i2) {
     return v > v2 || (v == v2 && i < i2);
 }
 
-template <int EPL>
-__device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_idx_row, float* s_val_row,
-                               double* s_ex_row) {
-    const float* l = a.logits + (uint64_t)t * (a.E + 1);
-    // this lane's candidates e = i*64 + lane, sorted by (logit desc, id asc)
-    float v[EPL];
-    int id[EPL];
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    const float o = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                           0xF, false));
+    return fmaxf(v, o);
+}
+
+// Whole-wave maximum, returned to every lane.
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = dpp_max_step<kDppQuadXor1, 0xF>(v);
+    v = dpp_max_step<kDppQuadXor2, 0xF>(v);
+    v = dpp_max_step<kDppRowHalfMirror, 0xF>(v);
+    v = dpp_max_step<kDppRowMirror, 0xF>(v);
+    v = dpp_max_step<kDppRowBcast15, 0xA>(v);
+    v = dpp_max_step<kDppRowBcast31, 0xC>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v = dpp_sum_f64<64>(v);
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ double dot4_f64(const f32x4 w, const f32x4 v, double acc) {
+    acc = __builtin_fma((double)w.x, (double)v.x, acc);
+    acc = __builtin_fma((double)w.y, (double)v.y, acc);
+    acc = __builtin_fma((double)w.z, (double)v.z, acc);
+    return __builtin_fma((double)w.w, (double)v.w, acc);
+}
+
+// Exact router logits of one token against two router rows (one wave; f32
+// products are exact in f64, the sum is f64), rounded once to f32.
+__device__ __forceinline__ void exact_dot2(const float* w0, const float* w1, const float* xr, int H, int lane,
+                                           float& r0, float& r1) {
+    double a0 = 0.0, a1 = 0.0;
+    const int nch = H >> 8;
+    int c = 0;
+    for (; c + 4 <= nch; c += 4) {
+        f32x4 xv[4], v0[4], v1[4];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const int e = i * 64 + lane;
-        const float lv = l[min(e, a.E - 1)];  // unconditional load, masked below
-        v[i] = e < a.E ? lv : -__builtin_huge_valf();
-        id[i] = e < a.E ? e : 0x7fffffff;
+        for (int i = 0; i < 4; ++i) {
+            const int o = (c + i) * 256 + 4 * lane;
+            xv[i] = *(const f32x4*)(xr + o);
+            v0[i] = *(const f32x4*)(w0 + o);
+            v1[i] = *(const f32x4*)(w1 + o);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { a0 = dot4_f64(v0[i], xv[i], a0); a1 = dot4_f64(v1[i], xv[i], a1); }
     }
+    for (; c < nch; ++c) {
+        const int o = c * 256 + 4 * lane;
+        const f32x4 xv = *(const f32x4*)(xr + o);
+        a0 = dot4_f64(*(const f32x4*)(w0 + o), xv, a0);
+        a1 = dot4_f64(*(const f32x4*)(w1 + o), xv, a1);
+    }
+    r0 = (float)wave_sum_f64(a0);
+    r1 = (float)wave_sum_f64(a1);
+}
+
+// Top-k of one token from per-lane candidates (expert e = i*64 + lane in
+// v[i]/id[i], -inf/INT_MAX for none), softmax over the selected logits and the
+// shared-expert gate.  One wave.
+template <int EPL>
+__device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EPL], int (&id)[EPL], float sg_logit,
+                               int32_t* s_idx_row, float* s_val_row, double* s_ex_row) {
 #pragma unroll
     for (int i = 1; i < EPL; ++i)
 #pragma unroll
@@ -215,7 +430,7 @@ __device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_id
             ex = exp_det((double)s_val_row[lane] - m);
             s_ex_row[lane] = ex;
         }
-        if (lane == a.K && a.S) a.sh_gate[t] = sigmoid_det(l[a.E]);
+        if (lane == a.K && a.S) a.sh_gate[t] = sigmoid_det(sg_logit);
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
         double sum = 0.0;
@@ -230,120 +445,119 @@ __device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_id
     }
 }
 
+// Top-k from exact logits.
+template <int EPL>
+__device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_idx_row, float* s_val_row,
+                               double* s_ex_row) {
+    const float* l = a.logits + (uint64_t)t * (a.E + 1);
+    float v[EPL];
+    int id[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        const int e = i * 64 + lane;
+        const float lv = l[min(e, a.E - 1)];  // unconditional load, masked below
+        v[i] = e < a.E ? lv : -__builtin_huge_valf();
+        id[i] = e < a.E ? e : 0x7fffffff;
+    }
+    select_softmax<EPL>(a, t, lane, v, id, a.S ? l[a.E] : 0.0f, s_idx_row, s_val_row, s_ex_row);
+}
+
+// Top-k from approximate logits L~ with bounds d (|L~ - L| <= d): thr = the
+// K-th largest lower bound L~ - d is <= the K-th largest exact logit, so every
+// expert with L~ + d < thr is strictly below the K-th selected value and
+// cannot be selected (whatever the tie rule).  The rest are recomputed
+// exactly and ranked as on the exact path; the selection is identical.
+template <int EPL>
+__device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s_idx_row, float* s_val_row,
+                                  double* s_ex_row) {
+    const float* l = a.logits + (uint64_t)t * (a.E + 1);
+    const float* bd = a.logit_bound + (uint64_t)t * a.E;
+    float lo[EPL], up[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        const int e = i * 64 + lane;
+        const int ec = min(e, a.E - 1);
+        const float L = l[ec], d = bd[ec];
+        lo[i] = e < a.E ? L - d : -__builtin_huge_valf();
+        up[i] = e < a.E ? L + d : -__builtin_huge_valf();
+    }
+    // K-th largest lower bound (with multiplicity)
+    float s[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) s[i] = lo[i];
+#pragma unroll
+    for (int i = 1; i < EPL; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j)
+            if (s[j] > s[j - 1]) { const float tv = s[j]; s[j] = s[j - 1]; s[j - 1] = tv; }
+    float thr = -__builtin_huge_valf();
+    int removed = 0;
+    for (int j = 0; j < a.K; ++j) {
+        const float mx = wave_max_f32(s[0]);
+        const bool pop = s[0] == mx;
+        removed += __builtin_popcountll(__ballot(pop));
+        if (pop) {
+#pragma unroll
+            for (int i = 0; i + 1 < EPL; ++i) s[i] = s[i + 1];
+            s[EPL - 1] = -__builtin_huge_valf();
+        }
+        if (removed >= a.K) { thr = mx; break; }
+    }
+    // exact logits of the candidates, two rows per pass
+    const float* xr = a.x + (uint64_t)t * a.H;
+    float v[EPL];
+    int id[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        const int e = i * 64 + lane;
+        const bool cand = e < a.E && up[i] >= thr;
+        v[i] = -__builtin_huge_valf();
+        id[i] = e < a.E ? e : 0x7fffffff;
+        uint64_t m = __ballot(cand);
+        while (m) {
+            const int b0 = __builtin_ctzll(m);
+            m &= m - 1;
+            int b1 = b0;
+            if (m) { b1 = __builtin_ctzll(m); m &= m - 1; }
+            float r0, r1;
+            exact_dot2(a.w_router + (uint64_t)(i * 64 + b0) * a.router_ld,
+                       a.w_router + (uint64_t)(i * 64 + b1) * a.router_ld, xr, a.H, lane, r0, r1);
+            if (lane == b0) v[i] = r0;
+            if (lane == b1) v[i] = r1;
+        }
+    }
+    float sg = 0.0f;
+    if (a.S) {
+        float sg2;
+        exact_dot2(a.w_sh_norm, a.w_sh_norm, xr, a.H, lane, sg, sg2);
+    }
+    select_softmax<EPL>(a, t, lane, v, id, sg, s_idx_row, s_val_row, s_ex_row);
+}
+
+template <bool REFINE>
 __device__ __forceinline__ void topk_dispatch(const TopkArgs& a, int t, int lane, int32_t* s_idx_row,
                                               float* s_val_row, double* s_ex_row) {
     const int epl = (a.E + 63) >> 6;
-    if (epl <= 1) topk_one_token<1>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
-    else if (epl <= 2) topk_one_token<2>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
-    else if (epl <= 4) topk_one_token<4>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
-    else if (epl <= 8) topk_one_token<8>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
-    else topk_one_token<16>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+#define QMOE_TOPK_CASE(N)                                                   \
+    if (REFINE) topk_refine_token<N>(a, t, lane, s_idx_row, s_val_row, s_ex_row); \
+    else topk_one_token<N>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+    if (epl <= 1) { QMOE_TOPK_CASE(1) }
+    else if (epl <= 2) { QMOE_TOPK_CASE(2) }
+    else if (epl <= 4) { QMOE_TOPK_CASE(4) }
+    else if (epl <= 8) { QMOE_TOPK_CASE(8) }
+    else { QMOE_TOPK_CASE(16) }
+#undef QMOE_TOPK_CASE
 }
 
-// Scan of per-block histograms, expert offsets, active list, slot table, MFMA
-// tile list and the stable scatter.  Runs in ONE block (blockDim a multiple of
-// 64, at least 256).
-__device__ void scan_and_scatter(const TopkArgs& a, int32_t* s_scan /* >= E+1 ints */, int32_t* s_misc /* >= 64 */) {
-    const int tid = threadIdx.x;
-    const int nthr = blockDim.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int nwaves = nthr >> 6;
-    // 1. per-expert exclusive base per top-k block (in place) and totals
-    for (int e = tid; e < a.E; e += nthr) {
-        int run = 0;
-        for (int b = 0; b < a.nblk; ++b) {
-            const int c = a.hist[(uint64_t)b * a.E + e];
-            a.hist[(uint64_t)b * a.E + e] = run;
-            run += c;
-        }
-        s_scan[e] = run;
-    }
-    __syncthreads();
-    // 2. exclusive scans over experts: rows, active flags, MFMA tiles.  Chunks of
-    //    64 experts are scanned by separate waves, then chunk totals are combined.
-    const int nchunk = (a.E + 63) >> 6;  // <= 16
-    int c_rows = 0, c_act = 0, c_tiles = 0, inc = 0, inc_act = 0, inc_t = 0, e = 0;
-    if (wave < nchunk) {
-        e = wave * 64 + lane;
-        c_rows = e < a.E ? s_scan[e] : 0;
-        c_act = c_rows > 0 ? 1 : 0;
-        c_tiles = (c_rows + kMfmaTileM - 1) / kMfmaTileM;
-        inc = wave_incl_scan_i32(c_rows);
-        inc_act = wave_incl_scan_i32(c_act);
-        inc_t = wave_incl_scan_i32(c_tiles);
-        if (lane == 63) { s_misc[3 * wave] = inc; s_misc[3 * wave + 1] = inc_act; s_misc[3 * wave + 2] = inc_t; }
-    }
-    __syncthreads();
-    if (wave < nchunk) {
-        int base = 0, base_act = 0, base_t = 0;
-        for (int w = 0; w < wave; ++w) { base += s_misc[3 * w]; base_act += s_misc[3 * w + 1]; base_t += s_misc[3 * w + 2]; }
-        if (e < a.E) {
-            const int off = base + inc - c_rows;
-            a.offsets[e] = off;
-            s_scan[e] = off;  // offsets kept in LDS for the scatter
-            if (c_act) {
-                const int slot = base_act + inc_act - 1;
-                a.active[slot] = e;
-                a.slot_info[slot] = make_int4(e, off, c_rows, 0);
-            }
-            const int t0 = base_t + inc_t - c_tiles;
-            for (int i = 0; i < c_tiles && t0 + i < a.max_tiles; ++i)
-                a.tiles[t0 + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, c_rows - i * kMfmaTileM), 0);
-        }
-        if (wave == nchunk - 1 && lane == 63) {
-            const int A = a.T * a.K;
-            int n_act = base_act + inc_act;
-            int n_tiles = base_t + inc_t;
-            a.offsets[a.E] = A;
-            a.offsets[a.E + 1] = A + a.S * a.T;
-            if (a.S) {
-                a.active[n_act] = a.E;
-                a.slot_info[n_act] = make_int4(a.E, A, a.T, 0);
-                n_act++;
-                const int nt = (a.T + kMfmaTileM - 1) / kMfmaTileM;
-                for (int i = 0; i < nt && n_tiles < a.max_tiles; ++i)
-                    a.tiles[n_tiles++] = make_int4(a.E, A + i * kMfmaTileM, min(kMfmaTileM, a.T - i * kMfmaTileM), 0);
-            }
-            a.counters[0] = n_act;
-            a.counters[1] = n_tiles;
-        }
-    }
-    __syncthreads();
-    // 3. stable scatter: position = offset[e] + block base + rank inside block
-    const int A = a.T * a.K;
-    for (int asg = tid; asg < A; asg += nthr) {
-        const int t = asg / a.K;
-        const int ex = a.topk_idx[asg];
-        const int blk = t / kTopkTokensPerBlock;
-        const int p = s_scan[ex] + a.hist[(uint64_t)blk * a.E + ex] + a.local_rank[asg];
-        a.rows[p] = asg;
-        a.row_token[p] = t;
-        a.pos[asg] = p;
-    }
-    if (a.S) {
-        for (int t = tid; t < a.T; t += nthr) {
-            a.rows[A + t] = -1;
-            a.row_token[A + t] = t;
-        }
-    }
-    __syncthreads();
-    // 4. token of each slot's first row (lets the expert kernels fetch it without a lookup)
-    const int n_act = a.counters[0];
-    for (int i = tid; i < n_act; i += nthr) {
-        int4 si = a.slot_info[i];
-        si.w = a.row_token[si.y];
-        a.slot_info[i] = si;
-    }
-}
-
-// blockDim = 64 * kTopkTokensPerBlock: one wave per token.
-__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, int fused_scan) {
+// blockDim = 64 * kTopkTokensPerBlock: one wave per token.  Writes the
+// selection, the per-block expert histogram and each assignment's rank among
+// the block's assignments to the same expert (token order).
+template <bool REFINE>
+__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a) {
     __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
     __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
     __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
     __shared__ uint32_t s_mask[1024];  // per expert: bit ti set if block token ti chose it
-    __shared__ int32_t s_cnt[1024 + 1];
-    __shared__ int32_t s_misc[64];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kTopkTokensPerBlock;
@@ -351,11 +565,10 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, i
     for (int e = threadIdx.x; e < a.E; e += blockDim.x) s_mask[e] = 0;
     __syncthreads();
     if (wave < ntok) {
-        topk_dispatch(a, t0 + wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
+        topk_dispatch<REFINE>(a, t0 + wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
         if (lane < a.K) atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
     }
     __syncthreads();
-    // local rank of (token ti, slot j) = earlier block tokens that chose the same expert
     for (int asg = threadIdx.x; asg < ntok * a.K; asg += blockDim.x) {
         const int ti = asg / a.K;
         const int j = asg % a.K;
@@ -364,37 +577,20 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, i
     }
     for (int e = threadIdx.x; e < a.E; e += blockDim.x)
         a.hist[(uint64_t)blockIdx.x * a.E + e] = __builtin_popcount(s_mask[e]);
-    if (fused_scan) {
-        __syncthreads();
-        scan_and_scatter(a, s_cnt, s_misc);
-    }
 }
 
-// Whole routing for T <= kTopkTokensPerBlock in ONE block, everything in LDS:
-// top-k per token (one wave each), per-expert token masks, counts, offsets,
-// active slots (with the token of each slot's first row = lowest mask bit),
-// stable scatter (rank = earlier tokens in the expert's mask) and tiles.
-__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_route_small(TopkArgs a) {
-    __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
-    __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
-    __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
-    __shared__ uint32_t s_mask[1024];
-    __shared__ int32_t s_off[1024];
-    __shared__ int32_t s_misc[64];
+// Exclusive scans over experts of the per-expert counts in s_cnt: offsets,
+// active slots, expert->slot map, MFMA tiles, counters.  In one block of at
+// least E threads rounded to waves (E <= 1024).  first_token (optional, LDS)
+// gives the token of each expert's first row; otherwise the scatter sets it.
+__device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint32_t* first_token,
+                             int32_t* s_off, int32_t* s_misc) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int A = a.T * a.K;
-    for (int e = tid; e < a.E; e += blockDim.x) s_mask[e] = 0;
-    __syncthreads();
-    if (wave < a.T) {
-        topk_dispatch(a, wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
-        if (lane < a.K) atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
-    }
-    __syncthreads();
     const int nchunk = (a.E + 63) >> 6;
     int cnt = 0, act = 0, nt = 0, inc = 0, inc_act = 0, inc_t = 0, e = 0;
     if (wave < nchunk) {
         e = wave * 64 + lane;
-        cnt = e < a.E ? __builtin_popcount(s_mask[e]) : 0;
+        cnt = e < a.E ? s_cnt[e] : 0;
         act = cnt > 0 ? 1 : 0;
         nt = (cnt + kMfmaTileM - 1) / kMfmaTileM;
         inc = wave_incl_scan_i32(cnt);
@@ -409,18 +605,19 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_route_small(TopkAr
         if (e < a.E) {
             const int off = base + inc - cnt;
             a.offsets[e] = off;
-            s_off[e] = off;
+            if (s_off) s_off[e] = off;
             if (act) {
                 const int slot = base_act + inc_act - 1;
                 a.active[slot] = e;
-                a.slot_info[slot] = make_int4(e, off, cnt, __builtin_ctz(s_mask[e]));
+                a.expert_slot[e] = slot;
+                a.slot_info[slot] = make_int4(e, off, cnt, first_token ? (int)__builtin_ctz(first_token[e]) : 0);
             }
-            if (nt) {
-                const int t0 = base_t + inc_t - nt;
-                if (t0 < a.max_tiles) a.tiles[t0] = make_int4(e, off, cnt, 0);  // cnt <= T <= 16 < tile rows
-            }
+            const int tb = base_t + inc_t - nt;
+            for (int i = 0; i < nt && tb + i < a.max_tiles; ++i)
+                a.tiles[tb + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, cnt - i * kMfmaTileM), 0);
         }
         if (wave == nchunk - 1 && lane == 63) {
+            const int A = a.T * a.K;
             int n_act = base_act + inc_act;
             int n_tiles = base_t + inc_t;
             a.offsets[a.E] = A;
@@ -429,12 +626,40 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_route_small(TopkAr
                 a.active[n_act] = a.E;
                 a.slot_info[n_act] = make_int4(a.E, A, a.T, 0);
                 n_act++;
-                if (n_tiles < a.max_tiles) a.tiles[n_tiles++] = make_int4(a.E, A, a.T, 0);
+                const int ntt = (a.T + kMfmaTileM - 1) / kMfmaTileM;
+                for (int i = 0; i < ntt && n_tiles < a.max_tiles; ++i)
+                    a.tiles[n_tiles++] = make_int4(a.E, A + i * kMfmaTileM, min(kMfmaTileM, a.T - i * kMfmaTileM), 0);
             }
             a.counters[0] = n_act;
             a.counters[1] = n_tiles;
         }
     }
+}
+
+// Whole routing for T <= kTopkTokensPerBlock in ONE block, everything in LDS:
+// top-k per token (one wave each), per-expert token masks, counts, offsets,
+// active slots (with the token of each slot's first row = lowest mask bit),
+// stable scatter (rank = earlier tokens in the expert's mask) and tiles.
+__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_route_small(TopkArgs a) {
+    __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
+    __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
+    __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
+    __shared__ uint32_t s_mask[1024];
+    __shared__ int32_t s_cnt[1024];
+    __shared__ int32_t s_off[1024];
+    __shared__ int32_t s_misc[64];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int A = a.T * a.K;
+    for (int e = tid; e < a.E; e += blockDim.x) s_mask[e] = 0;
+    __syncthreads();
+    if (wave < a.T) {
+        topk_dispatch<false>(a, wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
+        if (lane < a.K) atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
+    }
+    __syncthreads();
+    for (int e = tid; e < a.E; e += blockDim.x) s_cnt[e] = __builtin_popcount(s_mask[e]);
+    __syncthreads();
+    scan_experts(a, s_cnt, s_mask, s_off, s_misc);
     __syncthreads();
     for (int asg = tid; asg < A; asg += blockDim.x) {
         const int t = asg / a.K, j = asg % a.K;
@@ -450,13 +675,91 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_route_small(TopkAr
     }
 }
 
-__global__ __launch_bounds__(1024) void k_scan_scatter(TopkArgs a) {
-    __shared__ int32_t s_cnt[1024 + 1];
+// Per-expert exclusive prefix of the per-block histograms (in place: hist
+// becomes each block's base inside its expert), then the expert scans.  One
+// block of 1024 threads: thread (q, e) owns a contiguous range of blocks of
+// expert e and keeps up to kScanChunk counts in registers, so each pass is
+// one round of independent loads.
+constexpr int kScanChunk = 64;
+
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_scan(TopkArgs a) {
+    __shared__ int32_t s_part[1024];
+    __shared__ int32_t s_cnt[1024];
     __shared__ int32_t s_misc[64];
-    scan_and_scatter(a, s_cnt, s_misc);
+    const int tid = threadIdx.x;
+    const int Q = min(16, 1024 / a.E);
+    const int q = tid / a.E, e = tid - q * a.E;
+    const bool mine = q < Q;
+    const int per = (a.nblk + Q - 1) / Q;
+    const int b0 = min(a.nblk, q * per), b1 = min(a.nblk, b0 + per);
+    int vals[kScanChunk];
+    int sum = 0;
+    if (mine) {
+        // 32-bit element offsets (hist holds nblk*E < 2^31 counts): cheap
+        // addresses let all of a chunk's loads issue before the first wait
+        const int32_t* col = a.hist + e;
+        for (int bb = b0; bb < b1; bb += kScanChunk) {
+            const int last = (b1 - 1) * a.E;
+#pragma unroll
+            for (int i = 0; i < kScanChunk; ++i) vals[i] = col[min((bb + i) * a.E, last)];
+#pragma unroll
+            for (int i = 0; i < kScanChunk; ++i) sum += bb + i < b1 ? vals[i] : 0;
+        }
+        s_part[tid] = sum;
+    }
+    __syncthreads();
+    if (mine) {
+        int run = 0;
+        for (int qq = 0; qq < q; ++qq) run += s_part[qq * a.E + e];
+        if (q == Q - 1) s_cnt[e] = run + sum;
+        if (b1 - b0 <= kScanChunk) {
+            int32_t* colw = a.hist + e;
+#pragma unroll
+            for (int i = 0; i < kScanChunk; ++i)
+                if (b0 + i < b1) {
+                    colw[(b0 + i) * a.E] = run;
+                    run += vals[i];
+                }
+        } else {
+            for (int b = b0; b < b1; ++b) {
+                const int c = a.hist[(uint64_t)b * a.E + e];
+                a.hist[(uint64_t)b * a.E + e] = run;
+                run += c;
+            }
+        }
+    }
+    __syncthreads();
+    scan_experts(a, s_cnt, nullptr, nullptr, s_misc);
 }
 
-hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, hipStream_t stream) {
+// Stable scatter: assignment (t, j) of expert e goes to row offsets[e] + its
+// block's base + its rank inside the block.  The first row of each expert
+// also records its token in the slot table.  Shared-expert rows follow in
+// token order.
+__global__ __launch_bounds__(256) void k_scatter(TopkArgs a) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int A = a.T * a.K;
+    if (i < A) {
+        const int t = i / a.K;
+        const int ex = a.topk_idx[i];
+        const int off = a.offsets[ex];
+        const int p = off + a.hist[(uint64_t)(t / kTopkTokensPerBlock) * a.E + ex] + a.local_rank[i];
+        a.rows[p] = i;
+        a.row_token[p] = t;
+        a.pos[i] = p;
+        if (p == off) ((int*)(a.slot_info + a.expert_slot[ex]))[3] = t;
+    } else if (a.S && i < A + a.T) {
+        a.rows[i] = -1;
+        a.row_token[i] = i - A;
+    }
+}
+
+bool route_uses_mfma(const LayerDesc& L, int T) {
+    return T > kTopkTokensPerBlock && T >= L.big_router_min_tokens;
+}
+
+static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, const float* x, int T, bool quant,
+                                      hipStream_t stream) {
     RouterArgs ra;
     ra.x = x;
     ra.w_router = L.w_router;
@@ -466,20 +769,27 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     ra.logits = ws.logits;
     ra.xq_qs = ws.xq_qs;
     ra.xq_ds = ws.xq_ds;
-    const int nq = (T + 3) / 4;
     ra.n_router_blocks = L.E + L.S;
+    const int nq = quant ? (T + 3) / 4 : 0;
     const dim3 grid(ra.n_router_blocks + nq);
     const int nch_per_wave = (L.H / 256 + 3) / 4;  // float4 chunks of 256 values per wave
     if (nch_per_wave <= 1) hipLaunchKernelGGL((k_router_quant<1>), grid, dim3(256), 0, stream, ra);
     else if (nch_per_wave <= 2) hipLaunchKernelGGL((k_router_quant<2>), grid, dim3(256), 0, stream, ra);
     else if (nch_per_wave <= 4) hipLaunchKernelGGL((k_router_quant<4>), grid, dim3(256), 0, stream, ra);
     else hipLaunchKernelGGL((k_router_quant<8>), grid, dim3(256), 0, stream, ra);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
+    return hipGetLastError();
+}
 
+hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, const RouteDebug& dbg,
+                        hipStream_t stream) {
     TopkArgs ta;
     ta.logits = ws.logits;
-    ta.T = T; ta.E = L.E; ta.K = L.K; ta.S = L.S;
+    ta.logit_bound = ws.logit_bound;
+    ta.x = x;
+    ta.w_router = L.w_router;
+    ta.router_ld = L.router_ld;
+    ta.w_sh_norm = L.w_sh_norm;
+    ta.T = T; ta.E = L.E; ta.K = L.K; ta.S = L.S; ta.H = L.H;
     ta.topk_idx = ws.topk_idx;
     ta.topk_w = ws.topk_w;
     ta.sh_gate = ws.sh_gate;
@@ -490,19 +800,49 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     ta.row_token = ws.row_token;
     ta.pos = ws.pos;
     ta.active = ws.active;
+    ta.expert_slot = ws.expert_slot;
     ta.slot_info = ws.slot_info;
     ta.counters = ws.counters;
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
     ta.nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
-    if (ta.nblk == 1) {
-        hipLaunchKernelGGL(k_route_small, dim3(1), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
-        return hipGetLastError();
+    hipError_t err;
+    if (route_uses_mfma(L, T)) {
+        RouterMfmaArgs ma;
+        ma.x = x;
+        ma.w = L.w_router;
+        ma.ld = L.router_ld;
+        ma.T = T; ma.H = L.H; ma.E = L.E;
+        ma.n_etiles = (L.E + kRtTile - 1) / kRtTile;
+        ma.n_tiles = ((T + kRtTile - 1) / kRtTile) * ma.n_etiles;
+        ma.logits = ws.logits;
+        ma.bound = ws.logit_bound;
+        ma.xq_qs = ws.xq_qs;
+        ma.xq_ds = ws.xq_ds;
+        hipLaunchKernelGGL(k_router_mfma, dim3(ma.n_tiles + (T + 3) / 4), dim3(256), 0, stream, ma);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+        hipLaunchKernelGGL(k_topk<true>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+        if (dbg.approx &&
+            (err = hipMemcpy2DAsync(dbg.approx, L.E * sizeof(float), ws.logits, (L.E + 1) * sizeof(float),
+                                    L.E * sizeof(float), T, hipMemcpyDeviceToDevice, stream)) != hipSuccess)
+            return err;
+        if (dbg.bound && (err = hipMemcpyAsync(dbg.bound, ws.logit_bound, (size_t)T * L.E * sizeof(float),
+                                               hipMemcpyDeviceToDevice, stream)) != hipSuccess)
+            return err;
+        if (dbg.exact_logits && (err = launch_router_exact(L, ws, x, T, false, stream)) != hipSuccess) return err;
+    } else {
+        if ((err = launch_router_exact(L, ws, x, T, true, stream)) != hipSuccess) return err;
+        if (ta.nblk == 1) {
+            hipLaunchKernelGGL(k_route_small, dim3(1), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
+            return hipGetLastError();
+        }
+        hipLaunchKernelGGL(k_topk<false>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
     }
-    hipLaunchKernelGGL(k_topk, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta, 0);
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_scan_scatter, dim3(1), dim3(1024), 0, stream, ta);
+    hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, stream, ta);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL(k_scatter, dim3((T * L.K + L.S * T + 255) / 256), dim3(256), 0, stream, ta);
     return hipGetLastError();
 }
 

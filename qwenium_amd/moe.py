@@ -111,7 +111,8 @@ class MoELayer:
                 residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                 workspace: Optional[Workspace] = None, debug: bool = False, stream=None):
         """y[T][n_embd] = MoE(x) (+ residual).  With debug=True also returns the
-        routing intermediates (logits, topk_idx, topk_w, sh_gate, offsets, rows)."""
+        routing intermediates (logits, topk_idx, topk_w, sh_gate, offsets, rows, and
+        router_approx/router_bound, left NaN unless the batched MFMA router ran)."""
         del phase, il  # MoE has one topology (moe.h:55-57); il only names tensors in ggml
         if x.dim() != 2 or x.shape[1] != self.n_embd or x.dtype != torch.float32 or not x.is_cuda:
             raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got "
@@ -131,9 +132,12 @@ class MoELayer:
                 "sh_gate": torch.empty((T,), dtype=torch.float32, device=dev),
                 "offsets": torch.empty((E + 1,), dtype=torch.int32, device=dev),
                 "rows": torch.empty((T * k,), dtype=torch.int32, device=dev),
+                "router_approx": torch.full((T, E), float("nan"), dtype=torch.float32, device=dev),
+                "router_bound": torch.full((T, E), float("nan"), dtype=torch.float32, device=dev),
             }
             dbg = QmoeDebug(*(dbg_tensors[n].data_ptr() for n in
-                              ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows")))
+                              ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows",
+                               "router_approx", "router_bound")))
         check(lib().qmoe_layer_forward(
             self._handle, workspace._handle if workspace is not None else None,
             x.data_ptr(), int(T), y.data_ptr(),

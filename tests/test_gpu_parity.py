@@ -262,6 +262,62 @@ def test_mfma_35b_q4_0_t256(gpu):
     assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
 
 
+def check_router_bound(got, exact_logits):
+    """The batched router's approximate logits lie within their stated bound of
+    the exact logits; returns the largest |error| / bound."""
+    approx, bound = got["router_approx"], got["router_bound"]
+    assert np.isfinite(approx).all() and np.isfinite(bound).all(), "batched router did not run"
+    err = np.abs(approx.astype(np.float64) - exact_logits.astype(np.float64))
+    ratio = err / bound.astype(np.float64)
+    assert ratio.max() <= 1.0, f"approximate logit outside its bound (max |err|/bound {ratio.max():.3f})"
+    return float(ratio.max())
+
+
+@pytest.mark.parametrize("T", [17, 33, 100, 300])
+def test_batched_router_forced_small_layer(gpu, monkeypatch, T):
+    """bf16-MFMA router + exact refinement forced at small T: tile edges in tokens and
+    experts (E=16 < one 64-expert tile)."""
+    monkeypatch.setenv("QMOE_BIG_ROUTER_MIN_TOKENS", "1")
+    spec = LayerSpec(256, 16, 4, 128, True, TYPE_Q4_0)
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=300 + T)
+    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+    check_router_bound(got, d_ref["logits"])
+
+
+def test_batched_router_35b_t300(gpu):
+    """The default threshold (256 tokens) selects the batched router."""
+    spec = synthetic.QWEN35B
+    y, got, y_ref, d_ref, *_ = run_pair(spec, 300, seed=31)
+    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+    assert check_router_bound(got, d_ref["logits"]) < 0.5
+
+
+@pytest.mark.parametrize("dup", ["pairs", "all"])
+def test_batched_router_ties(gpu, monkeypatch, dup):
+    """Exactly tied logits through the refinement: duplicated router rows ("pairs"), or
+    every row equal ("all": every expert is a candidate and the lowest ids win)."""
+    monkeypatch.setenv("QMOE_BIG_ROUTER_MIN_TOKENS", "1")
+    spec = LayerSpec(256, 128, 8, 128, False, TYPE_Q8_0)
+    tensors = synthetic.make_layer_tensors(spec, 41)
+    r = tensors["router"].data.view(spec.n_experts, spec.n_embd)
+    if dup == "pairs":
+        for a, b in ((3, 90), (4, 12), (0, 127), (64, 65), (63, 64)):
+            r[b].copy_(r[a])
+    else:
+        r.copy_(r[0:1].expand_as(r))
+    layer = synthetic.make_layer(spec, 41, tensors=tensors)
+    x = synthetic.make_x(spec, 40, 41)
+    y, dbg = layer.forward(x, debug=True)
+    torch.cuda.synchronize()
+    ref = host_layer(spec, tensors)
+    y_ref, d_ref = ref.forward(x.cpu().numpy(), debug=True)
+    got = {k: v.cpu().numpy() for k, v in dbg.items()}
+    assert_parity(y.cpu().numpy(), got, y_ref, d_ref, spec, min_identical=1.0)
+    check_router_bound(got, d_ref["logits"])
+    if dup == "all":
+        assert (got["topk_idx"] == np.arange(spec.top_k)[None, :]).all()
+
+
 def test_prefill_35b_q4_0_t4096(gpu):
     """The 4096-token prefill workload: routing checked for every token, outputs on
     a sample of tokens (a token's output depends on that token only)."""
@@ -280,6 +336,7 @@ def test_prefill_35b_q4_0_t4096(gpu):
     np.testing.assert_array_equal(dbg["topk_idx"].cpu().numpy(), idx)
     np.testing.assert_array_equal(dbg["offsets"].cpu().numpy(), off)
     np.testing.assert_array_equal(dbg["rows"].cpu().numpy(), rows)
+    check_router_bound({k: dbg[k].cpu().numpy() for k in ("router_approx", "router_bound")}, logits)
     counts = np.diff(off)
     assert counts.sum() == T * spec.top_k and counts.max() < 4 * T * spec.top_k / spec.n_experts
     sample = np.random.default_rng(0).choice(T, 48, replace=False)
