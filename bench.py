@@ -68,6 +68,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, os.cpu_count())")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after the run, copy this many MiB device-to-device 4 times (calibration dispatches "
+                         "for HBM traffic counters)")
     return ap.parse_args()
 
 
@@ -227,13 +230,21 @@ def main() -> int:
     D_prof = float(np.mean([distinct[sched[i % period]] for i in range(n_prof)]))
     gu_us = float(phase_us[1])
 
+    # HBM traffic per launch of the dominant kernel, measured by rocprofv3 FETCH_SIZE /
+    # WRITE_SIZE passes and scaled by a known-size copy (summary committed under profiles/)
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", f"traffic_{args.workload}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
     if args.workload == "decode":
         gu_bytes = (D_prof + 1) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * F * 8
         achieved = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {
             "bound": "hbm", "kernel": "k_gateup_stream (gate+up expert GEMV, prefetching persistent waves)",
             "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None, "bytes_per_launch": gu_bytes, "avg_launch_us": gu_us,
+            "traffic": traffic, "bytes_per_launch": gu_bytes, "avg_launch_us": gu_us,
         }
         layer_rate = {
             "distinct_experts_mean": D_mean, "algorithmic_bytes_per_step": layer_bytes,
@@ -246,7 +257,7 @@ def main() -> int:
         roofline = {
             "bound": "mfma", "kernel": "k_expert_mfma<gate/up> (int8 MFMA grouped GEMM, f64-exact block epilogue)",
             "achieved": achieved, "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s", "frac": achieved / MFMA_I8_PEAK_TOPS,
-            "traffic": None, "ops_per_launch": ops_gu, "avg_launch_us": gu_us,
+            "traffic": traffic, "ops_per_launch": ops_gu, "avg_launch_us": gu_us,
         }
         layer_rate = {
             "distinct_experts_mean": D_mean, "int8_ops_per_step": layer_ops,
@@ -293,6 +304,17 @@ def main() -> int:
                       f"ggml-semantics CPU restatement (oracle/liboracle.so, OpenMP) on {cpu_model()}",
         }
         log(f"cpu baseline {cpu['value']:.4g} tok/s on {threads} threads")
+
+    if args.copy_mib > 0:
+        n = args.copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copies: 4 x {args.copy_mib} MiB device-to-device")
+        del src, dst
 
     out = {
         "metric": metric,

@@ -137,23 +137,58 @@ __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
 // ---------------------------------------------------------------------------
 // Q: SwiGLU h = silu(g)*u of each (row, ffn index), then Q8_0 quantization of
 // the h rows (the activation quantization ggml applies to src1 of the down
-// mul_mat_id).  One 32-lane group per block of 32 values.
+// mul_mat_id).  Each lane takes 4 consecutive values; the 8 lanes of a 32-value
+// block reduce with DPP (quad xor 1, quad xor 2, half-row mirror) and store
+// their quants as one dword each.
 // ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp8_max(float v) {
+    const float o = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    return fmaxf(v, o);
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp8_add(int v) {
+    return v + __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+
 __global__ __launch_bounds__(256) void k_quant_h(ExpertArgs a) {
     const int nrows = a.offsets[a.E + 1];
-    const int nblk = a.F >> 5;
-    const int g = blockIdx.x * 8 + (threadIdx.x >> 5);
-    if (g >= nrows * nblk) return;
-    const int p = g / nblk, b = g % nblk, l32 = threadIdx.x & 31;
-    const float2 gu = a.gubuf[(uint64_t)p * a.F + 32 * b + l32];
-    const float v = silu_mul_det(gu.x, gu.y);  // h = silu(g) * u
-    const float amax = group_max_f32<32>(__builtin_fabsf(v));
+    const int nq = a.F >> 2;  // quads per row (a multiple of 16: blocks never straddle rows or waves)
+    const int gq = blockIdx.x * 256 + threadIdx.x;
+    if ((gq & ~63) >= nrows * nq) return;  // whole waves past the end
+    const bool live = gq < nrows * nq;     // uniform over each 8-lane block
+    const int gqc = live ? gq : 0;
+    const int p = gqc / nq, q = gqc - p * nq;
+    const f32x4* src = (const f32x4*)(a.gubuf + (uint64_t)p * a.F + 4 * q);
+    const f32x4 v0 = src[0], v1 = src[1];  // (g0, u0, g1, u1), (g2, u2, g3, u3)
+    float h[4];
+    h[0] = silu_mul_det(v0.x, v0.y);
+    h[1] = silu_mul_det(v0.z, v0.w);
+    h[2] = silu_mul_det(v1.x, v1.y);
+    h[3] = silu_mul_det(v1.z, v1.w);
+    float amax = fmaxf(fmaxf(__builtin_fabsf(h[0]), __builtin_fabsf(h[1])),
+                       fmaxf(__builtin_fabsf(h[2]), __builtin_fabsf(h[3])));
+    amax = dpp8_max<kDppQuadXor1>(amax);
+    amax = dpp8_max<kDppQuadXor2>(amax);
+    amax = dpp8_max<kDppRowHalfMirror>(amax);
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    const int q = (int)__builtin_rintf(v * id);
-    const int sum = group_sum_i32<32>(q);
-    a.hq_qs[(uint64_t)p * a.F + 32 * b + l32] = (int8_t)q;
-    if (l32 == 0) a.hq_ds[(uint64_t)p * nblk + b] = make_float2(fp16_to_f32(f32_to_fp16(d)), __builtin_bit_cast(float, sum));
+    uint32_t word = 0;
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int qv = (int)__builtin_rintf(h[i] * id);
+        sum += qv;
+        word |= ((uint32_t)qv & 0xffu) << (8 * i);
+    }
+    sum = dpp8_add<kDppQuadXor1>(sum);
+    sum = dpp8_add<kDppQuadXor2>(sum);
+    sum = dpp8_add<kDppRowHalfMirror>(sum);
+    if (!live) return;
+    *(uint32_t*)(a.hq_qs + (uint64_t)p * a.F + 4 * q) = word;
+    if ((q & 7) == 0)
+        a.hq_ds[(uint64_t)p * (a.F >> 5) + (q >> 3)] = make_float2(fp16_to_f32(f32_to_fp16(d)), __builtin_bit_cast(float, sum));
 }
 
 // ---------------------------------------------------------------------------
@@ -303,7 +338,7 @@ hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T,
 hipError_t launch_quant_h(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
     const ExpertArgs a = make_expert_args(L, ws, T);
     const int max_rows = T * L.K + L.S * T;
-    const int qblocks = (max_rows * (L.F / 32) + 7) / 8;
+    const int qblocks = (max_rows * (L.F / 4) + 255) / 256;
     hipLaunchKernelGGL(k_quant_h, dim3(qblocks), dim3(256), 0, stream, a);
     return hipGetLastError();
 }

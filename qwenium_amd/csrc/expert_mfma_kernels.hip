@@ -56,19 +56,21 @@ struct MfmaArgs {
 };
 
 // 16 int8 weights of block `blk` (0 = first of the pair, 1 = second), k-half kh,
-// as signed int8 in 4 dwords.
+// as 4 dwords of int8 operands.  Q4_0 lanes get 16 * (nibble - 8): with
+// x = q ^ 0x88888888 (flips bit 3 of every nibble), (x << 4*(1-kh)) & 0xF0F0F0F0
+// puts the wanted nibble, as a two's complement value, in each byte's high
+// half, so the MFMA sums 16 * isum (the 1/16 is folded into the staged
+// activation scales, exactly).  Q8_0 lanes get the quants as stored.
 template <int WT>
-__device__ __forceinline__ v4i weight_frag(const WPair<WT>& w, int blk, int kh);
+__device__ __forceinline__ v4i weight_frag(const WPair<WT>& w, int blk, int sh);
 
 template <>
-__device__ __forceinline__ v4i weight_frag<kTypeQ4_0>(const WPair<kTypeQ4_0>& w, int blk, int kh) {
+__device__ __forceinline__ v4i weight_frag<kTypeQ4_0>(const WPair<kTypeQ4_0>& w, int blk, int sh) {
     v4i r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t q = blk == 0 ? __builtin_amdgcn_alignbyte(w.w[i + 1], w.w[i], 2) : w.w[5 + i];
-        const uint32_t nib = kh == 0 ? (q & 0x0f0f0f0fu) : ((q >> 4) & 0x0f0f0f0fu);
-        // nibble v in [0,15] -> v - 8 as int8, per byte, no inter-byte carry
-        r[i] = (int)((nib + 0x78787878u) ^ 0x80808080u);
+        r[i] = (int)(((q ^ 0x88888888u) << sh) & 0xF0F0F0F0u);
     }
     return r;
 }
@@ -106,15 +108,17 @@ __global__ __launch_bounds__(256, 2) void k_expert_mfma(MfmaArgs a) {
     const int col = lane & 31, kh = lane >> 5;
     const bool sh = e >= a.E;
 
-    // weight rows of this lane's two output columns
-    const uint8_t* wrow[2];
+    // weight rows of this lane's two output columns: wave-uniform slab base +
+    // 32-bit row offset (an expert's slab is far below 4 GiB)
+    const uint8_t* wbase[2];
+    uint32_t woff[2];
     int out_idx[2];
     if (GATEUP) {
         const int f = y * 64 + ws * 32 + col;
-        const uint8_t* g0 = sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2;
-        const uint8_t* u0 = sh ? a.sh1 : a.w1 + (uint64_t)e * a.w1_nb2;
-        wrow[0] = g0 + (uint64_t)f * (sh ? a.sh0_nb1 : a.w0_nb1);
-        wrow[1] = u0 + (uint64_t)f * (sh ? a.sh1_nb1 : a.w1_nb1);
+        wbase[0] = sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2;
+        wbase[1] = sh ? a.sh1 : a.w1 + (uint64_t)e * a.w1_nb2;
+        woff[0] = (uint32_t)(f * (sh ? a.sh0_nb1 : a.w0_nb1));
+        woff[1] = (uint32_t)(f * (sh ? a.sh1_nb1 : a.w1_nb1));
         out_idx[0] = out_idx[1] = f;
     } else {
         const uint8_t* base = sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2;
@@ -122,37 +126,48 @@ __global__ __launch_bounds__(256, 2) void k_expert_mfma(MfmaArgs a) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             out_idx[c] = y * 128 + ws * 64 + c * 32 + col;
-            wrow[c] = base + (uint64_t)out_idx[c] * nb1;
+            wbase[c] = base;
+            woff[c] = (uint32_t)(out_idx[c] * nb1);
         }
     }
+    constexpr uint32_t kPairBytes = 2 * BlockTraits<WT>::kBytes;
 
     // staging assignment: 16-byte chunk (m = tid/16 + 16q, c16 = tid%16), q < 4;
-    // scales (m = tid%64, block tid/64 + 4q), q < 2
-    const int8_t* xsrc[4];
+    // scales (m = tid%64, block tid/64 + 4q), q < 2.  The row lookups are
+    // issued together, before any of them is used.
+    const int nblk_k = a.K >> 5;
+    int srow[5];
+#pragma unroll
+    for (int q = 0; q < 5; ++q) {
+        const int m = q < 4 ? (tid >> 4) + 16 * q : (tid & 63);
+        const int pr = p0 + min(m, nr - 1);
+        srow[q] = GATEUP ? a.row_token[pr] : pr;
+    }
+    // activation sources as 32-bit offsets from the uniform a_qs / a_ds bases
+    // (R*K and R*K/32 stay far below 2^32); rows past the tile read as zero
+    uint32_t xoff[4];
+    bool xlive[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int m = (tid >> 4) + 16 * q;
-        const int pr = p0 + min(m, nr - 1);
-        xsrc[q] = m < nr ? a.a_qs + (uint64_t)(GATEUP ? a.row_token[pr] : pr) * a.K + 16 * (tid & 15) : nullptr;
+        xlive[q] = (tid >> 4) + 16 * q < nr;
+        xoff[q] = (uint32_t)srow[q] * (uint32_t)a.K + 16u * (tid & 15);
     }
-    const int nblk_k = a.K >> 5;
-    const float2* dsrc;
-    {
-        const int m = tid & 63;
-        const int pr = p0 + min(m, nr - 1);
-        dsrc = m < nr ? a.a_ds + (uint64_t)(GATEUP ? a.row_token[pr] : pr) * nblk_k : nullptr;
-    }
+    const bool dlive = (tid & 63) < nr;
+    const uint32_t doff = (uint32_t)srow[4] * (uint32_t)nblk_k;
+    // Q4_0 fragments carry 16x the weight quants (see weight_frag)
+    constexpr double kDxScale = WT == kTypeQ4_0 ? 0.0625 : 1.0;
     u32x4 px[4];
-    double pd[2];
+    float pd[2];  // raw f32 scales: converted when stored, so the loads are not waited on early
     auto stage_load = [&](int kc) {
         const int kcn = min(kKC, a.K - kc);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            px[q] = (xsrc[q] && 16 * (tid & 15) < kcn) ? *(const u32x4*)(xsrc[q] + kc) : u32x4{0u, 0u, 0u, 0u};
+            px[q] = (xlive[q] && 16 * (tid & 15) < kcn) ? *(const u32x4*)(a.a_qs + (xoff[q] + (uint32_t)kc))
+                                                        : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int bb = (tid >> 6) + 4 * q;
-            pd[q] = (dsrc && 32 * bb < kcn) ? (double)dsrc[(kc >> 5) + bb].x : 0.0;
+            pd[q] = (dlive && 32 * bb < kcn) ? a.a_ds[doff + (uint32_t)((kc >> 5) + bb)].x : 0.0f;
         }
     };
     stage_load(0);
@@ -163,54 +178,67 @@ __global__ __launch_bounds__(256, 2) void k_expert_mfma(MfmaArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[c][r] = 0.0;
 
+    const int frag_sel = WT == kTypeQ4_0 ? 4 * (1 - kh) : kh;
     const bool active = 32 * ms < nr;  // wave-uniform: rows 32*ms.. of the tile exist
     const int npairs = a.K >> 6;
-    WPair<WT> wc[2], wn[2];
-    if (active) {
-        wc[0].load(wrow[0], 0);
-        wc[1].load(wrow[1], 0);
-    }
-    int pidx = 0;
-    for (int kc = 0; kc < a.K; kc += kKC) {
-        const int kcn = min(kKC, a.K - kc);  // multiple of 64
+    constexpr int kPairsPerChunk = kKC / 64;
+    const int8_t* xrow = s_x + (32 * ms + col) * kRowStride + 16 * kh;
+
+    // one pair (two quant blocks) of the wave's two column tiles
+    auto pair_step = [&](const WPair<WT> (&w)[2], int pidx) {
+        const int bp = 2 * (pidx % kPairsPerChunk);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int b = bp + sub;
+            const v4i af = *(const v4i*)(xrow + 32 * b);
+            const v16i z = {};
+            const v16i is0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, weight_frag<WT>(w[0], sub, frag_sel), z, 0, 0, 0);
+            const v16i is1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, weight_frag<WT>(w[1], sub, frag_sel), z, 0, 0, 0);
+            const double* drow = s_d + b * kTileM + 32 * ms + 4 * kh;
+            double dx[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) dx[4 * i + j] = drow[8 * i + j];
+            const double dw0 = (double)(sub == 0 ? w[0].dA() : w[0].dB());
+            const double dw1 = (double)(sub == 0 ? w[1].dA() : w[1].dB());
+            // fp32(d_w)*fp32(d_x) (times 1/16 for Q4_0) is exact in f64; the block term and the sum are exact
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[0][r] = __builtin_fma(dw0 * dx[r], (double)is0[r], acc[0][r]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[1][r] = __builtin_fma(dw1 * dx[r], (double)is1[r], acc[1][r]);
+        }
+    };
+    // chunk boundary: publish the prefetched activation chunk, prefetch the next
+    auto stage_chunk = [&](int kc) {
         __syncthreads();  // the previous chunk's LDS reads are done
 #pragma unroll
         for (int q = 0; q < 4; ++q) *(u32x4*)(s_x + ((tid >> 4) + 16 * q) * kRowStride + 16 * (tid & 15)) = px[q];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) s_d[((tid >> 6) + 4 * q) * kTileM + (tid & 63)] = pd[q];
+        for (int q = 0; q < 2; ++q) s_d[((tid >> 6) + 4 * q) * kTileM + (tid & 63)] = (double)pd[q] * kDxScale;
         __syncthreads();
         if (kc + kKC < a.K) stage_load(kc + kKC);
-        if (!active) continue;
-        const int8_t* xrow = s_x + (32 * ms + col) * kRowStride + 16 * kh;
-        for (int bp = 0; bp < kcn / 32; bp += 2, ++pidx) {
+    };
+
+    // Weight pairs one ahead: wn loads while wc computes.  The next chunk is
+    // published at the end of the iteration that finishes the current one.
+    WPair<WT> wc[2], wn[2];
+    if (active) {
+        wc[0].load32(wbase[0], woff[0]);
+        wc[1].load32(wbase[1], woff[1]);
+    }
+    stage_chunk(0);
+    for (int pidx = 0; pidx < npairs; ++pidx) {
+        if (active) {
             if (pidx + 1 < npairs) {
-                wn[0].load(wrow[0], pidx + 1);
-                wn[1].load(wrow[1], pidx + 1);
+                wn[0].load32(wbase[0], woff[0] + (pidx + 1) * kPairBytes);
+                wn[1].load32(wbase[1], woff[1] + (pidx + 1) * kPairBytes);
             }
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
-                const int b = bp + sub;
-                const v4i af = *(const v4i*)(xrow + 32 * b);
-                const v16i z = {};
-                const v16i is0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, weight_frag<WT>(wc[0], sub, kh), z, 0, 0, 0);
-                const v16i is1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, weight_frag<WT>(wc[1], sub, kh), z, 0, 0, 0);
-                const double* drow = s_d + b * kTileM + 32 * ms + 4 * kh;
-                double dx[16];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) dx[4 * i + j] = drow[8 * i + j];
-                const double dw0 = (double)(sub == 0 ? wc[0].dA() : wc[0].dB());
-                const double dw1 = (double)(sub == 0 ? wc[1].dA() : wc[1].dB());
-                // fp32(d_w)*fp32(d_x) is exact in f64; the block term and the sum are exact
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[0][r] = __builtin_fma(dw0 * dx[r], (double)is0[r], acc[0][r]);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[1][r] = __builtin_fma(dw1 * dx[r], (double)is1[r], acc[1][r]);
-            }
-            wc[0] = wn[0];
-            wc[1] = wn[1];
+            pair_step(wc, pidx);
         }
+        if ((pidx + 1) % kPairsPerChunk == 0 && pidx + 1 < npairs) stage_chunk((pidx + 1) * 64);
+        wc[0] = wn[0];
+        wc[1] = wn[1];
     }
     if (!active) return;
     // output: lane holds column `col` of each MFMA tile, rows 8i + 4kh + j of the wave's 32

@@ -272,6 +272,14 @@ template <> struct WPair<kTypeQ4_0> {
         w[4] = a1.x; w[5] = a1.y; w[6] = a1.z; w[7] = a1.w;
         w[8] = b[8];
     }
+    // pair at byte offset `off` (32-bit) from a wave-uniform base: saddr loads
+    __device__ __forceinline__ void load32(const uint8_t* base, uint32_t off) {
+        const u32x4a4 a0 = *(const u32x4a4*)(base + off);
+        const u32x4a4 a1 = *(const u32x4a4*)(base + (off + 16u));
+        w[0] = a0.x; w[1] = a0.y; w[2] = a0.z; w[3] = a0.w;
+        w[4] = a1.x; w[5] = a1.y; w[6] = a1.z; w[7] = a1.w;
+        w[8] = *(const uint32_t*)(base + (off + 32u));
+    }
     // scales (as f32) of block A and block B
     __device__ __forceinline__ float dA() const { return fp16_to_f32(w[0]); }
     __device__ __forceinline__ float dB() const { return fp16_to_f32(w[4] >> 16); }
@@ -309,6 +317,14 @@ template <> struct WPair<kTypeQ8_0> {
             w[4 * i + 0] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
         }
         w[16] = b[16];
+    }
+    __device__ __forceinline__ void load32(const uint8_t* base, uint32_t off) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4a4 a = *(const u32x4a4*)(base + (off + 16u * i));
+            w[4 * i + 0] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
+        }
+        w[16] = *(const uint32_t*)(base + (off + 64u));
     }
     __device__ __forceinline__ float dA() const { return fp16_to_f32(w[0]); }
     __device__ __forceinline__ float dB() const { return fp16_to_f32(w[8] >> 16); }
