@@ -6,14 +6,20 @@ Workloads (Qwen3.6-35B-A3B MoE layer shape: hidden 2048, 256 experts, top-8 +
 block layout, f32 router N(0,0.02), f32 activations N(0,1)):
 
   decode  (default)  10 tokens, Q4_0 experts.  HBM-bound.  Steps rotate over
-                     --layers distinct layers (8 x 0.87 GB by default, far above
+                     --layers distinct layers (8 x 0.45 GB by default, far above
                      the 256 MB Infinity Cache) and --batches input batches.
-  prefill            4096 tokens, Q4_0 experts.  int8-MFMA-bound.
+  prefill            4096 tokens, Q4_0 experts.  int8-MFMA path.
+  skewed             2048 tokens, Q8_0 experts, Zipf(1.2)-skewed routing: ~50% of
+                     assignments on 8 hot experts, ~46 experts empty.
+  stack              40 consecutive layers, each x <- x + MoE(RMSNorm(x) * w):
+                     --tokens 1 / 10 (default) / 64 (decode) or 8192 (prefill).
 
-A step is one layer forward over one batch.  Output: ONE JSON line with value
-= tokens/s of the layer, the roofline of the dominant kernel (per-launch
-duration from HIP events the library records on its own stream) and the CPU
-oracle timed on the host cores over a bounded sample.
+A step is one layer forward over one batch (stack: one pass over all 40
+layers).  Output: ONE JSON line with value = tokens/s, the roofline of the
+dominant kernel (per-launch duration from HIP events the library records on its
+own stream; HBM traffic per launch from the committed rocprofv3 counter
+summary, when one exists for the workload) and the CPU oracle timed on the
+host cores over a bounded sample.
 """
 from __future__ import annotations
 
@@ -32,10 +38,13 @@ HBM_PEAK_GBS = 8000.0
 MFMA_I8_PEAK_TOPS = 5000.0
 
 WORKLOADS = {
-    # name: (tokens, weight type name, default layers, default batches, default steps, warmup)
-    "decode": (10, "Q4_0", 8, 16, 2000, 64),
-    "prefill": (4096, "Q4_0", 4, 2, 64, 8),
+    # name: (tokens, layer spec name, default layers, default batches, default steps, warmup)
+    "decode": (10, "QWEN35B", 8, 16, 2000, 64),
+    "prefill": (4096, "QWEN35B", 4, 2, 64, 8),
+    "skewed": (2048, "QWEN35B_SKEW", 4, 2, 64, 8),
+    "stack": (10, "QWEN35B", 40, 2, 32, 4),
 }
+STACK_LAYERS = 40
 
 
 def log(msg: str) -> None:
@@ -122,41 +131,85 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from qwenium_amd import Workspace, lib, synthetic
+    from qwenium_amd import TYPE_Q4_0, Workspace, lib, rms_norm, synthetic
     from qwenium_amd._lib import check, row_bytes
 
-    T0, wname, L0, B0, S0, W0 = WORKLOADS[args.workload]
+    T0, spec_name, L0, B0, S0, W0 = WORKLOADS[args.workload]
+    spec = getattr(synthetic, spec_name)
+    stack = args.workload == "stack"
     T = args.tokens or T0
-    L = args.layers or L0
+    L = STACK_LAYERS if stack else (args.layers or L0)
     B = args.batches or B0
     steps_req = args.steps or S0
     warmup = args.warmup if args.warmup is not None else W0
-    spec = synthetic.QWEN35B
     H, E, K, F = spec.n_embd, spec.n_experts, spec.top_k, spec.ffn_dim
+    wname = "Q4_0" if spec.wtype == TYPE_Q4_0 else "Q8_0"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
     log(f"workload {args.workload}: T={T}, generating {L} layers ({wname}) and {B} input batches on the GPU")
-    layers, tensors = [], []
+    layers, tensors, norms = [], [], []
     for l in range(L):
         t = synthetic.make_layer_tensors(spec, args.seed, layer=l, device=dev)
         tensors.append(t)
         layers.append(synthetic.make_layer(spec, args.seed, layer=l, tensors=t))
+        if stack:
+            norms.append(synthetic.make_norm_weight(spec, args.seed, l, device=dev))
     xs = [synthetic.make_x(spec, T, args.seed, batch=b, device=dev) for b in range(B)]
     ws = Workspace(layers[0], T)
     y = torch.empty((T, H), dtype=torch.float32, device=dev)
+    hbuf = torch.empty((T, H), dtype=torch.float32, device=dev)
+    xbuf = [torch.empty((T, H), dtype=torch.float32, device=dev) for _ in range(2)]
     torch.cuda.synchronize()
 
-    period = int(np.lcm(L, B))
-    sched = [(s % L, s % B) for s in range(period)]
+    def stack_pass(b, keep=None):
+        """x <- x + MoE_l(RMSNorm(x) * w_l) for l = 0..L-1 (qwen36.cpp:297-304); keep[l] gets layer l's input."""
+        cur = xs[b]
+        for l in range(L):
+            if keep is not None and l in keep:
+                keep[l] = cur.clone()
+            rms_norm(cur, norms[l], synthetic.NORM_EPS, out=hbuf)
+            nxt = xbuf[l & 1]
+            layers[l].forward(hbuf, out=nxt, workspace=ws, residual=cur)
+            cur = nxt
+        return cur
 
-    # routing statistics per (layer, batch): distinct routed experts hit
-    distinct = {}
-    for (l, b) in sched:
-        _, dbg = layers[l].forward(xs[b], out=y, workspace=ws, debug=True)
-        distinct[(l, b)] = int(torch.unique(dbg["topk_idx"]).numel())
+    if stack:
+        period = B
+        sched = [(None, s % B) for s in range(period)]
+    else:
+        period = int(np.lcm(L, B))
+        sched = [(s % L, s % B) for s in range(period)]
+
+    def run_step(i):
+        l, b = sched[i % period]
+        if stack:
+            stack_pass(b)
+        else:
+            layers[l].forward(xs[b], out=y, workspace=ws)
+
+    # routing statistics: distinct routed experts hit per (layer, batch) forward
+    distinct = []
+    if stack:
+        cur = xs[0]
+        for l in range(L):
+            rms_norm(cur, norms[l], synthetic.NORM_EPS, out=hbuf)
+            _, dbg = layers[l].forward(hbuf, out=xbuf[l & 1], workspace=ws, residual=cur, debug=True)
+            distinct.append(int(torch.unique(dbg["topk_idx"]).numel()))
+            cur = xbuf[l & 1]
+    else:
+        for (l, b) in sched:
+            _, dbg = layers[l].forward(xs[b], out=y, workspace=ws, debug=True)
+            distinct.append(int(torch.unique(dbg["topk_idx"]).numel()))
     torch.cuda.synchronize()
-    D_mean = float(np.mean([distinct[p] for p in sched]))
+    D_mean = float(np.mean(distinct))
+    skew_stats = None
+    if spec.skew is not None:
+        counts = torch.bincount(dbg["topk_idx"].reshape(-1).long(), minlength=E).cpu().numpy()
+        hot = spec.skew.hot_experts(E)
+        skew_stats = {"hot8_share": float(counts[hot].sum() / counts.sum()), "empty_experts": int((counts == 0).sum()),
+                      "max_rows": int(counts.max()), "nonempty_min_rows": int(counts[counts > 0].min())}
+        log(f"skew: {skew_stats}")
 
     rb_h = row_bytes(spec.wtype, H)
     rb_f = row_bytes(spec.wtype, F)
@@ -167,10 +220,7 @@ def main() -> int:
     ops_gu = 2.0 * R * 2 * F * H      # int8 multiply-adds x2, gate + up
     ops_dn = 2.0 * R * H * F
     layer_ops = ops_gu + ops_dn
-
-    def run_step(i):
-        l, b = sched[i % period]
-        layers[l].forward(xs[b], out=y, workspace=ws)
+    mfma_path = T >= 128               # the library's default switch to the grouped int8-MFMA GEMMs
 
     log(f"warmup {warmup} steps")
     for i in range(warmup):
@@ -210,15 +260,17 @@ def main() -> int:
     tok_per_s = steps * T / (gpu_ms / 1e3)
     log(f"{ms_per_step * 1e3:.2f} us/step, {tok_per_s:.4g} tok/s (wall {wall:.3f}s)")
 
-    # per-phase timing on the library's stream: eager steps queued behind a
+    # per-phase timing on the library's stream: eager layer forwards queued behind a
     # bounded sleep kernel so host launch latency never shows up as GPU time
     n_prof = args.profile_steps or (256 if T <= 64 else 16)
-    log(f"profiling {n_prof} steps with phase events")
+    log(f"profiling {n_prof} layer forwards with phase events")
     pe = PhaseEvents(n_prof)
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2.4e9 * 0.05))  # ~50 ms at 2.4 GHz
+    prof_layers = []
     for i in range(n_prof):
-        l, b = sched[i % period]
+        l, b = (i % L, 0) if stack else sched[i % period]
+        prof_layers.append(l)
         check(lib().qmoe_layer_set_phase_events(layers[l]._handle, pe.arr(i)))
         layers[l].forward(xs[b], out=y, workspace=ws)
         check(lib().qmoe_layer_set_phase_events(layers[l]._handle, None))
@@ -227,18 +279,18 @@ def main() -> int:
     pe.close()
     phase_us = phase.mean(axis=0)
     log("phase us: route %.2f gate/up %.2f h-quant+down %.2f combine %.2f" % tuple(phase_us))
-    D_prof = float(np.mean([distinct[sched[i % period]] for i in range(n_prof)]))
+    D_prof = D_mean if stack else float(np.mean([distinct[i % period] for i in range(n_prof)]))
     gu_us = float(phase_us[1])
 
     # HBM traffic per launch of the dominant kernel, measured by rocprofv3 FETCH_SIZE /
     # WRITE_SIZE passes and scaled by a known-size copy (summary committed under profiles/)
     traffic = None
     tpath = os.path.join(REPO, "profiles", f"traffic_{args.workload}.json")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath) and not stack:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
-    if args.workload == "decode":
+    if not mfma_path:
         gu_bytes = (D_prof + 1) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * F * 8
         achieved = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {
@@ -246,12 +298,6 @@ def main() -> int:
             "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic, "bytes_per_launch": gu_bytes, "avg_launch_us": gu_us,
         }
-        layer_rate = {
-            "distinct_experts_mean": D_mean, "algorithmic_bytes_per_step": layer_bytes,
-            "achieved_GBs": layer_bytes / (ms_per_step * 1e-3) / 1e9,
-            "frac_of_hbm_peak": layer_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        }
-        metric = "MoE-layer tokens/s at 35B-A3B shape (decode batch 10, Q4_0)"
     else:
         achieved = ops_gu / (gu_us * 1e-6) / 1e12
         roofline = {
@@ -259,38 +305,72 @@ def main() -> int:
             "achieved": achieved, "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s", "frac": achieved / MFMA_I8_PEAK_TOPS,
             "traffic": traffic, "ops_per_launch": ops_gu, "avg_launch_us": gu_us,
         }
-        layer_rate = {
-            "distinct_experts_mean": D_mean, "int8_ops_per_step": layer_ops,
-            "achieved_TOPs": layer_ops / (ms_per_step * 1e-3) / 1e12,
-            "frac_of_int8_mfma_peak": layer_ops / (ms_per_step * 1e-3) / 1e12 / MFMA_I8_PEAK_TOPS,
-        }
-        metric = f"MoE-layer tokens/s at 35B-A3B shape (prefill {T} tokens, Q4_0)"
+    layer_us = ms_per_step * 1e3 / (L if stack else 1)
+    layer_rate = {
+        "distinct_experts_mean": D_mean, "algorithmic_bytes_per_layer": layer_bytes,
+        "hbm_GBs": layer_bytes / (layer_us * 1e-6) / 1e9,
+        "frac_of_hbm_peak": layer_bytes / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "int8_ops_per_layer": layer_ops,
+        "int8_TOPs": layer_ops / (layer_us * 1e-6) / 1e12,
+        "frac_of_int8_mfma_peak": layer_ops / (layer_us * 1e-6) / 1e12 / MFMA_I8_PEAK_TOPS,
+        "us_per_layer": layer_us,
+    }
+    if skew_stats is not None:
+        layer_rate["routing"] = skew_stats
+    if stack:
+        layer_rate["us_per_token"] = ms_per_step * 1e3 / T
+    if stack:
+        metric = f"MoE-stack tokens/s (40 layers of the 35B-A3B MoE block with RMSNorm, {T} tokens, {wname})"
+    elif args.workload == "decode":
+        metric = f"MoE-layer tokens/s at 35B-A3B shape (decode batch {T}, {wname})"
+    elif args.workload == "skewed":
+        metric = f"MoE-layer tokens/s at 35B-A3B shape (Zipf-skewed routing, {T} tokens, {wname})"
+    else:
+        metric = f"MoE-layer tokens/s at 35B-A3B shape (prefill {T} tokens, {wname})"
 
-    # parity of one step against the CPU oracle, and the CPU baseline
+    # parity against the CPU oracle (stack: layers 0 and L-1 on their actual inputs), and the CPU baseline
     result_parity = None
     cpu = None
     if not args.no_cpu:
         from oracle import pyoracle as po
 
-        host = {k: v.data.cpu().numpy() for k, v in tensors[0].items()}
-        host["router"] = host["router"].reshape(E, H)
-        ref = po.Layer(H, E, K, F, spec.shared, spec.wtype, host)
-        x0 = xs[0].cpu().numpy()
+        def host_layer(l):
+            host = {k: v.data.cpu().numpy() for k, v in tensors[l].items()}
+            host["router"] = host["router"].reshape(E, H)
+            return po.Layer(H, E, K, F, spec.shared, spec.wtype, host)
+
         n_chk = min(T, 32)
-        y_gpu, dbg = layers[0].forward(xs[0], workspace=ws, debug=True)
-        torch.cuda.synchronize()
-        y_ref, d_ref = ref.forward(x0[:n_chk], debug=True)
-        y_gpu = y_gpu.cpu().numpy()[:n_chk]
-        rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
-        result_parity = {
-            "tokens_checked": n_chk,
-            "routing_bit_exact": bool(np.array_equal(dbg["topk_idx"].cpu().numpy()[:n_chk], d_ref["topk_idx"])),
-            "max_abs_err_over_rms": float(np.max(np.abs(y_gpu - y_ref)) / rms),
-            "bit_identical_frac": float(np.mean(y_gpu.view(np.int32) == y_ref.view(np.int32))),
-        }
+        checks = []
+        if stack:
+            keep = {0: None, L - 1: None}
+            stack_pass(0, keep=keep)
+            torch.cuda.synchronize()
+            for l in (0, L - 1):
+                xin = keep[l]
+                rms_norm(xin, norms[l], synthetic.NORM_EPS, out=hbuf)
+                yl, dbg = layers[l].forward(hbuf, workspace=ws, residual=xin, debug=True)
+                torch.cuda.synchronize()
+                hh = po.rms_norm(xin.cpu().numpy()[:n_chk], norms[l].cpu().numpy(), synthetic.NORM_EPS)
+                yr, dr = host_layer(l).forward(hh, debug=True)
+                yr = yr + xin.cpu().numpy()[:n_chk]
+                checks.append((l, yl.cpu().numpy()[:n_chk], yr, dbg["topk_idx"].cpu().numpy()[:n_chk], dr["topk_idx"]))
+        else:
+            yl, dbg = layers[0].forward(xs[0], workspace=ws, debug=True)
+            torch.cuda.synchronize()
+            yr, dr = host_layer(0).forward(xs[0].cpu().numpy()[:n_chk], debug=True)
+            checks.append((0, yl.cpu().numpy()[:n_chk], yr, dbg["topk_idx"].cpu().numpy()[:n_chk], dr["topk_idx"]))
+        result_parity = {"tokens_checked": n_chk, "layers_checked": [c[0] for c in checks]}
+        for (l, yg, yr, ig, ir) in checks:
+            rms = float(np.sqrt(np.mean(yr.astype(np.float64) ** 2)))
+            result_parity[f"layer{l}"] = {
+                "routing_bit_exact": bool(np.array_equal(ig, ir)),
+                "max_abs_err_over_rms": float(np.max(np.abs(yg - yr)) / rms),
+                "bit_identical_frac": float(np.mean(yg.view(np.int32) == yr.view(np.int32))),
+            }
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        n_cpu_tok = min(T, 10 if args.workload == "decode" else 256)
-        xc = x0[:n_cpu_tok]
+        ref = host_layer(0)
+        n_cpu_tok = min(T, 10 if T <= 64 else 256)
+        xc = xs[0].cpu().numpy()[:n_cpu_tok]
         ref.forward(xc, nthreads=threads)  # warm
         iters, t_cpu = 0, 0.0
         t_start = time.perf_counter()
@@ -298,10 +378,12 @@ def main() -> int:
             ref.forward(xc, nthreads=threads)
             iters += 1
             t_cpu = time.perf_counter() - t_start
+        layer_tok_s = iters * n_cpu_tok / t_cpu
         cpu = {
-            "value": iters * n_cpu_tok / t_cpu, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{iters} forwards of layer 0 on {n_cpu_tok} tokens of batch 0 in {t_cpu:.1f}s; "
-                      f"ggml-semantics CPU restatement (oracle/liboracle.so, OpenMP) on {cpu_model()}",
+            "value": layer_tok_s / (L if stack else 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{iters} forwards of layer 0 on {n_cpu_tok} tokens of batch 0 in {t_cpu:.1f}s"
+                      + (f", divided by the {L} layers of the stack" if stack else "")
+                      + f"; ggml-semantics CPU restatement (oracle/liboracle.so, OpenMP) on {cpu_model()}",
         }
         log(f"cpu baseline {cpu['value']:.4g} tok/s on {threads} threads")
 
@@ -327,13 +409,14 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x q8_0 int8 dot, f64-exact accumulation, f32 activations",
+        "dtype": f"{wname.lower()} x q8_0 int8 dot, f64-exact accumulation, f32 activations",
         "data": "synthetic (seeded, generated on device; random-init weights of the 35B-A3B MoE layer shape)",
         "config": {
-            "workload": f"Qwen3.6-35B-A3B MoE layer, {args.workload} {T} tokens: hidden {H}, {E} experts, "
-                        f"top-{K} + shared, ffn {F}, {wname}",
+            "workload": (f"{L} x Qwen3.6-35B-A3B MoE block (RMSNorm + MoE + residual), {T} tokens" if stack else
+                         f"Qwen3.6-35B-A3B MoE layer, {args.workload} {T} tokens") +
+                        f": hidden {H}, {E} experts, top-{K} + shared, ffn {F}, {wname}",
             "tokens": T, "hidden": H, "experts": E, "top_k": K, "ffn": F, "shared_expert": spec.shared,
-            "weight_type": wname, "distinct_layers": L, "distinct_batches": B,
+            "weight_type": wname, "layers": L, "distinct_batches": B,
             "timing": "eager" if args.eager else f"hip graph of {period} steps",
         },
         "layer": layer_rate,

@@ -29,6 +29,37 @@ def x_stream(batch: int) -> int:
     return (1 << 40) + batch
 
 
+@dataclasses.dataclass(frozen=True)
+class Skew:
+    """Routing skew by construction (a shared direction u = 1/sqrt(H) in every
+    coordinate): x += c*u and router row e += beta_e*u, so logit e gains the
+    constant c*beta_e (plus beta_e*(z.u), N(0, beta_e^2) per token).  Experts
+    are ranked by a seeded permutation; rank r (1-based) gets bias
+    c*beta = -a*s*ln(r) (a Zipf(s) log-profile) and the last `n_empty` ranks
+    get `empty_bias` (never selected).  a = 0.6 puts ~50% of a 2048-token
+    batch's top-8 assignments on the 8 hot experts, with ~46 experts empty."""
+    s: float = 1.2
+    a: float = 0.6
+    n_empty: int = 40
+    empty_bias: float = -40.0
+    c: float = 8.0
+    perm_seed: int = 7
+
+    def biases(self, n_experts: int):
+        import numpy as np
+
+        rank_of = np.empty(n_experts, np.int64)
+        rank_of[np.random.default_rng(self.perm_seed).permutation(n_experts)] = np.arange(1, n_experts + 1)
+        b = -self.a * self.s * np.log(rank_of.astype(np.float64))
+        b[rank_of > n_experts - self.n_empty] = self.empty_bias
+        return b  # logit bias c*beta_e per expert id
+
+    def hot_experts(self, n_experts: int, n: int = 8):
+        import numpy as np
+
+        return np.argsort(-self.biases(n_experts), kind="stable")[:n]
+
+
 @dataclasses.dataclass
 class LayerSpec:
     n_embd: int
@@ -39,6 +70,7 @@ class LayerSpec:
     wtype: int = TYPE_Q4_0
     sigma: float = 0.02
     router_sigma: float = 0.02
+    skew: Optional[Skew] = None
 
     @property
     def hparams(self) -> Hparams:
@@ -49,6 +81,7 @@ class LayerSpec:
 CONFIG1 = LayerSpec(1024, 16, 2, 512, False, TYPE_Q8_0)       # ggml CPU-path case
 QWEN35B = LayerSpec(2048, 256, 8, 512, True, TYPE_Q4_0)       # Qwen3.6-35B-A3B MoE layer
 QWEN35B_Q8 = LayerSpec(2048, 256, 8, 512, True, TYPE_Q8_0)    # same shape, Q8_0 weights
+QWEN35B_SKEW = LayerSpec(2048, 256, 8, 512, True, TYPE_Q8_0, skew=Skew())  # Zipf-skewed routing, Q8_0
 
 
 def layer_bytes(spec: LayerSpec) -> dict:
@@ -71,8 +104,11 @@ def make_layer_tensors(spec: LayerSpec, seed: int, layer: int = 0, device="cuda"
     """Generates one layer's tensors on `device` as GGMLTensor views."""
     H, E, F, wt = spec.n_embd, spec.n_experts, spec.ffn_dim, spec.wtype
     t = {}
-    t["router"] = GGMLTensor(synth_f32(E * H, seed, stream_id(layer, "router"), 0.0, spec.router_sigma,
-                                       device=device), TYPE_F32, (H, E))
+    router = synth_f32(E * H, seed, stream_id(layer, "router"), 0.0, spec.router_sigma, device=device)
+    if spec.skew is not None:
+        beta = torch.tensor(spec.skew.biases(E) / spec.skew.c / H ** 0.5, dtype=torch.float32, device=device)
+        router = (router.view(E, H) + beta[:, None]).reshape(-1)
+    t["router"] = GGMLTensor(router, TYPE_F32, (H, E))
     for slot in ("gate", "up"):
         t[slot] = GGMLTensor(synth_quant(wt, E * F, H, seed, stream_id(layer, slot), spec.sigma, device=device),
                              wt, (H, F, E))
@@ -97,5 +133,22 @@ def make_layer(spec: LayerSpec, seed: int, layer: int = 0, device="cuda",
 
 
 def make_x(spec: LayerSpec, n_tokens: int, seed: int, batch: int = 0, device="cuda") -> torch.Tensor:
-    return synth_f32(n_tokens * spec.n_embd, seed, x_stream(batch), 0.0, 1.0, device=device).view(
+    x = synth_f32(n_tokens * spec.n_embd, seed, x_stream(batch), 0.0, 1.0, device=device).view(
         n_tokens, spec.n_embd)
+    if spec.skew is not None:
+        x = x + torch.tensor(spec.skew.c / spec.n_embd ** 0.5, dtype=torch.float32, device=device)
+    return x
+
+
+def norm_stream(layer: int) -> int:
+    """RNG stream of the pre-MoE RMSNorm weight of stack layer `layer`."""
+    return (1 << 41) + layer
+
+
+def make_norm_weight(spec: LayerSpec, seed: int, layer: int, device="cuda") -> torch.Tensor:
+    """Pre-MoE RMSNorm weight of a stack layer: N(1, 0.02)."""
+    return synth_f32(spec.n_embd, seed, norm_stream(layer), 1.0, 0.02, device=device)
+
+
+# Pre-MoE RMSNorm epsilon of the layer stack (qwen36.cpp:298 reads it from the GGUF; 1e-6 here).
+NORM_EPS = 1e-6
