@@ -117,6 +117,11 @@ int qmoe_layer_n_embd(const qmoe_layer* layer);
 int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_workspace** out);
 int qmoe_workspace_destroy(qmoe_workspace* ws);
 int32_t qmoe_workspace_capacity(const qmoe_workspace* ws);
+/* Synchronizes the device and reports, in *fault, whether any forward on this
+ * workspace gave up a bounded cross-block wait (1) or not (0); clears the
+ * word.  A raised word means that forward's routing is not to be trusted.  No
+ * counterpart in the reference (ggml runs ops one after another). */
+int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault);
 
 /* Replaces MoELayer::build (moe.h:58-63, moe.cpp:55-177):
  *   y[T][n_embd] = MoE(x[T][n_embd])  (+ residual[T][n_embd] when non-NULL,

@@ -32,6 +32,7 @@ EXPORTED = (
     "qmoe_workspace_create",
     "qmoe_workspace_destroy",
     "qmoe_workspace_capacity",
+    "qmoe_workspace_check",
     "qmoe_layer_forward",
     "qmoe_layer_set_phase_events",
     "qmoe_rms_norm",
@@ -107,6 +108,8 @@ def lib() -> ctypes.CDLL:
     L.qmoe_workspace_destroy.argtypes = [vp]
     L.qmoe_workspace_capacity.restype = ctypes.c_int32
     L.qmoe_workspace_capacity.argtypes = [vp]
+    L.qmoe_workspace_check.restype = ctypes.c_int
+    L.qmoe_workspace_check.argtypes = [vp, ctypes.POINTER(ctypes.c_int32)]
     L.qmoe_layer_forward.restype = ctypes.c_int
     L.qmoe_layer_forward.argtypes = [vp, vp, vp, ctypes.c_int32, vp, vp, P(QmoeDebug), vp]
     L.qmoe_layer_set_phase_events.restype = ctypes.c_int

@@ -60,9 +60,17 @@ struct GuItem {
     int e, p0, nrows, f0;
 };
 
+// Activation source of the gate/up kernel: the quantized token rows and the
+// row -> token map, in LDS (decode: staged once per block) or in global memory.
+struct XSrc {
+    const int8_t* qs;     // [T][H]
+    const float2* ds;     // [T][H/32]
+    const int32_t* rtok;  // [R]
+};
+
 template <int WT, int LPR, int RPW>
-__device__ __forceinline__ void gu_load(const ExpertArgs& a, const int4* s_slots, int item, int ips, int sub, int lp,
-                                        GuItem<WT, LPR, RPW>& it) {
+__device__ __forceinline__ void gu_load(const ExpertArgs& a, const XSrc& xs, const int4* s_slots, int item, int ips,
+                                        int sub, int lp, GuItem<WT, LPR, RPW>& it) {
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
     const int4 si = s_slots[item / ips];
@@ -81,19 +89,20 @@ __device__ __forceinline__ void gu_load(const ExpertArgs& a, const int4* s_slots
         it.wg[m].load(gb + (uint64_t)f * gnb1, pair);
         it.wu[m].load(ub + (uint64_t)f * unb1, pair);
     }
-    it.x.load(a.xq_qs + (uint64_t)tok * a.H, a.xq_ds + (uint64_t)tok * (a.H >> 5), pair);
+    it.x.load(xs.qs + (uint64_t)tok * a.H, xs.ds + (uint64_t)tok * (a.H >> 5), pair);
 }
 
 template <int WT, int LPR, int RPW>
-__device__ __forceinline__ void gu_compute(const ExpertArgs& a, const GuItem<WT, LPR, RPW>& it, int sub, int lp) {
+__device__ __forceinline__ void gu_compute(const ExpertArgs& a, const XSrc& xs, const GuItem<WT, LPR, RPW>& it,
+                                           int sub, int lp) {
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
     const bool live = lp < (a.H >> 6);
     XPair x = it.x;
     for (int c = 0; c < it.nrows; ++c) {
         if (c > 0) {
-            const int tok = it.e >= a.E ? c : a.row_token[it.p0 + c];
-            x.load(a.xq_qs + (uint64_t)tok * a.H, a.xq_ds + (uint64_t)tok * (a.H >> 5), min(lp, (a.H >> 6) - 1));
+            const int tok = it.e >= a.E ? c : xs.rtok[it.p0 + c];
+            x.load(xs.qs + (uint64_t)tok * a.H, xs.ds + (uint64_t)tok * (a.H >> 5), min(lp, (a.H >> 6) - 1));
         }
 #pragma unroll
         for (int m = 0; m < NI; ++m) {
@@ -104,11 +113,30 @@ __device__ __forceinline__ void gu_compute(const ExpertArgs& a, const GuItem<WT,
     }
 }
 
-template <int WT, int LPR, int RPW>
+// LDS layout of the gate/up kernel: slot table, then (XLDS) the T quantized
+// token rows, their scales and the row -> token map.
+__host__ __device__ constexpr size_t gu_lds_slots(int E) { return (size_t)(E + 1) * 16; }
+__host__ __device__ constexpr size_t gu_lds_bytes(int E, int T, int H, int R, bool xlds) {
+    return gu_lds_slots(E) + (xlds ? (size_t)T * H + (size_t)T * (H / 32) * 8 + (size_t)((R + 3) & ~3) * 4 : 0);
+}
+
+template <int WT, int LPR, int RPW, bool XLDS>
 __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
     __shared__ int s_nact;
     int4* s_slots = (int4*)s_dyn;
+    XSrc xs{a.xq_qs, a.xq_ds, a.row_token};
+    if (XLDS) {
+        // the T token rows (16-byte chunks), their scales and the row map: one round of loads
+        int8_t* lq = (int8_t*)(s_dyn + gu_lds_slots(a.E));
+        float2* ld = (float2*)(lq + (size_t)a.T * a.H);
+        int32_t* lr = (int32_t*)(ld + (size_t)a.T * (a.H >> 5));
+        const int nq = a.T * a.H / 16, nd = a.T * (a.H >> 5) / 2, R = a.offsets[a.E + 1];
+        for (int i = threadIdx.x; i < nq; i += blockDim.x) ((u32x4*)lq)[i] = ((const u32x4*)a.xq_qs)[i];
+        for (int i = threadIdx.x; i < nd; i += blockDim.x) ((u32x4*)ld)[i] = ((const u32x4*)a.xq_ds)[i];
+        for (int i = threadIdx.x; i < R; i += blockDim.x) lr[i] = a.row_token[i];
+        xs = XSrc{lq, ld, lr};
+    }
     const int n_act = stage_slots(a, s_slots, &s_nact);
     const int ips = a.F / RPW;
     const int n_items = n_act * ips;
@@ -119,16 +147,16 @@ __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
     if (item >= n_items) return;
     // ping-pong: while one buffer is computed the other one's loads are in flight
     GuItem<WT, LPR, RPW> b0, b1;
-    gu_load(a, s_slots, item, ips, sub, lp, b0);
+    gu_load(a, xs, s_slots, item, ips, sub, lp, b0);
     for (;;) {
         int nitem = item + tw;
-        if (nitem < n_items) gu_load(a, s_slots, nitem, ips, sub, lp, b1);
-        gu_compute(a, b0, sub, lp);
+        if (nitem < n_items) gu_load(a, xs, s_slots, nitem, ips, sub, lp, b1);
+        gu_compute(a, xs, b0, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
         nitem = item + tw;
-        if (nitem < n_items) gu_load(a, s_slots, nitem, ips, sub, lp, b0);
-        gu_compute(a, b1, sub, lp);
+        if (nitem < n_items) gu_load(a, xs, s_slots, nitem, ips, sub, lp, b0);
+        gu_compute(a, xs, b1, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
     }
@@ -205,8 +233,8 @@ struct DnItem {
 };
 
 template <int WT, int LPR, int RPW>
-__device__ __forceinline__ void dn_load(const ExpertArgs& a, const int4* s_slots, int item, int ips, int sub, int lp,
-                                        DnItem<WT, LPR, RPW>& it) {
+__device__ __forceinline__ void dn_load(const ExpertArgs& a, const XSrc& hs, const int4* s_slots, int item, int ips,
+                                        int sub, int lp, DnItem<WT, LPR, RPW>& it) {
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
     const int4 si = s_slots[item / ips];
@@ -218,18 +246,26 @@ __device__ __forceinline__ void dn_load(const ExpertArgs& a, const int4* s_slots
     const int pair = min(lp, (a.F >> 6) - 1);
 #pragma unroll
     for (int m = 0; m < NI; ++m) it.w[m].load(db + (uint64_t)(it.n0 + m * RPI + sub) * dnb1, pair);
-    it.x.load(a.hq_qs + (uint64_t)it.p0 * a.F, a.hq_ds + (uint64_t)it.p0 * (a.F >> 5), pair);
+    if (sh && hs.qs) it.x.load(hs.qs, hs.ds, pair);  // uniform branches keep the address spaces known
+    else it.x.load(a.hq_qs + (uint64_t)it.p0 * a.F, a.hq_ds + (uint64_t)it.p0 * (a.F >> 5), pair);
 }
 
 template <int WT, int LPR, int RPW>
-__device__ __forceinline__ void dn_compute(const ExpertArgs& a, const DnItem<WT, LPR, RPW>& it, int sub, int lp) {
+__device__ __forceinline__ void dn_compute(const ExpertArgs& a, const XSrc& hs, const DnItem<WT, LPR, RPW>& it,
+                                           int sub, int lp) {
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
     const bool live = lp < (a.F >> 6);
+    const bool sh = it.e >= a.E;
     XPair x = it.x;
     for (int c = 0; c < it.nrows; ++c) {
         const int p = it.p0 + c;
-        if (c > 0) x.load(a.hq_qs + (uint64_t)p * a.F, a.hq_ds + (uint64_t)p * (a.F >> 5), min(lp, (a.F >> 6) - 1));
+        if (c > 0) {
+            // shared-expert rows come from the block's LDS copy (hs), routed rows from global memory
+            const int pair = min(lp, (a.F >> 6) - 1);
+            if (sh && hs.qs) x.load(hs.qs + (uint64_t)c * a.F, hs.ds + (uint64_t)c * (a.F >> 5), pair);
+            else x.load(a.hq_qs + (uint64_t)p * a.F, a.hq_ds + (uint64_t)p * (a.F >> 5), pair);
+        }
 #pragma unroll
         for (int m = 0; m < NI; ++m) {
             const double y = dpp_sum_f64<LPR>(live ? pair_dot<WT>(it.w[m], x) : 0.0);
@@ -238,11 +274,29 @@ __device__ __forceinline__ void dn_compute(const ExpertArgs& a, const DnItem<WT,
     }
 }
 
-template <int WT, int LPR, int RPW>
+// LDS of the down kernel: slot table, then (SHLDS) the shared expert's T rows
+// of quantized h (the slot with the most rows at decode sizes).
+__host__ __device__ constexpr size_t dn_lds_bytes(int E, int T, int F, bool shlds) {
+    return (size_t)(E + 1) * 16 + (shlds ? (size_t)T * F + (size_t)T * (F / 32) * 8 : 0);
+}
+
+template <int WT, int LPR, int RPW, bool SHLDS>
 __global__ __launch_bounds__(256) void k_down_stream(ExpertArgs a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
     __shared__ int s_nact;
     int4* s_slots = (int4*)s_dyn;
+    XSrc hs{nullptr, nullptr, nullptr};
+    if (SHLDS) {
+        int8_t* lq = (int8_t*)(s_dyn + (size_t)(a.E + 1) * 16);
+        float2* ld = (float2*)(lq + (size_t)a.T * a.F);
+        const int A = a.T * a.K;  // the shared rows follow the T*K routed rows
+        const int nq = a.T * a.F / 16, nd = a.T * (a.F >> 5) / 2;
+        const u32x4* gq = (const u32x4*)(a.hq_qs + (uint64_t)A * a.F);
+        const u32x4* gd = (const u32x4*)(a.hq_ds + (uint64_t)A * (a.F >> 5));
+        for (int i = threadIdx.x; i < nq; i += blockDim.x) ((u32x4*)lq)[i] = gq[i];
+        for (int i = threadIdx.x; i < nd; i += blockDim.x) ((u32x4*)ld)[i] = gd[i];
+        hs = XSrc{lq, ld, nullptr};
+    }
     const int n_act = stage_slots(a, s_slots, &s_nact);
     const int ips = a.H / RPW;
     const int n_items = n_act * ips;
@@ -252,16 +306,16 @@ __global__ __launch_bounds__(256) void k_down_stream(ExpertArgs a) {
     int item = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (item >= n_items) return;
     DnItem<WT, LPR, RPW> b0, b1;
-    dn_load(a, s_slots, item, ips, sub, lp, b0);
+    dn_load(a, hs, s_slots, item, ips, sub, lp, b0);
     for (;;) {
         int nitem = item + tw;
-        if (nitem < n_items) dn_load(a, s_slots, nitem, ips, sub, lp, b1);
-        dn_compute(a, b0, sub, lp);
+        if (nitem < n_items) dn_load(a, hs, s_slots, nitem, ips, sub, lp, b1);
+        dn_compute(a, hs, b0, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
         nitem = item + tw;
-        if (nitem < n_items) dn_load(a, s_slots, nitem, ips, sub, lp, b0);
-        dn_compute(a, b1, sub, lp);
+        if (nitem < n_items) dn_load(a, hs, s_slots, nitem, ips, sub, lp, b0);
+        dn_compute(a, hs, b1, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
     }
@@ -277,12 +331,23 @@ static int stream_blocks(KernelT kernel, size_t lds, int n_items_max, int n_cu) 
     return std::max(1, std::min(want, n_cu * per_cu));
 }
 
+// Token rows are staged in LDS when they take at most this many bytes per block.
+constexpr size_t kGuXLdsMax = 32 * 1024;
+
 template <int WT, int LPR, int RPW>
 static hipError_t launch_gateup_v(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
-    const size_t lds = (size_t)(a.E + 1) * sizeof(int4);
-    auto kern = k_gateup_stream<WT, LPR, RPW>;
-    const int g = stream_blocks(kern, lds, max_slots * (a.F / RPW), n_cu);
-    hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+    const int R = a.T * a.K + a.S * a.T;
+    const bool xlds = gu_lds_bytes(a.E, a.T, a.H, R, true) - gu_lds_slots(a.E) <= kGuXLdsMax;
+    const size_t lds = gu_lds_bytes(a.E, a.T, a.H, R, xlds);
+    if (xlds) {
+        auto kern = k_gateup_stream<WT, LPR, RPW, true>;
+        const int g = stream_blocks(kern, lds, max_slots * (a.F / RPW), n_cu);
+        hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+    } else {
+        auto kern = k_gateup_stream<WT, LPR, RPW, false>;
+        const int g = stream_blocks(kern, lds, max_slots * (a.F / RPW), n_cu);
+        hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+    }
     return hipGetLastError();
 }
 
@@ -297,10 +362,17 @@ static hipError_t launch_gateup(const ExpertArgs& a, int max_slots, int n_cu, hi
 template <int WT, int LPR>
 static hipError_t launch_down_v(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
     constexpr int RPW = 2 * (64 / LPR);  // two load instructions per item
-    const size_t lds = (size_t)(a.E + 1) * sizeof(int4);
-    auto kern = k_down_stream<WT, LPR, RPW>;
-    const int g = stream_blocks(kern, lds, max_slots * (a.H / RPW), n_cu);
-    hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+    const bool shlds = a.S && dn_lds_bytes(a.E, a.T, a.F, true) - dn_lds_bytes(a.E, a.T, a.F, false) <= kGuXLdsMax;
+    const size_t lds = dn_lds_bytes(a.E, a.T, a.F, shlds);
+    if (shlds) {
+        auto kern = k_down_stream<WT, LPR, RPW, true>;
+        const int g = stream_blocks(kern, lds, max_slots * (a.H / RPW), n_cu);
+        hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+    } else {
+        auto kern = k_down_stream<WT, LPR, RPW, false>;
+        const int g = stream_blocks(kern, lds, max_slots * (a.H / RPW), n_cu);
+        hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+    }
     return hipGetLastError();
 }
 

@@ -145,6 +145,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.expert_slot = (int32_t*)take((size_t)E * sizeof(int32_t));
     ws.slot_info = (int4*)take((size_t)(E + 1) * sizeof(int4));
     ws.counters = (int32_t*)take(16 * sizeof(int32_t));
+    ws.sync = (int32_t*)take(kSyncWords * sizeof(int32_t));
     ws.tiles = (int4*)take((size_t)max_tiles * sizeof(int4));
     ws.gubuf = (float2*)take(R * F * sizeof(float2));
     ws.hq_qs = (int8_t*)take(R * F);
@@ -298,6 +299,14 @@ int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_works
         return hip_fail(err, "hipMalloc(workspace)");
     }
     qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, &ws->w, base);
+    // the signalling area starts at zero (generation 0, no flags raised)
+    err = hipMemset(ws->w.sync, 0, qmoe::kSyncWords * sizeof(int32_t));
+    if (err == hipSuccess) err = hipDeviceSynchronize();
+    if (err != hipSuccess) {
+        (void)hipFree(base);
+        delete ws;
+        return hip_fail(err, "hipMemset(workspace sync area)");
+    }
     (void)hipGetDevice(&ws->device);
     *out = ws;
     return QMOE_OK;
@@ -311,6 +320,19 @@ int qmoe_workspace_destroy(qmoe_workspace* ws) {
 }
 
 int32_t qmoe_workspace_capacity(const qmoe_workspace* ws) { return ws ? ws->w.cap_T : 0; }
+
+int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault) {
+    g_last_error.clear();
+    if (!ws || !fault) return fail(QMOE_ERR_NULL, "qmoe: ws and fault expected non-null, got null");
+    hipError_t err = hipDeviceSynchronize();
+    int32_t v = 0;
+    if (err == hipSuccess) err = hipMemcpy(&v, ws->w.sync + qmoe::kSyncErr, sizeof(v), hipMemcpyDeviceToHost);
+    if (err == hipSuccess && v) err = hipMemset(ws->w.sync + qmoe::kSyncErr, 0, sizeof(int32_t));
+    if (err == hipSuccess) err = hipDeviceSynchronize();
+    if (err != hipSuccess) return hip_fail(err, "workspace check");
+    *fault = v;
+    return QMOE_OK;
+}
 
 int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, int32_t n_tokens, float* y,
                        const float* residual, const qmoe_debug* dbg, void* hip_stream) {

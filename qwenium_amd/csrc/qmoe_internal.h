@@ -9,6 +9,12 @@ namespace qmoe {
 // Tokens handled by one top-k block; the per-block histogram granularity of
 // the stable counting sort.
 constexpr int kTopkTokensPerBlock = 16;
+// Cross-block signalling area of a workspace: generation counter of the
+// fused decode routing, its error flag, and one flag per router block.
+constexpr int kSyncWords = 512;
+constexpr int kSyncGen = 0;
+constexpr int kSyncErr = 1;
+constexpr int kSyncFlags = 64;     // flags start here (448 router blocks max)
 // Row tile of the prefill grouped GEMM (rows of one expert per tile).
 constexpr int kMfmaTileM = 64;
 
@@ -55,6 +61,7 @@ struct Workspace {
     int32_t* expert_slot = nullptr; // [E] slot of each active expert
     int4* slot_info = nullptr;    // [E+1] per active slot {expert, first row, rows, 0}
     int32_t* counters = nullptr;  // [16] n_active, n_tiles, ...
+    int32_t* sync = nullptr;      // [kSyncWords] zeroed at creation: generation, error flag, block flags
     int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
     float2* gubuf = nullptr;      // [R][F] (gate, up) projections
     int8_t* hq_qs = nullptr;      // [R][F]   Q8_0 quants of h = silu(g)*u

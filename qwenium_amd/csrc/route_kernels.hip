@@ -636,35 +636,39 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
     }
 }
 
-// Whole routing for T <= kTopkTokensPerBlock in ONE block, everything in LDS:
-// top-k per token (one wave each), per-expert token masks, counts, offsets,
-// active slots (with the token of each slot's first row = lowest mask bit),
-// stable scatter (rank = earlier tokens in the expert's mask) and tiles.
-__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_route_small(TopkArgs a) {
-    __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
-    __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
-    __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
-    __shared__ uint32_t s_mask[1024];
-    __shared__ int32_t s_cnt[1024];
-    __shared__ int32_t s_off[1024];
-    __shared__ int32_t s_misc[64];
+// Whole routing for T <= kTopkTokensPerBlock in ONE block of 1024 threads,
+// everything in LDS: top-k per token (one wave each), per-expert token masks,
+// counts, offsets, active slots (with the token of each slot's first row =
+// lowest mask bit), stable scatter (rank = earlier tokens in the expert's
+// mask) and tiles.  Reads the exact logits from a.logits.
+struct SmallRouteLds {
+    int32_t idx[kTopkTokensPerBlock][kMaxTopK];
+    float val[kTopkTokensPerBlock][kMaxTopK];
+    double ex[kTopkTokensPerBlock][kMaxTopK + 1];
+    uint32_t mask[1024];
+    int32_t cnt[1024];
+    int32_t off[1024];
+    int32_t misc[64];
+};
+
+__device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int A = a.T * a.K;
-    for (int e = tid; e < a.E; e += blockDim.x) s_mask[e] = 0;
+    for (int e = tid; e < a.E; e += blockDim.x) L.mask[e] = 0;
     __syncthreads();
     if (wave < a.T) {
-        topk_dispatch<false>(a, wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
-        if (lane < a.K) atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
+        topk_dispatch<false>(a, wave, lane, L.idx[wave], L.val[wave], L.ex[wave]);
+        if (lane < a.K) atomicOr(&L.mask[L.idx[wave][lane]], 1u << wave);
     }
     __syncthreads();
-    for (int e = tid; e < a.E; e += blockDim.x) s_cnt[e] = __builtin_popcount(s_mask[e]);
+    for (int e = tid; e < a.E; e += blockDim.x) L.cnt[e] = __builtin_popcount(L.mask[e]);
     __syncthreads();
-    scan_experts(a, s_cnt, s_mask, s_off, s_misc);
+    scan_experts(a, L.cnt, L.mask, L.off, L.misc);
     __syncthreads();
     for (int asg = tid; asg < A; asg += blockDim.x) {
         const int t = asg / a.K, j = asg % a.K;
-        const int ex = s_idx[t][j];
-        const int p = s_off[ex] + __builtin_popcount(s_mask[ex] & ((1u << t) - 1u));
+        const int ex = L.idx[t][j];
+        const int p = L.off[ex] + __builtin_popcount(L.mask[ex] & ((1u << t) - 1u));
         a.rows[p] = asg;
         a.row_token[p] = t;
         a.pos[asg] = p;
@@ -675,12 +679,140 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_route_small(TopkAr
     }
 }
 
+// Fused decode routing (T <= kTopkTokensPerBlock): block b computes router
+// rows 4b..4b+3 (row E is the shared-expert gate) for all tokens, four waves
+// per row (wave q takes the 256-column slabs q, q+4, ...; the four partial
+// sums are added in quarter order), with x staged through LDS in column
+// chunks as wide as 48 KiB allows, and quantizes tokens t = b (mod gridDim.x);
+// then raises its flag.  Block 0 waits for every other block's flag (it waits
+// on nothing else, and the other blocks wait on nothing), then runs the whole
+// routing on the exact logits.  Flags carry the forward's generation number,
+// so nothing is reset between forwards.
+constexpr int kRdRows = 4;          // router rows per block
+constexpr int kRdSlab = 256;        // columns per lane-float4 sweep
+constexpr int kMaxRdSlabs = 8;      // fused decode routing for H <= 2048
+constexpr int kRdXBytes = 48 * 1024;
+constexpr int kMaxSpins = 1 << 22;  // bounded wait: a flag that never comes raises the error word
+constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
+
+union RouteDecodeLds {
+    float x[kRdXBytes / 4];
+    SmallRouteLds route;
+};
+
+template <int NSW>  // slabs of the router row per wave: ceil(H / 256 / 4)
+__global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits, int8_t* xq_qs, float2* xq_ds,
+                                                       int32_t* sync) {
+    __shared__ __align__(16) RouteDecodeLds S;
+    __shared__ double s_part[kRdRows][4][kTopkTokensPerBlock];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nb = gridDim.x;
+    const int gen = __hip_atomic_load(sync + kSyncGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    const int E1 = a.E + a.S;
+    const int r = wave >> 2, qtr = wave & 3;
+    const int e = blockIdx.x * kRdRows + r;
+    const bool has_row = e < E1;
+    const float* wrow = e < a.E ? a.w_router + (uint64_t)min(e, a.E - 1) * a.router_ld : (a.S ? a.w_sh_norm : a.w_router);
+    const int nslab = a.H / kRdSlab;
+    f32x4 w[NSW];
+#pragma unroll
+    for (int i = 0; i < NSW; ++i) w[i] = *(const f32x4*)(wrow + min(qtr + 4 * i, nslab - 1) * kRdSlab + 4 * lane);
+    double acc[kTopkTokensPerBlock];
+#pragma unroll
+    for (int t = 0; t < kTopkTokensPerBlock; ++t) acc[t] = 0.0;
+    // chunk = as many slabs as fit: T * chunk * 4 bytes <= kRdXBytes
+    const int cslabs = max(1, min(nslab, kRdXBytes / (a.T * kRdSlab * 4)));
+    const int ccols = cslabs * kRdSlab;
+    constexpr int kStagePerThread = kRdXBytes / 16 / 1024;  // float4 moves per thread per chunk
+    for (int s0 = 0; s0 < nslab; s0 += cslabs) {
+        const int ns = min(cslabs, nslab - s0);
+        const int q4 = ns * kRdSlab / 4;  // float4 per token in this chunk
+        __syncthreads();                  // the previous chunk's reads are done
+        f32x4 v[kStagePerThread];
+#pragma unroll
+        for (int j = 0; j < kStagePerThread; ++j) {
+            const int i = tid + 1024 * j;
+            const int t = min(i / q4, a.T - 1), q = i % q4;
+            v[j] = *(const f32x4*)(a.x + (uint64_t)t * a.H + s0 * kRdSlab + 4 * q);
+        }
+#pragma unroll
+        for (int j = 0; j < kStagePerThread; ++j) {
+            const int i = tid + 1024 * j;
+            if (i < a.T * q4) *(f32x4*)(&S.x[(i / q4) * ccols + 4 * (i % q4)]) = v[j];
+        }
+        __syncthreads();
+        if (has_row) {
+#pragma unroll
+            for (int i = 0; i < NSW; ++i) {
+                const int c = qtr + 4 * i;
+                if (c < s0 || c >= s0 + ns) continue;  // uniform per wave; w[] keeps static indices
+                const double w0 = w[i].x, w1 = w[i].y, w2 = w[i].z, w3 = w[i].w;
+#pragma unroll
+                for (int t = 0; t < kTopkTokensPerBlock; ++t) {
+                    if (t < a.T) {
+                        const f32x4 xv = *(const f32x4*)(&S.x[t * ccols + (c - s0) * kRdSlab + 4 * lane]);
+                        acc[t] = __builtin_fma(w0, (double)xv.x, acc[t]);
+                        acc[t] = __builtin_fma(w1, (double)xv.y, acc[t]);
+                        acc[t] = __builtin_fma(w2, (double)xv.z, acc[t]);
+                        acc[t] = __builtin_fma(w3, (double)xv.w, acc[t]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kTopkTokensPerBlock; ++t) {
+        if (t < a.T) {
+            const double sum = dpp_sum_f64<64>(acc[t]);
+            if (lane == 63) s_part[r][qtr][t] = sum;
+        }
+    }
+    __syncthreads();
+    if (tid < kRdRows * a.T) {
+        const int rr = tid / a.T, t = tid % a.T;
+        const int er = blockIdx.x * kRdRows + rr;
+        if (er < E1) {
+            const double sum = ((s_part[rr][0][t] + s_part[rr][1][t]) + s_part[rr][2][t]) + s_part[rr][3][t];
+            // written through to memory (agent-scope store): block 0 reads it after the flags
+            __hip_atomic_store(logits + (uint64_t)t * (a.E + 1) + er, (float)sum, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // activation quantization: token t by block t % nb, wave (t / nb) % 16
+    for (int t = blockIdx.x; t < a.T; t += nb)
+        if (wave == (t / nb) % 16) quant_token_row(a.x, a.H, t, lane, xq_qs, xq_ds);
+    // each wave's write-through logit stores complete before the block's flag (a
+    // release fence would write back the whole L2 once per wave)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (blockIdx.x != 0) {
+        if (tid == 0) __hip_atomic_store(sync + kSyncFlags + blockIdx.x, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // block 0: wait for the other blocks' flags (lane l watches blocks 1 + l + 64 i)
+    if (wave == 0) {
+        bool done = false;
+        for (int it = 0; it < kMaxSpins && !done; ++it) {
+            bool mine = true;
+            for (int bb = 1 + lane; bb < nb; bb += 64)
+                mine = mine && __hip_atomic_load(sync + kSyncFlags + bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen;
+            done = __all(mine);
+            if (!done) __builtin_amdgcn_s_sleep(2);
+        }
+        if (!done && lane == 0) __hip_atomic_store(sync + kSyncErr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // drop stale cached logits (L1 and this XCD's L2)
+    }
+    __syncthreads();
+    route_small_body(a, S.route);
+    if (tid == 0) __hip_atomic_store(sync + kSyncGen, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Per-expert exclusive prefix of the per-block histograms (in place: hist
 // becomes each block's base inside its expert), then the expert scans.  One
 // block of 1024 threads: thread (q, e) owns a contiguous range of blocks of
 // expert e and keeps up to kScanChunk counts in registers, so each pass is
 // one round of independent loads.
-constexpr int kScanChunk = 64;
+constexpr int kScanChunk = 32;
 
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_scan(TopkArgs a) {
     __shared__ int32_t s_part[1024];
@@ -831,12 +963,17 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
                                                hipMemcpyDeviceToDevice, stream)) != hipSuccess)
             return err;
         if (dbg.exact_logits && (err = launch_router_exact(L, ws, x, T, false, stream)) != hipSuccess) return err;
+    } else if (ta.nblk == 1 && L.H <= kMaxRdSlabs * kRdSlab &&
+               (L.E + L.S + kRdRows - 1) / kRdRows <= kMaxRdBlocks) {
+        // decode: one launch (n_embd <= 2048)
+        const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
+        const int nslab = L.H / kRdSlab;
+        const dim3 g(nb), b(64 * kTopkTokensPerBlock);
+        if (nslab <= 4) hipLaunchKernelGGL(k_route_decode<1>, g, b, 0, stream, ta, ws.logits, ws.xq_qs, ws.xq_ds, ws.sync);
+        else hipLaunchKernelGGL(k_route_decode<2>, g, b, 0, stream, ta, ws.logits, ws.xq_qs, ws.xq_ds, ws.sync);
+        return hipGetLastError();
     } else {
         if ((err = launch_router_exact(L, ws, x, T, true, stream)) != hipSuccess) return err;
-        if (ta.nblk == 1) {
-            hipLaunchKernelGGL(k_route_small, dim3(1), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
-            return hipGetLastError();
-        }
         hipLaunchKernelGGL(k_topk<false>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
         if ((err = hipGetLastError()) != hipSuccess) return err;
     }

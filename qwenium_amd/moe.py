@@ -67,6 +67,13 @@ class Workspace:
     def capacity(self) -> int:
         return int(lib().qmoe_workspace_capacity(self._handle))
 
+    def check(self) -> int:
+        """Synchronizes; 1 if a forward on this workspace gave up a bounded
+        cross-block wait since the last check (its routing is not to be trusted)."""
+        v = ctypes.c_int32()
+        check(lib().qmoe_workspace_check(self._handle, ctypes.byref(v)))
+        return int(v.value)
+
     def close(self) -> None:
         if getattr(self, "_handle", None):
             lib().qmoe_workspace_destroy(self._handle)

@@ -155,6 +155,7 @@ def test_workspace_and_misc_checks_without_gpu():
     ws = ctypes.c_void_p()
     assert L.qmoe_workspace_create(None, 16, ctypes.byref(ws)) == QMOE_ERR_NULL
     assert L.qmoe_workspace_capacity(None) == 0
+    assert L.qmoe_workspace_check(None, None) == 1  # QMOE_ERR_NULL
     assert L.qmoe_rms_norm(FAKE, None, 0, 2048, 1e-6, FAKE, None) == QMOE_OK
     assert L.qmoe_rms_norm(None, None, 3, 2048, 1e-6, FAKE, None) == QMOE_ERR_NULL
     assert L.qmoe_synth_quant(FAKE, TYPE_F32, 4, 64, 0, 0, 0.02, None) == QMOE_ERR_TYPE

@@ -415,3 +415,25 @@ def test_stack_40_layers_t10(gpu):
         rms = float(np.sqrt(np.mean(yr.astype(np.float64) ** 2)))
         assert np.max(np.abs(yg - yr)) <= TOL * rms, f"layer {l}"
         assert np.mean(yg.view(np.int32) == yr.view(np.int32)) >= 0.999, f"layer {l}"
+
+
+@pytest.mark.parametrize("n_experts,T", [(256, 10), (1024, 16), (16, 3)])
+def test_fused_decode_routing_repeated(gpu, n_experts, T):
+    """The fused decode routing (router blocks signal block 0 with per-forward
+    generation flags) over several forwards on one workspace: every forward's
+    routing matches the oracle, and no bounded wait gave up."""
+    from qwenium_amd import Workspace
+
+    spec = LayerSpec(256, n_experts, 8 if n_experts >= 8 else 2, 64, True, TYPE_Q4_0)
+    tensors = synthetic.make_layer_tensors(spec, 17)
+    layer = synthetic.make_layer(spec, 17, tensors=tensors)
+    ref = host_layer(spec, tensors)
+    ws = Workspace(layer, 16)
+    for batch in range(5):
+        x = synthetic.make_x(spec, T, 17, batch=batch)
+        y, dbg = layer.forward(x, workspace=ws, debug=True)
+        torch.cuda.synchronize()
+        y_ref, d_ref = ref.forward(x.cpu().numpy(), debug=True)
+        got = {k: v.cpu().numpy() for k, v in dbg.items()}
+        assert_parity(y.cpu().numpy(), got, y_ref, d_ref, spec, min_identical=1.0)
+    assert ws.check() == 0
