@@ -138,9 +138,10 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
 /* Optional per-phase timing for benchmarks and profilers.  events points to
  * QMOE_N_PHASE_EVENTS hipEvent_t created by the caller (or is NULL to disable).
  * While set, each qmoe_layer_forward records them on its stream: [0] before
- * routing, [1] after routing, [2] after the gate/up expert kernel, [3] after
- * the down expert kernel, [4] after the combine.  No counterpart in the
- * reference (ggml schedules the graph itself). */
+ * routing, [1] and [2] at the start and end of the gate/up expert kernel
+ * (recorded by that launch itself), [3] after the down expert kernel, [4]
+ * after the combine (at decode sizes the combine runs inside the down kernel).
+ * No counterpart in the reference (ggml schedules the graph itself). */
 #define QMOE_N_PHASE_EVENTS 5
 int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events);
 

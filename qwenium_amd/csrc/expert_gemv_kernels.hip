@@ -321,6 +321,130 @@ __global__ __launch_bounds__(256) void k_down_stream(ExpertArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// G2+G3 at decode sizes (T <= kTopkTokensPerBlock, K + S <= kDcMaxSteps):
+// token-major down projection with the combine in its epilogue.  Work item =
+// (token t, RPI consecutive output rows n); a wave walks t's selected experts
+// in slot order j = 0..K-1, then the shared expert, and accumulates
+//     acc = w_0*y_0;  acc = acc + w_j*y_j;  acc = acc + y_sh*sigma_t;  (+ residual)
+// in f32, each product and sum separately rounded -- the combine of
+// moe.cpp:134-151,169-174, in the same order as k_combine, so the outputs are
+// the same bits.  Each step's weights (RPI rows of W_down[e_j]) and activation
+// row (Q8_0 of h for assignment (t, j)) are loaded kDcAhead steps ahead.  An
+// expert used by several tokens (the shared one by all) is read once per
+// token; those repeats hit the L2.
+// ---------------------------------------------------------------------------
+constexpr int kDcMaxSteps = 16;
+constexpr int kDcAhead = 4;
+
+struct DownCombineArgs {
+    int H, F, E, K, S, T;
+    const uint8_t* w_down; uint64_t down_nb1, down_nb2;
+    const uint8_t* w_sh_down; uint64_t sh_down_nb1;
+    const int32_t* topk_idx; const float* topk_w; const int32_t* pos; const float* sh_gate;
+    const int8_t* hq_qs; const float2* hq_ds;
+    const float* residual; float* y;
+};
+
+template <int WT>
+struct DcStep {
+    WPair<WT> w;
+    XPair x;
+};
+
+template <int WT, int LPR>
+__global__ __launch_bounds__(256) void k_down_combine(DownCombineArgs a) {
+#pragma clang fp contract(off)
+    constexpr int RPI = 64 / LPR;
+    __shared__ int32_t s_e[kTopkTokensPerBlock][kDcMaxSteps];   // expert of step j (E: shared)
+    __shared__ int32_t s_p[kTopkTokensPerBlock][kDcMaxSteps];   // activation row of step j
+    __shared__ float s_w[kTopkTokensPerBlock][kDcMaxSteps];     // weight of step j (sigma_t for the shared step)
+    const int nj = a.K + a.S;
+    const int A = a.T * a.K;
+    for (int i = threadIdx.x; i < a.T * nj; i += blockDim.x) {
+        const int t = i / nj, j = i % nj;
+        const bool routed = j < a.K;
+        s_e[t][j] = routed ? a.topk_idx[t * a.K + j] : a.E;
+        s_p[t][j] = routed ? a.pos[t * a.K + j] : A + t;
+        s_w[t][j] = routed ? a.topk_w[t * a.K + j] : a.sh_gate[t];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int sub = lane / LPR, lp = lane % LPR;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int n_items = a.T * (a.H / RPI);
+    if (item >= n_items) return;
+    const int t = item % a.T;          // tokens fastest: neighbouring waves share experts' rows in L2
+    const int n = (item / a.T) * RPI + sub;
+    const int pair = min(lp, (a.F >> 6) - 1);
+    const bool live = lp < (a.F >> 6);
+    auto load = [&](int j, DcStep<WT>& st) {
+        const int e = s_e[t][j];
+        const bool sh = e >= a.E;
+        const uint8_t* row = sh ? a.w_sh_down + (uint64_t)n * a.sh_down_nb1
+                                : a.w_down + (uint64_t)e * a.down_nb2 + (uint64_t)n * a.down_nb1;
+        st.w.load(row, pair);
+        const int p = s_p[t][j];
+        st.x.load(a.hq_qs + (uint64_t)p * a.F, a.hq_ds + (uint64_t)p * (a.F >> 5), pair);
+    };
+    DcStep<WT> buf[kDcAhead];
+#pragma unroll
+    for (int j = 0; j < kDcAhead; ++j)
+        if (j < nj) load(j, buf[j]);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kDcMaxSteps; ++j) {
+        if (j < nj) {
+            const double yd = dpp_sum_f64<LPR>(live ? pair_dot<WT>(buf[j % kDcAhead].w, buf[j % kDcAhead].x) : 0.0);
+            if (j + kDcAhead < nj) load(j + kDcAhead, buf[j % kDcAhead]);
+            const float yv = (float)yd;
+            const float wj = s_w[t][j];
+            if (j == 0) acc = wj * yv;
+            else if (j < a.K) acc = acc + wj * yv;
+            else acc = acc + yv * wj;  // shared expert: y_sh * sigma_t
+        }
+    }
+    if (lp == LPR - 1) {
+        if (a.residual) acc = acc + a.residual[(uint64_t)t * a.H + n];
+        a.y[(uint64_t)t * a.H + n] = acc;
+    }
+}
+
+bool down_combine_fused(const LayerDesc& L, int T) {
+    return T <= kTopkTokensPerBlock && L.K + L.S <= kDcMaxSteps && T < L.mfma_min_tokens;
+}
+
+template <int WT, int LPR>
+static hipError_t launch_down_combine_v(const DownCombineArgs& a, hipStream_t stream) {
+    constexpr int RPI = 64 / LPR;
+    const int n_items = a.T * (a.H / RPI);
+    hipLaunchKernelGGL((k_down_combine<WT, LPR>), dim3((n_items + 3) / 4), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+template <int WT>
+static hipError_t launch_down_combine_t(const DownCombineArgs& a, hipStream_t stream) {
+    const int npairs = a.F / 64;
+    if (npairs <= 4) return launch_down_combine_v<WT, 4>(a, stream);
+    if (npairs <= 8) return launch_down_combine_v<WT, 8>(a, stream);
+    if (npairs <= 16) return launch_down_combine_v<WT, 16>(a, stream);
+    if (npairs <= 32) return launch_down_combine_v<WT, 32>(a, stream);
+    return launch_down_combine_v<WT, 64>(a, stream);
+}
+
+hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
+                               hipStream_t stream) {
+    DownCombineArgs a;
+    a.H = L.H; a.F = L.F; a.E = L.E; a.K = L.K; a.S = L.S; a.T = T;
+    a.w_down = L.w_down; a.down_nb1 = L.down_nb1; a.down_nb2 = L.down_nb2;
+    a.w_sh_down = L.w_sh_down; a.sh_down_nb1 = L.sh_down_nb1;
+    a.topk_idx = ws.topk_idx; a.topk_w = ws.topk_w; a.pos = ws.pos; a.sh_gate = ws.sh_gate;
+    a.hq_qs = ws.hq_qs; a.hq_ds = ws.hq_ds;
+    a.residual = residual; a.y = y;
+    return (L.dn_type == kTypeQ4_0) ? launch_down_combine_t<kTypeQ4_0>(a, stream)
+                                    : launch_down_combine_t<kTypeQ8_0>(a, stream);
+}
+
 // Persistent grid: every block resident at once (blocks per CU from the
 // occupancy calculator), never more waves than items.
 template <typename KernelT>
@@ -335,28 +459,30 @@ static int stream_blocks(KernelT kernel, size_t lds, int n_items_max, int n_cu) 
 constexpr size_t kGuXLdsMax = 32 * 1024;
 
 template <int WT, int LPR, int RPW>
-static hipError_t launch_gateup_v(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
+static hipError_t launch_gateup_v(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream, hipEvent_t e0,
+                                  hipEvent_t e1) {
     const int R = a.T * a.K + a.S * a.T;
     const bool xlds = gu_lds_bytes(a.E, a.T, a.H, R, true) - gu_lds_slots(a.E) <= kGuXLdsMax;
     const size_t lds = gu_lds_bytes(a.E, a.T, a.H, R, xlds);
     if (xlds) {
         auto kern = k_gateup_stream<WT, LPR, RPW, true>;
         const int g = stream_blocks(kern, lds, max_slots * (a.F / RPW), n_cu);
-        hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+        launch_timed(kern, dim3(g), dim3(256), lds, stream, e0, e1, a);
     } else {
         auto kern = k_gateup_stream<WT, LPR, RPW, false>;
         const int g = stream_blocks(kern, lds, max_slots * (a.F / RPW), n_cu);
-        hipLaunchKernelGGL(kern, dim3(g), dim3(256), lds, stream, a);
+        launch_timed(kern, dim3(g), dim3(256), lds, stream, e0, e1, a);
     }
     return hipGetLastError();
 }
 
 template <int WT>
-static hipError_t launch_gateup(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
+static hipError_t launch_gateup(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream, hipEvent_t e0,
+                                hipEvent_t e1) {
     const int npairs = a.H / 64;
-    if (npairs <= 16) return launch_gateup_v<WT, 16, 4>(a, max_slots, n_cu, stream);
-    if (npairs <= 32) return launch_gateup_v<WT, 32, 2>(a, max_slots, n_cu, stream);
-    return launch_gateup_v<WT, 64, 2>(a, max_slots, n_cu, stream);
+    if (npairs <= 16) return launch_gateup_v<WT, 16, 4>(a, max_slots, n_cu, stream, e0, e1);
+    if (npairs <= 32) return launch_gateup_v<WT, 32, 2>(a, max_slots, n_cu, stream, e0, e1);
+    return launch_gateup_v<WT, 64, 2>(a, max_slots, n_cu, stream, e0, e1);
 }
 
 template <int WT, int LPR>
@@ -400,11 +526,12 @@ static ExpertArgs make_expert_args(const LayerDesc& L, const Workspace& ws, int 
     return a;
 }
 
-hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
+hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
+                                 hipEvent_t ev_start, hipEvent_t ev_stop) {
     const ExpertArgs a = make_expert_args(L, ws, T);
     const int max_slots = min(L.E, T * L.K) + L.S;
-    return (L.gu_type == kTypeQ4_0) ? launch_gateup<kTypeQ4_0>(a, max_slots, L.n_cu, stream)
-                                    : launch_gateup<kTypeQ8_0>(a, max_slots, L.n_cu, stream);
+    return (L.gu_type == kTypeQ4_0) ? launch_gateup<kTypeQ4_0>(a, max_slots, L.n_cu, stream, ev_start, ev_stop)
+                                    : launch_gateup<kTypeQ8_0>(a, max_slots, L.n_cu, stream, ev_start, ev_stop);
 }
 
 hipError_t launch_quant_h(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {

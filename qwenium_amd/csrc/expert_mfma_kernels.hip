@@ -277,7 +277,8 @@ static int mfma_max_tiles(const LayerDesc& L, const Workspace& ws, int T) {
                                  (L.S ? (T + kTileM - 1) / kTileM : 0));
 }
 
-hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
+hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
+                              hipEvent_t ev_start, hipEvent_t ev_stop) {
     MfmaArgs a = base_args(L, ws);
     a.w0 = L.w_gate; a.w0_nb1 = L.gate_nb1; a.w0_nb2 = L.gate_nb2;
     a.w1 = L.w_up; a.w1_nb1 = L.up_nb1; a.w1_nb2 = L.up_nb2;
@@ -288,8 +289,10 @@ hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hi
     a.n_out = L.F;
     a.n_y = L.F / 64;
     const dim3 grid(mfma_max_tiles(L, ws, T) * a.n_y + 8);
-    if (L.gu_type == kTypeQ4_0) hipLaunchKernelGGL((k_expert_mfma<kTypeQ4_0, true>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((k_expert_mfma<kTypeQ8_0, true>), grid, dim3(256), 0, stream, a);
+    if (L.gu_type == kTypeQ4_0)
+        launch_timed(k_expert_mfma<kTypeQ4_0, true>, grid, dim3(256), 0, stream, ev_start, ev_stop, a);
+    else
+        launch_timed(k_expert_mfma<kTypeQ8_0, true>, grid, dim3(256), 0, stream, ev_start, ev_stop, a);
     return hipGetLastError();
 }
 

@@ -384,18 +384,26 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
     if (err == hipSuccess) err = qmoe::launch_route(d, v, x, n_tokens, rdbg, stream);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
     const bool mfma = n_tokens >= d.mfma_min_tokens;
-    err = mark(1);
-    if (err == hipSuccess)
-        err = mfma ? qmoe::launch_gateup_mfma(d, v, n_tokens, stream) : qmoe::launch_experts_gateup(d, v, n_tokens, stream);
+    // events [1] and [2] are taken by the gate/up launch itself (its own start and end)
+    hipEvent_t e1 = layer->record_phases ? layer->phase_events[1] : nullptr;
+    hipEvent_t e2 = layer->record_phases ? layer->phase_events[2] : nullptr;
+    err = mfma ? qmoe::launch_gateup_mfma(d, v, n_tokens, stream, e1, e2)
+               : qmoe::launch_experts_gateup(d, v, n_tokens, stream, e1, e2);
     if (err != hipSuccess) return hip_fail(err, "gate/up expert kernel");
-    err = mark(2);
-    if (err == hipSuccess) err = qmoe::launch_quant_h(d, v, n_tokens, stream);
-    if (err == hipSuccess)
-        err = mfma ? qmoe::launch_down_mfma(d, v, n_tokens, stream) : qmoe::launch_experts_down(d, v, n_tokens, stream);
-    if (err != hipSuccess) return hip_fail(err, "down expert kernel");
-    err = mark(3);
-    if (err == hipSuccess) err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream);
-    if (err != hipSuccess) return hip_fail(err, "combine kernel");
+    err = qmoe::launch_quant_h(d, v, n_tokens, stream);
+    if (qmoe::down_combine_fused(d, n_tokens)) {
+        // decode: the combine runs in the down kernel's epilogue
+        if (err == hipSuccess) err = qmoe::launch_down_combine(d, v, n_tokens, y, residual, stream);
+        if (err != hipSuccess) return hip_fail(err, "down+combine kernel");
+        err = mark(3);
+    } else {
+        if (err == hipSuccess)
+            err = mfma ? qmoe::launch_down_mfma(d, v, n_tokens, stream) : qmoe::launch_experts_down(d, v, n_tokens, stream);
+        if (err != hipSuccess) return hip_fail(err, "down expert kernel");
+        err = mark(3);
+        if (err == hipSuccess) err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream);
+        if (err != hipSuccess) return hip_fail(err, "combine kernel");
+    }
     err = mark(4);
     if (err != hipSuccess) return hip_fail(err, "phase event record");
     if (dbg) {

@@ -220,6 +220,17 @@ __device__ __forceinline__ int wave_incl_scan_i32(int v) {
     return v;
 }
 
+// Orders one wave's LDS accesses across its lanes (a lane reads what another
+// lane of the same wave wrote): compiler barrier, LDS counter drained, wave
+// barrier.  Unlike a memory fence it does not wait for the wave's global
+// stores.
+__device__ __forceinline__ void wave_lds_sync() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Whole-wave arg-max; the winner is returned to every lane.
 __device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
     dpp_argmax_step<kDppQuadXor1, 0xF>(bv, bi);

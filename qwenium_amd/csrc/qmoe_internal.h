@@ -1,6 +1,7 @@
 // qmoe_internal.h -- host-side layer/workspace structures and kernel launchers.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -72,6 +73,16 @@ struct Workspace {
 
 size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* carve, void* base);
 
+// Launch with optional start/stop events recorded by the launch itself.
+template <typename K, typename... Args>
+inline void launch_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, hipEvent_t ev_start,
+                         hipEvent_t ev_stop, Args... args) {
+    if (ev_start || ev_stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, ev_start, ev_stop, 0u, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+}
+
 // --- launchers (each enqueues on `stream`, returns hipError_t of the launch) ---
 // Routing: logits, top-k + softmax + shared gate, counting sort.  Large T
 // routes through the bf16-MFMA router with exact refinement; exact_logits
@@ -84,13 +95,22 @@ struct RouteDebug {
 bool route_uses_mfma(const LayerDesc& L, int T);
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, const RouteDebug& dbg,
                         hipStream_t stream);
-hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+// ev_start / ev_stop (optional): events recorded at the kernel's own start and
+// end (profiling of the dominant kernel without marker overhead).
+hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
+                                 hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 hipError_t launch_experts_down(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_quant_h(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
-hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
+                              hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 hipError_t launch_down_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
                           hipStream_t stream);
+// Decode sizes: token-major down projection with the combine in its epilogue
+// (replaces launch_experts_down + launch_combine when down_combine_fused()).
+bool down_combine_fused(const LayerDesc& L, int T);
+hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
+                               hipStream_t stream);
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream);
 hipError_t launch_synth_f32(float* dst, int64_t n, uint64_t seed, uint64_t stream_id, double mean, double sigma,
                             hipStream_t stream);

@@ -418,8 +418,7 @@ __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EP
         }
     }
     // lanes below read what lane 0 wrote to LDS: order the wave's LDS accesses
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_sync();
     // softmax over the selected logits (slot 0 holds the maximum): exps in
     // parallel lanes, the sum in slot order, the divisions in parallel lanes
     {
@@ -431,15 +430,13 @@ __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EP
             s_ex_row[lane] = ex;
         }
         if (lane == a.K && a.S) a.sh_gate[t] = sigmoid_det(sg_logit);
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
+        wave_lds_sync();
         double sum = 0.0;
         if (lane == 0) {
             for (int j = 0; j < a.K; ++j) sum = sum + s_ex_row[j];
             s_ex_row[kMaxTopK] = sum;
         }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
+        wave_lds_sync();
         sum = s_ex_row[kMaxTopK];
         if (lane < a.K) a.topk_w[(uint64_t)t * a.K + lane] = (float)(ex / sum);
     }
@@ -680,18 +677,19 @@ __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
 }
 
 // Fused decode routing (T <= kTopkTokensPerBlock): block b computes router
-// rows 4b..4b+3 (row E is the shared-expert gate) for all tokens, four waves
-// per row (wave q takes the 256-column slabs q, q+4, ...; the four partial
-// sums are added in quarter order), with x staged through LDS in column
-// chunks as wide as 48 KiB allows, and quantizes tokens t = b (mod gridDim.x);
-// then raises its flag.  Block 0 waits for every other block's flag (it waits
-// on nothing else, and the other blocks wait on nothing), then runs the whole
-// routing on the exact logits.  Flags carry the forward's generation number,
-// so nothing is reset between forwards.
-constexpr int kRdRows = 4;          // router rows per block
+// rows 2b, 2b+1 (row E is the shared-expert gate) for all tokens, eight waves
+// per row (wave p takes the 256-column slabs p, p+8; the eight partial sums
+// are added in order), with x staged through LDS in column chunks as wide as
+// 96 KiB allows (all of H for T <= 12 at H = 2048), and quantizes tokens
+// t = b (mod gridDim.x); then raises its flag.  Block 0 waits for every other
+// block's flag (it waits on nothing else, and the other blocks wait on
+// nothing), then runs the whole routing on the exact logits.  Flags carry the
+// forward's generation number, so nothing is reset between forwards.
+constexpr int kRdRows = 2;          // router rows per block
+constexpr int kRdParts = 8;         // waves per row
 constexpr int kRdSlab = 256;        // columns per lane-float4 sweep
-constexpr int kMaxRdSlabs = 8;      // fused decode routing for H <= 2048
-constexpr int kRdXBytes = 48 * 1024;
+constexpr int kMaxRdSlabs = 16;     // fused decode routing for H <= 4096
+constexpr int kRdXBytes = 96 * 1024;
 constexpr int kMaxSpins = 1 << 22;  // bounded wait: a flag that never comes raises the error word
 constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
 
@@ -700,23 +698,25 @@ union RouteDecodeLds {
     SmallRouteLds route;
 };
 
-template <int NSW>  // slabs of the router row per wave: ceil(H / 256 / 4)
+template <int NSW>  // slabs of the router row per wave: ceil(H / 256 / 8)
 __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits, int8_t* xq_qs, float2* xq_ds,
                                                        int32_t* sync) {
-    __shared__ __align__(16) RouteDecodeLds S;
-    __shared__ double s_part[kRdRows][4][kTopkTokensPerBlock];
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    RouteDecodeLds& S = *(RouteDecodeLds*)s_dyn;
+    __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nb = gridDim.x;
     const int gen = __hip_atomic_load(sync + kSyncGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
     const int E1 = a.E + a.S;
-    const int r = wave >> 2, qtr = wave & 3;
+    const int r = wave / kRdParts, part = wave % kRdParts;
     const int e = blockIdx.x * kRdRows + r;
     const bool has_row = e < E1;
     const float* wrow = e < a.E ? a.w_router + (uint64_t)min(e, a.E - 1) * a.router_ld : (a.S ? a.w_sh_norm : a.w_router);
     const int nslab = a.H / kRdSlab;
     f32x4 w[NSW];
 #pragma unroll
-    for (int i = 0; i < NSW; ++i) w[i] = *(const f32x4*)(wrow + min(qtr + 4 * i, nslab - 1) * kRdSlab + 4 * lane);
+    for (int i = 0; i < NSW; ++i)
+        w[i] = *(const f32x4*)(wrow + min(part + kRdParts * i, nslab - 1) * kRdSlab + 4 * lane);
     double acc[kTopkTokensPerBlock];
 #pragma unroll
     for (int t = 0; t < kTopkTokensPerBlock; ++t) acc[t] = 0.0;
@@ -744,7 +744,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
         if (has_row) {
 #pragma unroll
             for (int i = 0; i < NSW; ++i) {
-                const int c = qtr + 4 * i;
+                const int c = part + kRdParts * i;
                 if (c < s0 || c >= s0 + ns) continue;  // uniform per wave; w[] keeps static indices
                 const double w0 = w[i].x, w1 = w[i].y, w2 = w[i].z, w3 = w[i].w;
 #pragma unroll
@@ -764,7 +764,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     for (int t = 0; t < kTopkTokensPerBlock; ++t) {
         if (t < a.T) {
             const double sum = dpp_sum_f64<64>(acc[t]);
-            if (lane == 63) s_part[r][qtr][t] = sum;
+            if (lane == 63) s_part[r][part][t] = sum;
         }
     }
     __syncthreads();
@@ -772,7 +772,9 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
         const int rr = tid / a.T, t = tid % a.T;
         const int er = blockIdx.x * kRdRows + rr;
         if (er < E1) {
-            const double sum = ((s_part[rr][0][t] + s_part[rr][1][t]) + s_part[rr][2][t]) + s_part[rr][3][t];
+            double sum = s_part[rr][0][t];
+#pragma unroll
+            for (int q = 1; q < kRdParts; ++q) sum = sum + s_part[rr][q][t];
             // written through to memory (agent-scope store): block 0 reads it after the flags
             __hip_atomic_store(logits + (uint64_t)t * (a.E + 1) + er, (float)sum, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -965,12 +967,22 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
         if (dbg.exact_logits && (err = launch_router_exact(L, ws, x, T, false, stream)) != hipSuccess) return err;
     } else if (ta.nblk == 1 && L.H <= kMaxRdSlabs * kRdSlab &&
                (L.E + L.S + kRdRows - 1) / kRdRows <= kMaxRdBlocks) {
-        // decode: one launch (n_embd <= 2048)
+        // decode: one launch
         const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
         const int nslab = L.H / kRdSlab;
         const dim3 g(nb), b(64 * kTopkTokensPerBlock);
-        if (nslab <= 4) hipLaunchKernelGGL(k_route_decode<1>, g, b, 0, stream, ta, ws.logits, ws.xq_qs, ws.xq_ds, ws.sync);
-        else hipLaunchKernelGGL(k_route_decode<2>, g, b, 0, stream, ta, ws.logits, ws.xq_qs, ws.xq_ds, ws.sync);
+        const size_t lds = sizeof(RouteDecodeLds);  // above the 64 KiB default window: raise it
+        if (nslab <= kRdParts) {
+            if ((err = hipFuncSetAttribute((const void*)k_route_decode<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds)) != hipSuccess)
+                return err;
+            hipLaunchKernelGGL(k_route_decode<1>, g, b, lds, stream, ta, ws.logits, ws.xq_qs, ws.xq_ds, ws.sync);
+        } else {
+            if ((err = hipFuncSetAttribute((const void*)k_route_decode<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds)) != hipSuccess)
+                return err;
+            hipLaunchKernelGGL(k_route_decode<2>, g, b, lds, stream, ta, ws.logits, ws.xq_qs, ws.xq_ds, ws.sync);
+        }
         return hipGetLastError();
     } else {
         if ((err = launch_router_exact(L, ws, x, T, true, stream)) != hipSuccess) return err;
