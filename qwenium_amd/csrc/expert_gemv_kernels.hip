@@ -68,12 +68,19 @@ struct XSrc {
     const int32_t* rtok;  // [R]
 };
 
+// Item order over slots: the shared expert's slot (last in the table, with a
+// row per token: the heaviest items) first, then the routed experts.
+__device__ __forceinline__ int item_slot(int item, int ips, int n_act, int S) {
+    const int k = item / ips;
+    return S ? (k == 0 ? n_act - 1 : k - 1) : k;
+}
+
 template <int WT, int LPR, int RPW>
-__device__ __forceinline__ void gu_load(const ExpertArgs& a, const XSrc& xs, const int4* s_slots, int item, int ips,
-                                        int sub, int lp, GuItem<WT, LPR, RPW>& it) {
+__device__ __forceinline__ void gu_load(const ExpertArgs& a, const XSrc& xs, const int4* s_slots, int n_act, int item,
+                                        int ips, int sub, int lp, GuItem<WT, LPR, RPW>& it) {
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
-    const int4 si = s_slots[item / ips];
+    const int4 si = s_slots[item_slot(item, ips, n_act, a.S)];
     it.e = si.x; it.p0 = si.y; it.nrows = si.z;
     it.f0 = (item % ips) * RPW;
     const int tok = si.w;
@@ -147,15 +154,15 @@ __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
     if (item >= n_items) return;
     // ping-pong: while one buffer is computed the other one's loads are in flight
     GuItem<WT, LPR, RPW> b0, b1;
-    gu_load(a, xs, s_slots, item, ips, sub, lp, b0);
+    gu_load(a, xs, s_slots, n_act, item, ips, sub, lp, b0);
     for (;;) {
         int nitem = item + tw;
-        if (nitem < n_items) gu_load(a, xs, s_slots, nitem, ips, sub, lp, b1);
+        if (nitem < n_items) gu_load(a, xs, s_slots, n_act, nitem, ips, sub, lp, b1);
         gu_compute(a, xs, b0, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
         nitem = item + tw;
-        if (nitem < n_items) gu_load(a, xs, s_slots, nitem, ips, sub, lp, b0);
+        if (nitem < n_items) gu_load(a, xs, s_slots, n_act, nitem, ips, sub, lp, b0);
         gu_compute(a, xs, b1, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
@@ -335,7 +342,6 @@ __global__ __launch_bounds__(256) void k_down_stream(ExpertArgs a) {
 // token; those repeats hit the L2.
 // ---------------------------------------------------------------------------
 constexpr int kDcMaxSteps = 16;
-constexpr int kDcAhead = 4;
 
 struct DownCombineArgs {
     int H, F, E, K, S, T;
@@ -352,7 +358,7 @@ struct DcStep {
     XPair x;
 };
 
-template <int WT, int LPR>
+template <int WT, int LPR, int kDcAhead>  // kDcAhead: steps whose loads are in flight
 __global__ __launch_bounds__(256) void k_down_combine(DownCombineArgs a) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
@@ -414,22 +420,26 @@ bool down_combine_fused(const LayerDesc& L, int T) {
     return T <= kTopkTokensPerBlock && L.K + L.S <= kDcMaxSteps && T < L.mfma_min_tokens;
 }
 
+// Steps in flight: 2 (default; measured fastest at the 35B decode shape: fewer
+// registers, more resident waves) or 4.
 template <int WT, int LPR>
-static hipError_t launch_down_combine_v(const DownCombineArgs& a, hipStream_t stream) {
+static hipError_t launch_down_combine_v(const DownCombineArgs& a, int ahead, hipStream_t stream) {
     constexpr int RPI = 64 / LPR;
     const int n_items = a.T * (a.H / RPI);
-    hipLaunchKernelGGL((k_down_combine<WT, LPR>), dim3((n_items + 3) / 4), dim3(256), 0, stream, a);
+    const dim3 g((n_items + 3) / 4), b(256);
+    if (ahead <= 2) hipLaunchKernelGGL((k_down_combine<WT, LPR, 2>), g, b, 0, stream, a);
+    else hipLaunchKernelGGL((k_down_combine<WT, LPR, 4>), g, b, 0, stream, a);
     return hipGetLastError();
 }
 
 template <int WT>
-static hipError_t launch_down_combine_t(const DownCombineArgs& a, hipStream_t stream) {
+static hipError_t launch_down_combine_t(const DownCombineArgs& a, int ahead, hipStream_t stream) {
     const int npairs = a.F / 64;
-    if (npairs <= 4) return launch_down_combine_v<WT, 4>(a, stream);
-    if (npairs <= 8) return launch_down_combine_v<WT, 8>(a, stream);
-    if (npairs <= 16) return launch_down_combine_v<WT, 16>(a, stream);
-    if (npairs <= 32) return launch_down_combine_v<WT, 32>(a, stream);
-    return launch_down_combine_v<WT, 64>(a, stream);
+    if (npairs <= 4) return launch_down_combine_v<WT, 4>(a, ahead, stream);
+    if (npairs <= 8) return launch_down_combine_v<WT, 8>(a, ahead, stream);
+    if (npairs <= 16) return launch_down_combine_v<WT, 16>(a, ahead, stream);
+    if (npairs <= 32) return launch_down_combine_v<WT, 32>(a, ahead, stream);
+    return launch_down_combine_v<WT, 64>(a, ahead, stream);
 }
 
 hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
@@ -441,8 +451,8 @@ hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, f
     a.topk_idx = ws.topk_idx; a.topk_w = ws.topk_w; a.pos = ws.pos; a.sh_gate = ws.sh_gate;
     a.hq_qs = ws.hq_qs; a.hq_ds = ws.hq_ds;
     a.residual = residual; a.y = y;
-    return (L.dn_type == kTypeQ4_0) ? launch_down_combine_t<kTypeQ4_0>(a, stream)
-                                    : launch_down_combine_t<kTypeQ8_0>(a, stream);
+    return (L.dn_type == kTypeQ4_0) ? launch_down_combine_t<kTypeQ4_0>(a, L.dc_ahead, stream)
+                                    : launch_down_combine_t<kTypeQ8_0>(a, L.dc_ahead, stream);
 }
 
 // Persistent grid: every block resident at once (blocks per CU from the

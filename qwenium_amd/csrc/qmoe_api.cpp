@@ -263,6 +263,11 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 1) d.mfma_min_tokens = (int)std::min<long>(v, 1 << 30);
     }
+    // decode down+combine prefetch depth (tuning)
+    if (const char* env = std::getenv("QMOE_DC_AHEAD")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v >= 1) d.dc_ahead = (int)std::min<long>(v, 4);
+    }
     // token count from which routing runs the batched bf16-MFMA router
     if (const char* env = std::getenv("QMOE_BIG_ROUTER_MIN_TOKENS")) {
         const long v = std::strtol(env, nullptr, 10);

@@ -37,6 +37,7 @@ struct LayerDesc {
     int n_cu = 256;                         // compute units of the layer's device
     int mfma_min_tokens = 128;              // token count from which the int8-MFMA path runs
     int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs
+    int dc_ahead = 2;                       // decode down+combine: steps with loads in flight (2 or 4)
 };
 
 // Device scratch.  R = T*K + S*T rows: routed assignments sorted by expert,
