@@ -318,11 +318,6 @@ struct TopkArgs {
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 constexpr int kMaxTopK = 64;
 
-// (v, i) beats (v2, i2): larger logit first, ties to the lower expert id.
-__device__ __forceinline__ bool better(float v, int i, float v2, int i2) {
-    return v > v2 || (v == v2 && i < i2);
-}
-
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_max_step(float v) {
     const float o = __builtin_bit_cast(
@@ -386,34 +381,73 @@ __device__ __forceinline__ void exact_dot2(const float* w0, const float* w1, con
     r1 = (float)wave_sum_f64(a1);
 }
 
+// Selection keys: the float's bits mapped to an unsigned order (negative values
+// flipped, positive values with the sign bit set) in the high word, ~id in the
+// low word, so the larger key is the larger logit and, among equal logits,
+// the lower expert id.  Key 0 is below every real entry (no candidate).
+__device__ __forceinline__ uint64_t sel_key(float v, int id) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)id;
+}
+__device__ __forceinline__ int sel_id(uint64_t k) { return (int)~(uint32_t)k; }
+__device__ __forceinline__ float sel_val(uint64_t k) {
+    const uint32_t o = (uint32_t)(k >> 32);
+    return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_u64_step(uint64_t k) {
+    const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, ROW_MASK, 0xF, false);
+    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, ROW_MASK, 0xF, false);
+    const uint64_t o = ((uint64_t)ohi << 32) | olo;
+    return o > k ? o : k;
+}
+
+// Whole-wave maximum key, returned to every lane (branch-free).
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+    k = dpp_max_u64_step<kDppQuadXor1, 0xF>(k);
+    k = dpp_max_u64_step<kDppQuadXor2, 0xF>(k);
+    k = dpp_max_u64_step<kDppRowHalfMirror, 0xF>(k);
+    k = dpp_max_u64_step<kDppRowMirror, 0xF>(k);
+    k = dpp_max_u64_step<kDppRowBcast15, 0xA>(k);
+    k = dpp_max_u64_step<kDppRowBcast31, 0xC>(k);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 // Top-k of one token from per-lane candidates (expert e = i*64 + lane in
-// v[i]/id[i], -inf/INT_MAX for none), softmax over the selected logits and the
-// shared-expert gate.  One wave.
+// v[i]/id[i], id INT_MAX for none), softmax over the selected logits and the
+// shared-expert gate.  One wave.  Each lane sorts its keys (compare-exchange
+// network), then K rounds take the wave maximum of the lanes' heads and the
+// winning lane pops its head.
 template <int EPL>
 __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EPL], int (&id)[EPL], float sg_logit,
                                int32_t* s_idx_row, float* s_val_row, double* s_ex_row) {
+    uint64_t key[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) key[i] = id[i] == 0x7fffffff ? 0ull : sel_key(v[i], id[i]);
 #pragma unroll
     for (int i = 1; i < EPL; ++i)
 #pragma unroll
         for (int j = i; j > 0; --j) {
-            if (better(v[j], id[j], v[j - 1], id[j - 1])) {
-                const float tv = v[j]; v[j] = v[j - 1]; v[j - 1] = tv;
-                const int ti = id[j]; id[j] = id[j - 1]; id[j - 1] = ti;
-            }
+            const uint64_t hi = key[j - 1] > key[j] ? key[j - 1] : key[j];
+            const uint64_t lo = key[j - 1] > key[j] ? key[j] : key[j - 1];
+            key[j - 1] = hi;
+            key[j] = lo;
         }
     for (int j = 0; j < a.K; ++j) {
-        float bv = v[0];
-        int bi = id[0];
-        wave_argmax(bv, bi);
-        if (id[0] == bi) {  // the winning lane pops its head
+        const uint64_t best = wave_max_key(key[0]);
+        const bool pop = key[0] == best;  // exactly one lane: keys are distinct
 #pragma unroll
-            for (int i = 0; i + 1 < EPL; ++i) { v[i] = v[i + 1]; id[i] = id[i + 1]; }
-            v[EPL - 1] = -__builtin_huge_valf();
-            id[EPL - 1] = 0x7fffffff;
-        }
+        for (int i = 0; i + 1 < EPL; ++i) key[i] = pop ? key[i + 1] : key[i];
+        key[EPL - 1] = pop ? 0ull : key[EPL - 1];
         if (lane == 0) {
+            const int bi = sel_id(best);
             s_idx_row[j] = bi;
-            s_val_row[j] = bv;
+            s_val_row[j] = sel_val(best);
             a.topk_idx[(uint64_t)t * a.K + j] = bi;
         }
     }
