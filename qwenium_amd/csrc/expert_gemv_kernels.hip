@@ -358,23 +358,43 @@ struct DcStep {
     XPair x;
 };
 
+// Step tables of the block's tokens: expert (E = shared), activation row and
+// combine weight (sigma_t for the shared step) of step j of token t.
+struct DcTables {
+    int32_t e[kTopkTokensPerBlock][kDcMaxSteps];
+    int32_t p[kTopkTokensPerBlock][kDcMaxSteps];
+    float w[kTopkTokensPerBlock][kDcMaxSteps];
+};
+
+__device__ __forceinline__ void dc_fill_tables(const DownCombineArgs& a, DcTables& s, int t_lo, int t_hi) {
+    const int nj = a.K + a.S;
+    const int A = a.T * a.K;
+    for (int i = threadIdx.x; i < (t_hi - t_lo) * nj; i += blockDim.x) {
+        const int t = t_lo + i / nj, j = i % nj;
+        const bool routed = j < a.K;
+        s.e[t][j] = routed ? a.topk_idx[t * a.K + j] : a.E;
+        s.p[t][j] = routed ? a.pos[t * a.K + j] : A + t;
+        s.w[t][j] = routed ? a.topk_w[t * a.K + j] : a.sh_gate[t];
+    }
+}
+
+// Combine order of the reference's ggml graph: w_0*y_0, then + w_j*y_j, then + y_sh*sigma_t.
+__device__ __forceinline__ void dc_combine(float& acc, int j, int K, float wj, double yd) {
+#pragma clang fp contract(off)
+    const float yv = (float)yd;
+    if (j == 0) acc = wj * yv;
+    else if (j < K) acc = acc + wj * yv;
+    else acc = acc + yv * wj;
+}
+
 template <int WT, int LPR, int kDcAhead>  // kDcAhead: steps whose loads are in flight
 __global__ __launch_bounds__(256) void k_down_combine(DownCombineArgs a) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
-    __shared__ int32_t s_e[kTopkTokensPerBlock][kDcMaxSteps];   // expert of step j (E: shared)
-    __shared__ int32_t s_p[kTopkTokensPerBlock][kDcMaxSteps];   // activation row of step j
-    __shared__ float s_w[kTopkTokensPerBlock][kDcMaxSteps];     // weight of step j (sigma_t for the shared step)
-    const int nj = a.K + a.S;
-    const int A = a.T * a.K;
-    for (int i = threadIdx.x; i < a.T * nj; i += blockDim.x) {
-        const int t = i / nj, j = i % nj;
-        const bool routed = j < a.K;
-        s_e[t][j] = routed ? a.topk_idx[t * a.K + j] : a.E;
-        s_p[t][j] = routed ? a.pos[t * a.K + j] : A + t;
-        s_w[t][j] = routed ? a.topk_w[t * a.K + j] : a.sh_gate[t];
-    }
+    __shared__ DcTables s;
+    dc_fill_tables(a, s, 0, a.T);
     __syncthreads();
+    const int nj = a.K + a.S;
     const int lane = threadIdx.x & 63;
     const int sub = lane / LPR, lp = lane % LPR;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -385,12 +405,11 @@ __global__ __launch_bounds__(256) void k_down_combine(DownCombineArgs a) {
     const int pair = min(lp, (a.F >> 6) - 1);
     const bool live = lp < (a.F >> 6);
     auto load = [&](int j, DcStep<WT>& st) {
-        const int e = s_e[t][j];
-        const bool sh = e >= a.E;
-        const uint8_t* row = sh ? a.w_sh_down + (uint64_t)n * a.sh_down_nb1
-                                : a.w_down + (uint64_t)e * a.down_nb2 + (uint64_t)n * a.down_nb1;
+        const int e = s.e[t][j];
+        const uint8_t* row = e >= a.E ? a.w_sh_down + (uint64_t)n * a.sh_down_nb1
+                                      : a.w_down + (uint64_t)e * a.down_nb2 + (uint64_t)n * a.down_nb1;
         st.w.load(row, pair);
-        const int p = s_p[t][j];
+        const int p = s.p[t][j];
         st.x.load(a.hq_qs + (uint64_t)p * a.F, a.hq_ds + (uint64_t)p * (a.F >> 5), pair);
     };
     DcStep<WT> buf[kDcAhead];
@@ -403,14 +422,79 @@ __global__ __launch_bounds__(256) void k_down_combine(DownCombineArgs a) {
         if (j < nj) {
             const double yd = dpp_sum_f64<LPR>(live ? pair_dot<WT>(buf[j % kDcAhead].w, buf[j % kDcAhead].x) : 0.0);
             if (j + kDcAhead < nj) load(j + kDcAhead, buf[j % kDcAhead]);
-            const float yv = (float)yd;
-            const float wj = s_w[t][j];
-            if (j == 0) acc = wj * yv;
-            else if (j < a.K) acc = acc + wj * yv;
-            else acc = acc + yv * wj;  // shared expert: y_sh * sigma_t
+            dc_combine(acc, j, a.K, s.w[t][j], yd);
         }
     }
     if (lp == LPR - 1) {
+        if (a.residual) acc = acc + a.residual[(uint64_t)t * a.H + n];
+        a.y[(uint64_t)t * a.H + n] = acc;
+    }
+}
+
+// Token-per-block variant: the block's 4 waves take 4*RPI consecutive output
+// rows of one token, whose NJ activation rows (Q8_0 h: quants, then {scale,
+// sum} pairs) are staged once in LDS; every step's weight pair is loaded
+// before the staging, so one memory latency covers all NJ steps.
+__host__ __device__ constexpr size_t dc_lds_bytes(int F, int nj) {
+    return (size_t)nj * F + (size_t)nj * (F / 32) * 8;
+}
+
+template <int WT, int LPR, int NJ>
+__global__ __launch_bounds__(256) void k_down_combine_tok(DownCombineArgs a) {
+#pragma clang fp contract(off)
+    constexpr int RPI = 64 / LPR;
+    __shared__ DcTables s;
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    const int rg = blockIdx.x / a.T;
+    const int t = blockIdx.x - rg * a.T;  // tokens fastest: neighbouring blocks share experts' rows in L2
+    dc_fill_tables(a, s, t, t + 1);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / LPR, lp = lane % LPR;
+    const int n_raw = (rg * 4 + wave) * RPI + sub;
+    const int n = min(n_raw, a.H - 1);
+    const int pair = min(lp, (a.F >> 6) - 1);
+    const bool live = lp < (a.F >> 6);
+    WPair<WT> w[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int e = s.e[t][j];
+        const uint8_t* row = e >= a.E ? a.w_sh_down + (uint64_t)n * a.sh_down_nb1
+                                      : a.w_down + (uint64_t)e * a.down_nb2 + (uint64_t)n * a.down_nb1;
+        w[j].load(row, pair);
+    }
+    int8_t* lq = (int8_t*)s_dyn;
+    float2* ld = (float2*)(lq + (size_t)NJ * a.F);
+    const int qc = a.F >> 4, dc = a.F >> 6;  // 16-byte chunks per row: quants, {scale, sum} pairs
+    const int nc = NJ * (qc + dc);
+    for (int i0 = threadIdx.x; i0 < nc; i0 += 512) {
+        u32x4 v[2];
+        u32x4* dst[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = min(i0 + 256 * u, nc - 1);
+            const int j = i / (qc + dc), c = i - j * (qc + dc);
+            const int p = s.p[t][j];
+            if (c < qc) {
+                v[u] = ((const u32x4*)(a.hq_qs + (uint64_t)p * a.F))[c];
+                dst[u] = (u32x4*)(lq + (size_t)j * a.F) + c;
+            } else {
+                v[u] = ((const u32x4*)(a.hq_ds + (uint64_t)p * (a.F >> 5)))[c - qc];
+                dst[u] = (u32x4*)(ld + (size_t)j * (a.F >> 5)) + (c - qc);
+            }
+        }
+        *dst[0] = v[0];
+        if (i0 + 256 < nc) *dst[1] = v[1];
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        XPair x;
+        x.load(lq + (size_t)j * a.F, ld + (size_t)j * (a.F >> 5), pair);
+        dc_combine(acc, j, a.K, s.w[t][j], dpp_sum_f64<LPR>(live ? pair_dot<WT>(w[j], x) : 0.0));
+    }
+    if (lp == LPR - 1 && n_raw < a.H) {
         if (a.residual) acc = acc + a.residual[(uint64_t)t * a.H + n];
         a.y[(uint64_t)t * a.H + n] = acc;
     }
@@ -420,11 +504,18 @@ bool down_combine_fused(const LayerDesc& L, int T) {
     return T <= kTopkTokensPerBlock && L.K + L.S <= kDcMaxSteps && T < L.mfma_min_tokens;
 }
 
-// Steps in flight: 2 (default; measured fastest at the 35B decode shape: fewer
-// registers, more resident waves) or 4.
+// K + S = 9 steps (8 routed + shared) whose activation rows fit in 64 KiB of
+// LDS: the token-per-block kernel (9 Q4_0 weight pairs are 81 VGPRs).
+// Otherwise steps stream with `ahead` (2 or 4) in flight.
 template <int WT, int LPR>
 static hipError_t launch_down_combine_v(const DownCombineArgs& a, int ahead, hipStream_t stream) {
     constexpr int RPI = 64 / LPR;
+    const int nj = a.K + a.S;
+    if (nj == 9 && dc_lds_bytes(a.F, nj) <= 64 * 1024 && ahead <= 2) {
+        const dim3 g(a.T * ((a.H + 4 * RPI - 1) / (4 * RPI))), b(256);
+        hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 9>), g, b, dc_lds_bytes(a.F, nj), stream, a);
+        return hipGetLastError();
+    }
     const int n_items = a.T * (a.H / RPI);
     const dim3 g((n_items + 3) / 4), b(256);
     if (ahead <= 2) hipLaunchKernelGGL((k_down_combine<WT, LPR, 2>), g, b, 0, stream, a);
