@@ -75,15 +75,14 @@ __device__ __forceinline__ int item_slot(int item, int ips, int n_act, int S) {
     return S ? (k == 0 ? n_act - 1 : k - 1) : k;
 }
 
+// Weights of one item (RPW rows of gate and of up of the slot's expert).
 template <int WT, int LPR, int RPW>
-__device__ __forceinline__ void gu_load(const ExpertArgs& a, const XSrc& xs, const int4* s_slots, int n_act, int item,
-                                        int ips, int sub, int lp, GuItem<WT, LPR, RPW>& it) {
+__device__ __forceinline__ void gu_load_w(const ExpertArgs& a, const int4 si, int item, int ips, int sub, int lp,
+                                          GuItem<WT, LPR, RPW>& it) {
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
-    const int4 si = s_slots[item_slot(item, ips, n_act, a.S)];
     it.e = si.x; it.p0 = si.y; it.nrows = si.z;
     it.f0 = (item % ips) * RPW;
-    const int tok = si.w;
     const bool sh = it.e >= a.E;
     const uint8_t* gb = sh ? a.w_sh_gate : a.w_gate + (uint64_t)it.e * a.gate_nb2;
     const uint8_t* ub = sh ? a.w_sh_up : a.w_up + (uint64_t)it.e * a.up_nb2;
@@ -96,7 +95,21 @@ __device__ __forceinline__ void gu_load(const ExpertArgs& a, const XSrc& xs, con
         it.wg[m].load(gb + (uint64_t)f * gnb1, pair);
         it.wu[m].load(ub + (uint64_t)f * unb1, pair);
     }
-    it.x.load(xs.qs + (uint64_t)tok * a.H, xs.ds + (uint64_t)tok * (a.H >> 5), pair);
+}
+
+// Activations of the item's first row (token tok).
+template <int WT, int LPR, int RPW>
+__device__ __forceinline__ void gu_load_x(const ExpertArgs& a, const XSrc& xs, int tok, int lp,
+                                          GuItem<WT, LPR, RPW>& it) {
+    it.x.load(xs.qs + (uint64_t)tok * a.H, xs.ds + (uint64_t)tok * (a.H >> 5), min(lp, (a.H >> 6) - 1));
+}
+
+template <int WT, int LPR, int RPW>
+__device__ __forceinline__ void gu_load(const ExpertArgs& a, const XSrc& xs, const int4* s_slots, int n_act, int item,
+                                        int ips, int sub, int lp, GuItem<WT, LPR, RPW>& it) {
+    const int4 si = s_slots[item_slot(item, ips, n_act, a.S)];
+    gu_load_w(a, si, item, ips, sub, lp, it);
+    gu_load_x(a, xs, si.w, lp, it);
 }
 
 template <int WT, int LPR, int RPW>
@@ -120,6 +133,10 @@ __device__ __forceinline__ void gu_compute(const ExpertArgs& a, const XSrc& xs, 
     }
 }
 
+// Token rows staged in LDS by the gate/up kernel: at most 32 KiB of quants
+// (8 chunks of 16 bytes per thread of a 256-thread block).
+constexpr int kGuStageChunks = 8;
+
 // LDS layout of the gate/up kernel: slot table, then (XLDS) the T quantized
 // token rows, their scales and the row -> token map.
 __host__ __device__ constexpr size_t gu_lds_slots(int E) { return (size_t)(E + 1) * 16; }
@@ -127,37 +144,64 @@ __host__ __device__ constexpr size_t gu_lds_bytes(int E, int T, int H, int R, bo
     return gu_lds_slots(E) + (xlds ? (size_t)T * H + (size_t)T * (H / 32) * 8 + (size_t)((R + 3) & ~3) * 4 : 0);
 }
 
+// Copies n (>= 1) 16-byte chunks global -> LDS with all of a thread's loads
+// (at most MAXC) issued before its first store: one memory round trip.  Loads
+// past n re-read the last chunk (unconditional loads keep v[] in registers).
+template <int MAXC>
+__device__ __forceinline__ void stage_chunks(u32x4* dst, const u32x4* src, int n) {
+    u32x4 v[MAXC];
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u) v[u] = src[min((int)threadIdx.x + 256 * u, n - 1)];
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < n) dst[i] = v[u];
+    }
+}
+
 template <int WT, int LPR, int RPW, bool XLDS>
 __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
-    __shared__ int s_nact;
     int4* s_slots = (int4*)s_dyn;
-    XSrc xs{a.xq_qs, a.xq_ds, a.row_token};
-    if (XLDS) {
-        // the T token rows (16-byte chunks), their scales and the row map: one round of loads
-        int8_t* lq = (int8_t*)(s_dyn + gu_lds_slots(a.E));
-        float2* ld = (float2*)(lq + (size_t)a.T * a.H);
-        int32_t* lr = (int32_t*)(ld + (size_t)a.T * (a.H >> 5));
-        const int nq = a.T * a.H / 16, nd = a.T * (a.H >> 5) / 2, R = a.offsets[a.E + 1];
-        for (int i = threadIdx.x; i < nq; i += blockDim.x) ((u32x4*)lq)[i] = ((const u32x4*)a.xq_qs)[i];
-        for (int i = threadIdx.x; i < nd; i += blockDim.x) ((u32x4*)ld)[i] = ((const u32x4*)a.xq_ds)[i];
-        for (int i = threadIdx.x; i < R; i += blockDim.x) lr[i] = a.row_token[i];
-        xs = XSrc{lq, ld, lr};
-    }
-    const int n_act = stage_slots(a, s_slots, &s_nact);
+    const int n_act = __builtin_amdgcn_readfirstlane(a.counters[0]);
     const int ips = a.F / RPW;
     const int n_items = n_act * ips;
     const int lane = threadIdx.x & 63;
     const int sub = lane / LPR, lp = lane % LPR;
     const int tw = gridDim.x * (blockDim.x >> 6);
     int item = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (item >= n_items) return;
-    // ping-pong: while one buffer is computed the other one's loads are in flight
+    // ping-pong: while one buffer is computed the other one's loads are in flight.  The
+    // first two items' weights are requested before the block stages its tables, with
+    // their slot entries read from global memory.
     GuItem<WT, LPR, RPW> b0, b1;
-    gu_load(a, xs, s_slots, n_act, item, ips, sub, lp, b0);
+    int4 si0 = make_int4(0, 0, 0, 0), si1 = si0;
+    if (item < n_items) {
+        si0 = a.slot_info[item_slot(item, ips, n_act, a.S)];
+        gu_load_w(a, si0, item, ips, sub, lp, b0);
+        if (item + tw < n_items) {
+            si1 = a.slot_info[item_slot(item + tw, ips, n_act, a.S)];
+            gu_load_w(a, si1, item + tw, ips, sub, lp, b1);
+        }
+    }
+    XSrc xs{a.xq_qs, a.xq_ds, a.row_token};
+    if (XLDS) {
+        // the T token rows (16-byte chunks), their scales and the row map
+        int8_t* lq = (int8_t*)(s_dyn + gu_lds_slots(a.E));
+        float2* ld = (float2*)(lq + (size_t)a.T * a.H);
+        int32_t* lr = (int32_t*)(ld + (size_t)a.T * (a.H >> 5));
+        const int nq = a.T * a.H / 16, nd = a.T * (a.H >> 5) / 2, R = a.offsets[a.E + 1];
+        stage_chunks<kGuStageChunks>((u32x4*)lq, (const u32x4*)a.xq_qs, nq);
+        stage_chunks<2>((u32x4*)ld, (const u32x4*)a.xq_ds, nd);
+        for (int i = threadIdx.x; i < R; i += blockDim.x) lr[i] = a.row_token[i];
+        xs = XSrc{lq, ld, lr};
+    }
+    for (int i = threadIdx.x; i < n_act; i += blockDim.x) s_slots[i] = a.slot_info[i];
+    __syncthreads();
+    if (item >= n_items) return;
+    gu_load_x(a, xs, si0.w, lp, b0);
+    if (item + tw < n_items) gu_load_x(a, xs, si1.w, lp, b1);
     for (;;) {
         int nitem = item + tw;
-        if (nitem < n_items) gu_load(a, xs, s_slots, n_act, nitem, ips, sub, lp, b1);
         gu_compute(a, xs, b0, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
@@ -166,6 +210,8 @@ __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
         gu_compute(a, xs, b1, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
+        nitem = item + tw;
+        if (nitem < n_items) gu_load(a, xs, s_slots, n_act, nitem, ips, sub, lp, b1);
     }
 }
 
@@ -432,67 +478,79 @@ __global__ __launch_bounds__(256) void k_down_combine(DownCombineArgs a) {
 }
 
 // Token-per-block variant: the block's 4 waves take 4*RPI consecutive output
-// rows of one token, whose NJ activation rows (Q8_0 h: quants, then {scale,
-// sum} pairs) are staged once in LDS; every step's weight pair is loaded
-// before the staging, so one memory latency covers all NJ steps.
+// rows of one token, whose nj (<= NJ) activation rows (Q8_0 h: quants, then
+// {scale, sum} pairs) are staged once in LDS.  Loads are issued in the order
+// they are consumed -- the staging chunks (MAXC per thread), then every step's
+// weight pair -- so step j computes while the later steps' weights arrive.
 __host__ __device__ constexpr size_t dc_lds_bytes(int F, int nj) {
     return (size_t)nj * F + (size_t)nj * (F / 32) * 8;
 }
+__host__ __device__ constexpr int dc_stage_chunks(int F, int nj) { return nj * (F / 16 + F / 64); }
 
-template <int WT, int LPR, int NJ>
+template <int WT, int LPR, int NJ, int MAXC>
 __global__ __launch_bounds__(256) void k_down_combine_tok(DownCombineArgs a) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
-    __shared__ DcTables s;
     extern __shared__ __align__(16) uint8_t s_dyn[];
     const int rg = blockIdx.x / a.T;
     const int t = blockIdx.x - rg * a.T;  // tokens fastest: neighbouring blocks share experts' rows in L2
-    dc_fill_tables(a, s, t, t + 1);
-    __syncthreads();
+    const int nj = a.K + a.S;
+    // the token's steps (wave-uniform: scalar loads); steps past nj repeat the last one
+    int se[NJ], sp[NJ];
+    float sw[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int jj = min(j, nj - 1);
+        const bool routed = jj < a.K;
+        se[j] = routed ? a.topk_idx[t * a.K + jj] : a.E;
+        sp[j] = routed ? a.pos[t * a.K + jj] : a.T * a.K + t;
+        sw[j] = routed ? a.topk_w[t * a.K + jj] : a.sh_gate[t];
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane / LPR, lp = lane % LPR;
     const int n_raw = (rg * 4 + wave) * RPI + sub;
     const int n = min(n_raw, a.H - 1);
     const int pair = min(lp, (a.F >> 6) - 1);
     const bool live = lp < (a.F >> 6);
+    // staging loads (chunks past nc re-read the last one; only chunks < nc are stored)
+    int8_t* lq = (int8_t*)s_dyn;
+    float2* ld = (float2*)(lq + (size_t)nj * a.F);
+    const int qc = a.F >> 4, dc = a.F >> 6;  // 16-byte chunks per row: quants, {scale, sum} pairs
+    const int nc = nj * (qc + dc);
+    u32x4 v[MAXC];
+    u32x4* dst[MAXC];
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u) {
+        const int i = min((int)threadIdx.x + 256 * u, nc - 1);
+        const int j = i / (qc + dc), c = i - j * (qc + dc);
+        int p = sp[0];
+#pragma unroll
+        for (int k = 1; k < NJ; ++k) p = j == k ? sp[k] : p;
+        const bool q = c < qc;
+        const u32x4* src = q ? (const u32x4*)(a.hq_qs + (uint64_t)p * a.F) + c
+                             : (const u32x4*)(a.hq_ds + (uint64_t)p * (a.F >> 5)) + (c - qc);
+        v[u] = *src;
+        dst[u] = q ? (u32x4*)(lq + (size_t)j * a.F) + c : (u32x4*)(ld + (size_t)j * (a.F >> 5)) + (c - qc);
+    }
     WPair<WT> w[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int e = s.e[t][j];
-        const uint8_t* row = e >= a.E ? a.w_sh_down + (uint64_t)n * a.sh_down_nb1
-                                      : a.w_down + (uint64_t)e * a.down_nb2 + (uint64_t)n * a.down_nb1;
+        const uint8_t* row = se[j] >= a.E ? a.w_sh_down + (uint64_t)n * a.sh_down_nb1
+                                          : a.w_down + (uint64_t)se[j] * a.down_nb2 + (uint64_t)n * a.down_nb1;
         w[j].load(row, pair);
     }
-    int8_t* lq = (int8_t*)s_dyn;
-    float2* ld = (float2*)(lq + (size_t)NJ * a.F);
-    const int qc = a.F >> 4, dc = a.F >> 6;  // 16-byte chunks per row: quants, {scale, sum} pairs
-    const int nc = NJ * (qc + dc);
-    for (int i0 = threadIdx.x; i0 < nc; i0 += 512) {
-        u32x4 v[2];
-        u32x4* dst[2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int i = min(i0 + 256 * u, nc - 1);
-            const int j = i / (qc + dc), c = i - j * (qc + dc);
-            const int p = s.p[t][j];
-            if (c < qc) {
-                v[u] = ((const u32x4*)(a.hq_qs + (uint64_t)p * a.F))[c];
-                dst[u] = (u32x4*)(lq + (size_t)j * a.F) + c;
-            } else {
-                v[u] = ((const u32x4*)(a.hq_ds + (uint64_t)p * (a.F >> 5)))[c - qc];
-                dst[u] = (u32x4*)(ld + (size_t)j * (a.F >> 5)) + (c - qc);
-            }
-        }
-        *dst[0] = v[0];
-        if (i0 + 256 < nc) *dst[1] = v[1];
-    }
+    for (int u = 0; u < MAXC; ++u)
+        if ((int)threadIdx.x + 256 * u < nc) *dst[u] = v[u];
     __syncthreads();
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        XPair x;
-        x.load(lq + (size_t)j * a.F, ld + (size_t)j * (a.F >> 5), pair);
-        dc_combine(acc, j, a.K, s.w[t][j], dpp_sum_f64<LPR>(live ? pair_dot<WT>(w[j], x) : 0.0));
+        if (j < nj) {
+            XPair x;
+            x.load(lq + (size_t)j * a.F, ld + (size_t)j * (a.F >> 5), pair);
+            dc_combine(acc, j, a.K, sw[j], dpp_sum_f64<LPR>(live ? pair_dot<WT>(w[j], x) : 0.0));
+        }
     }
     if (lp == LPR - 1 && n_raw < a.H) {
         if (a.residual) acc = acc + a.residual[(uint64_t)t * a.H + n];
@@ -504,16 +562,19 @@ bool down_combine_fused(const LayerDesc& L, int T) {
     return T <= kTopkTokensPerBlock && L.K + L.S <= kDcMaxSteps && T < L.mfma_min_tokens;
 }
 
-// K + S = 9 steps (8 routed + shared) whose activation rows fit in 64 KiB of
-// LDS: the token-per-block kernel (9 Q4_0 weight pairs are 81 VGPRs).
-// Otherwise steps stream with `ahead` (2 or 4) in flight.
+// Up to 9 steps (8 routed + shared) whose activation rows fit in 64 KiB of
+// LDS and 1024 staging chunks: the token-per-block kernel (9 Q4_0 weight pairs
+// are 81 VGPRs).  Otherwise steps stream with `ahead` (2 or 4) in flight.
 template <int WT, int LPR>
 static hipError_t launch_down_combine_v(const DownCombineArgs& a, int ahead, hipStream_t stream) {
     constexpr int RPI = 64 / LPR;
     const int nj = a.K + a.S;
-    if (nj == 9 && dc_lds_bytes(a.F, nj) <= 64 * 1024 && ahead <= 2) {
+    const int nc = dc_stage_chunks(a.F, nj);
+    if (nj <= 9 && dc_lds_bytes(a.F, nj) <= 64 * 1024 && nc <= 1024 && ahead <= 2) {
         const dim3 g(a.T * ((a.H + 4 * RPI - 1) / (4 * RPI))), b(256);
-        hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 9>), g, b, dc_lds_bytes(a.F, nj), stream, a);
+        const size_t lds = dc_lds_bytes(a.F, nj);
+        if (nc <= 512) hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 9, 2>), g, b, lds, stream, a);
+        else hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 9, 4>), g, b, lds, stream, a);
         return hipGetLastError();
     }
     const int n_items = a.T * (a.H / RPI);
