@@ -222,17 +222,6 @@ __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
 // block reduce with DPP (quad xor 1, quad xor 2, half-row mirror) and store
 // their quants as one dword each.
 // ---------------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ float dpp8_max(float v) {
-    const float o = __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-    return fmaxf(v, o);
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp8_add(int v) {
-    return v + __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
-}
-
 __global__ __launch_bounds__(256) void k_quant_h(ExpertArgs a) {
     const int nrows = a.offsets[a.E + 1];
     const int nq = a.F >> 2;  // quads per row (a multiple of 16: blocks never straddle rows or waves)
@@ -270,6 +259,118 @@ __global__ __launch_bounds__(256) void k_quant_h(ExpertArgs a) {
     *(uint32_t*)(a.hq_qs + (uint64_t)p * a.F + 4 * q) = word;
     if ((q & 7) == 0)
         a.hq_ds[(uint64_t)p * (a.F >> 5) + (q >> 3)] = make_float2(fp16_to_f32(f32_to_fp16(d)), __builtin_bit_cast(float, sum));
+}
+
+// ---------------------------------------------------------------------------
+// G1+Q at decode sizes: gate/up, SwiGLU and the Q8_0 quantization of h in one
+// launch.  Block = (slot v of the decode slot list, 32 consecutive ffn rows:
+// one Q8_0 block of h per token row); 8 waves of 4 rows of gate and of up.
+// The block stages its slot's token rows (Q8_0 of x) in LDS -- loads issued
+// before the weight loads, so they land first -- computes g and u for every
+// row into LDS, then one lane per value does h = silu(g)*u and 32 lanes
+// quantize a row's block: the same operations as k_quant_h, so the same bits.
+// ---------------------------------------------------------------------------
+constexpr int kGqWaves = 8;  // waves per block
+constexpr int kGqRpw = 4;    // ffn rows per wave: kGqWaves * kGqRpw = 32
+
+__host__ __device__ constexpr size_t gq_lds_bytes(int T, int H) { return (size_t)T * H + (size_t)T * (H / 32) * 8; }
+
+template <int WT, int LPR>
+__global__ __launch_bounds__(kGqWaves * 64) void k_gateup_q(ExpertArgs a, const int4* dslots) {
+#pragma clang fp contract(off)
+    constexpr int RPI = 64 / LPR;
+    constexpr int NI = kGqRpw / RPI;
+    constexpr int NT = kGqWaves * 64;
+    static_assert(NI >= 1 && NI * RPI == kGqRpw, "rows per wave");
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    __shared__ float2 s_gu[kTopkTokensPerBlock][32];
+    const int nfb = a.F >> 5;
+    const int v = blockIdx.x / nfb;
+    const int fb = blockIdx.x - v * nfb;
+    const int4 si = dslots[v];
+    if (si.x < 0) return;  // past the forward's active slots (whole block)
+    const int e = si.x, p0 = si.y, nrows = si.z;
+    const uint32_t mask = (uint32_t)si.w;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int sub = lane / LPR, lp = lane % LPR;
+    const int pair = min(lp, (a.H >> 6) - 1);  // lanes past the row re-read the last pair; their sums are dropped
+    const bool live = lp < (a.H >> 6);
+    // token rows of the slot -> LDS: quants [nrows][H], then {d, sum} [nrows][H/32]
+    int8_t* lq = (int8_t*)s_dyn;
+    float2* ld = (float2*)(lq + (size_t)nrows * a.H);
+    const int cq = a.H >> 4, cpr = cq + (a.H >> 6);  // 16-byte chunks per row
+    const int nc = nrows * cpr;
+    constexpr int kStage = 2;  // chunks per thread per round (a round covers 2 rows at H = 2048)
+    u32x4 xv[kStage];
+    u32x4* xdst[kStage];
+    auto stage_load = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = min(base + NT * u + tid, nc - 1);
+            const int c = i / cpr, k = i - c * cpr;
+            uint32_t m = mask;  // token of row c: the c-th set bit
+            for (int b = 0; b < c; ++b) m &= m - 1u;
+            const int tok = __builtin_ctz(m);
+            const bool q = k < cq;
+            const u32x4* src = q ? (const u32x4*)(a.xq_qs + (uint64_t)tok * a.H) + k
+                                 : (const u32x4*)(a.xq_ds + (uint64_t)tok * (a.H >> 5)) + (k - cq);
+            xv[u] = *src;
+            xdst[u] = q ? (u32x4*)(lq + (size_t)c * a.H) + k : (u32x4*)(ld + (size_t)c * (a.H >> 5)) + (k - cq);
+        }
+    };
+    auto stage_store = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < kStage; ++u)
+            if (base + NT * u + tid < nc) *xdst[u] = xv[u];
+    };
+    stage_load(0);
+    // weights: rows fb*32 + wave*4 + m*RPI + sub of gate and up
+    const bool sh = e >= a.E;
+    const uint8_t* gb = sh ? a.w_sh_gate : a.w_gate + (uint64_t)e * a.gate_nb2;
+    const uint8_t* ub = sh ? a.w_sh_up : a.w_up + (uint64_t)e * a.up_nb2;
+    const uint64_t gnb1 = sh ? a.sh_gate_nb1 : a.gate_nb1;
+    const uint64_t unb1 = sh ? a.sh_up_nb1 : a.up_nb1;
+    const int fw = fb * 32 + wave * kGqRpw;
+    WPair<WT> wg[NI], wu[NI];
+#pragma unroll
+    for (int m = 0; m < NI; ++m) {
+        const int f = fw + m * RPI + sub;
+        wg[m].load(gb + (uint64_t)f * gnb1, pair);
+        wu[m].load(ub + (uint64_t)f * unb1, pair);
+    }
+    stage_store(0);
+    for (int base = kStage * NT; base < nc; base += kStage * NT) {  // rows past the first round
+        stage_load(base);
+        stage_store(base);
+    }
+    __syncthreads();
+    for (int c = 0; c < nrows; ++c) {
+        // unpack the weights per row: hoisting the unpacked nibbles out of the
+        // loop costs registers (residency) that single-row slots never repay
+#pragma unroll
+        for (int m = 0; m < NI; ++m) {
+#pragma unroll
+            for (int k = 0; k < (int)(sizeof(wg[m].w) / 4); ++k) {
+                asm volatile("" : "+v"(wg[m].w[k]));
+                asm volatile("" : "+v"(wu[m].w[k]));
+            }
+        }
+        XPair x;
+        x.load(lq + (size_t)c * a.H, ld + (size_t)c * (a.H >> 5), pair);
+#pragma unroll
+        for (int m = 0; m < NI; ++m) {
+            const double g = dpp_sum_f64<LPR>(live ? pair_dot<WT>(wg[m], x) : 0.0);
+            const double u = dpp_sum_f64<LPR>(live ? pair_dot<WT>(wu[m], x) : 0.0);
+            if (lp == LPR - 1) s_gu[c][wave * kGqRpw + m * RPI + sub] = make_float2((float)g, (float)u);
+        }
+    }
+    __syncthreads();
+    if (tid < nrows * 32) {  // whole 32-lane groups: row c = tid / 32, value fl
+        const int c = tid >> 5, fl = tid & 31;
+        const float2 gu = s_gu[c][fl];
+        const int p = p0 + c;
+        swiglu_q8_block32(gu.x, gu.y, fl, a.hq_qs + (uint64_t)p * a.F + fb * 32, a.hq_ds + (uint64_t)p * nfb + fb);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -694,6 +795,33 @@ hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T,
     const int max_slots = min(L.E, T * L.K) + L.S;
     return (L.gu_type == kTypeQ4_0) ? launch_gateup<kTypeQ4_0>(a, max_slots, L.n_cu, stream, ev_start, ev_stop)
                                     : launch_gateup<kTypeQ8_0>(a, max_slots, L.n_cu, stream, ev_start, ev_stop);
+}
+
+// The fused decode gate/up needs the decode slot list (fused decode routing),
+// 16..64 lanes per H row (H in (512, 4096]) and the token rows within 64 KiB of LDS.
+bool gateup_q_fused(const LayerDesc& L, int T) {
+    return route_decode_fused(L, T) && down_combine_fused(L, T) && L.H > 512 && L.H <= 4096 &&
+           gq_lds_bytes(T, L.H) <= 64 * 1024;
+}
+
+template <int WT>
+static hipError_t launch_gateup_q_t(const ExpertArgs& a, const int4* dslots, int max_v, hipStream_t stream,
+                                    hipEvent_t e0, hipEvent_t e1) {
+    const int npairs = a.H / 64;
+    const dim3 g(max_v * (a.F / 32)), b(kGqWaves * 64);
+    const size_t lds = gq_lds_bytes(a.T, a.H);
+    if (npairs <= 16) launch_timed(k_gateup_q<WT, 16>, g, b, lds, stream, e0, e1, a, dslots);
+    else if (npairs <= 32) launch_timed(k_gateup_q<WT, 32>, g, b, lds, stream, e0, e1, a, dslots);
+    else launch_timed(k_gateup_q<WT, 64>, g, b, lds, stream, e0, e1, a, dslots);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup_q(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream, hipEvent_t ev_start,
+                           hipEvent_t ev_stop) {
+    const ExpertArgs a = make_expert_args(L, ws, T);
+    const int max_v = min(L.E, T * L.K) + L.S;
+    return (L.gu_type == kTypeQ4_0) ? launch_gateup_q_t<kTypeQ4_0>(a, ws.dslots, max_v, stream, ev_start, ev_stop)
+                                    : launch_gateup_q_t<kTypeQ8_0>(a, ws.dslots, max_v, stream, ev_start, ev_stop);
 }
 
 hipError_t launch_quant_h(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {

@@ -144,6 +144,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.active = (int32_t*)take((size_t)(E + 1) * sizeof(int32_t));
     ws.expert_slot = (int32_t*)take((size_t)E * sizeof(int32_t));
     ws.slot_info = (int4*)take((size_t)(E + 1) * sizeof(int4));
+    ws.dslots = (int4*)take((size_t)(E + 2) * sizeof(int4));
     ws.counters = (int32_t*)take(16 * sizeof(int32_t));
     ws.sync = (int32_t*)take(kSyncWords * sizeof(int32_t));
     ws.tiles = (int4*)take((size_t)max_tiles * sizeof(int4));
@@ -392,10 +393,16 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
     // events [1] and [2] are taken by the gate/up launch itself (its own start and end)
     hipEvent_t e1 = layer->record_phases ? layer->phase_events[1] : nullptr;
     hipEvent_t e2 = layer->record_phases ? layer->phase_events[2] : nullptr;
-    err = mfma ? qmoe::launch_gateup_mfma(d, v, n_tokens, stream, e1, e2)
-               : qmoe::launch_experts_gateup(d, v, n_tokens, stream, e1, e2);
-    if (err != hipSuccess) return hip_fail(err, "gate/up expert kernel");
-    err = qmoe::launch_quant_h(d, v, n_tokens, stream);
+    if (qmoe::gateup_q_fused(d, n_tokens)) {
+        // decode: SwiGLU and the Q8_0 of h run in the gate/up kernel
+        err = qmoe::launch_gateup_q(d, v, n_tokens, stream, e1, e2);
+        if (err != hipSuccess) return hip_fail(err, "gate/up+quant expert kernel");
+    } else {
+        err = mfma ? qmoe::launch_gateup_mfma(d, v, n_tokens, stream, e1, e2)
+                   : qmoe::launch_experts_gateup(d, v, n_tokens, stream, e1, e2);
+        if (err != hipSuccess) return hip_fail(err, "gate/up expert kernel");
+        err = qmoe::launch_quant_h(d, v, n_tokens, stream);
+    }
     if (qmoe::down_combine_fused(d, n_tokens)) {
         // decode: the combine runs in the down kernel's epilogue
         if (err == hipSuccess) err = qmoe::launch_down_combine(d, v, n_tokens, y, residual, stream);

@@ -379,6 +379,43 @@ struct XPair {
     }
 };
 
+// Within-8-lane (and wider) reductions for the h quantization.
+template <int CTRL>
+__device__ __forceinline__ float dpp8_max(float v) {
+    const float o = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    return fmaxf(v, o);
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp8_add(int v) {
+    return v + __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+
+// h = silu(g)*u of one value per lane and the Q8_0 quantization of the 32-value
+// block held by a whole aligned 32-lane group (lane fl = value fl): ggml's
+// quantize_row_q8_0 (d = fp16(amax/127), q = rint(h*127/amax)) plus the block's
+// quant sum.  Writes the lane's quant to qs[fl] and, from lane 0, {d, sum}.
+__device__ __forceinline__ void swiglu_q8_block32(float g, float u, int fl, int8_t* qs, float2* ds) {
+    const float h = silu_mul_det(g, u);
+    float amax = __builtin_fabsf(h);
+    amax = dpp8_max<kDppQuadXor1>(amax);
+    amax = dpp8_max<kDppQuadXor2>(amax);
+    amax = dpp8_max<kDppRowHalfMirror>(amax);
+    amax = dpp8_max<kDppRowMirror>(amax);
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const int qv = (int)__builtin_rintf(h * id);
+    int sum = qv;
+    sum = dpp8_add<kDppQuadXor1>(sum);
+    sum = dpp8_add<kDppQuadXor2>(sum);
+    sum = dpp8_add<kDppRowHalfMirror>(sum);
+    sum = dpp8_add<kDppRowMirror>(sum);
+    sum += __shfl_xor(sum, 16);
+    qs[fl] = (int8_t)qv;
+    if (fl == 0) *ds = make_float2(fp16_to_f32(f32_to_fp16(d)), __builtin_bit_cast(float, sum));
+}
+
 // Exact contribution of one weight pair against one activation pair (f64).
 template <int WT>
 __device__ __forceinline__ double pair_dot(const WPair<WT>& w, const XPair& x) {

@@ -309,6 +309,7 @@ struct TopkArgs {
     int32_t* active;      // [E+1]
     int32_t* expert_slot; // [E]
     int4* slot_info;      // [E+1] {expert, first row, rows, token of first row}
+    int4* dslots;         // [E+2] decode slot list (fused decode routing only, else null)
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
@@ -642,10 +643,19 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
                 a.active[slot] = e;
                 a.expert_slot[e] = slot;
                 a.slot_info[slot] = make_int4(e, off, cnt, first_token ? (int)__builtin_ctz(first_token[e]) : 0);
+                if (a.dslots && first_token) a.dslots[a.S + slot] = make_int4(e, off, cnt, (int)first_token[e]);
             }
             const int tb = base_t + inc_t - nt;
             for (int i = 0; i < nt && tb + i < a.max_tiles; ++i)
                 a.tiles[tb + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, cnt - i * kMfmaTileM), 0);
+        }
+        if (wave == nchunk - 1 && a.dslots && first_token) {
+            // decode slot list: the shared expert first (all T tokens), then the
+            // active experts; entries up to the most slots a forward can have say "none"
+            const int n_routed = __builtin_amdgcn_readlane(base_act + inc_act, 63);
+            const int max_v = min(a.E, a.T * a.K) + a.S;
+            for (int i = n_routed + a.S + lane; i < max_v; i += 64) a.dslots[i] = make_int4(-1, 0, 0, 0);
+            if (a.S && lane == 0) a.dslots[0] = make_int4(a.E, a.T * a.K, a.T, (int)((1u << a.T) - 1u));
         }
         if (wave == nchunk - 1 && lane == 63) {
             const int A = a.T * a.K;
@@ -926,6 +936,11 @@ bool route_uses_mfma(const LayerDesc& L, int T) {
     return T > kTopkTokensPerBlock && T >= L.big_router_min_tokens;
 }
 
+bool route_decode_fused(const LayerDesc& L, int T) {
+    return !route_uses_mfma(L, T) && T <= kTopkTokensPerBlock && L.H <= kMaxRdSlabs * kRdSlab &&
+           (L.E + L.S + kRdRows - 1) / kRdRows <= kMaxRdBlocks;
+}
+
 static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, const float* x, int T, bool quant,
                                       hipStream_t stream) {
     RouterArgs ra;
@@ -970,6 +985,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     ta.active = ws.active;
     ta.expert_slot = ws.expert_slot;
     ta.slot_info = ws.slot_info;
+    ta.dslots = nullptr;
     ta.counters = ws.counters;
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
@@ -999,9 +1015,9 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
                                                hipMemcpyDeviceToDevice, stream)) != hipSuccess)
             return err;
         if (dbg.exact_logits && (err = launch_router_exact(L, ws, x, T, false, stream)) != hipSuccess) return err;
-    } else if (ta.nblk == 1 && L.H <= kMaxRdSlabs * kRdSlab &&
-               (L.E + L.S + kRdRows - 1) / kRdRows <= kMaxRdBlocks) {
-        // decode: one launch
+    } else if (route_decode_fused(L, T)) {
+        // decode: one launch; it also writes the decode slot list
+        ta.dslots = ws.dslots;
         const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
         const int nslab = L.H / kRdSlab;
         const dim3 g(nb), b(64 * kTopkTokensPerBlock);
