@@ -262,8 +262,9 @@ __global__ __launch_bounds__(256) void k_quant_h(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// G1+Q at decode sizes: gate/up, SwiGLU and the Q8_0 quantization of h in one
-// launch.  Block = (slot v of the decode slot list, 32 consecutive ffn rows:
+// G1+Q at decode sizes: gate/up, SwiGLU and the Q8_0 quantization of h of the
+// routed experts in one launch (the decode routing launch does the shared
+// expert's).  Block = (slot v of the decode slot list, 32 consecutive ffn rows:
 // one Q8_0 block of h per token row); 8 waves of 4 rows of gate and of up.
 // The block stages its slot's token rows (Q8_0 of x) in LDS -- loads issued
 // before the weight loads, so they land first -- computes g and u for every
@@ -819,7 +820,7 @@ static hipError_t launch_gateup_q_t(const ExpertArgs& a, const int4* dslots, int
 hipError_t launch_gateup_q(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream, hipEvent_t ev_start,
                            hipEvent_t ev_stop) {
     const ExpertArgs a = make_expert_args(L, ws, T);
-    const int max_v = min(L.E, T * L.K) + L.S;
+    const int max_v = min(L.E, T * L.K);  // routed slots; the routing launch does the shared expert
     return (L.gu_type == kTypeQ4_0) ? launch_gateup_q_t<kTypeQ4_0>(a, ws.dslots, max_v, stream, ev_start, ev_stop)
                                     : launch_gateup_q_t<kTypeQ8_0>(a, ws.dslots, max_v, stream, ev_start, ev_stop);
 }

@@ -63,7 +63,7 @@ struct Workspace {
     int32_t* expert_slot = nullptr; // [E] slot of each active expert
     int4* slot_info = nullptr;    // [E+1] per active slot {expert, first row, rows, 0}
     int4* dslots = nullptr;       // [E+2] decode slot list {expert, first row, rows, token mask}:
-                                  // shared first, then active experts; -1 expert pads to min(E, T*K) + S
+                                  // active routed experts, then expert -1 up to min(E, T*K)
     int32_t* counters = nullptr;  // [16] n_active, n_tiles, ...
     int32_t* sync = nullptr;      // [kSyncWords] zeroed at creation: generation, error flag, block flags
     int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
@@ -106,8 +106,9 @@ hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T,
                                  hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 hipError_t launch_experts_down(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
 hipError_t launch_quant_h(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
-// Decode: gate/up + SwiGLU + Q8_0 of h in one launch over ws.dslots
-// (replaces launch_experts_gateup + launch_quant_h when gateup_q_fused()).
+// Decode: gate/up + SwiGLU + Q8_0 of h of the routed experts in one launch
+// over ws.dslots (replaces launch_experts_gateup + launch_quant_h when
+// gateup_q_fused(); the decode routing launch computes the shared expert's h).
 bool gateup_q_fused(const LayerDesc& L, int T);
 hipError_t launch_gateup_q(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
                            hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);

@@ -9,6 +9,8 @@
 #include "qmoe_device.h"
 #include "qmoe_internal.h"
 
+#include <algorithm>
+
 namespace qmoe {
 
 // ---------------------------------------------------------------------------
@@ -86,9 +88,7 @@ __device__ __forceinline__ void router_row(const RouterArgs& a, int e, float* s_
 // Q8_0 quantization of one token row (one wave; lane b handles 32-value
 // blocks b, b+64, ...): d = fp16(amax/127), q = rint(x * 127/amax), and the
 // block's quant sum for the Q4_0 offset term.
-__device__ __forceinline__ void quant_token_row(const float* x, int H, int t, int lane, int8_t* xq_qs,
-                                                float2* xq_ds) {
-    const float* xr = x + (uint64_t)t * H;
+__device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, int8_t* qs, float2* ds) {
     const int nb = H >> 5;
     for (int b = lane; b < nb; b += 64) {
         const f32x4* src = (const f32x4*)(xr + 32 * b);
@@ -117,11 +117,16 @@ __device__ __forceinline__ void quant_token_row(const float* x, int H, int t, in
             }
             packed[i] = word;
         }
-        u32x4* dst = (u32x4*)(xq_qs + (uint64_t)t * H + 32 * b);
+        u32x4* dst = (u32x4*)(qs + 32 * b);
         dst[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
         dst[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
-        xq_ds[(uint64_t)t * nb + b] = make_float2(df, __builtin_bit_cast(float, sum));
+        ds[b] = make_float2(df, __builtin_bit_cast(float, sum));
     }
+}
+
+__device__ __forceinline__ void quant_token_row(const float* x, int H, int t, int lane, int8_t* xq_qs,
+                                                float2* xq_ds) {
+    quant_x_row(x + (uint64_t)t * H, H, lane, xq_qs + (uint64_t)t * H, xq_ds + (uint64_t)t * (H >> 5));
 }
 
 // Blocks [0, n_router_blocks) compute router rows; any further blocks
@@ -643,19 +648,18 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
                 a.active[slot] = e;
                 a.expert_slot[e] = slot;
                 a.slot_info[slot] = make_int4(e, off, cnt, first_token ? (int)__builtin_ctz(first_token[e]) : 0);
-                if (a.dslots && first_token) a.dslots[a.S + slot] = make_int4(e, off, cnt, (int)first_token[e]);
+                if (a.dslots && first_token) a.dslots[slot] = make_int4(e, off, cnt, (int)first_token[e]);
             }
             const int tb = base_t + inc_t - nt;
             for (int i = 0; i < nt && tb + i < a.max_tiles; ++i)
                 a.tiles[tb + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, cnt - i * kMfmaTileM), 0);
         }
         if (wave == nchunk - 1 && a.dslots && first_token) {
-            // decode slot list: the shared expert first (all T tokens), then the
-            // active experts; entries up to the most slots a forward can have say "none"
+            // decode slot list: the active routed experts, then "none" up to the
+            // most a forward can have (the shared expert is not in it)
             const int n_routed = __builtin_amdgcn_readlane(base_act + inc_act, 63);
-            const int max_v = min(a.E, a.T * a.K) + a.S;
-            for (int i = n_routed + a.S + lane; i < max_v; i += 64) a.dslots[i] = make_int4(-1, 0, 0, 0);
-            if (a.S && lane == 0) a.dslots[0] = make_int4(a.E, a.T * a.K, a.T, (int)((1u << a.T) - 1u));
+            const int max_v = min(a.E, a.T * a.K);
+            for (int i = n_routed + lane; i < max_v; i += 64) a.dslots[i] = make_int4(-1, 0, 0, 0);
         }
         if (wave == nchunk - 1 && lane == 63) {
             const int A = a.T * a.K;
@@ -742,14 +746,86 @@ union RouteDecodeLds {
     SmallRouteLds route;
 };
 
-template <int NSW>  // slabs of the router row per wave: ceil(H / 256 / 8)
+// Shared expert at decode: its gate/up, SwiGLU and Q8_0 of h do not depend on
+// the routing, so blocks after the router blocks compute them meanwhile on
+// otherwise idle CUs.  Block j takes ffn rows 32*(j % nfb) .. +32 (one Q8_0
+// block of h) for tokens tpg*(j / nfb) .. +tpg: it quantizes those x rows into
+// LDS (quant_x_row, as the router blocks do for the workspace), computes g and
+// u with one wave per RPW rows, then 32 lanes per token do silu(g)*u and the
+// block's Q8_0 (swiglu_q8_block32, as the routed experts) into h rows T*K + t.
+struct SharedGuArgs {
+    const uint8_t* w_gate; const uint8_t* w_up;  // shared expert gate/up [F] rows
+    uint64_t gate_nb1, up_nb1;
+    int F;
+    int n_blocks;  // shared-expert blocks after the router blocks (0: none)
+    int tpg;       // tokens per block
+    int8_t* hq_qs; float2* hq_ds;
+};
+
+template <int WT, int LPR>
+__device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const SharedGuArgs& sg, int j, uint8_t* s_dyn) {
+#pragma clang fp contract(off)
+    constexpr int RPI = 64 / LPR;
+    constexpr int RPW = RPI > 2 ? RPI : 2;  // ffn rows per wave
+    constexpr int NI = RPW / RPI;
+    constexpr int NWA = 32 / RPW;           // waves with rows (of 16)
+    const int nfb = sg.F >> 5;
+    const int fb = j % nfb, t0 = (j / nfb) * sg.tpg;
+    const int nt = min(sg.tpg, a.T - t0);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int sub = lane / LPR, lp = lane % LPR;
+    const int pair = min(lp, (a.H >> 6) - 1);
+    const bool live = lp < (a.H >> 6);
+    WPair<WT> wg[NI], wu[NI];
+    if (wave < NWA) {
+#pragma unroll
+        for (int m = 0; m < NI; ++m) {
+            const int f = fb * 32 + wave * RPW + m * RPI + sub;
+            wg[m].load(sg.w_gate + (uint64_t)f * sg.gate_nb1, pair);
+            wu[m].load(sg.w_up + (uint64_t)f * sg.up_nb1, pair);
+        }
+    }
+    int8_t* lq = (int8_t*)s_dyn;                              // [tpg][H] quants
+    float2* ld = (float2*)(lq + (size_t)sg.tpg * a.H);        // [tpg][H/32] {d, sum}
+    float2* lgu = ld + (size_t)sg.tpg * (a.H >> 5);           // [tpg][32] (g, u)
+    if (wave < nt) quant_x_row(a.x + (uint64_t)(t0 + wave) * a.H, a.H, lane, lq + (size_t)wave * a.H,
+                               ld + (size_t)wave * (a.H >> 5));
+    __syncthreads();
+    if (wave < NWA) {
+        for (int c = 0; c < nt; ++c) {
+            XPair x;
+            x.load(lq + (size_t)c * a.H, ld + (size_t)c * (a.H >> 5), pair);
+#pragma unroll
+            for (int m = 0; m < NI; ++m) {
+                const double g = dpp_sum_f64<LPR>(live ? pair_dot<WT>(wg[m], x) : 0.0);
+                const double u = dpp_sum_f64<LPR>(live ? pair_dot<WT>(wu[m], x) : 0.0);
+                if (lp == LPR - 1) lgu[c * 32 + wave * RPW + m * RPI + sub] = make_float2((float)g, (float)u);
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < nt * 32) {
+        const int c = tid >> 5, fl = tid & 31;
+        const float2 gu = lgu[c * 32 + fl];
+        const uint64_t p = (uint64_t)a.T * a.K + t0 + c;
+        swiglu_q8_block32(gu.x, gu.y, fl, sg.hq_qs + p * sg.F + fb * 32, sg.hq_ds + p * nfb + fb);
+    }
+}
+
+template <int NSW, int SWT, int SLPR>  // NSW: router slabs per wave (ceil(H/256/8)); SWT: shared type (0: none)
 __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits, int8_t* xq_qs, float2* xq_ds,
-                                                       int32_t* sync) {
+                                                       int32_t* sync, SharedGuArgs sg) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
     RouteDecodeLds& S = *(RouteDecodeLds*)s_dyn;
     __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int nb = gridDim.x;
+    const int nb = gridDim.x - sg.n_blocks;  // router blocks
+    if constexpr (SWT != 0) {
+        if ((int)blockIdx.x >= nb) {
+            shared_gateup_block<SWT, SLPR>(a, sg, blockIdx.x - nb, s_dyn);
+            return;
+        }
+    }
     const int gen = __hip_atomic_load(sync + kSyncGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
     const int E1 = a.E + a.S;
     const int r = wave / kRdParts, part = wave % kRdParts;
@@ -1016,23 +1092,42 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
             return err;
         if (dbg.exact_logits && (err = launch_router_exact(L, ws, x, T, false, stream)) != hipSuccess) return err;
     } else if (route_decode_fused(L, T)) {
-        // decode: one launch; it also writes the decode slot list
+        // decode: one launch; it also writes the decode slot list and, when the
+        // fused gate/up runs next, computes the shared expert's h on idle CUs
         ta.dslots = ws.dslots;
         const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
         const int nslab = L.H / kRdSlab;
-        const dim3 g(nb), b(64 * kTopkTokensPerBlock);
-        const size_t lds = sizeof(RouteDecodeLds);  // above the 64 KiB default window: raise it
-        if (nslab <= kRdParts) {
-            if ((err = hipFuncSetAttribute((const void*)k_route_decode<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)lds)) != hipSuccess)
-                return err;
-            hipLaunchKernelGGL(k_route_decode<1>, g, b, lds, stream, ta, ws.logits, ws.xq_qs, ws.xq_ds, ws.sync);
-        } else {
-            if ((err = hipFuncSetAttribute((const void*)k_route_decode<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)lds)) != hipSuccess)
-                return err;
-            hipLaunchKernelGGL(k_route_decode<2>, g, b, lds, stream, ta, ws.logits, ws.xq_qs, ws.xq_ds, ws.sync);
+        SharedGuArgs sg{};
+        if (L.S && gateup_q_fused(L, T)) {
+            const int nfb = L.F / 32;
+            const int groups = std::max(1, std::min(T, (L.n_cu - nb) / nfb));
+            sg.tpg = (T + groups - 1) / groups;
+            sg.n_blocks = nfb * ((T + sg.tpg - 1) / sg.tpg);
+            sg.w_gate = L.w_sh_gate; sg.w_up = L.w_sh_up;
+            sg.gate_nb1 = L.sh_gate_nb1; sg.up_nb1 = L.sh_up_nb1;
+            sg.F = L.F;
+            sg.hq_qs = ws.hq_qs; sg.hq_ds = ws.hq_ds;
         }
+        const dim3 g(nb + sg.n_blocks), b(64 * kTopkTokensPerBlock);
+        const size_t lds = sizeof(RouteDecodeLds);  // above the 64 KiB default window: raise it
+        const int lpr = L.H <= 1024 ? 16 : (L.H <= 2048 ? 32 : 64);
+        const void* kern;
+        if (nslab <= kRdParts) {
+            if (!sg.n_blocks) kern = (const void*)k_route_decode<1, 0, 32>;
+            else if (L.gu_type == kTypeQ4_0) kern = lpr == 16 ? (const void*)k_route_decode<1, kTypeQ4_0, 16>
+                                                              : (const void*)k_route_decode<1, kTypeQ4_0, 32>;
+            else kern = lpr == 16 ? (const void*)k_route_decode<1, kTypeQ8_0, 16>
+                                  : (const void*)k_route_decode<1, kTypeQ8_0, 32>;
+        } else {
+            if (!sg.n_blocks) kern = (const void*)k_route_decode<2, 0, 64>;
+            else kern = L.gu_type == kTypeQ4_0 ? (const void*)k_route_decode<2, kTypeQ4_0, 64>
+                                               : (const void*)k_route_decode<2, kTypeQ8_0, 64>;
+        }
+        if ((err = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
+            return err;
+        int32_t* sync = ws.sync;
+        void* args[] = {&ta, (void*)&ws.logits, (void*)&ws.xq_qs, (void*)&ws.xq_ds, &sync, &sg};
+        if ((err = hipLaunchKernel(kern, g, b, args, lds, stream)) != hipSuccess) return err;
         return hipGetLastError();
     } else {
         if ((err = launch_router_exact(L, ws, x, T, true, stream)) != hipSuccess) return err;
