@@ -265,24 +265,32 @@ __global__ __launch_bounds__(256) void k_quant_h(ExpertArgs a) {
 // G1+Q at decode sizes: gate/up, SwiGLU and the Q8_0 quantization of h of the
 // routed experts in one launch (the decode routing launch does the shared
 // expert's).  Block = (slot v of the decode slot list, 32 consecutive ffn rows:
-// one Q8_0 block of h per token row); 8 waves of 4 rows of gate and of up.
+// one Q8_0 block of h per token row); NW waves of 32/NW rows of gate and of up.
 // The block stages its slot's token rows (Q8_0 of x) in LDS -- loads issued
 // before the weight loads, so they land first -- computes g and u for every
 // row into LDS, then one lane per value does h = silu(g)*u and 32 lanes
 // quantize a row's block: the same operations as k_quant_h, so the same bits.
 // ---------------------------------------------------------------------------
-constexpr int kGqWaves = 8;  // waves per block
-constexpr int kGqRpw = 4;    // ffn rows per wave: kGqWaves * kGqRpw = 32
+
+#ifndef GQ_Q4_WAVES
+#define GQ_Q4_WAVES 8
+#endif
+#ifndef GQ_MIN_WAVES
+#define GQ_MIN_WAVES 1
+#endif
+template <int WT> constexpr int kGqWaves = GQ_Q4_WAVES;  // waves per block (rows per wave: 32 / waves)
+template <> constexpr int kGqWaves<kTypeQ8_0> = 8;
 
 __host__ __device__ constexpr size_t gq_lds_bytes(int T, int H) { return (size_t)T * H + (size_t)T * (H / 32) * 8; }
 
-template <int WT, int LPR>
-__global__ __launch_bounds__(kGqWaves * 64) void k_gateup_q(ExpertArgs a, const int4* dslots) {
+template <int WT, int LPR, int NW>
+__global__ __launch_bounds__(NW * 64, GQ_MIN_WAVES) void k_gateup_q(ExpertArgs a, const int4* dslots) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
-    constexpr int NI = kGqRpw / RPI;
-    constexpr int NT = kGqWaves * 64;
-    static_assert(NI >= 1 && NI * RPI == kGqRpw, "rows per wave");
+    constexpr int RPW = 32 / NW;  // ffn rows per wave
+    constexpr int NI = RPW / RPI;
+    constexpr int NT = NW * 64;
+    static_assert(NI >= 1 && NI * RPI == RPW, "rows per wave");
     extern __shared__ __align__(16) uint8_t s_dyn[];
     __shared__ float2 s_gu[kTopkTokensPerBlock][32];
     const int nfb = a.F >> 5;
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(kGqWaves * 64) void k_gateup_q(ExpertArgs a, const 
     const uint8_t* ub = sh ? a.w_sh_up : a.w_up + (uint64_t)e * a.up_nb2;
     const uint64_t gnb1 = sh ? a.sh_gate_nb1 : a.gate_nb1;
     const uint64_t unb1 = sh ? a.sh_up_nb1 : a.up_nb1;
-    const int fw = fb * 32 + wave * kGqRpw;
+    const int fw = fb * 32 + wave * RPW;
     WPair<WT> wg[NI], wu[NI];
 #pragma unroll
     for (int m = 0; m < NI; ++m) {
@@ -356,18 +364,32 @@ __global__ __launch_bounds__(kGqWaves * 64) void k_gateup_q(ExpertArgs a, const 
                 asm volatile("" : "+v"(wu[m].w[k]));
             }
         }
-        XPair x;
-        x.load(lq + (size_t)c * a.H, ld + (size_t)c * (a.H >> 5), pair);
+        // activations stream through 4 registers, one 16-byte chunk at a time,
+        // re-read from LDS for each row group so its weights die after use
+        const u32x4* xq = (const u32x4*)(lq + (size_t)c * a.H + 64 * pair);
+        const u32x4 xd = *(const u32x4*)(ld + (size_t)c * (a.H >> 5) + 2 * pair);  // {dA, sumA, dB, sumB}
+        const int za = -WPair<WT>::kZero * (int)xd.y, zb = -WPair<WT>::kZero * (int)xd.w;
+        const float dxa = __builtin_bit_cast(float, (uint32_t)xd.x), dxb = __builtin_bit_cast(float, (uint32_t)xd.z);
 #pragma unroll
         for (int m = 0; m < NI; ++m) {
-            const double g = dpp_sum_f64<LPR>(live ? pair_dot<WT>(wg[m], x) : 0.0);
-            const double u = dpp_sum_f64<LPR>(live ? pair_dot<WT>(wu[m], x) : 0.0);
-            if (lp == LPR - 1) s_gu[c][wave * kGqRpw + m * RPI + sub] = make_float2((float)g, (float)u);
+            u32x4 xc = xq[0];
+            int ga = wg[m].template dot_chunk<0>(xc, za), ua = wu[m].template dot_chunk<0>(xc, za);
+            xc = xq[1];
+            ga = wg[m].template dot_chunk<1>(xc, ga); ua = wu[m].template dot_chunk<1>(xc, ua);
+            xc = xq[2];
+            int gb = wg[m].template dot_chunk<2>(xc, zb), ub = wu[m].template dot_chunk<2>(xc, zb);
+            xc = xq[3];
+            gb = wg[m].template dot_chunk<3>(xc, gb); ub = wu[m].template dot_chunk<3>(xc, ub);
+            const double pg = __builtin_fma((double)(wg[m].dA() * dxa), (double)ga, (double)(wg[m].dB() * dxb) * (double)gb);
+            const double pu = __builtin_fma((double)(wu[m].dA() * dxa), (double)ua, (double)(wu[m].dB() * dxb) * (double)ub);
+            const double g = dpp_sum_f64<LPR>(live ? pg : 0.0);
+            const double u = dpp_sum_f64<LPR>(live ? pu : 0.0);
+            if (lp == LPR - 1) s_gu[c][wave * RPW + m * RPI + sub] = make_float2((float)g, (float)u);
         }
     }
     __syncthreads();
-    if (tid < nrows * 32) {  // whole 32-lane groups: row c = tid / 32, value fl
-        const int c = tid >> 5, fl = tid & 31;
+    for (int i = tid; i < nrows * 32; i += NT) {  // whole 32-lane groups: row c = i / 32, value fl
+        const int c = i >> 5, fl = i & 31;
         const float2 gu = s_gu[c][fl];
         const int p = p0 + c;
         swiglu_q8_block32(gu.x, gu.y, fl, a.hq_qs + (uint64_t)p * a.F + fb * 32, a.hq_ds + (uint64_t)p * nfb + fb);
@@ -809,11 +831,12 @@ template <int WT>
 static hipError_t launch_gateup_q_t(const ExpertArgs& a, const int4* dslots, int max_v, hipStream_t stream,
                                     hipEvent_t e0, hipEvent_t e1) {
     const int npairs = a.H / 64;
-    const dim3 g(max_v * (a.F / 32)), b(kGqWaves * 64);
+    const dim3 g(max_v * (a.F / 32));
     const size_t lds = gq_lds_bytes(a.T, a.H);
-    if (npairs <= 16) launch_timed(k_gateup_q<WT, 16>, g, b, lds, stream, e0, e1, a, dslots);
-    else if (npairs <= 32) launch_timed(k_gateup_q<WT, 32>, g, b, lds, stream, e0, e1, a, dslots);
-    else launch_timed(k_gateup_q<WT, 64>, g, b, lds, stream, e0, e1, a, dslots);
+    constexpr int NW = kGqWaves<WT>;
+    if (npairs <= 16) launch_timed(k_gateup_q<WT, 16, NW>, g, dim3(NW * 64), lds, stream, e0, e1, a, dslots);
+    else if (npairs <= 32) launch_timed(k_gateup_q<WT, 32, NW>, g, dim3(NW * 64), lds, stream, e0, e1, a, dslots);
+    else launch_timed(k_gateup_q<WT, 64, 8>, g, dim3(512), lds, stream, e0, e1, a, dslots);
     return hipGetLastError();
 }
 

@@ -316,6 +316,22 @@ template <> struct WPair<kTypeQ4_0> {
         }
         return acc;
     }
+    // The same dots split by 16-byte chunk c of the pair's 64 activation quants
+    // (chunks 0, 1: block A; 2, 3: block B), for callers that stream the
+    // activations through a few registers.  dot_chunk<0>(..., -8*sumA) then
+    // dot_chunk<1> equals dotA; <2> and <3> likewise dotB.
+    template <int C>
+    __device__ __forceinline__ int dot_chunk(u32x4 x, int acc) const {
+        const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = C < 2 ? __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2) : w[5 + i];
+            const uint32_t n = (C & 1) ? (q >> 4) & 0x0f0f0f0fu : q & 0x0f0f0f0fu;
+            acc = __builtin_amdgcn_sdot4((int)n, (int)xv[i], acc, false);
+        }
+        return acc;
+    }
+    static constexpr int kZero = 8;  // quant offset: value = q - 8
 };
 
 template <> struct WPair<kTypeQ8_0> {
@@ -354,6 +370,17 @@ template <> struct WPair<kTypeQ8_0> {
         for (int i = 0; i < 8; ++i) acc = __builtin_amdgcn_sdot4((int)w[9 + i], (int)xs[i], acc, false);
         return acc;
     }
+    template <int C>
+    __device__ __forceinline__ int dot_chunk(u32x4 x, int acc) const {
+        const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = C < 2 ? __builtin_amdgcn_alignbyte(w[4 * C + i + 1], w[4 * C + i], 2) : w[9 + 4 * (C - 2) + i];
+            acc = __builtin_amdgcn_sdot4((int)q, (int)xv[i], acc, false);
+        }
+        return acc;
+    }
+    static constexpr int kZero = 0;
 };
 
 // Activation pair in the workspace layout: qs[64] int8 + {dA, sumA, dB, sumB}.
