@@ -291,10 +291,17 @@ def main() -> int:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
     if not mfma_path:
-        gu_bytes = (D_prof + 1) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * F * 8
+        if T <= 16:
+            # k_gateup_q: routed experts' gate+up rows, the token rows of x (Q8_0), h written as
+            # Q8_0 (the shared expert's gate/up runs inside the routing launch)
+            gu_bytes = D_prof * 2 * F * rb_h + T * (H + H // 32 * 8) + T * K * (F + F // 32 * 8)
+            gu_kernel = "k_gateup_q (routed gate+up expert GEMV with SwiGLU and Q8_0 of h, one Q8_0 block per workgroup)"
+        else:
+            gu_bytes = (D_prof + 1) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * F * 8
+            gu_kernel = "k_gateup_stream (gate+up expert GEMV, prefetching persistent waves)"
         achieved = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {
-            "bound": "hbm", "kernel": "k_gateup_stream (gate+up expert GEMV, prefetching persistent waves)",
+            "bound": "hbm", "kernel": gu_kernel,
             "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic, "bytes_per_launch": gu_bytes, "avg_launch_us": gu_us,
         }

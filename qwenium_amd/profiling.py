@@ -3,6 +3,9 @@
     python -m qwenium_amd.profiling stats <prefix>_kernel_stats.csv
         per-kernel calls / average / total duration as a markdown table
 
+    python -m qwenium_amd.profiling medians <prefix>_kernel_trace.csv [--prefix qmoe::]
+        per-dispatch median / mean duration, VGPRs and grid of the matching kernels
+
     python -m qwenium_amd.profiling counters <prefix>_counter_collection.csv [--kernel SUBSTR]
         per-kernel mean of every collected counter (one dispatch = one sample)
 
@@ -37,6 +40,25 @@ def kernel_stats(path: str) -> str:
         out.append("| `%s` | %s | %.2f | %.2f | %.2f | %.1f | %.2f |" % (
             r["Name"][:110], r["Calls"], float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3,
             float(r["MaxNs"]) / 1e3, float(r["TotalDurationNs"]) / 1e3, float(r["Percentage"])))
+    return "\n".join(out)
+
+
+def dispatch_medians(path: str, prefix: str = "qmoe::") -> str:
+    """Markdown table of per-dispatch durations of kernels whose name contains `prefix`."""
+    durs = defaultdict(list)
+    info = {}
+    for r in _rows(path):
+        name = r["Kernel_Name"]
+        if prefix not in name:
+            continue
+        durs[name].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        info[name] = (r.get("Workgroup_Size_X"), r.get("Grid_Size_X"))
+    out = ["| kernel | dispatches | median us | mean us | workgroup | grid (threads, last dispatch) |",
+           "|---|---:|---:|---:|---:|---:|"]
+    for name, d in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
+        d = sorted(d)
+        wg, g = info[name]
+        out.append("| `%s` | %d | %.2f | %.2f | %s | %s |" % (name[:110], len(d), d[len(d) // 2], sum(d) / len(d), wg, g))
     return "\n".join(out)
 
 
@@ -107,6 +129,9 @@ def main(argv=None) -> int:
     sub = ap.add_subparsers(dest="cmd", required=True)
     s = sub.add_parser("stats")
     s.add_argument("csv")
+    m = sub.add_parser("medians")
+    m.add_argument("csv")
+    m.add_argument("--prefix", default="qmoe::")
     c = sub.add_parser("counters")
     c.add_argument("csv")
     c.add_argument("--kernel", default=None)
@@ -120,6 +145,8 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.cmd == "stats":
         print(kernel_stats(a.csv))
+    elif a.cmd == "medians":
+        print(dispatch_medians(a.csv, a.prefix))
     elif a.cmd == "counters":
         means = counter_means(a.csv, a.kernel)
         names = sorted({c for m in means.values() for c in m})
