@@ -163,6 +163,53 @@ int qmoe_synth_f32(float* dst, int64_t n, uint64_t seed, uint64_t stream,
 int qmoe_synth_quant(void* dst, int32_t type, int64_t n_rows, int64_t row_len,
                      uint64_t seed, uint64_t stream, double sigma, void* hip_stream);
 
+/* ---------------------------------------------------------------------------
+ * GGUF ingestion: replaces GGUFLoader (src/loader/gguf_loader.cpp) for the
+ * tensors of the MoE path.  The file is memory-mapped; tensor bytes are copied
+ * unchanged, since the GGUF block layout is the layer's input layout.
+ * ------------------------------------------------------------------------- */
+typedef struct qmoe_gguf qmoe_gguf;
+
+/* One inventory entry (gguf_loader.cpp:474-497): ggml type id, shape (ggml ne
+ * order, unused dims 1), absolute file offset of its data (data start aligned
+ * as at gguf_loader.cpp:84-85 + the entry's offset) and byte size
+ * (type size * elements / block size, gguf_loader.cpp:213). */
+typedef struct qmoe_gguf_tensor {
+    int32_t  type;
+    int32_t  n_dims;
+    int64_t  ne[4];
+    uint64_t file_offset;
+    uint64_t nbytes;
+} qmoe_gguf_tensor;
+
+/* Replaces GGUFLoader::load_model (gguf_loader.cpp:46-91): maps `path`, checks
+ * the magic ("GGUF") and version (2 or 3), parses the key/value metadata (arrays
+ * are skipped, as the reference does for every key it does not consume) and the
+ * tensor inventory.  Errors name what was expected and what was found. */
+int qmoe_gguf_open(const char* path, qmoe_gguf** out);
+void qmoe_gguf_close(qmoe_gguf* gguf);
+/* Header facts: version, inventory size, metadata size, data start offset. */
+int qmoe_gguf_info(const qmoe_gguf* gguf, uint32_t* version, int64_t* n_tensors, int64_t* n_kv,
+                   uint64_t* data_offset);
+/* Scalar metadata (the raw_kv lookups of the model recipes, e.g.
+ * "qwen35moe.expert_count", qwen36.cpp:23-25).  The key must hold that type. */
+int qmoe_gguf_get_u32(const qmoe_gguf* gguf, const char* key, uint32_t* out);
+int qmoe_gguf_get_f32(const qmoe_gguf* gguf, const char* key, float* out);
+/* *out points into the handle; valid until qmoe_gguf_close. */
+int qmoe_gguf_get_str(const qmoe_gguf* gguf, const char* key, const char** out);
+/* Inventory order access and lookup by name (GGUFLoader::get_tensor_metadata). */
+int qmoe_gguf_tensor_name(const qmoe_gguf* gguf, int64_t index, const char** out);
+int qmoe_gguf_find(const qmoe_gguf* gguf, const char* name, qmoe_gguf_tensor* out);
+/* Replaces get_tensor_data + ggml_backend_tensor_set (gguf_loader.cpp:621-639):
+ * copies the tensor's bytes to host memory / to device memory (stream-ordered,
+ * returns once the file mapping has been read).  dst must hold nbytes. */
+int qmoe_gguf_read(const qmoe_gguf* gguf, const char* name, void* dst, uint64_t dst_bytes);
+int qmoe_gguf_upload(const qmoe_gguf* gguf, const char* name, void* dst_device, uint64_t dst_bytes,
+                     void* hip_stream);
+/* The contiguous ggml view of an uploaded tensor: data = device_data, nb from
+ * the type's block geometry (nb[0] = block bytes, nb[1] = row bytes, ...). */
+int qmoe_gguf_tensor_view(const qmoe_gguf_tensor* t, const void* device_data, qmoe_tensor* out);
+
 #ifdef __cplusplus
 }
 #endif

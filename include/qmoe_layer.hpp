@@ -7,6 +7,7 @@
 // ggml nodes; forward() here enqueues the layer on a HIP stream instead.
 #pragma once
 
+#include <cstdint>
 #include <stdexcept>
 #include <string>
 
@@ -60,6 +61,50 @@ public:
 private:
     Hparams hp_;
     qmoe_layer* layer_ = nullptr;
+};
+
+// GGUF ingestion (replaces GGUFLoader, src/loader/gguf_loader.cpp): failures
+// throw std::runtime_error with the loader's message, as GGUFLoadError does.
+class GGUF {
+public:
+    explicit GGUF(const std::string& path) { check(qmoe_gguf_open(path.c_str(), &g_)); }
+    ~GGUF() { qmoe_gguf_close(g_); }
+    GGUF(const GGUF&) = delete;
+    GGUF& operator=(const GGUF&) = delete;
+
+    uint32_t get_u32(const std::string& key) const {
+        uint32_t v = 0;
+        check(qmoe_gguf_get_u32(g_, key.c_str(), &v));
+        return v;
+    }
+    float get_f32(const std::string& key) const {
+        float v = 0.0f;
+        check(qmoe_gguf_get_f32(g_, key.c_str(), &v));
+        return v;
+    }
+    std::string get_str(const std::string& key) const {
+        const char* v = nullptr;
+        check(qmoe_gguf_get_str(g_, key.c_str(), &v));
+        return v;
+    }
+    qmoe_gguf_tensor find(const std::string& name) const {
+        qmoe_gguf_tensor t{};
+        check(qmoe_gguf_find(g_, name.c_str(), &t));
+        return t;
+    }
+    // Copies tensor `name` into device memory `dst` (at least find(name).nbytes)
+    // and returns its ggml view there.
+    qmoe_tensor upload(const std::string& name, void* dst, uint64_t dst_bytes, void* stream = nullptr) const {
+        const qmoe_gguf_tensor t = find(name);
+        check(qmoe_gguf_upload(g_, name.c_str(), dst, dst_bytes, stream));
+        qmoe_tensor v{};
+        check(qmoe_gguf_tensor_view(&t, dst, &v));
+        return v;
+    }
+    const qmoe_gguf* handle() const { return g_; }
+
+private:
+    qmoe_gguf* g_ = nullptr;
 };
 
 // A contiguous ggml-style view (ne[0] fastest) of device data.

@@ -38,6 +38,17 @@ EXPORTED = (
     "qmoe_rms_norm",
     "qmoe_synth_f32",
     "qmoe_synth_quant",
+    "qmoe_gguf_open",
+    "qmoe_gguf_close",
+    "qmoe_gguf_info",
+    "qmoe_gguf_get_u32",
+    "qmoe_gguf_get_f32",
+    "qmoe_gguf_get_str",
+    "qmoe_gguf_tensor_name",
+    "qmoe_gguf_find",
+    "qmoe_gguf_read",
+    "qmoe_gguf_upload",
+    "qmoe_gguf_tensor_view",
 )
 
 
@@ -70,6 +81,16 @@ class QmoeDebug(ctypes.Structure):
         ("rows", ctypes.c_void_p),
         ("router_approx", ctypes.c_void_p),
         ("router_bound", ctypes.c_void_p),
+    ]
+
+
+class QmoeGgufTensor(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_int32),
+        ("n_dims", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("file_offset", ctypes.c_uint64),
+        ("nbytes", ctypes.c_uint64),
     ]
 
 
@@ -122,6 +143,29 @@ def lib() -> ctypes.CDLL:
     L.qmoe_synth_quant.restype = ctypes.c_int
     L.qmoe_synth_quant.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64,
                                    ctypes.c_uint64, ctypes.c_double, vp]
+    cp = ctypes.c_char_p
+    L.qmoe_gguf_open.restype = ctypes.c_int
+    L.qmoe_gguf_open.argtypes = [cp, P(vp)]
+    L.qmoe_gguf_close.restype = None
+    L.qmoe_gguf_close.argtypes = [vp]
+    L.qmoe_gguf_info.restype = ctypes.c_int
+    L.qmoe_gguf_info.argtypes = [vp, P(ctypes.c_uint32), P(ctypes.c_int64), P(ctypes.c_int64), P(ctypes.c_uint64)]
+    L.qmoe_gguf_get_u32.restype = ctypes.c_int
+    L.qmoe_gguf_get_u32.argtypes = [vp, cp, P(ctypes.c_uint32)]
+    L.qmoe_gguf_get_f32.restype = ctypes.c_int
+    L.qmoe_gguf_get_f32.argtypes = [vp, cp, P(ctypes.c_float)]
+    L.qmoe_gguf_get_str.restype = ctypes.c_int
+    L.qmoe_gguf_get_str.argtypes = [vp, cp, P(cp)]
+    L.qmoe_gguf_tensor_name.restype = ctypes.c_int
+    L.qmoe_gguf_tensor_name.argtypes = [vp, ctypes.c_int64, P(cp)]
+    L.qmoe_gguf_find.restype = ctypes.c_int
+    L.qmoe_gguf_find.argtypes = [vp, cp, P(QmoeGgufTensor)]
+    L.qmoe_gguf_read.restype = ctypes.c_int
+    L.qmoe_gguf_read.argtypes = [vp, cp, vp, ctypes.c_uint64]
+    L.qmoe_gguf_upload.restype = ctypes.c_int
+    L.qmoe_gguf_upload.argtypes = [vp, cp, vp, ctypes.c_uint64, vp]
+    L.qmoe_gguf_tensor_view.restype = ctypes.c_int
+    L.qmoe_gguf_tensor_view.argtypes = [P(QmoeGgufTensor), vp, P(QmoeTensor)]
     _lib = L
     return L
 

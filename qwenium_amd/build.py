@@ -23,6 +23,7 @@ SOURCES = [
     "expert_mfma_kernels.hip",
     "misc_kernels.hip",
     "qmoe_api.cpp",
+    "gguf.cpp",
 ]
 ARCH = os.environ.get("QMOE_OFFLOAD_ARCH", "gfx950")
 

@@ -111,6 +111,11 @@ int hip_fail(hipError_t err, const char* what) {
 
 namespace qmoe {
 
+// Error reporting for the other host sources of the library (same thread-local text).
+void clear_error() { g_last_error.clear(); }
+int set_error(int code, const std::string& msg) { return fail(code, msg); }
+int hip_error(hipError_t err, const char* what) { return hip_fail(err, what); }
+
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Carves the workspace buffers out of `base` (when non-null) and returns the byte size.

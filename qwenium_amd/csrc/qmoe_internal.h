@@ -3,6 +3,8 @@
 
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
+
+#include <string>
 #include <stdint.h>
 
 namespace qmoe {
@@ -85,6 +87,11 @@ inline void launch_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_
     else
         hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
 }
+
+// Error reporting shared by the host sources (qmoe_last_error() text, status code).
+void clear_error();
+int set_error(int code, const std::string& msg);
+int hip_error(hipError_t err, const char* what);
 
 // --- launchers (each enqueues on `stream`, returns hipError_t of the launch) ---
 // Routing: logits, top-k + softmax + shared gate, counting sort.  Large T

@@ -18,6 +18,8 @@
 #include <string>
 #include <vector>
 
+#include <unistd.h>
+
 #include "qmoe_layer.hpp"
 
 static int g_failures = 0;
@@ -186,10 +188,55 @@ static void ConstructorThrowsWithoutSharedWeights() {
     EXPECT(!threw, "valid layer constructs");
 }
 
+// GGUF ingestion through the C++ wrapper (no GPU): a hand-built v3 file with
+// the architecture string, one u32 hparam and one Q8_0 tensor [64, 2].
+static void GGUFLoaderReadsBlockTensors() {
+    std::vector<uint8_t> b;
+    auto put = [&](const void* p, size_t n) { b.insert(b.end(), (const uint8_t*)p, (const uint8_t*)p + n); };
+    auto u32 = [&](uint32_t v) { put(&v, 4); };
+    auto u64 = [&](uint64_t v) { put(&v, 8); };
+    auto str = [&](const std::string& s) { u64(s.size()); put(s.data(), s.size()); };
+    u32(0x46554747u); u32(3); u64(1); u64(2);
+    str("general.architecture"); u32(8); str("qwen35moe");
+    str("qwen35moe.expert_count"); u32(4); u32(256);
+    str("blk.0.ffn_down_exps.weight"); u32(2); u64(64); u64(2); u32(QMOE_TYPE_Q8_0); u64(0);
+    const size_t data_start = (b.size() + 31) / 32 * 32;
+    b.resize(data_start, 0);
+    std::vector<uint8_t> data(2 * 2 * 34);
+    for (size_t i = 0; i < data.size(); ++i) data[i] = (uint8_t)(i * 7 + 3);
+    put(data.data(), data.size());
+    const std::string path = "/tmp/qmoe_cpp_test_" + std::to_string((long long)getpid()) + ".gguf";
+    FILE* f = std::fopen(path.c_str(), "wb");
+    EXPECT(f != nullptr, "temp file");
+    if (!f) return;
+    std::fwrite(b.data(), 1, b.size(), f);
+    std::fclose(f);
+    {
+        qmoe::GGUF g(path);
+        EXPECT(g.get_str("general.architecture") == "qwen35moe", "architecture");
+        EXPECT(g.get_u32("qwen35moe.expert_count") == 256, "expert_count");
+        const qmoe_gguf_tensor t = g.find("blk.0.ffn_down_exps.weight");
+        EXPECT(t.type == QMOE_TYPE_Q8_0 && t.n_dims == 2 && t.ne[0] == 64 && t.ne[1] == 2, "inventory entry");
+        EXPECT(t.file_offset == data_start && t.nbytes == data.size(), "data offset and size");
+        std::vector<uint8_t> got(t.nbytes);
+        qmoe::check(qmoe_gguf_read(g.handle(), "blk.0.ffn_down_exps.weight", got.data(), got.size()));
+        EXPECT(got == data, "tensor bytes");
+        bool threw = false;
+        try {
+            g.find("blk.0.ffn_up_exps.weight");
+        } catch (const std::runtime_error& e) {
+            threw = std::string(e.what()).find("expected present, got absent") != std::string::npos;
+        }
+        EXPECT(threw, "missing tensor throws");
+    }
+    std::remove(path.c_str());
+}
+
 int main(int argc, char** argv) {
     const bool host_only = argc > 1 && std::string(argv[1]) == "--host-only";
     struct Case { const char* name; void (*fn)(); bool gpu; } cases[] = {
         {"ConstructorThrowsWithoutSharedWeights", ConstructorThrowsWithoutSharedWeights, false},
+        {"GGUFLoaderReadsBlockTensors", GGUFLoaderReadsBlockTensors, false},
         {"BuildSucceedsNoSharedExpert", BuildSucceedsNoSharedExpert, true},
         {"BuildSucceedsWithSharedExpert", BuildSucceedsWithSharedExpert, true},
         {"OutputIsFinite", OutputIsFinite, true},
