@@ -168,9 +168,9 @@ def main() -> int:
         for l in range(L):
             if keep is not None and l in keep:
                 keep[l] = cur.clone()
-            rms_norm(cur, norms[l], synthetic.NORM_EPS, out=hbuf)
             nxt = xbuf[l & 1]
-            layers[l].forward(hbuf, out=nxt, workspace=ws, residual=cur)
+            # the block's slice in one call: nxt = cur + MoE(RMSNorm(cur) * w_l)
+            layers[l].forward_norm(cur, norms[l], synthetic.NORM_EPS, out=nxt, workspace=ws)
             cur = nxt
         return cur
 

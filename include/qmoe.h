@@ -145,6 +145,16 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
 #define QMOE_N_PHASE_EVENTS 5
 int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events);
 
+/* The caller slice of the reference's block (qwen36.cpp:297-304 and 427-432)
+ * in one call: y = x + MoE(RMSNorm(x) * norm_w), RMSNorm as qmoe_rms_norm.
+ * At decode sizes the routing launch normalizes x while staging it and the
+ * residual add is the combine epilogue (no separate [T][H] passes); otherwise
+ * the workspace holds the normalized x.  Bits equal qmoe_rms_norm followed by
+ * qmoe_layer_forward(residual = x).  No counterpart as one call in the
+ * reference; for callers that own the whole block. */
+int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* norm_w,
+                            float eps, int32_t n_tokens, float* y, const qmoe_debug* dbg, void* hip_stream);
+
 /* Replaces build_rms_norm (norm.cpp:15-26): y = x / sqrt(mean(x^2) + eps) * w,
  * per token (ggml_rms_norm followed by ggml_mul).  w may be NULL (no scale). */
 int qmoe_rms_norm(const float* x, const float* w, int32_t n_tokens, int32_t n_embd,

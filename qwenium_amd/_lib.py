@@ -34,6 +34,7 @@ EXPORTED = (
     "qmoe_workspace_capacity",
     "qmoe_workspace_check",
     "qmoe_layer_forward",
+    "qmoe_layer_forward_norm",
     "qmoe_layer_set_phase_events",
     "qmoe_rms_norm",
     "qmoe_synth_f32",
@@ -133,6 +134,8 @@ def lib() -> ctypes.CDLL:
     L.qmoe_workspace_check.argtypes = [vp, ctypes.POINTER(ctypes.c_int32)]
     L.qmoe_layer_forward.restype = ctypes.c_int
     L.qmoe_layer_forward.argtypes = [vp, vp, vp, ctypes.c_int32, vp, vp, P(QmoeDebug), vp]
+    L.qmoe_layer_forward_norm.restype = ctypes.c_int
+    L.qmoe_layer_forward_norm.argtypes = [vp, vp, vp, vp, ctypes.c_float, ctypes.c_int32, vp, P(QmoeDebug), vp]
     L.qmoe_layer_set_phase_events.restype = ctypes.c_int
     L.qmoe_layer_set_phase_events.argtypes = [vp, P(vp)]
     L.qmoe_rms_norm.restype = ctypes.c_int

@@ -157,6 +157,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.hq_qs = (int8_t*)take(R * F);
     ws.hq_ds = (float2*)take(R * (F / 32) * sizeof(float2));
     ws.ybuf = (float*)take(R * H * sizeof(float));
+    ws.xn = (float*)take((size_t)T * H * sizeof(float));
     ws.max_tiles = max_tiles;
     ws.cap_T = T; ws.H = H; ws.E = E; ws.K = K; ws.F = F;
     ws.base = base;
@@ -345,8 +346,10 @@ int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault) {
     return QMOE_OK;
 }
 
-int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, int32_t n_tokens, float* y,
-                       const float* residual, const qmoe_debug* dbg, void* hip_stream) {
+// y = MoE(x) + residual, or with norm_w: y = x + MoE(RMSNorm(x) * norm_w).
+static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const float* x, int32_t n_tokens, float* y,
+                        const float* residual, const float* norm_w, float norm_eps, const qmoe_debug* dbg,
+                        void* hip_stream) {
     g_last_error.clear();
     if (!layer) return fail(QMOE_ERR_NULL, "qmoe: layer expected non-null, got null");
     if (n_tokens < 0)
@@ -355,8 +358,9 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
     if (!x) return fail(QMOE_ERR_NULL, "qmoe: x expected a device pointer, got null");
     if (!y) return fail(QMOE_ERR_NULL, "qmoe: y expected a device pointer, got null");
     if (x == y) return fail(QMOE_ERR_VALUE, "qmoe: y expected a buffer distinct from x, got x");
-    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)residual & 15u))
-        return fail(QMOE_ERR_VALUE, "qmoe: x/y/residual expected 16-byte aligned device pointers, got a misaligned one");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)residual & 15u) || ((uintptr_t)norm_w & 15u))
+        return fail(QMOE_ERR_VALUE,
+                    "qmoe: x/y/residual/norm_w expected 16-byte aligned device pointers, got a misaligned one");
     const LayerDesc& d = layer->d;
     if (!ws) {
         if (!layer->own_ws || layer->own_ws->w.cap_T < n_tokens) {
@@ -392,7 +396,18 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
         rdbg.approx = dbg->router_approx;
         rdbg.bound = dbg->router_bound;
     }
-    if (err == hipSuccess) err = qmoe::launch_route(d, v, x, n_tokens, rdbg, stream);
+    const float* xin = x;  // the layer's (normalized) input
+    const float* route_norm = nullptr;
+    if (norm_w) {
+        residual = x;
+        if (qmoe::route_decode_fused(d, n_tokens)) {
+            route_norm = norm_w;  // the decode routing normalizes while it stages x
+        } else {
+            if (err == hipSuccess) err = qmoe::launch_rms_norm(x, norm_w, n_tokens, d.H, norm_eps, v.xn, stream);
+            xin = v.xn;
+        }
+    }
+    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, n_tokens, rdbg, stream, route_norm, norm_eps);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
     const bool mfma = n_tokens >= d.mfma_min_tokens;
     // events [1] and [2] are taken by the gate/up launch itself (its own start and end)
@@ -444,6 +459,19 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
         }
     }
     return QMOE_OK;
+}
+
+int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, int32_t n_tokens, float* y,
+                       const float* residual, const qmoe_debug* dbg, void* hip_stream) {
+    return forward_impl(layer, ws, x, n_tokens, y, residual, nullptr, 0.0f, dbg, hip_stream);
+}
+
+int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* norm_w, float eps,
+                            int32_t n_tokens, float* y, const qmoe_debug* dbg, void* hip_stream) {
+    g_last_error.clear();
+    if (!norm_w) return fail(QMOE_ERR_NULL, "qmoe: norm_w expected a device pointer, got null");
+    if (!(eps >= 0.0f)) return fail(QMOE_ERR_VALUE, "qmoe: eps expected >= 0, got " + std::to_string(eps));
+    return forward_impl(layer, ws, x, n_tokens, y, nullptr, norm_w, eps, dbg, hip_stream);
 }
 
 int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events) {

@@ -154,6 +154,22 @@ class MoELayer:
             return y, dbg_tensors
         return y
 
+    def forward_norm(self, x: torch.Tensor, norm_weight: torch.Tensor, eps: float, *,
+                     out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None, stream=None):
+        """The block's caller slice in one call (qwen36.cpp:297-304):
+        y = x + MoE(RMSNorm(x) * norm_weight).  Same bits as
+        forward(rms_norm(x, norm_weight, eps), residual=x)."""
+        if x.dim() != 2 or x.shape[1] != self.n_embd or x.dtype != torch.float32 or not x.is_cuda:
+            raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got "
+                             f"{tuple(x.shape)} {x.dtype} on {x.device}")
+        x = x.contiguous()
+        w = norm_weight.contiguous()
+        y = out if out is not None else torch.empty_like(x)
+        check(lib().qmoe_layer_forward_norm(
+            self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), w.data_ptr(),
+            float(eps), int(x.shape[0]), y.data_ptr(), None, _stream_ptr(stream)))
+        return y
+
     __call__ = forward
 
 

@@ -380,8 +380,9 @@ def test_skewed_q8_0_t2048(gpu):
 
 
 def test_stack_40_layers_t10(gpu):
-    """40 consecutive blocks x <- x + MoE_l(RMSNorm(x) * w_l) at decode batch 10; layers 0
-    and 39 checked against the oracle on their actual inputs."""
+    """40 consecutive blocks x <- x + MoE_l(RMSNorm(x) * w_l) at decode batch 10 through the
+    fused-norm call; layers 0 and 39 checked against the oracle on their actual inputs (and
+    against the unfused rms_norm + forward)."""
     from qwenium_amd import Workspace, rms_norm
 
     spec = synthetic.QWEN35B
@@ -396,13 +397,15 @@ def test_stack_40_layers_t10(gpu):
         if ws is None:
             ws = Workspace(layer, T)
         wn = synthetic.make_norm_weight(spec, seed, l)
-        rms_norm(x, wn, synthetic.NORM_EPS, out=h)
         if l in (0, L - 1):
+            rms_norm(x, wn, synthetic.NORM_EPS, out=h)
             y, dbg = layer.forward(h, workspace=ws, residual=x, debug=True)
+            y_fused = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws)
             torch.cuda.synchronize()
+            assert torch.equal(y, y_fused), f"layer {l}: fused RMSNorm path"
             keep[l] = (x.cpu().numpy(), wn.cpu().numpy(), t, y.cpu().numpy(), dbg["topk_idx"].cpu().numpy())
         else:
-            y = layer.forward(h, workspace=ws, residual=x)
+            y = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws)
         x = y
         del t, layer
     torch.cuda.synchronize()
@@ -437,3 +440,25 @@ def test_fused_decode_routing_repeated(gpu, n_experts, T):
         got = {k: v.cpu().numpy() for k, v in dbg.items()}
         assert_parity(y.cpu().numpy(), got, y_ref, d_ref, spec, min_identical=1.0)
     assert ws.check() == 0
+
+
+@pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 300),
+                                     ("config1", 5), ("config1", 32), ("h4096", 10)])
+def test_forward_norm_matches_unfused(gpu, which, T):
+    """y = x + MoE(RMSNorm(x) * w) in one call (the decode routing normalizes while it
+    stages x; other sizes normalize into the workspace) gives the bits of rms_norm
+    followed by forward(residual=x)."""
+    from qwenium_amd import Workspace, rms_norm
+
+    spec = {"35b": synthetic.QWEN35B, "config1": synthetic.CONFIG1,
+            "h4096": synthetic.LayerSpec(4096, 16, 2, 64, True, synthetic.TYPE_Q4_0)}[which]
+    seed = 21
+    layer = synthetic.make_layer(spec, seed)
+    ws = Workspace(layer, T)
+    x = synthetic.make_x(spec, T, seed, batch=T)
+    wn = synthetic.make_norm_weight(spec, seed, 0)
+    y_fused = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws)
+    y_ref = layer.forward(rms_norm(x, wn, synthetic.NORM_EPS), residual=x, workspace=ws)
+    torch.cuda.synchronize()
+    assert ws.check() == 0
+    assert torch.equal(y_fused, y_ref)
