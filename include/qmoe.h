@@ -147,9 +147,8 @@ int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events);
 
 /* The caller slice of the reference's block (qwen36.cpp:297-304 and 427-432)
  * in one call: y = x + MoE(RMSNorm(x) * norm_w), RMSNorm as qmoe_rms_norm.
- * At decode sizes the routing launch normalizes x while staging it and the
- * residual add is the combine epilogue (no separate [T][H] passes); otherwise
- * the workspace holds the normalized x.  Bits equal qmoe_rms_norm followed by
+ * The normalized rows live in the workspace and the residual add is the
+ * combine epilogue.  Bits equal qmoe_rms_norm followed by
  * qmoe_layer_forward(residual = x).  No counterpart as one call in the
  * reference; for callers that own the whole block. */
 int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* norm_w,

@@ -11,6 +11,41 @@ namespace qmoe {
 // mean rounded to f32, scale = 1/sqrtf(mean + eps), y = (x*scale)*w.
 // One block per token.
 // ---------------------------------------------------------------------------
+// Values of the token row held in registers (NV = ceil(H/256) per thread): every
+// load in flight at once and x read once.  Same per-thread summation order as
+// k_rms_norm below (thread i adds x[i], x[i+256], ... in turn), so the same bits.
+template <int NV>
+__global__ __launch_bounds__(256) void k_rms_norm_reg(const float* x, const float* w, int H, float eps, float* y) {
+#pragma clang fp contract(off)
+    __shared__ double s_part[4];
+    const int t = blockIdx.x;
+    const float* xr = x + (uint64_t)t * H;
+    float v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        v[k] = i < H ? xr[i] : 0.0f;
+    }
+    double acc = 0.0;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+        if ((int)threadIdx.x + 256 * k < H) acc += (double)(v[k] * v[k]);
+    acc = group_sum_f64<64>(acc);
+    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const double sum = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    const float mean = (float)(sum / (double)H);
+    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < H) {
+            const float u = v[k] * scale;
+            y[(uint64_t)t * H + i] = w ? u * w[i] : u;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void k_rms_norm(const float* x, const float* w, int H, float eps, float* y) {
 #pragma clang fp contract(off)
     __shared__ double s_part[4];
@@ -34,7 +69,11 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* x, const float* w
 }
 
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream) {
-    hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
+    const int nv = (H + 255) / 256;
+    if (nv <= 4) hipLaunchKernelGGL(k_rms_norm_reg<4>, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
+    else if (nv <= 8) hipLaunchKernelGGL(k_rms_norm_reg<8>, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
+    else if (nv <= 16) hipLaunchKernelGGL(k_rms_norm_reg<16>, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
+    else hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
     return hipGetLastError();
 }
 

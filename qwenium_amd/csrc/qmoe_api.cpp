@@ -397,17 +397,13 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const float* x, i
         rdbg.bound = dbg->router_bound;
     }
     const float* xin = x;  // the layer's (normalized) input
-    const float* route_norm = nullptr;
     if (norm_w) {
+        // the normalized rows go to the workspace; the residual add is the combine epilogue
         residual = x;
-        if (qmoe::route_decode_fused(d, n_tokens)) {
-            route_norm = norm_w;  // the decode routing normalizes while it stages x
-        } else {
-            if (err == hipSuccess) err = qmoe::launch_rms_norm(x, norm_w, n_tokens, d.H, norm_eps, v.xn, stream);
-            xin = v.xn;
-        }
+        if (err == hipSuccess) err = qmoe::launch_rms_norm(x, norm_w, n_tokens, d.H, norm_eps, v.xn, stream);
+        xin = v.xn;
     }
-    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, n_tokens, rdbg, stream, route_norm, norm_eps);
+    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, n_tokens, rdbg, stream);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
     const bool mfma = n_tokens >= d.mfma_min_tokens;
     // events [1] and [2] are taken by the gate/up launch itself (its own start and end)

@@ -106,11 +106,8 @@ struct RouteDebug {
 bool route_uses_mfma(const LayerDesc& L, int T);
 // One-launch decode routing (T <= 16); it also writes ws.dslots.
 bool route_decode_fused(const LayerDesc& L, int T);
-// norm_w (decode routing only): x is the un-normalized input and the routing
-// applies the pre-MoE RMSNorm (x * scale) * norm_w itself, bit-identical to
-// launch_rms_norm's output.
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, const RouteDebug& dbg,
-                        hipStream_t stream, const float* norm_w = nullptr, float norm_eps = 0.0f);
+                        hipStream_t stream);
 // ev_start / ev_stop (optional): events recorded at the kernel's own start and
 // end (profiling of the dominant kernel without marker overhead).
 hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,

@@ -87,11 +87,8 @@ __device__ __forceinline__ void router_row(const RouterArgs& a, int e, float* s_
 
 // Q8_0 quantization of one token row (one wave; lane b handles 32-value
 // blocks b, b+64, ...): d = fp16(amax/127), q = rint(x * 127/amax), and the
-// block's quant sum for the Q4_0 offset term.  With a norm weight nw the row is
-// RMSNorm(x) * nw = (x * scale) * nw first (the values k_rms_norm writes).
-__device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, int8_t* qs, float2* ds,
-                                            const float* nw = nullptr, float scale = 1.0f) {
-#pragma clang fp contract(off)
+// block's quant sum for the Q4_0 offset term.
+__device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, int8_t* qs, float2* ds) {
     const int nb = H >> 5;
     for (int b = lane; b < nb; b += 64) {
         const f32x4* src = (const f32x4*)(xr + 32 * b);
@@ -100,17 +97,6 @@ __device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, in
         for (int i = 0; i < 8; ++i) {
             const f32x4 q = src[i];
             v[4 * i + 0] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
-        }
-        if (nw) {
-            const f32x4* wsrc = (const f32x4*)(nw + 32 * b);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const f32x4 w = wsrc[i];
-                v[4 * i + 0] = (v[4 * i + 0] * scale) * w.x;
-                v[4 * i + 1] = (v[4 * i + 1] * scale) * w.y;
-                v[4 * i + 2] = (v[4 * i + 2] * scale) * w.z;
-                v[4 * i + 3] = (v[4 * i + 3] * scale) * w.w;
-            }
         }
         float amax = 0.0f;
 #pragma unroll
@@ -139,47 +125,8 @@ __device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, in
 }
 
 __device__ __forceinline__ void quant_token_row(const float* x, int H, int t, int lane, int8_t* xq_qs,
-                                                float2* xq_ds, const float* nw = nullptr, float scale = 1.0f) {
-    quant_x_row(x + (uint64_t)t * H, H, lane, xq_qs + (uint64_t)t * H, xq_ds + (uint64_t)t * (H >> 5), nw, scale);
-}
-
-// RMSNorm scales 1/sqrt(mean(x^2) + eps) of tokens [t0, t0 + nt), nt <= 16, in a
-// block of 1024 threads, with k_rms_norm's summation order exactly: token tt is
-// summed by 256 threads (group tt % 4, round tt / 4), thread i adding x[i],
-// x[i+256], ... in f64, then 64-lane group sums and (w0 + w1) + (w2 + w3) -- so
-// the scales equal k_rms_norm's bit for bit.  All rounds' loads go out together.
-__device__ __forceinline__ void rms_scales_1024(const float* x, int H, float eps, int t0, int nt,
-                                                double (*s_part)[16], float* s_scale) {
-#pragma clang fp contract(off)
-    const int tid = threadIdx.x, grp = tid >> 8, lt = tid & 255;
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    const int ni = H >> 8;
-    for (int i = 0; i < ni; ++i) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tt = r * 4 + grp;
-            if (tt < nt) {
-                const float v = x[(uint64_t)(t0 + tt) * H + lt + 256 * i];
-                acc[r] += (double)(v * v);
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const double sum = group_sum_f64<64>(acc[r]);
-        if ((tid & 63) == 0) s_part[r][tid >> 6] = sum;
-    }
-    __syncthreads();
-    if (lt < 4) {
-        const int tt = lt * 4 + grp;
-        if (tt < nt) {
-            const double* q = &s_part[lt][grp * 4];
-            const double sum = (q[0] + q[1]) + (q[2] + q[3]);
-            const float mean = (float)(sum / (double)H);
-            s_scale[tt] = 1.0f / __builtin_sqrtf(mean + eps);
-        }
-    }
-    __syncthreads();
+                                                float2* xq_ds) {
+    quant_x_row(x + (uint64_t)t * H, H, lane, xq_qs + (uint64_t)t * H, xq_ds + (uint64_t)t * (H >> 5));
 }
 
 // Blocks [0, n_router_blocks) compute router rows; any further blocks
@@ -368,8 +315,6 @@ struct TopkArgs {
     int32_t* expert_slot; // [E]
     int4* slot_info;      // [E+1] {expert, first row, rows, token of first row}
     int4* dslots;         // [E+2] decode slot list (fused decode routing only, else null)
-    const float* norm_w;  // decode routing only: pre-MoE RMSNorm weight [H] applied to x (null: none)
-    float norm_eps;
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
@@ -818,8 +763,7 @@ struct SharedGuArgs {
 };
 
 template <int WT, int LPR>
-__device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const SharedGuArgs& sg, int j, uint8_t* s_dyn,
-                                                    double (*s_norm_part)[16], float* s_scale) {
+__device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const SharedGuArgs& sg, int j, uint8_t* s_dyn) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
     constexpr int RPW = RPI > 2 ? RPI : 2;  // ffn rows per wave
@@ -844,9 +788,8 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
     int8_t* lq = (int8_t*)s_dyn;                              // [tpg][H] quants
     float2* ld = (float2*)(lq + (size_t)sg.tpg * a.H);        // [tpg][H/32] {d, sum}
     float2* lgu = ld + (size_t)sg.tpg * (a.H >> 5);           // [tpg][32] (g, u)
-    if (a.norm_w) rms_scales_1024(a.x, a.H, a.norm_eps, t0, nt, s_norm_part, s_scale);
     if (wave < nt) quant_x_row(a.x + (uint64_t)(t0 + wave) * a.H, a.H, lane, lq + (size_t)wave * a.H,
-                               ld + (size_t)wave * (a.H >> 5), a.norm_w, a.norm_w ? s_scale[wave] : 1.0f);
+                               ld + (size_t)wave * (a.H >> 5));
     __syncthreads();
     if (wave < NWA) {
         for (int c = 0; c < nt; ++c) {
@@ -875,13 +818,11 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     extern __shared__ __align__(16) uint8_t s_dyn[];
     RouteDecodeLds& S = *(RouteDecodeLds*)s_dyn;
     __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
-    __shared__ double s_norm_part[4][16];
-    __shared__ float s_scale[kTopkTokensPerBlock];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nb = gridDim.x - sg.n_blocks;  // router blocks
     if constexpr (SWT != 0) {
         if ((int)blockIdx.x >= nb) {
-            shared_gateup_block<SWT, SLPR>(a, sg, blockIdx.x - nb, s_dyn, s_norm_part, s_scale);
+            shared_gateup_block<SWT, SLPR>(a, sg, blockIdx.x - nb, s_dyn);
             return;
         }
     }
@@ -899,9 +840,6 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     double acc[kTopkTokensPerBlock];
 #pragma unroll
     for (int t = 0; t < kTopkTokensPerBlock; ++t) acc[t] = 0.0;
-    // fused pre-MoE RMSNorm: every block computes the T scales (k_rms_norm's order)
-    // and stages (x * scale) * w
-    if (a.norm_w) rms_scales_1024(a.x, a.H, a.norm_eps, 0, a.T, s_norm_part, s_scale);
     // chunk = as many slabs as fit: T * chunk * 4 bytes <= kRdXBytes
     const int cslabs = max(1, min(nslab, kRdXBytes / (a.T * kRdSlab * 4)));
     const int ccols = cslabs * kRdSlab;
@@ -916,11 +854,6 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
             const int i = tid + 1024 * j;
             const int t = min(i / q4, a.T - 1), q = i % q4;
             v[j] = *(const f32x4*)(a.x + (uint64_t)t * a.H + s0 * kRdSlab + 4 * q);
-            if (a.norm_w) {
-                const f32x4 wv = *(const f32x4*)(a.norm_w + s0 * kRdSlab + 4 * q);
-                const float c = s_scale[t];
-                v[j] = f32x4{(v[j].x * c) * wv.x, (v[j].y * c) * wv.y, (v[j].z * c) * wv.z, (v[j].w * c) * wv.w};
-            }
         }
 #pragma unroll
         for (int j = 0; j < kStagePerThread; ++j) {
@@ -969,8 +902,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     }
     // activation quantization: token t by block t % nb, wave (t / nb) % 16
     for (int t = blockIdx.x; t < a.T; t += nb)
-        if (wave == (t / nb) % 16)
-            quant_token_row(a.x, a.H, t, lane, xq_qs, xq_ds, a.norm_w, a.norm_w ? s_scale[t] : 1.0f);
+        if (wave == (t / nb) % 16) quant_token_row(a.x, a.H, t, lane, xq_qs, xq_ds);
     // each wave's write-through logit stores complete before the block's flag (a
     // release fence would write back the whole L2 once per wave)
     __builtin_amdgcn_s_waitcnt(0);
@@ -1108,11 +1040,8 @@ static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, c
 }
 
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, const RouteDebug& dbg,
-                        hipStream_t stream, const float* norm_w, float norm_eps) {
-    if (norm_w && !route_decode_fused(L, T)) return hipErrorInvalidValue;  // callers normalize first
+                        hipStream_t stream) {
     TopkArgs ta;
-    ta.norm_w = norm_w;
-    ta.norm_eps = norm_eps;
     ta.logits = ws.logits;
     ta.logit_bound = ws.logit_bound;
     ta.x = x;
