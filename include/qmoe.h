@@ -145,6 +145,45 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
 #define QMOE_N_PHASE_EVENTS 5
 int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events);
 
+/* ---------------------------------------------------------------------------
+ * Expert-dispatch telemetry (SURVEY-ranked "next" item; no counterpart wired
+ * into the reference's forward pass).
+ * ------------------------------------------------------------------------- */
+/* Optional device histogram: while set, every forward of `layer` adds its
+ * per-expert dispatch counts (the routing's count sort; T*top_k in total) to
+ * device_counts[n_experts] (u64, zeroed by the caller), stream-ordered, no host
+ * sync.  NULL stops it. */
+int qmoe_layer_set_expert_counts(qmoe_layer* layer, uint64_t* device_counts);
+
+/* Replaces MoEMetrics (src/telemetry/metrics.h:13-17). */
+typedef struct qmoe_moe_metrics {
+    uint64_t cold_dispatch_count;  /* dispatches to an expert outside the resident set */
+} qmoe_moe_metrics;
+
+/* Replaces MoEResidencyTracker (src/layers/moe_residency.{h,cpp}): per-expert
+ * dispatch frequencies, the resident set (top resident_k experts by frequency,
+ * frequency > 0, descending; equal frequencies ordered as the reference's
+ * std::partial_sort over ascending ids orders them) and the cold counter
+ * (incremented when the dispatched expert was not resident at dispatch time).
+ * resident_k is clamped to n_experts; n_experts <= 0, resident_k <= 0 and ids
+ * outside [0, n_experts) fail with the reference's messages.  Host-only. */
+typedef struct qmoe_residency qmoe_residency;
+int qmoe_residency_create(int32_t n_experts, int32_t resident_k, qmoe_residency** out);
+void qmoe_residency_destroy(qmoe_residency* tracker);
+/* record_dispatch for each id in turn (e.g. a forward's topk_idx, token-major). */
+int qmoe_residency_record(qmoe_residency* tracker, const int32_t* expert_ids, int64_t n);
+/* One batch from a dispatch histogram (counts[n_experts], e.g. copied from the
+ * qmoe_layer_set_expert_counts buffer): the batch is cold by the resident set
+ * at its start, then the set is refreshed once.  No counterpart in the
+ * reference; for single-dispatch batches it equals qmoe_residency_record. */
+int qmoe_residency_record_counts(qmoe_residency* tracker, const uint64_t* counts, int32_t n);
+int qmoe_residency_is_resident(const qmoe_residency* tracker, int32_t expert_id);
+int qmoe_residency_metrics(const qmoe_residency* tracker, qmoe_moe_metrics* out);
+/* Writes up to cap ids of the resident set (descending frequency); returns its size. */
+int32_t qmoe_residency_resident_set(const qmoe_residency* tracker, int32_t* out, int32_t cap);
+int qmoe_residency_frequencies(const qmoe_residency* tracker, uint64_t* out, int32_t cap);
+void qmoe_residency_reset(qmoe_residency* tracker);
+
 /* The caller slice of the reference's block (qwen36.cpp:297-304 and 427-432)
  * in one call: y = x + MoE(RMSNorm(x) * norm_w), RMSNorm as qmoe_rms_norm.
  * The normalized rows live in the workspace and the residual add is the

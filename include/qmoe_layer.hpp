@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "qmoe.h"
 
@@ -47,6 +48,9 @@ public:
     MoELayer& operator=(const MoELayer&) = delete;
 
     int n_embd() const { return qmoe_layer_n_embd(layer_); }
+    // Device histogram u64[n_experts] that every later forward adds its
+    // per-expert dispatch counts to (nullptr stops it).
+    void set_expert_counts(uint64_t* device_counts) { check(qmoe_layer_set_expert_counts(layer_, device_counts)); }
     const Hparams& hparams() const { return hp_; }
     qmoe_layer* handle() const { return layer_; }
 
@@ -105,6 +109,57 @@ public:
 
 private:
     qmoe_gguf* g_ = nullptr;
+};
+
+// MoE expert-dispatch telemetry (replaces MoEResidencyTracker,
+// src/layers/moe_residency.h:35-69, and MoEMetrics, src/telemetry/metrics.h:15-17):
+// the same methods and the same std::runtime_error messages.
+struct MoEMetrics {
+    uint64_t cold_dispatch_count = 0;
+};
+
+class MoEResidencyTracker {
+public:
+    MoEResidencyTracker(int n_experts, int resident_k) : n_(n_experts) {
+        check(qmoe_residency_create(n_experts, resident_k, &r_));
+        freq_.resize((size_t)n_experts);
+    }
+    ~MoEResidencyTracker() { qmoe_residency_destroy(r_); }
+    MoEResidencyTracker(const MoEResidencyTracker&) = delete;
+    MoEResidencyTracker& operator=(const MoEResidencyTracker&) = delete;
+
+    void record_dispatch(int expert_id) {
+        const int32_t id = expert_id;
+        check(qmoe_residency_record(r_, &id, 1));
+    }
+    // n dispatches in order (e.g. a forward's top-k ids, token-major).
+    void record_dispatches(const int32_t* expert_ids, int64_t n) { check(qmoe_residency_record(r_, expert_ids, n)); }
+    // One batch from a per-expert dispatch histogram (n_experts counts).
+    void record_counts(const uint64_t* counts) { check(qmoe_residency_record_counts(r_, counts, n_)); }
+    bool is_resident(int expert_id) const { return qmoe_residency_is_resident(r_, expert_id) != 0; }
+    uint64_t cold_dispatch_count() const { return snapshot_metrics().cold_dispatch_count; }
+    MoEMetrics snapshot_metrics() const {
+        qmoe_moe_metrics m{};
+        check(qmoe_residency_metrics(r_, &m));
+        return MoEMetrics{m.cold_dispatch_count};
+    }
+    const std::vector<int>& resident_set() const {
+        resident_.resize((size_t)n_);
+        const int32_t k = qmoe_residency_resident_set(r_, resident_.data(), n_);
+        resident_.resize((size_t)k);
+        return resident_;
+    }
+    const std::vector<uint64_t>& frequencies() const {
+        check(qmoe_residency_frequencies(r_, freq_.data(), n_));
+        return freq_;
+    }
+    void reset() { qmoe_residency_reset(r_); }
+
+private:
+    int n_;
+    qmoe_residency* r_ = nullptr;
+    mutable std::vector<int> resident_;
+    mutable std::vector<uint64_t> freq_;
 };
 
 // A contiguous ggml-style view (ne[0] fastest) of device data.

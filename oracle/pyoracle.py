@@ -18,9 +18,17 @@ LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
 TYPE_F32, TYPE_Q4_0, TYPE_Q8_0 = 0, 2, 8
 
 
+REFERENCE_DIR = "/root/reference"
+
+
 def build() -> str:
-    """Compiles liboracle.so with oracle/Makefile (gcc; no GPU involved)."""
+    """Compiles liboracle.so with oracle/Makefile (gcc; no GPU involved) and,
+    where the reference tree is present, oracle/_ref/libresidency_ref.so from
+    the reference's own MoEResidencyTracker source."""
     subprocess.run(["make", "-s", "-C", ORACLE_DIR, "-B", "CC=gcc", "liboracle.so"], check=True)
+    if os.path.exists(os.path.join(REFERENCE_DIR, "src", "layers", "moe_residency.cpp")):
+        subprocess.run(["make", "-s", "-C", ORACLE_DIR, "-B", "CXX=g++", f"REF={REFERENCE_DIR}",
+                        "_ref/libresidency_ref.so"], check=True)
     return LIB_PATH
 
 

@@ -50,6 +50,16 @@ EXPORTED = (
     "qmoe_gguf_read",
     "qmoe_gguf_upload",
     "qmoe_gguf_tensor_view",
+    "qmoe_layer_set_expert_counts",
+    "qmoe_residency_create",
+    "qmoe_residency_destroy",
+    "qmoe_residency_record",
+    "qmoe_residency_record_counts",
+    "qmoe_residency_is_resident",
+    "qmoe_residency_metrics",
+    "qmoe_residency_resident_set",
+    "qmoe_residency_frequencies",
+    "qmoe_residency_reset",
 )
 
 
@@ -93,6 +103,10 @@ class QmoeGgufTensor(ctypes.Structure):
         ("file_offset", ctypes.c_uint64),
         ("nbytes", ctypes.c_uint64),
     ]
+
+
+class QmoeMoeMetrics(ctypes.Structure):
+    _fields_ = [("cold_dispatch_count", ctypes.c_uint64)]
 
 
 class QmoeError(RuntimeError):
@@ -169,6 +183,26 @@ def lib() -> ctypes.CDLL:
     L.qmoe_gguf_upload.argtypes = [vp, cp, vp, ctypes.c_uint64, vp]
     L.qmoe_gguf_tensor_view.restype = ctypes.c_int
     L.qmoe_gguf_tensor_view.argtypes = [P(QmoeGgufTensor), vp, P(QmoeTensor)]
+    L.qmoe_layer_set_expert_counts.restype = ctypes.c_int
+    L.qmoe_layer_set_expert_counts.argtypes = [vp, vp]
+    L.qmoe_residency_create.restype = ctypes.c_int
+    L.qmoe_residency_create.argtypes = [ctypes.c_int32, ctypes.c_int32, P(vp)]
+    L.qmoe_residency_destroy.restype = None
+    L.qmoe_residency_destroy.argtypes = [vp]
+    L.qmoe_residency_record.restype = ctypes.c_int
+    L.qmoe_residency_record.argtypes = [vp, P(ctypes.c_int32), ctypes.c_int64]
+    L.qmoe_residency_record_counts.restype = ctypes.c_int
+    L.qmoe_residency_record_counts.argtypes = [vp, P(ctypes.c_uint64), ctypes.c_int32]
+    L.qmoe_residency_is_resident.restype = ctypes.c_int
+    L.qmoe_residency_is_resident.argtypes = [vp, ctypes.c_int32]
+    L.qmoe_residency_metrics.restype = ctypes.c_int
+    L.qmoe_residency_metrics.argtypes = [vp, P(QmoeMoeMetrics)]
+    L.qmoe_residency_resident_set.restype = ctypes.c_int32
+    L.qmoe_residency_resident_set.argtypes = [vp, P(ctypes.c_int32), ctypes.c_int32]
+    L.qmoe_residency_frequencies.restype = ctypes.c_int
+    L.qmoe_residency_frequencies.argtypes = [vp, P(ctypes.c_uint64), ctypes.c_int32]
+    L.qmoe_residency_reset.restype = None
+    L.qmoe_residency_reset.argtypes = [vp]
     _lib = L
     return L
 

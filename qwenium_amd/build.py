@@ -24,6 +24,7 @@ SOURCES = [
     "misc_kernels.hip",
     "qmoe_api.cpp",
     "gguf.cpp",
+    "residency.cpp",
 ]
 ARCH = os.environ.get("QMOE_OFFLOAD_ARCH", "gfx950")
 

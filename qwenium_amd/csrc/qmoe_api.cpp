@@ -470,6 +470,15 @@ int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* 
     return forward_impl(layer, ws, x, n_tokens, y, nullptr, norm_w, eps, dbg, hip_stream);
 }
 
+int qmoe_layer_set_expert_counts(qmoe_layer* layer, uint64_t* device_counts) {
+    g_last_error.clear();
+    if (!layer) return fail(QMOE_ERR_NULL, "qmoe: layer expected non-null, got null");
+    if ((uintptr_t)device_counts & 7u)
+        return fail(QMOE_ERR_VALUE, "qmoe: device_counts expected 8-byte aligned, got a misaligned pointer");
+    layer->d.expert_counts = (unsigned long long*)device_counts;
+    return QMOE_OK;
+}
+
 int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events) {
     g_last_error.clear();
     if (!layer) return fail(QMOE_ERR_NULL, "qmoe: layer expected non-null, got null");

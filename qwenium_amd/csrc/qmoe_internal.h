@@ -40,6 +40,7 @@ struct LayerDesc {
     int mfma_min_tokens = 128;              // token count from which the int8-MFMA path runs
     int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs
     int dc_ahead = 2;                       // decode down+combine: steps with loads in flight (2 or 4)
+    unsigned long long* expert_counts = nullptr;  // optional device [E]: += each forward's per-expert dispatches
 };
 
 // Device scratch.  R = T*K + S*T rows: routed assignments sorted by expert,

@@ -315,6 +315,7 @@ struct TopkArgs {
     int32_t* expert_slot; // [E]
     int4* slot_info;      // [E+1] {expert, first row, rows, token of first row}
     int4* dslots;         // [E+2] decode slot list (fused decode routing only, else null)
+    unsigned long long* expert_counts;  // optional [E]: per-expert dispatch counts accumulated
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
@@ -645,6 +646,7 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
             if (s_off) s_off[e] = off;
             if (act) {
                 const int slot = base_act + inc_act - 1;
+                if (a.expert_counts) atomicAdd(a.expert_counts + e, (unsigned long long)cnt);
                 a.active[slot] = e;
                 a.expert_slot[e] = slot;
                 a.slot_info[slot] = make_int4(e, off, cnt, first_token ? (int)__builtin_ctz(first_token[e]) : 0);
@@ -1062,6 +1064,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     ta.expert_slot = ws.expert_slot;
     ta.slot_info = ws.slot_info;
     ta.dslots = nullptr;
+    ta.expert_counts = L.expert_counts;
     ta.counters = ws.counters;
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;

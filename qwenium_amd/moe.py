@@ -114,6 +114,19 @@ class MoELayer:
         except Exception:
             pass
 
+    def set_expert_counts(self, counts: Optional[torch.Tensor]) -> None:
+        """Attaches a device dispatch histogram: while set, every forward adds
+        its per-expert dispatch counts (T*top_k in total) to `counts`, a cuda
+        int64 [n_experts] tensor (read as u64), on the forward's stream.  None
+        detaches it.  The layer keeps the tensor alive while attached."""
+        if counts is not None:
+            if (counts.dtype != torch.int64 or not counts.is_cuda or counts.dim() != 1
+                    or counts.shape[0] != self.hp.n_experts or not counts.is_contiguous()):
+                raise ValueError(f"counts expected a contiguous cuda int64 [{self.hp.n_experts}] tensor, got "
+                                 f"{tuple(counts.shape)} {counts.dtype} on {counts.device}")
+        check(lib().qmoe_layer_set_expert_counts(self._handle, counts.data_ptr() if counts is not None else None))
+        self._expert_counts = counts
+
     def forward(self, x: torch.Tensor, phase: int = Phase.Prefill, il: int = 0, *,
                 residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                 workspace: Optional[Workspace] = None, debug: bool = False, stream=None):

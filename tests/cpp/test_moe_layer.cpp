@@ -9,6 +9,9 @@
 // logits equal the router column exactly) and checks ids [6,1] and weights
 // 0.7310586 / 0.2689414.
 //
+// The Res* cases restate the reference's MoEResidencyTracker tests
+// (tests/unit/test_moe_residency.cpp:17-182) through the C++ wrapper.
+//
 // Usage: test_moe_layer [--host-only]   (--host-only: checks that need no GPU)
 #include <hip/hip_runtime.h>
 
@@ -232,11 +235,141 @@ static void GGUFLoaderReadsBlockTensors() {
     std::remove(path.c_str());
 }
 
+// ---- MoEResidencyTracker: the reference's cases (tests/unit/test_moe_residency.cpp:17-182) ----
+template <class F>
+static bool throws_runtime(F f, const char* needle) {
+    try {
+        f();
+    } catch (const std::runtime_error& e) {
+        return std::string(e.what()).find(needle) != std::string::npos;
+    }
+    return false;
+}
+
+static void dispatch_n(qmoe::MoEResidencyTracker& t, int id, int n) {
+    for (int i = 0; i < n; ++i) t.record_dispatch(id);
+}
+
+static void ResConstructionSucceeds() {
+    qmoe::MoEResidencyTracker t(8, 3);
+    EXPECT(t.cold_dispatch_count() == 0 && t.resident_set().empty(), "fresh tracker");
+}
+static void ResFrequenciesStartAtZero() {
+    qmoe::MoEResidencyTracker t(4, 2);
+    bool zero = t.frequencies().size() == 4;
+    for (uint64_t f : t.frequencies()) zero = zero && f == 0;
+    EXPECT(zero, "zero frequencies");
+}
+static void ResInvalidNExpertsThrows() {
+    EXPECT(throws_runtime([] { qmoe::MoEResidencyTracker t(0, 1); }, "n_experts must be > 0; got 0"), "n_experts 0");
+}
+static void ResInvalidResidentKThrows() {
+    EXPECT(throws_runtime([] { qmoe::MoEResidencyTracker t(8, 0); }, "resident_k must be > 0; got 0"), "resident_k 0");
+}
+static void ResResidentSetTracksTopKByFrequency() {
+    qmoe::MoEResidencyTracker t(8, 2);
+    dispatch_n(t, 0, 4);
+    dispatch_n(t, 1, 3);
+    dispatch_n(t, 2, 2);
+    dispatch_n(t, 3, 1);
+    EXPECT(t.resident_set().size() == 2, "two resident");
+    EXPECT(t.is_resident(0) && t.is_resident(1) && !t.is_resident(2) && !t.is_resident(3), "experts 0 and 1");
+    EXPECT(t.resident_set()[0] == 0 && t.resident_set()[1] == 1, "descending frequency");
+}
+static void ResResidentSetRespectsClamping() {
+    qmoe::MoEResidencyTracker t(3, 10);
+    for (int e = 0; e < 3; ++e) t.record_dispatch(e);
+    EXPECT(t.resident_set().size() == 3 && t.is_resident(0) && t.is_resident(1) && t.is_resident(2), "k clamped to 3");
+}
+static void ResResidentSetExcludesZeroFrequencyExperts() {
+    qmoe::MoEResidencyTracker t(8, 3);
+    t.record_dispatch(4);
+    EXPECT(t.resident_set().size() == 1 && t.is_resident(4), "only expert 4");
+}
+static void ResColdCounterIncrementsOnNonResidentDispatch() {
+    qmoe::MoEResidencyTracker t(8, 3);
+    dispatch_n(t, 0, 5);
+    dispatch_n(t, 1, 4);
+    dispatch_n(t, 2, 3);
+    EXPECT(t.is_resident(0) && t.is_resident(1) && t.is_resident(2), "0, 1, 2 resident");
+    const uint64_t before = t.cold_dispatch_count();
+    t.record_dispatch(7);
+    EXPECT(t.cold_dispatch_count() == before + 1, "cold +1");
+}
+static void ResColdCounterStaysStableOnResidentDispatch() {
+    qmoe::MoEResidencyTracker t(8, 3);
+    dispatch_n(t, 0, 5);
+    dispatch_n(t, 1, 4);
+    dispatch_n(t, 2, 3);
+    const uint64_t before = t.cold_dispatch_count();
+    t.record_dispatch(0);
+    EXPECT(t.cold_dispatch_count() == before, "cold unchanged");
+}
+static void ResColdCounterEarlyDispatchesAreAllCold() {
+    qmoe::MoEResidencyTracker t(4, 2);
+    t.record_dispatch(0);
+    EXPECT(t.cold_dispatch_count() == 1, "first dispatch cold");
+}
+static void ResSnapshotMetricsMatchesColdCount() {
+    qmoe::MoEResidencyTracker t(8, 3);
+    dispatch_n(t, 0, 5);
+    t.record_dispatch(5);
+    EXPECT(t.snapshot_metrics().cold_dispatch_count == t.cold_dispatch_count(), "snapshot");
+}
+static void ResResetClearsAllState() {
+    qmoe::MoEResidencyTracker t(8, 3);
+    dispatch_n(t, 0, 4);
+    t.record_dispatch(5);
+    t.reset();
+    bool zero = t.cold_dispatch_count() == 0 && t.resident_set().empty();
+    for (uint64_t f : t.frequencies()) zero = zero && f == 0;
+    EXPECT(zero, "reset");
+}
+static void ResResetAllowsReuseFromCleanState() {
+    qmoe::MoEResidencyTracker t(4, 1);
+    t.record_dispatch(0);
+    t.reset();
+    t.record_dispatch(2);
+    EXPECT(t.cold_dispatch_count() == 1 && t.is_resident(2), "clean reuse");
+}
+static void ResOutOfRangeExpertIdThrowsLow() {
+    qmoe::MoEResidencyTracker t(8, 3);
+    EXPECT(throws_runtime([&] { t.record_dispatch(-1); }, "expert_id=-1 out of range [0, 8)"), "id -1");
+}
+static void ResOutOfRangeExpertIdThrowsHigh() {
+    qmoe::MoEResidencyTracker t(8, 3);
+    EXPECT(throws_runtime([&] { t.record_dispatch(8); }, "expert_id=8 out of range [0, 8)"), "id 8");
+}
+static void ResFrequenciesAccumulateCorrectly() {
+    qmoe::MoEResidencyTracker t(4, 2);
+    t.record_dispatch(0);
+    t.record_dispatch(0);
+    t.record_dispatch(1);
+    const std::vector<uint64_t> want{2, 1, 0, 0};
+    EXPECT(t.frequencies() == want, "frequencies");
+}
+
 int main(int argc, char** argv) {
     const bool host_only = argc > 1 && std::string(argv[1]) == "--host-only";
     struct Case { const char* name; void (*fn)(); bool gpu; } cases[] = {
         {"ConstructorThrowsWithoutSharedWeights", ConstructorThrowsWithoutSharedWeights, false},
         {"GGUFLoaderReadsBlockTensors", GGUFLoaderReadsBlockTensors, false},
+        {"ResConstructionSucceeds", ResConstructionSucceeds, false},
+        {"ResFrequenciesStartAtZero", ResFrequenciesStartAtZero, false},
+        {"ResInvalidNExpertsThrows", ResInvalidNExpertsThrows, false},
+        {"ResInvalidResidentKThrows", ResInvalidResidentKThrows, false},
+        {"ResResidentSetTracksTopKByFrequency", ResResidentSetTracksTopKByFrequency, false},
+        {"ResResidentSetRespectsClamping", ResResidentSetRespectsClamping, false},
+        {"ResResidentSetExcludesZeroFrequencyExperts", ResResidentSetExcludesZeroFrequencyExperts, false},
+        {"ResColdCounterIncrementsOnNonResidentDispatch", ResColdCounterIncrementsOnNonResidentDispatch, false},
+        {"ResColdCounterStaysStableOnResidentDispatch", ResColdCounterStaysStableOnResidentDispatch, false},
+        {"ResColdCounterEarlyDispatchesAreAllCold", ResColdCounterEarlyDispatchesAreAllCold, false},
+        {"ResSnapshotMetricsMatchesColdCount", ResSnapshotMetricsMatchesColdCount, false},
+        {"ResResetClearsAllState", ResResetClearsAllState, false},
+        {"ResResetAllowsReuseFromCleanState", ResResetAllowsReuseFromCleanState, false},
+        {"ResOutOfRangeExpertIdThrowsLow", ResOutOfRangeExpertIdThrowsLow, false},
+        {"ResOutOfRangeExpertIdThrowsHigh", ResOutOfRangeExpertIdThrowsHigh, false},
+        {"ResFrequenciesAccumulateCorrectly", ResFrequenciesAccumulateCorrectly, false},
         {"BuildSucceedsNoSharedExpert", BuildSucceedsNoSharedExpert, true},
         {"BuildSucceedsWithSharedExpert", BuildSucceedsWithSharedExpert, true},
         {"OutputIsFinite", OutputIsFinite, true},
