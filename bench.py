@@ -13,6 +13,10 @@ block layout, f32 router N(0,0.02), f32 activations N(0,1)):
                      assignments on 8 hot experts, ~46 experts empty.
   stack              40 consecutive layers, each x <- x + MoE(RMSNorm(x) * w):
                      --tokens 1 / 10 (default) / 64 (decode) or 8192 (prefill).
+  gemma4-decode      Gemma 4 26B-A4B GeGLU MoE layer (hidden 2816, 128 experts,
+  gemma4-prefill     top-8, ffn 704, fused gate_up, no shared expert), 10 / 4096
+                     tokens, Q4_0; a step is build_moe_geglu(expert_in, router_in)
+                     on inputs prepared from the residual rows beforehand.
 
 A step is one layer forward over one batch (stack: one pass over all 40
 layers).  Output: ONE JSON line with value = tokens/s, the roofline of the
@@ -43,6 +47,8 @@ WORKLOADS = {
     "prefill": (4096, "QWEN35B", 4, 2, 64, 8),
     "skewed": (2048, "QWEN35B_SKEW", 4, 2, 64, 8),
     "stack": (10, "QWEN35B", 40, 2, 32, 4),
+    "gemma4-decode": (10, "GEMMA4", 8, 16, 2000, 64),
+    "gemma4-prefill": (4096, "GEMMA4", 4, 2, 64, 8),
 }
 STACK_LAYERS = 40
 
@@ -124,14 +130,14 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the MoE layer on one MI355X); "
-              f"--gpus {args.gpus} is not supported.  Expert-parallel sharding is described in DESIGN.md.",
+              f"--gpus {args.gpus} is not supported: expert-parallel sharding across GPUs is not built.",
               file=sys.stderr, flush=True)
         return 2
 
     import numpy as np
     import torch
 
-    from qwenium_amd import TYPE_Q4_0, Workspace, lib, rms_norm, synthetic
+    from qwenium_amd import TYPE_Q4_0, Workspace, gemma4_moe_inputs, lib, rms_norm, synthetic
     from qwenium_amd._lib import check, row_bytes
 
     T0, spec_name, L0, B0, S0, W0 = WORKLOADS[args.workload]
@@ -156,6 +162,11 @@ def main() -> int:
         if stack:
             norms.append(synthetic.make_norm_weight(spec, args.seed, l, device=dev))
     xs = [synthetic.make_x(spec, T, args.seed, batch=b, device=dev) for b in range(B)]
+    geglu = spec.geglu
+    if geglu:
+        # build_moe_geglu's two inputs per batch (gemma4.cpp:555-563), prepared outside the timed steps
+        g4_norms = synthetic.make_gemma4_norms(spec, args.seed, 0, device=dev)
+        g4_in = [gemma4_moe_inputs(x, *g4_norms, synthetic.NORM_EPS) for x in xs]
     ws = Workspace(layers[0], T)
     y = torch.empty((T, H), dtype=torch.float32, device=dev)
     hbuf = torch.empty((T, H), dtype=torch.float32, device=dev)
@@ -181,12 +192,17 @@ def main() -> int:
         period = int(np.lcm(L, B))
         sched = [(s % L, s % B) for s in range(period)]
 
+    def layer_forward(l, b, **kw):
+        if geglu:
+            return layers[l].forward_routed(g4_in[b][0], g4_in[b][1], out=y, workspace=ws, **kw)
+        return layers[l].forward(xs[b], out=y, workspace=ws, **kw)
+
     def run_step(i):
         l, b = sched[i % period]
         if stack:
             stack_pass(b)
         else:
-            layers[l].forward(xs[b], out=y, workspace=ws)
+            layer_forward(l, b)
 
     # routing statistics: distinct routed experts hit per (layer, batch) forward
     distinct = []
@@ -199,7 +215,7 @@ def main() -> int:
             cur = xbuf[l & 1]
     else:
         for (l, b) in sched:
-            _, dbg = layers[l].forward(xs[b], out=y, workspace=ws, debug=True)
+            _, dbg = layer_forward(l, b, debug=True)
             distinct.append(int(torch.unique(dbg["topk_idx"]).numel()))
     torch.cuda.synchronize()
     D_mean = float(np.mean(distinct))
@@ -214,9 +230,10 @@ def main() -> int:
     rb_h = row_bytes(spec.wtype, H)
     rb_f = row_bytes(spec.wtype, F)
     expert_bytes = 2 * F * rb_h + H * rb_f
-    router_bytes = E * H * 4 + H * 4
-    R = T * K + T
-    layer_bytes = D_mean * expert_bytes + expert_bytes + router_bytes + 2 * T * H * 4
+    S = 1 if spec.shared else 0
+    router_bytes = E * H * 4 + S * H * 4
+    R = T * K + S * T
+    layer_bytes = (D_mean + S) * expert_bytes + router_bytes + (3 if geglu else 2) * T * H * 4
     ops_gu = 2.0 * R * 2 * F * H      # int8 multiply-adds x2, gate + up
     ops_dn = 2.0 * R * H * F
     layer_ops = ops_gu + ops_dn
@@ -272,7 +289,7 @@ def main() -> int:
         l, b = (i % L, 0) if stack else sched[i % period]
         prof_layers.append(l)
         check(lib().qmoe_layer_set_phase_events(layers[l]._handle, pe.arr(i)))
-        layers[l].forward(xs[b], out=y, workspace=ws)
+        layer_forward(l, b)
         check(lib().qmoe_layer_set_phase_events(layers[l]._handle, None))
     torch.cuda.synchronize()
     phase = pe.phases_us(n_prof)
@@ -295,9 +312,10 @@ def main() -> int:
             # k_gateup_q: routed experts' gate+up rows, the token rows of x (Q8_0), h written as
             # Q8_0 (the shared expert's gate/up runs inside the routing launch)
             gu_bytes = D_prof * 2 * F * rb_h + T * (H + H // 32 * 8) + T * K * (F + F // 32 * 8)
-            gu_kernel = "k_gateup_q (routed gate+up expert GEMV with SwiGLU and Q8_0 of h, one Q8_0 block per workgroup)"
+            gu_kernel = (f"k_gateup_q (routed gate+up expert GEMV with {'GeGLU' if geglu else 'SwiGLU'} and Q8_0 of h, "
+                         "one Q8_0 block per workgroup)")
         else:
-            gu_bytes = (D_prof + 1) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * F * 8
+            gu_bytes = (D_prof + S) * 2 * F * rb_h + T * (H + H // 32 * 8) + R * F * 8
             gu_kernel = "k_gateup_stream (gate+up expert GEMV, prefetching persistent waves)"
         achieved = gu_bytes / (gu_us * 1e-6) / 1e9
         roofline = {
@@ -328,6 +346,9 @@ def main() -> int:
         layer_rate["us_per_token"] = ms_per_step * 1e3 / T
     if stack:
         metric = f"MoE-stack tokens/s (40 layers of the 35B-A3B MoE block with RMSNorm, {T} tokens, {wname})"
+    elif geglu:
+        metric = (f"MoE-layer tokens/s at Gemma 4 26B-A4B shape (GeGLU, "
+                  f"{'decode batch' if T <= 64 else 'prefill'} {T}{'' if T <= 64 else ' tokens'}, {wname})")
     elif args.workload == "decode":
         metric = f"MoE-layer tokens/s at 35B-A3B shape (decode batch {T}, {wname})"
     elif args.workload == "skewed":
@@ -344,7 +365,8 @@ def main() -> int:
         def host_layer(l):
             host = {k: v.data.cpu().numpy() for k, v in tensors[l].items()}
             host["router"] = host["router"].reshape(E, H)
-            return po.Layer(H, E, K, F, spec.shared, spec.wtype, host)
+            return po.Layer(H, E, K, F, spec.shared, spec.wtype, host,
+                            act=po.ACT_GELU_TANH if geglu else po.ACT_SILU)
 
         n_chk = min(T, 32)
         checks = []
@@ -361,10 +383,11 @@ def main() -> int:
                 yr, dr = host_layer(l).forward(hh, debug=True)
                 yr = yr + xin.cpu().numpy()[:n_chk]
                 checks.append((l, yl.cpu().numpy()[:n_chk], yr, dbg["topk_idx"].cpu().numpy()[:n_chk], dr["topk_idx"]))
-        else:
-            yl, dbg = layers[0].forward(xs[0], workspace=ws, debug=True)
+        elif geglu:
+            yl, dbg = layers[0].forward_routed(g4_in[0][0], g4_in[0][1], workspace=ws, debug=True)
             torch.cuda.synchronize()
-            yr, dr = host_layer(0).forward(xs[0].cpu().numpy()[:n_chk], debug=True)
+            yr, dr = host_layer(0).forward(g4_in[0][0].cpu().numpy()[:n_chk], debug=True,
+                                           router_in=g4_in[0][1].cpu().numpy()[:n_chk])
             checks.append((0, yl.cpu().numpy()[:n_chk], yr, dbg["topk_idx"].cpu().numpy()[:n_chk], dr["topk_idx"]))
         result_parity = {"tokens_checked": n_chk, "layers_checked": [c[0] for c in checks]}
         for (l, yg, yr, ig, ir) in checks:
@@ -377,12 +400,13 @@ def main() -> int:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         ref = host_layer(0)
         n_cpu_tok = min(T, 10 if T <= 64 else 256)
-        xc = xs[0].cpu().numpy()[:n_cpu_tok]
-        ref.forward(xc, nthreads=threads)  # warm
+        xc = (g4_in[0][0] if geglu else xs[0]).cpu().numpy()[:n_cpu_tok]
+        xrc = g4_in[0][1].cpu().numpy()[:n_cpu_tok] if geglu else None
+        ref.forward(xc, nthreads=threads, router_in=xrc)  # warm
         iters, t_cpu = 0, 0.0
         t_start = time.perf_counter()
         while t_cpu < args.cpu_seconds:
-            ref.forward(xc, nthreads=threads)
+            ref.forward(xc, nthreads=threads, router_in=xrc)
             iters += 1
             t_cpu = time.perf_counter() - t_start
         layer_tok_s = iters * n_cpu_tok / t_cpu
@@ -417,11 +441,13 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": f"{wname.lower()} x q8_0 int8 dot, f64-exact accumulation, f32 activations",
-        "data": "synthetic (seeded, generated on device; random-init weights of the 35B-A3B MoE layer shape)",
+        "data": ("synthetic (seeded, generated on device; random-init weights of the "
+                 f"{'Gemma 4 26B-A4B' if geglu else '35B-A3B'} MoE layer shape)"),
         "config": {
             "workload": (f"{L} x Qwen3.6-35B-A3B MoE block (RMSNorm + MoE + residual), {T} tokens" if stack else
+                         f"Gemma 4 26B-A4B GeGLU MoE layer, {args.workload} {T} tokens" if geglu else
                          f"Qwen3.6-35B-A3B MoE layer, {args.workload} {T} tokens") +
-                        f": hidden {H}, {E} experts, top-{K} + shared, ffn {F}, {wname}",
+                        f": hidden {H}, {E} experts, top-{K}{' + shared' if spec.shared else ''}, ffn {F}, {wname}",
             "tokens": T, "hidden": H, "experts": E, "top_k": K, "ffn": F, "shared_expert": spec.shared,
             "weight_type": wname, "layers": L, "distinct_batches": B,
             "timing": "eager" if args.eager else f"hip graph of {period} steps",

@@ -146,8 +146,8 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
 int qmoe_layer_set_phase_events(qmoe_layer* layer, void* const* events);
 
 /* ---------------------------------------------------------------------------
- * Expert-dispatch telemetry (SURVEY-ranked "next" item; no counterpart wired
- * into the reference's forward pass).
+ * Expert-dispatch telemetry.  The reference's tracker (src/layers/
+ * moe_residency.h) has no caller in its forward pass; here the layer feeds it.
  * ------------------------------------------------------------------------- */
 /* Optional device histogram: while set, every forward of `layer` adds its
  * per-expert dispatch counts (the routing's count sort; T*top_k in total) to
@@ -192,6 +192,46 @@ void qmoe_residency_reset(qmoe_residency* tracker);
  * reference; for callers that own the whole block. */
 int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* norm_w,
                             float eps, int32_t n_tokens, float* y, const qmoe_debug* dbg, void* hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * Gemma 4 GeGLU MoE (replaces Gemma4ForwardPass::build_moe_geglu,
+ * src/models/gemma4.cpp:367-445).  The same router, top-k, softmax, count
+ * sort, grouped expert GEMMs and combine as the Qwen layer, with:
+ *   - gate and up in one tensor ffn_gate_up_exps [n_embd, 2*ffn_dim,
+ *     n_experts] (gate = rows 0..ffn_dim-1, up = the next ffn_dim rows of each
+ *     expert, the views at :403-409), Q4_0 or Q8_0;
+ *   - h = gelu(gate) * up (:423) with ggml's CPU gelu: the tanh form through
+ *     its fp16 table (|g| >= 10 passes g or 0 through);
+ *   - no shared expert (hp->has_shared_expert must be 0);
+ *   - the router reading its own input (:380).
+ * w_router is ffn_gate_inp.weight [n_embd, n_experts] F32; w_down_exps is
+ * ffn_down_exps.weight [ffn_dim, n_embd, n_experts].  The layer is destroyed
+ * with qmoe_layer_destroy; qmoe_layer_forward routes on x itself.
+ * ------------------------------------------------------------------------- */
+int qmoe_geglu_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_gate_up_exps,
+                            const qmoe_tensor* w_down_exps, const qmoe_hparams* hp, qmoe_layer** out);
+
+/* y = MoE(expert_in) with the routing computed from router_in ([n_tokens][n_embd]
+ * each; build_moe_geglu's expert_in / router_in).  Works for every layer; a
+ * shared expert's sigmoid gate also reads router_in. */
+int qmoe_layer_forward_routed(qmoe_layer* layer, qmoe_workspace* ws, const float* expert_in, const float* router_in,
+                              int32_t n_tokens, float* y, const qmoe_debug* dbg, void* hip_stream);
+
+/* The Gemma 4 MoE branch from the residual rows x (gemma4.cpp:555-565):
+ *   expert_in = rms_norm(x) * pre_norm_w            (blk.N.pre_ffw_norm_2)
+ *   router_in = (rms_norm(x) * (1/sqrtf(n_embd))) * router_scale_w  (ffn_gate_inp.scale)
+ *   y = build_moe_geglu(expert_in, router_in)
+ * both inputs from one pass over x, into the workspace.  y is the routed sum
+ * (the caller's post_ffw_norm_2 follows, :566). */
+int qmoe_layer_forward_gemma4(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* pre_norm_w,
+                              const float* router_scale_w, float eps, int32_t n_tokens, float* y,
+                              const qmoe_debug* dbg, void* hip_stream);
+/* The two inputs alone (n_embd <= 4096), into caller buffers. */
+int qmoe_gemma4_moe_inputs(const float* x, const float* pre_norm_w, const float* router_scale_w, float eps,
+                           int32_t n_tokens, int32_t n_embd, float* expert_in, float* router_in, void* hip_stream);
+/* Host: the 65536-entry fp16 gelu table the GeGLU kernels read (entry i =
+ * fp16(gelu(fp16 value i)); the inf and NaN codes map to themselves). */
+int qmoe_gelu_f16_table(uint16_t* out);
 
 /* Replaces build_rms_norm (norm.cpp:15-26): y = x / sqrt(mean(x^2) + eps) * w,
  * per token (ggml_rms_norm followed by ggml_mul).  w may be NULL (no scale). */

@@ -67,6 +67,45 @@ private:
     qmoe_layer* layer_ = nullptr;
 };
 
+// Gemma 4 GeGLU MoE (replaces Gemma4ForwardPass::build_moe_geglu,
+// src/models/gemma4.cpp:367-445): fused gate_up tensor, GeGLU-tanh, no shared
+// expert, the router on its own input.
+class GeGLUMoELayer {
+public:
+    using Hparams = MoELayer::Hparams;
+
+    GeGLUMoELayer(const qmoe_tensor* w_router, const qmoe_tensor* w_gate_up_exps, const qmoe_tensor* w_down_exps,
+                  const Hparams& hp)
+        : hp_(hp) {
+        const qmoe_hparams c{hp.n_experts, hp.top_k, hp.ffn_dim, hp.has_shared_expert ? 1 : 0};
+        check(qmoe_geglu_layer_create(w_router, w_gate_up_exps, w_down_exps, &c, &layer_));
+    }
+    ~GeGLUMoELayer() { qmoe_layer_destroy(layer_); }
+    GeGLUMoELayer(const GeGLUMoELayer&) = delete;
+    GeGLUMoELayer& operator=(const GeGLUMoELayer&) = delete;
+
+    int n_embd() const { return qmoe_layer_n_embd(layer_); }
+    const Hparams& hparams() const { return hp_; }
+    qmoe_layer* handle() const { return layer_; }
+
+    // build_moe_geglu(expert_in, router_in): y[n_tokens][n_embd], device pointers.
+    void forward(const float* expert_in, const float* router_in, int n_tokens, float* y, void* stream = nullptr,
+                 qmoe_workspace* ws = nullptr, const qmoe_debug* dbg = nullptr) {
+        check(qmoe_layer_forward_routed(layer_, ws, expert_in, router_in, n_tokens, y, dbg, stream));
+    }
+    // The MoE branch from the residual rows x (gemma4.cpp:555-565): both inputs
+    // (pre_ffw_norm_2, ffn_gate_inp.scale) prepared in one pass, then the layer.
+    void forward_gemma4(const float* x, const float* pre_norm_w, const float* router_scale_w, float eps, int n_tokens,
+                        float* y, void* stream = nullptr, qmoe_workspace* ws = nullptr,
+                        const qmoe_debug* dbg = nullptr) {
+        check(qmoe_layer_forward_gemma4(layer_, ws, x, pre_norm_w, router_scale_w, eps, n_tokens, y, dbg, stream));
+    }
+
+private:
+    Hparams hp_;
+    qmoe_layer* layer_ = nullptr;
+};
+
 // GGUF ingestion (replaces GGUFLoader, src/loader/gguf_loader.cpp): failures
 // throw std::runtime_error with the loader's message, as GGUFLoadError does.
 class GGUF {

@@ -39,6 +39,7 @@ class QoLayer(ctypes.Structure):
         ("w_router", ctypes.c_void_p), ("w_gate", ctypes.c_void_p), ("w_up", ctypes.c_void_p),
         ("w_down", ctypes.c_void_p), ("w_sh_gate", ctypes.c_void_p), ("w_sh_up", ctypes.c_void_p),
         ("w_sh_down", ctypes.c_void_p), ("w_sh_norm", ctypes.c_void_p),
+        ("act", ctypes.c_int), ("gate_up_fused", ctypes.c_int),
     ]
 
 
@@ -83,7 +84,11 @@ def lib() -> ctypes.CDLL:
         "qo_silu_mul": (f32, [f32, f32]),
         "qo_sigmoid": (f32, [f32]),
         "qo_rms_norm": (None, [vp, vp, i32, i32, f32, vp]),
+        "qo_gelu_f16": (f32, [f32]),
+        "qo_geglu_mul": (f32, [f32, f32]),
+        "qo_gemma4_moe_inputs": (None, [vp, vp, vp, i32, i32, f32, vp, vp]),
         "qo_moe_forward": (i32, [ctypes.POINTER(QoLayer), vp, i32, vp, ctypes.POINTER(QoDebug), i32]),
+        "qo_moe_forward_routed": (i32, [ctypes.POINTER(QoLayer), vp, vp, i32, vp, ctypes.POINTER(QoDebug), i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -165,18 +170,45 @@ def rms_norm(x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
     return y
 
 
+ACT_SILU, ACT_GELU_TANH = 0, 1
+
+
+def gelu_f16(x) -> np.ndarray:
+    """ggml's CPU gelu (fp16 table semantics), elementwise."""
+    x = np.asarray(x, dtype=np.float32)
+    return np.array([lib().qo_gelu_f16(float(v)) for v in x.reshape(-1)], dtype=np.float32).reshape(x.shape)
+
+
+def gemma4_moe_inputs(x: np.ndarray, w_pre: np.ndarray, w_rs: np.ndarray, eps: float):
+    """(expert_in, router_in) of the Gemma 4 MoE branch from the residual rows x."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, H = x.shape
+    ei, ri = np.empty_like(x), np.empty_like(x)
+    lib().qo_gemma4_moe_inputs(_p(x), _p(np.ascontiguousarray(w_pre, np.float32)),
+                               _p(np.ascontiguousarray(w_rs, np.float32)), T, H, eps, _p(ei), _p(ri))
+    return ei, ri
+
+
 class Layer:
-    """Host copy of one MoE layer in GGUF block layout (numpy uint8/float32)."""
+    """Host copy of one MoE layer in GGUF block layout (numpy uint8/float32).
+    act: ACT_SILU (SwiGLU) or ACT_GELU_TANH (GeGLU); with tensors["gate_up"]
+    (E x 2F rows: gate rows then up rows of each expert) instead of gate/up,
+    the fused Gemma 4 layout."""
 
-    def __init__(self, n_embd, n_experts, top_k, ffn_dim, shared, wtype, tensors: dict):
+    def __init__(self, n_embd, n_experts, top_k, ffn_dim, shared, wtype, tensors: dict, act: int = ACT_SILU):
         self.H, self.E, self.K, self.F, self.S, self.wtype = n_embd, n_experts, top_k, ffn_dim, bool(shared), wtype
+        self.act = act
         self.t = {k: np.ascontiguousarray(v) for k, v in tensors.items()}
+        fused = "gate_up" in self.t
+        names = ("router", "gate_up" if fused else "gate", "up", "down", "sh_gate", "sh_up", "sh_down", "sh_norm")
         self._c = QoLayer(n_embd, n_experts, top_k, ffn_dim, 1 if shared else 0, wtype,
-                          *(_p(self.t.get(n)) for n in
-                            ("router", "gate", "up", "down", "sh_gate", "sh_up", "sh_down", "sh_norm")))
+                          *(_p(self.t.get(n)) for n in names), act, 1 if fused else 0)
 
-    def forward(self, x: np.ndarray, nthreads: int = 0, debug: bool = False):
+    def forward(self, x: np.ndarray, nthreads: int = 0, debug: bool = False, router_in: np.ndarray | None = None):
+        """y = MoE(x); the router reads router_in when given (else x)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
+        xr = x if router_in is None else np.ascontiguousarray(router_in, dtype=np.float32)
+        assert xr.shape == x.shape
         T = x.shape[0]
         y = np.empty((T, self.H), dtype=np.float32)
         dbg = None
@@ -192,8 +224,8 @@ class Layer:
             }
             dbg = QoDebug(*(_p(d[n]) for n in
                             ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows", "h", "y", "sh_out")))
-        rc = lib().qo_moe_forward(ctypes.byref(self._c), _p(x), T, _p(y),
-                                  ctypes.byref(dbg) if dbg is not None else None, nthreads)
+        rc = lib().qo_moe_forward_routed(ctypes.byref(self._c), _p(x), _p(xr), T, _p(y),
+                                         ctypes.byref(dbg) if dbg is not None else None, nthreads)
         if rc != 0:
             raise RuntimeError(f"qo_moe_forward failed with code {rc}")
         return (y, d) if debug else y
@@ -203,8 +235,9 @@ SLOTS = ("router", "gate", "up", "down", "sh_gate", "sh_up", "sh_down", "sh_norm
 
 
 def synth_layer(n_embd, n_experts, top_k, ffn_dim, shared, wtype, seed, layer=0, sigma=0.02,
-                router_sigma=0.02) -> Layer:
-    """CPU generation of the same recipe as qwenium_amd.synthetic.make_layer_tensors."""
+                router_sigma=0.02, geglu=False) -> Layer:
+    """CPU generation of the same recipe as qwenium_amd.synthetic.make_layer_tensors
+    (geglu: the fused gate_up tensor and the GeGLU activation)."""
     H, E, F = n_embd, n_experts, ffn_dim
     sid = lambda slot: layer * 16 + SLOTS.index(slot)
     t = {"router": gen_normal_f32(seed, sid("router"), E * H, 0.0, router_sigma).reshape(E, H)}
@@ -216,6 +249,10 @@ def synth_layer(n_embd, n_experts, top_k, ffn_dim, shared, wtype, seed, layer=0,
             t[slot] = quantize(wtype, gen_normal_f32(seed, sid(slot), F * H, 0.0, sigma))
         t["sh_down"] = quantize(wtype, gen_normal_f32(seed, sid("sh_down"), H * F, 0.0, sigma))
         t["sh_norm"] = gen_normal_f32(seed, sid("sh_norm"), H, 0.0, router_sigma)
+    if geglu:
+        g, u = t.pop("gate").reshape(E, -1), t.pop("up").reshape(E, -1)
+        t["gate_up"] = np.concatenate([g, u], axis=1).reshape(-1)
+        return Layer(H, E, top_k, F, shared, wtype, t, act=ACT_GELU_TANH)
     return Layer(H, E, top_k, F, shared, wtype, t)
 
 

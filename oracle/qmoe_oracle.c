@@ -387,6 +387,27 @@ float qo_silu_mul(float g, float u) {
     return (float)(s * (double)u);
 }
 
+/* gelu_f32 of ggml (the value its CPU table stores before the fp16 rounding);
+ * the C expression parses as ((0.5f*x) * (1 + tanhf(((c*x) * (1 + ((a*x)*x)))))). */
+static float qo_gelu_tanh_f32(float x) {
+    const float a = 0.044715f;
+    const float c = 0.79788456080286535587989211986876f; /* sqrt(2/pi) */
+    return 0.5f * x * (1.0f + tanhf(c * x * (1.0f + a * x * x)));
+}
+
+float qo_gelu_f16(float x) {
+    if (x <= -10.0f) return 0.0f;
+    if (x >= 10.0f) return x;
+    const float xh = qo_fp16_to_fp32(qo_fp32_to_fp16(x));
+    return qo_fp16_to_fp32(qo_fp32_to_fp16(qo_gelu_tanh_f32(xh)));
+}
+
+float qo_geglu_mul(float g, float u) { return qo_gelu_f16(g) * u; }
+
+static float qo_act_mul(int act, float g, float u) {
+    return act == QO_ACT_GELU_TANH ? qo_geglu_mul(g, u) : qo_silu_mul(g, u);
+}
+
 float qo_sigmoid(float g) {
     return (float)(1.0 / (1.0 + qo_exp_det(-(double)g)));
 }
@@ -405,12 +426,35 @@ void qo_rms_norm(const float* x, const float* w, int T, int H, float eps, float*
     }
 }
 
+void qo_gemma4_moe_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps,
+                          float* expert_in, float* router_in) {
+    const float s = 1.0f / sqrtf((float)H);
+    for (int t = 0; t < T; ++t) {
+        const float* xt = x + (size_t)t * H;
+        double sum = 0.0;
+        for (int i = 0; i < H; ++i) sum += (double)(xt[i] * xt[i]);
+        const float mean = (float)(sum / (double)H);
+        const float scale = 1.0f / sqrtf(mean + eps);
+        for (int i = 0; i < H; ++i) {
+            const float v = xt[i] * scale;
+            expert_in[(size_t)t * H + i] = v * w_pre[i];
+            const float r = v * s;
+            router_in[(size_t)t * H + i] = r * w_rs[i];
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* Whole layer: router -> top-k -> expert-major grouped SwiGLU -> combine    */
 /* ------------------------------------------------------------------------ */
 int qo_moe_forward(const qo_layer* L, const float* x, int T, float* y,
                    qo_debug* dbg, int nthreads) {
-    if (!L || !x || !y || T < 0) return 1;
+    return qo_moe_forward_routed(L, x, x, T, y, dbg, nthreads);
+}
+
+int qo_moe_forward_routed(const qo_layer* L, const float* x, const float* xr, int T, float* y,
+                          qo_debug* dbg, int nthreads) {
+    if (!L || !x || !xr || !y || T < 0) return 1;
     const int H = L->n_embd, E = L->n_experts, k = L->top_k, F = L->ffn_dim;
     const int wt = L->expert_type;
     if (H % 32 || F % 32 || k < 1 || k > E || k > 64) return 2;
@@ -439,7 +483,7 @@ int qo_moe_forward(const qo_layer* L, const float* x, int T, float* y,
     float* yd = (float*)malloc(sizeof(float) * (size_t)A * H);
 
     /* 1. router logits (moe.cpp:72), top-k (:77-82), softmax (:88-94) */
-    qo_router_logits(L->w_router, x, T, H, E, logits);
+    qo_router_logits(L->w_router, xr, T, H, E, logits);
     qo_topk_softmax(logits, T, E, k, idx, wts);
     qo_sort_assignments(idx, T, E, k, offsets, rows, NULL);
 
@@ -447,7 +491,12 @@ int qo_moe_forward(const qo_layer* L, const float* x, int T, float* y,
 #pragma omp parallel for schedule(static)
     for (int t = 0; t < T; ++t) qo_quantize_q8_0_act(x + (size_t)t * H, xq + xq_row * t, H);
 
-    /* 2. gate/up mul_mat_id (moe.cpp:105-113) + silu*up (:117), expert-major */
+    /* 2. gate/up mul_mat_id (moe.cpp:105-113) + silu*up (:117) or gelu*up
+     *    (gemma4.cpp:419-423), expert-major */
+    const int act = L->act;
+    const size_t gu_rows = L->gate_up_fused ? 2 * (size_t)F : (size_t)F;  /* rows per expert */
+    const uint8_t* w_up_base = L->gate_up_fused ? (const uint8_t*)L->w_gate + (size_t)F * wrow_h
+                                                : (const uint8_t*)L->w_up;
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t ef = 0; ef < (int64_t)E * (F / 32); ++ef) {
         const int e = (int)(ef / (F / 32));
@@ -456,11 +505,11 @@ int qo_moe_forward(const qo_layer* L, const float* x, int T, float* y,
             const int64_t a = rows[p];
             const int t = (int)(a / k);
             for (int f = f0; f < f0 + 32; ++f) {
-                const uint8_t* wg = (const uint8_t*)L->w_gate + ((size_t)e * F + f) * wrow_h;
-                const uint8_t* wu = (const uint8_t*)L->w_up + ((size_t)e * F + f) * wrow_h;
+                const uint8_t* wg = (const uint8_t*)L->w_gate + ((size_t)e * gu_rows + f) * wrow_h;
+                const uint8_t* wu = w_up_base + ((size_t)e * gu_rows + f) * wrow_h;
                 const float g = qo_vec_dot(wt, wg, xq + xq_row * t, H);
                 const float u = qo_vec_dot(wt, wu, xq + xq_row * t, H);
-                h[a * F + f] = qo_silu_mul(g, u);
+                h[a * F + f] = qo_act_mul(act, g, u);
             }
         }
     }
@@ -494,12 +543,12 @@ int qo_moe_forward(const qo_layer* L, const float* x, int T, float* y,
             for (int f = 0; f < F; ++f) {
                 const float g = qo_vec_dot(wt, (const uint8_t*)L->w_sh_gate + (size_t)f * wrow_h, xq + xq_row * t, H);
                 const float u = qo_vec_dot(wt, (const uint8_t*)L->w_sh_up + (size_t)f * wrow_h, xq + xq_row * t, H);
-                hs[f] = qo_silu_mul(g, u);
+                hs[f] = qo_act_mul(act, g, u);
             }
             qo_quantize_q8_0_act(hs, hsq, F);
             for (int n = 0; n < H; ++n)
                 sh_out[(size_t)t * H + n] = qo_vec_dot(wt, (const uint8_t*)L->w_sh_down + (size_t)n * wrow_f, hsq, F);
-            sh_gate[t] = qo_sigmoid(qo_dot_f32_exact(L->w_sh_norm, x + (size_t)t * H, H));
+            sh_gate[t] = qo_sigmoid(qo_dot_f32_exact(L->w_sh_norm, xr + (size_t)t * H, H));
             free(hs);
             free(hsq);
         }

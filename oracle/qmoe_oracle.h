@@ -36,6 +36,21 @@
  *     ~1 ulp (pinned by tests/test_oracle_kat.py).
  * ggml's own f32 accumulation differs from these exact values by ~1e-6
  * relative, far inside the layer tolerance (2e-3 x output RMS).
+ *
+ * The Gemma 4 GeGLU variant (Gemma4ForwardPass::build_moe_geglu,
+ * src/models/gemma4.cpp:367-445, inputs prepared at :549-564):
+ *   - gelu is ggml's CPU ggml_vec_gelu_f32 with GGML_GELU_FP16 (vec.h of the
+ *     same ggml tag; the reference's tests/unit/test_ffn.cpp:172-175 notes the
+ *     f16 table): x <= -10 -> 0, x >= 10 -> x, else the entry of a table
+ *     indexed by fp16(x) that holds fp16(gelu_f32(x16)), with
+ *     gelu_f32(x) = 0.5f*x*(1 + tanhf(0.7978845608f*x*(1 + 0.044715f*x*x)))
+ *     in f32 (libm tanhf); then gelu(g)*u in f32 (ggml_mul, :423);
+ *   - gate and up are the two halves of one [n_embd, 2*ffn, E] tensor
+ *     (views at :403-409: gate rows 0..F-1, up rows F..2F-1 of each expert);
+ *   - the router reads its own input (:380): router_in =
+ *     ((rms_norm(x) * (1/sqrtf(n_embd))) * ffn_gate_inp.scale), three f32
+ *     roundings (ggml_rms_norm, ggml_scale, ggml_mul, :561-563), while the
+ *     experts read rms_norm(x) * pre_ffw_norm_2 (:555-557).
  */
 #ifndef QMOE_ORACLE_H
 #define QMOE_ORACLE_H
@@ -87,8 +102,14 @@ void  qo_topk_softmax(const float* logits, int T, int E, int k,
 void  qo_sort_assignments(const int32_t* idx, int T, int E, int k,
                           int32_t* offsets, int32_t* rows, int32_t* pos);
 float qo_silu_mul(float g, float u);         /* silu(g)*u via qo_exp_det */
+float qo_gelu_f16(float x);                  /* ggml CPU gelu (fp16 table semantics) */
+float qo_geglu_mul(float g, float u);        /* qo_gelu_f16(g)*u in f32 */
 float qo_sigmoid(float g);
 void  qo_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y);
+/* Gemma 4 MoE inputs from one residual row (gemma4.cpp:555-563):
+ * expert_in = (x*scale)*w_pre, router_in = ((x*scale)*(1/sqrtf(H)))*w_rs. */
+void  qo_gemma4_moe_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps,
+                           float* expert_in, float* router_in);
 
 /* ---- whole layer ------------------------------------------------------ */
 typedef struct qo_layer {
@@ -102,7 +123,11 @@ typedef struct qo_layer {
     const void*  w_sh_up;            /* F rows of H values */
     const void*  w_sh_down;          /* H rows of F values */
     const float* w_sh_norm;          /* [H] f32 shared-expert gate vector */
+    int act;                         /* QO_ACT_SILU (SwiGLU) or QO_ACT_GELU_TANH (GeGLU) */
+    int gate_up_fused;               /* 1: w_gate holds E x 2F rows (gate rows, then up rows, per expert) */
 } qo_layer;
+
+enum { QO_ACT_SILU = 0, QO_ACT_GELU_TANH = 1 };
 
 typedef struct qo_debug {            /* every pointer optional (NULL) */
     float*   logits;                 /* [T][E] */
@@ -120,6 +145,9 @@ typedef struct qo_debug {            /* every pointer optional (NULL) */
  * Returns 0 on success, nonzero on invalid arguments. */
 int qo_moe_forward(const qo_layer* L, const float* x, int T, float* y,
                    qo_debug* dbg, int nthreads);
+/* The same with the router reading xr[T][H] (x feeds the experts). */
+int qo_moe_forward_routed(const qo_layer* L, const float* x, const float* xr, int T, float* y,
+                          qo_debug* dbg, int nthreads);
 
 #ifdef __cplusplus
 }

@@ -51,6 +51,11 @@ EXPORTED = (
     "qmoe_gguf_upload",
     "qmoe_gguf_tensor_view",
     "qmoe_layer_set_expert_counts",
+    "qmoe_geglu_layer_create",
+    "qmoe_layer_forward_routed",
+    "qmoe_layer_forward_gemma4",
+    "qmoe_gemma4_moe_inputs",
+    "qmoe_gelu_f16_table",
     "qmoe_residency_create",
     "qmoe_residency_destroy",
     "qmoe_residency_record",
@@ -183,6 +188,16 @@ def lib() -> ctypes.CDLL:
     L.qmoe_gguf_upload.argtypes = [vp, cp, vp, ctypes.c_uint64, vp]
     L.qmoe_gguf_tensor_view.restype = ctypes.c_int
     L.qmoe_gguf_tensor_view.argtypes = [P(QmoeGgufTensor), vp, P(QmoeTensor)]
+    L.qmoe_geglu_layer_create.restype = ctypes.c_int
+    L.qmoe_geglu_layer_create.argtypes = [P(QmoeTensor)] * 3 + [P(QmoeHparams), P(vp)]
+    L.qmoe_layer_forward_routed.restype = ctypes.c_int
+    L.qmoe_layer_forward_routed.argtypes = [vp, vp, vp, vp, ctypes.c_int32, vp, P(QmoeDebug), vp]
+    L.qmoe_layer_forward_gemma4.restype = ctypes.c_int
+    L.qmoe_layer_forward_gemma4.argtypes = [vp, vp, vp, vp, vp, ctypes.c_float, ctypes.c_int32, vp, P(QmoeDebug), vp]
+    L.qmoe_gemma4_moe_inputs.restype = ctypes.c_int
+    L.qmoe_gemma4_moe_inputs.argtypes = [vp, vp, vp, ctypes.c_float, ctypes.c_int32, ctypes.c_int32, vp, vp, vp]
+    L.qmoe_gelu_f16_table.restype = ctypes.c_int
+    L.qmoe_gelu_f16_table.argtypes = [P(ctypes.c_uint16)]
     L.qmoe_layer_set_expert_counts.restype = ctypes.c_int
     L.qmoe_layer_set_expert_counts.argtypes = [vp, vp]
     L.qmoe_residency_create.restype = ctypes.c_int

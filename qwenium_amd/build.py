@@ -25,6 +25,7 @@ SOURCES = [
     "qmoe_api.cpp",
     "gguf.cpp",
     "residency.cpp",
+    "gelu_table.cpp",
 ]
 ARCH = os.environ.get("QMOE_OFFLOAD_ARCH", "gfx950")
 

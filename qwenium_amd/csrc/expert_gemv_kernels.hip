@@ -31,6 +31,8 @@ struct ExpertArgs {
     float2* gubuf;                             // [R][F] (gate, up) projections (f32)
     int8_t* hq_qs; float2* hq_ds;              // [R][F], [R][F/32] Q8_0 of hbuf
     float* ybuf;                               // [R][H] down outputs (unweighted)
+    int act;                                   // kActSilu or kActGeluTanh
+    const uint16_t* gelu_tab;                  // [65536] fp16 gelu table (GeGLU layers)
 };
 
 // Loads the slot table into LDS (all E+1 entries; those past n_active are
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Q: SwiGLU h = silu(g)*u of each (row, ffn index), then Q8_0 quantization of
+// Q: h = silu(g)*u (SwiGLU) or gelu(g)*u (GeGLU) of each (row, ffn index), then Q8_0 quantization of
 // the h rows (the activation quantization ggml applies to src1 of the down
 // mul_mat_id).  Each lane takes 4 consecutive values; the 8 lanes of a 32-value
 // block reduce with DPP (quad xor 1, quad xor 2, half-row mirror) and store
@@ -233,10 +235,10 @@ __global__ __launch_bounds__(256) void k_quant_h(ExpertArgs a) {
     const f32x4* src = (const f32x4*)(a.gubuf + (uint64_t)p * a.F + 4 * q);
     const f32x4 v0 = src[0], v1 = src[1];  // (g0, u0, g1, u1), (g2, u2, g3, u3)
     float h[4];
-    h[0] = silu_mul_det(v0.x, v0.y);
-    h[1] = silu_mul_det(v0.z, v0.w);
-    h[2] = silu_mul_det(v1.x, v1.y);
-    h[3] = silu_mul_det(v1.z, v1.w);
+    h[0] = act_mul(a.act, a.gelu_tab, v0.x, v0.y);
+    h[1] = act_mul(a.act, a.gelu_tab, v0.z, v0.w);
+    h[2] = act_mul(a.act, a.gelu_tab, v1.x, v1.y);
+    h[3] = act_mul(a.act, a.gelu_tab, v1.z, v1.w);
     float amax = fmaxf(fmaxf(__builtin_fabsf(h[0]), __builtin_fabsf(h[1])),
                        fmaxf(__builtin_fabsf(h[2]), __builtin_fabsf(h[3])));
     amax = dpp8_max<kDppQuadXor1>(amax);
@@ -392,7 +394,8 @@ __global__ __launch_bounds__(NW * 64, GQ_MIN_WAVES) void k_gateup_q(ExpertArgs a
         const int c = i >> 5, fl = i & 31;
         const float2 gu = s_gu[c][fl];
         const int p = p0 + c;
-        swiglu_q8_block32(gu.x, gu.y, fl, a.hq_qs + (uint64_t)p * a.F + fb * 32, a.hq_ds + (uint64_t)p * nfb + fb);
+        swiglu_q8_block32(gu.x, gu.y, fl, a.hq_qs + (uint64_t)p * a.F + fb * 32, a.hq_ds + (uint64_t)p * nfb + fb,
+                          a.act, a.gelu_tab);
     }
 }
 
@@ -809,6 +812,8 @@ static ExpertArgs make_expert_args(const LayerDesc& L, const Workspace& ws, int 
     a.counters = ws.counters; a.slot_info = ws.slot_info; a.offsets = ws.offsets; a.row_token = ws.row_token;
     a.xq_qs = ws.xq_qs; a.xq_ds = ws.xq_ds; a.gubuf = ws.gubuf; a.hq_qs = ws.hq_qs; a.hq_ds = ws.hq_ds;
     a.ybuf = ws.ybuf;
+    a.act = L.act;
+    a.gelu_tab = L.gelu_tab;
     return a;
 }
 

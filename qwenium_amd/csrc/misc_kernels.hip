@@ -78,6 +78,63 @@ hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float e
 }
 
 // ---------------------------------------------------------------------------
+// Gemma 4 MoE inputs (src/models/gemma4.cpp:555-563): from the residual row x,
+//   expert_in = rms_norm(x) * pre_ffw_norm_2            (build_rms_norm)
+//   router_in = (rms_norm(x) * s) * ffn_gate_inp.scale  (ggml_rms_norm, ggml_scale, ggml_mul)
+// with s = 1/sqrtf(n_embd): the row read once, the scale computed once, in
+// k_rms_norm's summation order (so rms_norm(x) has the same bits).
+// ---------------------------------------------------------------------------
+template <int NV>
+__global__ __launch_bounds__(256) void k_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int H,
+                                                       float eps, float s, float* ei, float* ri) {
+#pragma clang fp contract(off)
+    __shared__ double s_part[4];
+    const int t = blockIdx.x;
+    const float* xr = x + (uint64_t)t * H;
+    float v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        v[k] = i < H ? xr[i] : 0.0f;
+    }
+    double acc = 0.0;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+        if ((int)threadIdx.x + 256 * k < H) acc += (double)(v[k] * v[k]);
+    acc = group_sum_f64<64>(acc);
+    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const double sum = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    const float mean = (float)(sum / (double)H);
+    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < H) {
+            const float u = v[k] * scale;
+            ei[(uint64_t)t * H + i] = u * w_pre[i];
+            const float r = u * s;
+            ri[(uint64_t)t * H + i] = r * w_rs[i];
+        }
+    }
+}
+
+hipError_t launch_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps, float s,
+                                float* expert_in, float* router_in, hipStream_t stream) {
+    const int nv = (H + 255) / 256;
+    if (nv > 16) return hipErrorInvalidValue;
+    if (nv <= 4)
+        hipLaunchKernelGGL(k_gemma4_inputs<4>, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
+    else if (nv <= 8)
+        hipLaunchKernelGGL(k_gemma4_inputs<8>, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
+    else if (nv <= 12)
+        hipLaunchKernelGGL(k_gemma4_inputs<12>, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
+    else
+        hipLaunchKernelGGL(k_gemma4_inputs<16>, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Synthetic data: N(mean, sigma) from (seed, stream, index); quantized rows
 // use ggml's reference quantizers (quantize_row_q4_0_ref / _q8_0_ref).
 // ---------------------------------------------------------------------------

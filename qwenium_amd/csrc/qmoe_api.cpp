@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -158,6 +159,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.hq_ds = (float2*)take(R * (F / 32) * sizeof(float2));
     ws.ybuf = (float*)take(R * H * sizeof(float));
     ws.xn = (float*)take((size_t)T * H * sizeof(float));
+    ws.xr = (float*)take((size_t)T * H * sizeof(float));
     ws.max_tiles = max_tiles;
     ws.cap_T = T; ws.H = H; ws.E = E; ws.K = K; ws.F = F;
     ws.base = base;
@@ -284,6 +286,43 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
     return QMOE_OK;
 }
 
+int qmoe_geglu_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_gate_up_exps,
+                            const qmoe_tensor* w_down_exps, const qmoe_hparams* hp, qmoe_layer** out) {
+    g_last_error.clear();
+    if (!out) return fail(QMOE_ERR_NULL, "qmoe: out expected a non-null qmoe_layer**, got null");
+    *out = nullptr;
+    if (!hp) return fail(QMOE_ERR_NULL, "qmoe: hp expected non-null hparams, got null");
+    if (hp->has_shared_expert)
+        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"has_shared_expert\" expected 0 for the GeGLU MoE (Gemma 4 has none), got " +
+                                        std::to_string(hp->has_shared_expert));
+    if (!w_router) return fail(QMOE_ERR_NULL, slot_error("w_router", "a tensor", "null"));
+    if (hp->ffn_dim < 64 || hp->ffn_dim > 4096 || hp->ffn_dim % 64 != 0)
+        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"ffn_dim\" expected a multiple of 64 in [64, 4096], got " +
+                                        std::to_string(hp->ffn_dim));
+    const int64_t H = w_router->ne[0], E = hp->n_experts, F = hp->ffn_dim;
+    {
+        // [n_embd, 2*ffn_dim, n_experts]: gate rows 0..F-1, up rows F..2F-1 of each expert (gemma4.cpp:397-409)
+        const int64_t ne[3] = {H, 2 * F, E};
+        int rc = check_tensor("w_gate_up_exps", w_gate_up_exps, 3, ne, true);
+        if (rc) return rc;
+    }
+    qmoe_tensor gate = *w_gate_up_exps, up = *w_gate_up_exps;
+    gate.ne[1] = up.ne[1] = F;
+    up.data = (const uint8_t*)w_gate_up_exps->data + (uint64_t)F * w_gate_up_exps->nb[1];
+    int rc = qmoe_layer_create(w_router, &gate, &up, w_down_exps, nullptr, nullptr, nullptr, nullptr, hp, out);
+    if (rc) return rc;
+    const uint16_t* tab = nullptr;
+    hipError_t err = qmoe::gelu_table_device(&tab);
+    if (err != hipSuccess) {
+        qmoe_layer_destroy(*out);
+        *out = nullptr;
+        return hip_fail(err, "gelu table upload");
+    }
+    (*out)->d.act = qmoe::kActGeluTanh;
+    (*out)->d.gelu_tab = tab;
+    return QMOE_OK;
+}
+
 int qmoe_layer_destroy(qmoe_layer* layer) {
     if (!layer) return QMOE_OK;
     if (layer->own_ws) qmoe_workspace_destroy(layer->own_ws);
@@ -346,10 +385,23 @@ int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault) {
     return QMOE_OK;
 }
 
-// y = MoE(x) + residual, or with norm_w: y = x + MoE(RMSNorm(x) * norm_w).
-static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const float* x, int32_t n_tokens, float* y,
-                        const float* residual, const float* norm_w, float norm_eps, const qmoe_debug* dbg,
-                        void* hip_stream) {
+// What feeds one forward: x and optional residual, or x as the residual row of
+// a fused caller slice (norm_w: the Qwen pre-MoE RMSNorm; g4_pre_w + g4_rs_w:
+// the Gemma 4 expert and router inputs), or a separate router input xr.
+struct ForwardIn {
+    const float* x = nullptr;
+    const float* xr = nullptr;        // router input (null: the experts' input)
+    const float* residual = nullptr;
+    const float* norm_w = nullptr;    // y = x + MoE(RMSNorm(x) * norm_w)
+    const float* g4_pre_w = nullptr;  // y = MoE(rms(x)*pre_w) routed on (rms(x)/sqrt(H))*rs_w
+    const float* g4_rs_w = nullptr;
+    float eps = 0.0f;
+};
+
+static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& in, int32_t n_tokens, float* y,
+                        const qmoe_debug* dbg, void* hip_stream) {
+    const float* x = in.x;
+    const float* residual = in.residual;
     g_last_error.clear();
     if (!layer) return fail(QMOE_ERR_NULL, "qmoe: layer expected non-null, got null");
     if (n_tokens < 0)
@@ -358,9 +410,11 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const float* x, i
     if (!x) return fail(QMOE_ERR_NULL, "qmoe: x expected a device pointer, got null");
     if (!y) return fail(QMOE_ERR_NULL, "qmoe: y expected a device pointer, got null");
     if (x == y) return fail(QMOE_ERR_VALUE, "qmoe: y expected a buffer distinct from x, got x");
-    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)residual & 15u) || ((uintptr_t)norm_w & 15u))
+    if (in.xr == y) return fail(QMOE_ERR_VALUE, "qmoe: y expected a buffer distinct from router_in, got router_in");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)residual & 15u) || ((uintptr_t)in.norm_w & 15u) ||
+        ((uintptr_t)in.xr & 15u))
         return fail(QMOE_ERR_VALUE,
-                    "qmoe: x/y/residual/norm_w expected 16-byte aligned device pointers, got a misaligned one");
+                    "qmoe: x/y/residual/norm_w/router_in expected 16-byte aligned device pointers, got a misaligned one");
     const LayerDesc& d = layer->d;
     if (!ws) {
         if (!layer->own_ws || layer->own_ws->w.cap_T < n_tokens) {
@@ -396,14 +450,21 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const float* x, i
         rdbg.approx = dbg->router_approx;
         rdbg.bound = dbg->router_bound;
     }
-    const float* xin = x;  // the layer's (normalized) input
-    if (norm_w) {
+    const float* xin = x;                    // the experts' input
+    const float* xr = in.xr ? in.xr : x;     // the router's input
+    if (in.norm_w) {
         // the normalized rows go to the workspace; the residual add is the combine epilogue
         residual = x;
-        if (err == hipSuccess) err = qmoe::launch_rms_norm(x, norm_w, n_tokens, d.H, norm_eps, v.xn, stream);
+        if (err == hipSuccess) err = qmoe::launch_rms_norm(x, in.norm_w, n_tokens, d.H, in.eps, v.xn, stream);
+        xin = xr = v.xn;
+    } else if (in.g4_pre_w) {
+        const float s = 1.0f / std::sqrt((float)d.H);  // gemma4.cpp:561-562
+        if (err == hipSuccess)
+            err = qmoe::launch_gemma4_inputs(x, in.g4_pre_w, in.g4_rs_w, n_tokens, d.H, in.eps, s, v.xn, v.xr, stream);
         xin = v.xn;
+        xr = v.xr;
     }
-    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, n_tokens, rdbg, stream);
+    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, xr, n_tokens, rdbg, stream);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
     const bool mfma = n_tokens >= d.mfma_min_tokens;
     // events [1] and [2] are taken by the gate/up launch itself (its own start and end)
@@ -459,7 +520,10 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const float* x, i
 
 int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, int32_t n_tokens, float* y,
                        const float* residual, const qmoe_debug* dbg, void* hip_stream) {
-    return forward_impl(layer, ws, x, n_tokens, y, residual, nullptr, 0.0f, dbg, hip_stream);
+    ForwardIn in;
+    in.x = x;
+    in.residual = residual;
+    return forward_impl(layer, ws, in, n_tokens, y, dbg, hip_stream);
 }
 
 int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* norm_w, float eps,
@@ -467,7 +531,55 @@ int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* 
     g_last_error.clear();
     if (!norm_w) return fail(QMOE_ERR_NULL, "qmoe: norm_w expected a device pointer, got null");
     if (!(eps >= 0.0f)) return fail(QMOE_ERR_VALUE, "qmoe: eps expected >= 0, got " + std::to_string(eps));
-    return forward_impl(layer, ws, x, n_tokens, y, nullptr, norm_w, eps, dbg, hip_stream);
+    ForwardIn in;
+    in.x = x;
+    in.norm_w = norm_w;
+    in.eps = eps;
+    return forward_impl(layer, ws, in, n_tokens, y, dbg, hip_stream);
+}
+
+int qmoe_layer_forward_routed(qmoe_layer* layer, qmoe_workspace* ws, const float* expert_in, const float* router_in,
+                              int32_t n_tokens, float* y, const qmoe_debug* dbg, void* hip_stream) {
+    g_last_error.clear();
+    if (n_tokens > 0 && !router_in)
+        return fail(QMOE_ERR_NULL, "qmoe: router_in expected a device pointer, got null");
+    ForwardIn in;
+    in.x = expert_in;
+    in.xr = router_in;
+    return forward_impl(layer, ws, in, n_tokens, y, dbg, hip_stream);
+}
+
+int qmoe_layer_forward_gemma4(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* pre_norm_w,
+                              const float* router_scale_w, float eps, int32_t n_tokens, float* y, const qmoe_debug* dbg,
+                              void* hip_stream) {
+    g_last_error.clear();
+    if (!pre_norm_w || !router_scale_w)
+        return fail(QMOE_ERR_NULL, "qmoe: pre_norm_w and router_scale_w expected device pointers, got null");
+    if (((uintptr_t)pre_norm_w & 3u) || ((uintptr_t)router_scale_w & 3u))
+        return fail(QMOE_ERR_VALUE, "qmoe: pre_norm_w/router_scale_w expected 4-byte aligned, got a misaligned one");
+    if (!(eps >= 0.0f)) return fail(QMOE_ERR_VALUE, "qmoe: eps expected >= 0, got " + std::to_string(eps));
+    ForwardIn in;
+    in.x = x;
+    in.g4_pre_w = pre_norm_w;
+    in.g4_rs_w = router_scale_w;
+    in.eps = eps;
+    return forward_impl(layer, ws, in, n_tokens, y, dbg, hip_stream);
+}
+
+int qmoe_gemma4_moe_inputs(const float* x, const float* pre_norm_w, const float* router_scale_w, float eps,
+                           int32_t n_tokens, int32_t n_embd, float* expert_in, float* router_in, void* hip_stream) {
+    g_last_error.clear();
+    if (n_tokens < 0) return fail(QMOE_ERR_VALUE, "qmoe: n_tokens expected >= 0, got " + std::to_string(n_tokens));
+    if (n_tokens == 0) return QMOE_OK;
+    if (!x || !pre_norm_w || !router_scale_w || !expert_in || !router_in)
+        return fail(QMOE_ERR_NULL, "qmoe: x/pre_norm_w/router_scale_w/expert_in/router_in expected device pointers, got null");
+    if (n_embd < 1 || n_embd > 4096)
+        return fail(QMOE_ERR_VALUE, "qmoe: n_embd expected 1..4096, got " + std::to_string(n_embd));
+    if (!(eps >= 0.0f)) return fail(QMOE_ERR_VALUE, "qmoe: eps expected >= 0, got " + std::to_string(eps));
+    const float s = 1.0f / std::sqrt((float)n_embd);
+    hipError_t err = qmoe::launch_gemma4_inputs(x, pre_norm_w, router_scale_w, n_tokens, n_embd, eps, s, expert_in,
+                                                router_in, (hipStream_t)hip_stream);
+    return err == hipSuccess ? QMOE_OK : hip_fail(err, "gemma4 inputs kernel");
 }
 
 int qmoe_layer_set_expert_counts(qmoe_layer* layer, uint64_t* device_counts) {

@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "qmoe_internal.h"
+
 namespace qmoe {
 
 constexpr int kTypeF32 = 0;
@@ -134,6 +136,21 @@ __device__ __forceinline__ float silu_mul_det(float g, float u) {
     const double gd = (double)g;
     const double s = gd / (1.0 + exp_det(-gd));
     return (float)(s * (double)u);
+}
+
+// gelu(g)*u as ggml's CPU backend computes it: g <= -10 -> 0, g >= 10 -> g,
+// else the fp16 table entry of fp16(g) (tab: 65536 fp16 values, built on the
+// host from the tanh formula), widened, times u in f32.
+__device__ __forceinline__ float geglu_mul_tab(float g, float u, const uint16_t* tab) {
+    float gl;
+    if (g <= -10.0f) gl = 0.0f;
+    else if (g >= 10.0f) gl = g;
+    else gl = fp16_to_f32(tab[f32_to_fp16(g) & 0xffffu]);
+    return gl * u;
+}
+
+__device__ __forceinline__ float act_mul(int act, const uint16_t* gelu_tab, float g, float u) {
+    return act == kActGeluTanh ? geglu_mul_tab(g, u, gelu_tab) : silu_mul_det(g, u);
 }
 
 __device__ __forceinline__ float sigmoid_det(float g) {
@@ -418,12 +435,13 @@ __device__ __forceinline__ int dpp8_add(int v) {
     return v + __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
 }
 
-// h = silu(g)*u of one value per lane and the Q8_0 quantization of the 32-value
+// h = silu(g)*u (or gelu(g)*u) of one value per lane and the Q8_0 quantization of the 32-value
 // block held by a whole aligned 32-lane group (lane fl = value fl): ggml's
 // quantize_row_q8_0 (d = fp16(amax/127), q = rint(h*127/amax)) plus the block's
 // quant sum.  Writes the lane's quant to qs[fl] and, from lane 0, {d, sum}.
-__device__ __forceinline__ void swiglu_q8_block32(float g, float u, int fl, int8_t* qs, float2* ds) {
-    const float h = silu_mul_det(g, u);
+__device__ __forceinline__ void swiglu_q8_block32(float g, float u, int fl, int8_t* qs, float2* ds, int act = kActSilu,
+                                                  const uint16_t* gelu_tab = nullptr) {
+    const float h = act_mul(act, gelu_tab, g, u);
     float amax = __builtin_fabsf(h);
     amax = dpp8_max<kDppQuadXor1>(amax);
     amax = dpp8_max<kDppQuadXor2>(amax);

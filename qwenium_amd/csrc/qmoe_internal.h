@@ -20,6 +20,9 @@ constexpr int kSyncErr = 1;
 constexpr int kSyncFlags = 64;     // flags start here (448 router blocks max)
 // Row tile of the prefill grouped GEMM (rows of one expert per tile).
 constexpr int kMfmaTileM = 64;
+// Expert activations: SwiGLU (moe.cpp:117) or GeGLU-tanh (gemma4.cpp:423).
+constexpr int kActSilu = 0;
+constexpr int kActGeluTanh = 1;
 
 struct LayerDesc {
     int H = 0, E = 0, K = 0, F = 0, S = 0;  // n_embd, n_experts, top_k, ffn_dim, shared (0/1)
@@ -41,6 +44,8 @@ struct LayerDesc {
     int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs
     int dc_ahead = 2;                       // decode down+combine: steps with loads in flight (2 or 4)
     unsigned long long* expert_counts = nullptr;  // optional device [E]: += each forward's per-expert dispatches
+    int act = 0;                            // 0 SwiGLU (silu(g)*u), 1 GeGLU-tanh (gelu(g)*u, ggml's fp16 table)
+    const uint16_t* gelu_tab = nullptr;     // device [65536] fp16 gelu table of the layer's device (GeGLU)
 };
 
 // Device scratch.  R = T*K + S*T rows: routed assignments sorted by expert,
@@ -73,7 +78,8 @@ struct Workspace {
     float2* gubuf = nullptr;      // [R][F] (gate, up) projections
     int8_t* hq_qs = nullptr;      // [R][F]   Q8_0 quants of h = silu(g)*u
     float2* hq_ds = nullptr;      // [R][F/32] {d, bitcast(sum q)}
-    float* xn = nullptr;          // [T][H] RMSNorm(x)*w for fused-norm forwards off the decode path
+    float* xn = nullptr;          // [T][H] RMSNorm(x)*w for fused-norm forwards (the experts' input)
+    float* xr = nullptr;          // [T][H] the router's own input when it differs (Gemma 4 slice)
     float* ybuf = nullptr;        // [R][H] down outputs (unweighted)
     int max_tiles = 0;
 };
@@ -107,8 +113,10 @@ struct RouteDebug {
 bool route_uses_mfma(const LayerDesc& L, int T);
 // One-launch decode routing (T <= 16); it also writes ws.dslots.
 bool route_decode_fused(const LayerDesc& L, int T);
-hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, const RouteDebug& dbg,
-                        hipStream_t stream);
+// x: the experts' input (quantized to Q8_0); xr: the router's input (x for
+// the Qwen layer; the scaled norm for Gemma 4); the shared gate reads xr.
+hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
+                        const RouteDebug& dbg, hipStream_t stream);
 // ev_start / ev_stop (optional): events recorded at the kernel's own start and
 // end (profiling of the dominant kernel without marker overhead).
 hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
@@ -132,6 +140,13 @@ bool down_combine_fused(const LayerDesc& L, int T);
 hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
                                hipStream_t stream);
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream);
+// Gemma 4 MoE inputs from one pass over x (H <= 4096): expert_in = (x*scale)*w_pre,
+// router_in = ((x*scale)*s)*w_rs with scale = 1/sqrtf(mean(x^2) + eps).
+hipError_t launch_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps, float s,
+                                float* expert_in, float* router_in, hipStream_t stream);
+// ggml's CPU fp16 gelu table (65536 entries): host copy, and the current device's copy.
+void gelu_table_host(uint16_t* out);
+hipError_t gelu_table_device(const uint16_t** out);
 hipError_t launch_synth_f32(float* dst, int64_t n, uint64_t seed, uint64_t stream_id, double mean, double sigma,
                             hipStream_t stream);
 hipError_t launch_synth_quant(void* dst, int type, int64_t n_rows, int64_t row_len, uint64_t seed,

@@ -17,7 +17,8 @@ namespace qmoe {
 // R1: router logits (one wave per router row, all tokens) + activation quant
 // ---------------------------------------------------------------------------
 struct RouterArgs {
-    const float* x;         // [T][H]
+    const float* x;         // [T][H] router input
+    const float* xe;        // [T][H] expert input (quantized to Q8_0 here)
     const float* w_router;  // [E][ld]
     uint64_t router_ld;
     const float* w_sh_norm; // [H] or null
@@ -141,7 +142,7 @@ __global__ __launch_bounds__(256) void k_router_quant(RouterArgs a) {
         return;
     }
     const int t = (blockIdx.x - a.n_router_blocks) * 4 + wave;
-    if (t < a.T) quant_token_row(a.x, a.H, t, lane, a.xq_qs, a.xq_ds);
+    if (t < a.T) quant_token_row(a.xe, a.H, t, lane, a.xq_qs, a.xq_ds);
 }
 
 // ---------------------------------------------------------------------------
@@ -170,7 +171,8 @@ constexpr int kRtLd = kRtK + 8;      // LDS row stride in bf16: conflict-free 16
 constexpr float kRouterBoundRel = 8.0e-5f;
 
 struct RouterMfmaArgs {
-    const float* x;         // [T][H]
+    const float* x;         // [T][H] router input
+    const float* xe;        // [T][H] expert input (quantized to Q8_0 here)
     const float* w;         // [E][ld]
     uint64_t ld;
     int T, H, E;
@@ -198,7 +200,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if ((int)blockIdx.x >= a.n_tiles) {
         const int t = ((int)blockIdx.x - a.n_tiles) * 4 + wave;
-        if (t < a.T) quant_token_row(a.x, a.H, t, lane, a.xq_qs, a.xq_ds);
+        if (t < a.T) quant_token_row(a.xe, a.H, t, lane, a.xq_qs, a.xq_ds);
         return;
     }
     // XCD-aware order: blocks are dealt round-robin to the 8 XCDs, so block b
@@ -297,7 +299,8 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
 struct TopkArgs {
     const float* logits;       // [T][E+1] (approximate on the refined path)
     const float* logit_bound;  // [T][E]   refined path only
-    const float* x;            // [T][H]   refined path only
+    const float* x;            // [T][H]   router input: exact logits (refined path), decode router
+    const float* xe;           // [T][H]   expert input: its Q8_0 (decode routing launch)
     const float* w_router;     // [E][router_ld]
     uint64_t router_ld;
     const float* w_sh_norm;    // [H] or null
@@ -762,6 +765,7 @@ struct SharedGuArgs {
     int n_blocks;  // shared-expert blocks after the router blocks (0: none)
     int tpg;       // tokens per block
     int8_t* hq_qs; float2* hq_ds;
+    int act; const uint16_t* gelu_tab;  // the layer's activation
 };
 
 template <int WT, int LPR>
@@ -790,7 +794,7 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
     int8_t* lq = (int8_t*)s_dyn;                              // [tpg][H] quants
     float2* ld = (float2*)(lq + (size_t)sg.tpg * a.H);        // [tpg][H/32] {d, sum}
     float2* lgu = ld + (size_t)sg.tpg * (a.H >> 5);           // [tpg][32] (g, u)
-    if (wave < nt) quant_x_row(a.x + (uint64_t)(t0 + wave) * a.H, a.H, lane, lq + (size_t)wave * a.H,
+    if (wave < nt) quant_x_row(a.xe + (uint64_t)(t0 + wave) * a.H, a.H, lane, lq + (size_t)wave * a.H,
                                ld + (size_t)wave * (a.H >> 5));
     __syncthreads();
     if (wave < NWA) {
@@ -810,7 +814,7 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
         const int c = tid >> 5, fl = tid & 31;
         const float2 gu = lgu[c * 32 + fl];
         const uint64_t p = (uint64_t)a.T * a.K + t0 + c;
-        swiglu_q8_block32(gu.x, gu.y, fl, sg.hq_qs + p * sg.F + fb * 32, sg.hq_ds + p * nfb + fb);
+        swiglu_q8_block32(gu.x, gu.y, fl, sg.hq_qs + p * sg.F + fb * 32, sg.hq_ds + p * nfb + fb, sg.act, sg.gelu_tab);
     }
 }
 
@@ -904,7 +908,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     }
     // activation quantization: token t by block t % nb, wave (t / nb) % 16
     for (int t = blockIdx.x; t < a.T; t += nb)
-        if (wave == (t / nb) % 16) quant_token_row(a.x, a.H, t, lane, xq_qs, xq_ds);
+        if (wave == (t / nb) % 16) quant_token_row(a.xe, a.H, t, lane, xq_qs, xq_ds);
     // each wave's write-through logit stores complete before the block's flag (a
     // release fence would write back the whole L2 once per wave)
     __builtin_amdgcn_s_waitcnt(0);
@@ -1019,10 +1023,11 @@ bool route_decode_fused(const LayerDesc& L, int T) {
            (L.E + L.S + kRdRows - 1) / kRdRows <= kMaxRdBlocks;
 }
 
-static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, const float* x, int T, bool quant,
-                                      hipStream_t stream) {
+static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, const float* xr, const float* xe, int T,
+                                      bool quant, hipStream_t stream) {
     RouterArgs ra;
-    ra.x = x;
+    ra.x = xr;
+    ra.xe = xe;
     ra.w_router = L.w_router;
     ra.router_ld = L.router_ld;
     ra.w_sh_norm = L.w_sh_norm;
@@ -1041,12 +1046,13 @@ static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, c
     return hipGetLastError();
 }
 
-hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, int T, const RouteDebug& dbg,
-                        hipStream_t stream) {
+hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
+                        const RouteDebug& dbg, hipStream_t stream) {
     TopkArgs ta;
     ta.logits = ws.logits;
     ta.logit_bound = ws.logit_bound;
-    ta.x = x;
+    ta.x = xr;
+    ta.xe = x;
     ta.w_router = L.w_router;
     ta.router_ld = L.router_ld;
     ta.w_sh_norm = L.w_sh_norm;
@@ -1072,7 +1078,8 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     hipError_t err;
     if (route_uses_mfma(L, T)) {
         RouterMfmaArgs ma;
-        ma.x = x;
+        ma.x = xr;
+        ma.xe = x;
         ma.w = L.w_router;
         ma.ld = L.router_ld;
         ma.T = T; ma.H = L.H; ma.E = L.E;
@@ -1093,7 +1100,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
         if (dbg.bound && (err = hipMemcpyAsync(dbg.bound, ws.logit_bound, (size_t)T * L.E * sizeof(float),
                                                hipMemcpyDeviceToDevice, stream)) != hipSuccess)
             return err;
-        if (dbg.exact_logits && (err = launch_router_exact(L, ws, x, T, false, stream)) != hipSuccess) return err;
+        if (dbg.exact_logits && (err = launch_router_exact(L, ws, xr, x, T, false, stream)) != hipSuccess) return err;
     } else if (route_decode_fused(L, T)) {
         // decode: one launch; it also writes the decode slot list and, when the
         // fused gate/up runs next, computes the shared expert's h on idle CUs
@@ -1110,6 +1117,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
             sg.gate_nb1 = L.sh_gate_nb1; sg.up_nb1 = L.sh_up_nb1;
             sg.F = L.F;
             sg.hq_qs = ws.hq_qs; sg.hq_ds = ws.hq_ds;
+            sg.act = L.act; sg.gelu_tab = L.gelu_tab;
         }
         const dim3 g(nb + sg.n_blocks), b(64 * kTopkTokensPerBlock);
         const size_t lds = sizeof(RouteDecodeLds);  // above the 64 KiB default window: raise it
@@ -1133,7 +1141,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
         if ((err = hipLaunchKernel(kern, g, b, args, lds, stream)) != hipSuccess) return err;
         return hipGetLastError();
     } else {
-        if ((err = launch_router_exact(L, ws, x, T, true, stream)) != hipSuccess) return err;
+        if ((err = launch_router_exact(L, ws, xr, x, T, true, stream)) != hipSuccess) return err;
         hipLaunchKernelGGL(k_topk<false>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
         if ((err = hipGetLastError()) != hipSuccess) return err;
     }

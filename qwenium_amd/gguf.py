@@ -5,6 +5,7 @@ Reference behaviour mirrored:
   raw_kv lookups of the MoE hparams          src/models/qwen36.cpp:23-25, 44-53, 97-102
   per-block MoE tensor binding               src/core/model.cpp:233-255 (names in
                                              src/models/qwen36.cpp:543-547)
+  Gemma 4 MoE tensors and hparams             src/models/gemma4.cpp:96-98, 211-215, 297-303
 
 The GGUF block layout is the layer's input layout, so tensors are copied to
 the device byte for byte and wrapped as ggml views; nothing is repacked.
@@ -17,7 +18,7 @@ from typing import Optional
 import torch
 
 from ._lib import QmoeGgufTensor, QmoeTensor, check, lib
-from .moe import GGMLTensor, Hparams, MoELayer
+from .moe import GeGLUMoELayer, GGMLTensor, Hparams, MoELayer
 
 # MoE tensors of block i ("blk.<i>." + name), in the layer's slot order
 MOE_SLOTS = (
@@ -32,6 +33,14 @@ MOE_SLOTS = (
 )
 # Pre-MoE RMSNorm weight of a block (called post_attention_norm in the qwen35moe family, model.cpp:233-235)
 FFN_NORM = "post_attention_norm.weight"
+# Gemma 4 MoE tensors of block i (gemma4.cpp:211-215, 300-303) and its two MoE-branch norms
+GEMMA4_MOE_SLOTS = (
+    ("router", "ffn_gate_inp.weight"),
+    ("gate_up", "ffn_gate_up_exps.weight"),
+    ("down", "ffn_down_exps.weight"),
+)
+GEMMA4_PRE_NORM = "pre_ffw_norm_2.weight"
+GEMMA4_ROUTER_SCALE = "ffn_gate_inp.scale"
 
 
 class GGUFFile:
@@ -161,6 +170,23 @@ class GGUFFile:
     def ffn_norm(self, block: int, device="cuda") -> torch.Tensor:
         """The block's pre-MoE RMSNorm weight [n_embd] f32."""
         return self.upload(f"blk.{block}.{FFN_NORM}", device).data
+
+    def gemma4_moe_layer(self, block: int, device="cuda") -> GeGLUMoELayer:
+        """GeGLUMoELayer of Gemma 4 block `block` (gemma4.* hparams, fused gate_up)."""
+        hp = self.moe_hparams(arch="gemma4", block=block)
+        names = set(self.tensor_names())
+        t = {}
+        for slot, suffix in GEMMA4_MOE_SLOTS:
+            name = f"blk.{block}.{suffix}"
+            if name not in names:
+                raise ValueError(f"gemma4: missing tensor '{name}': expected in block weights, got absent")
+            t[slot] = self.upload(name, device)
+        return GeGLUMoELayer(t["router"], t["gate_up"], t["down"], hp)
+
+    def gemma4_moe_norms(self, block: int, device="cuda"):
+        """(pre_ffw_norm_2, ffn_gate_inp.scale) of Gemma 4 block `block`, [n_embd] f32 each."""
+        return (self.upload(f"blk.{block}.{GEMMA4_PRE_NORM}", device).data,
+                self.upload(f"blk.{block}.{GEMMA4_ROUTER_SCALE}", device).data)
 
 
 def tensor_view(t: QmoeGgufTensor, device_ptr: int) -> QmoeTensor:

@@ -5,6 +5,7 @@ Reference interface (rye-001/Qwenium):
   MoELayer::MoELayer(8 slots) src/layers/moe.h:44-53, src/layers/moe.cpp:27-53
   MoELayer::build(...)        src/layers/moe.h:58-63  -> MoELayer.forward here
   build_rms_norm(...)         src/layers/norm.cpp:15-26 -> rms_norm here
+  Gemma4ForwardPass::build_moe_geglu  src/models/gemma4.cpp:367-445 -> GeGLUMoELayer
 
 torch supplies device memory and the current HIP stream only; every
 computation runs in libqmoe's HIP kernels.
@@ -183,7 +184,98 @@ class MoELayer:
             float(eps), int(x.shape[0]), y.data_ptr(), None, _stream_ptr(stream)))
         return y
 
+    def forward_routed(self, expert_in: torch.Tensor, router_in: torch.Tensor, *, out: Optional[torch.Tensor] = None,
+                       workspace: Optional[Workspace] = None, debug: bool = False, stream=None):
+        """y = MoE(expert_in) routed on router_in (build_moe_geglu's two inputs,
+        gemma4.cpp:367-380); the shared expert's gate, if any, reads router_in."""
+        x = self._check_x(expert_in)
+        xr = self._check_x(router_in)
+        if xr.shape != x.shape:
+            raise ValueError(f"router_in expected shape {tuple(x.shape)}, got {tuple(xr.shape)}")
+        y = out if out is not None else torch.empty_like(x)
+        dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
+        check(lib().qmoe_layer_forward_routed(
+            self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), xr.data_ptr(),
+            int(x.shape[0]), y.data_ptr(), ctypes.byref(dbg) if dbg is not None else None, _stream_ptr(stream)))
+        return (y, dbg_tensors) if debug else y
+
+    def _check_x(self, x: torch.Tensor) -> torch.Tensor:
+        if x.dim() != 2 or x.shape[1] != self.n_embd or x.dtype != torch.float32 or not x.is_cuda:
+            raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got "
+                             f"{tuple(x.shape)} {x.dtype} on {x.device}")
+        return x.contiguous()
+
+    def _debug(self, T: int, dev):
+        E, k = self.hp.n_experts, self.hp.top_k
+        t = {
+            "logits": torch.empty((T, E), dtype=torch.float32, device=dev),
+            "topk_idx": torch.empty((T, k), dtype=torch.int32, device=dev),
+            "topk_w": torch.empty((T, k), dtype=torch.float32, device=dev),
+            "sh_gate": torch.empty((T,), dtype=torch.float32, device=dev),
+            "offsets": torch.empty((E + 1,), dtype=torch.int32, device=dev),
+            "rows": torch.empty((T * k,), dtype=torch.int32, device=dev),
+            "router_approx": torch.full((T, E), float("nan"), dtype=torch.float32, device=dev),
+            "router_bound": torch.full((T, E), float("nan"), dtype=torch.float32, device=dev),
+        }
+        dbg = QmoeDebug(*(t[n].data_ptr() for n in
+                          ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows", "router_approx",
+                           "router_bound")))
+        return dbg, t
+
     __call__ = forward
+
+
+class GeGLUMoELayer(MoELayer):
+    """Gemma 4's MoE (Gemma4ForwardPass::build_moe_geglu, gemma4.cpp:367-445):
+    the fused gate_up tensor [n_embd, 2*ffn_dim, n_experts], GeGLU-tanh
+    (ggml's CPU gelu), no shared expert, the router on its own input."""
+
+    def __init__(self, w_router: GGMLTensor, w_gate_up_exps: GGMLTensor, w_down_exps: GGMLTensor, hp: Hparams):
+        if hp.has_shared_expert:
+            raise ValueError("has_shared_expert expected False for the GeGLU MoE, got True")
+        self.hp = hp
+        self._weights = (w_router, w_gate_up_exps, w_down_exps)
+        descs = [w.desc() for w in self._weights]
+        c_hp = QmoeHparams(int(hp.n_experts), int(hp.top_k), int(hp.ffn_dim), 0)
+        h = ctypes.c_void_p()
+        check(lib().qmoe_geglu_layer_create(*(ctypes.byref(d) for d in descs), ctypes.byref(c_hp), ctypes.byref(h)))
+        self._handle = h
+        self.n_embd = int(lib().qmoe_layer_n_embd(h))
+
+    def forward_gemma4(self, x: torch.Tensor, pre_norm_weight: torch.Tensor, router_scale: torch.Tensor, eps: float,
+                       *, out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None,
+                       debug: bool = False, stream=None):
+        """The Gemma 4 MoE branch from the residual rows x (gemma4.cpp:555-565):
+        build_moe_geglu(rms_norm(x)*pre_norm_weight, (rms_norm(x)/sqrt(n_embd))*router_scale)."""
+        x = self._check_x(x)
+        w, rs = pre_norm_weight.contiguous(), router_scale.contiguous()
+        y = out if out is not None else torch.empty_like(x)
+        dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
+        check(lib().qmoe_layer_forward_gemma4(
+            self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), w.data_ptr(),
+            rs.data_ptr(), float(eps), int(x.shape[0]), y.data_ptr(), ctypes.byref(dbg) if dbg is not None else None,
+            _stream_ptr(stream)))
+        return (y, dbg_tensors) if debug else y
+
+
+def gemma4_moe_inputs(x: torch.Tensor, pre_norm_weight: torch.Tensor, router_scale: torch.Tensor, eps: float,
+                      stream=None):
+    """(expert_in, router_in) of the Gemma 4 MoE branch (gemma4.cpp:555-563)."""
+    x = x.contiguous()
+    ei, ri = torch.empty_like(x), torch.empty_like(x)
+    check(lib().qmoe_gemma4_moe_inputs(x.data_ptr(), pre_norm_weight.contiguous().data_ptr(),
+                                       router_scale.contiguous().data_ptr(), float(eps), int(x.shape[0]),
+                                       int(x.shape[1]), ei.data_ptr(), ri.data_ptr(), _stream_ptr(stream)))
+    return ei, ri
+
+
+def gelu_f16_table():
+    """The 65536-entry fp16 gelu table of the GeGLU kernels (numpy uint16)."""
+    import numpy as np
+
+    out = np.empty(65536, dtype=np.uint16)
+    check(lib().qmoe_gelu_f16_table(out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))))
+    return out
 
 
 def rms_norm(x: torch.Tensor, w: Optional[torch.Tensor], eps: float, out: Optional[torch.Tensor] = None,

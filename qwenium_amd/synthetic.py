@@ -15,7 +15,7 @@ from typing import Optional
 import torch
 
 from ._lib import TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, row_bytes
-from .moe import GGMLTensor, Hparams, MoELayer, synth_f32, synth_quant
+from .moe import GeGLUMoELayer, GGMLTensor, Hparams, MoELayer, synth_f32, synth_quant
 
 SLOTS = ("router", "gate", "up", "down", "sh_gate", "sh_up", "sh_down", "sh_norm")
 
@@ -71,6 +71,7 @@ class LayerSpec:
     sigma: float = 0.02
     router_sigma: float = 0.02
     skew: Optional[Skew] = None
+    geglu: bool = False  # Gemma 4 layout: fused gate_up tensor, GeGLU-tanh, router on its own input
 
     @property
     def hparams(self) -> Hparams:
@@ -82,6 +83,9 @@ CONFIG1 = LayerSpec(1024, 16, 2, 512, False, TYPE_Q8_0)       # ggml CPU-path ca
 QWEN35B = LayerSpec(2048, 256, 8, 512, True, TYPE_Q4_0)       # Qwen3.6-35B-A3B MoE layer
 QWEN35B_Q8 = LayerSpec(2048, 256, 8, 512, True, TYPE_Q8_0)    # same shape, Q8_0 weights
 QWEN35B_SKEW = LayerSpec(2048, 256, 8, 512, True, TYPE_Q8_0, skew=Skew())  # Zipf-skewed routing, Q8_0
+# Gemma 4 26B-A4B MoE layer (gemma4.h:72,89-91: n_embd 2816, 128 experts, top-8, expert ffn 704)
+GEMMA4 = LayerSpec(2816, 128, 8, 704, False, TYPE_Q4_0, geglu=True)
+GEMMA4_Q8 = LayerSpec(2816, 128, 8, 704, False, TYPE_Q8_0, geglu=True)
 
 
 def layer_bytes(spec: LayerSpec) -> dict:
@@ -112,6 +116,11 @@ def make_layer_tensors(spec: LayerSpec, seed: int, layer: int = 0, device="cuda"
     for slot in ("gate", "up"):
         t[slot] = GGMLTensor(synth_quant(wt, E * F, H, seed, stream_id(layer, slot), spec.sigma, device=device),
                              wt, (H, F, E))
+    if spec.geglu:
+        # one [H, 2F, E] tensor: each expert's gate rows, then its up rows (gemma4.cpp:397-409)
+        rb = row_bytes(wt, H)
+        g, u = t.pop("gate").data.view(E, F * rb), t.pop("up").data.view(E, F * rb)
+        t["gate_up"] = GGMLTensor(torch.cat([g, u], dim=1).reshape(-1), wt, (H, 2 * F, E))
     t["down"] = GGMLTensor(synth_quant(wt, E * H, F, seed, stream_id(layer, "down"), spec.sigma, device=device),
                            wt, (F, H, E))
     if spec.shared:
@@ -128,6 +137,8 @@ def make_layer_tensors(spec: LayerSpec, seed: int, layer: int = 0, device="cuda"
 def make_layer(spec: LayerSpec, seed: int, layer: int = 0, device="cuda",
                tensors: Optional[dict] = None) -> MoELayer:
     t = tensors if tensors is not None else make_layer_tensors(spec, seed, layer, device)
+    if spec.geglu:
+        return GeGLUMoELayer(t["router"], t["gate_up"], t["down"], spec.hparams)
     return MoELayer(t["router"], t["gate"], t["up"], t["down"], t.get("sh_gate"), t.get("sh_up"),
                     t.get("sh_down"), t.get("sh_norm"), spec.hparams)
 
@@ -148,6 +159,12 @@ def norm_stream(layer: int) -> int:
 def make_norm_weight(spec: LayerSpec, seed: int, layer: int, device="cuda") -> torch.Tensor:
     """Pre-MoE RMSNorm weight of a stack layer: N(1, 0.02)."""
     return synth_f32(spec.n_embd, seed, norm_stream(layer), 1.0, 0.02, device=device)
+
+
+def make_gemma4_norms(spec: LayerSpec, seed: int, layer: int, device="cuda"):
+    """(pre_ffw_norm_2, ffn_gate_inp.scale) of a Gemma 4 block: N(1, 0.02) each."""
+    return (synth_f32(spec.n_embd, seed, (1 << 42) + 2 * layer, 1.0, 0.02, device=device),
+            synth_f32(spec.n_embd, seed, (1 << 42) + 2 * layer + 1, 1.0, 0.02, device=device))
 
 
 # Pre-MoE RMSNorm epsilon of the layer stack (qwen36.cpp:298 reads it from the GGUF; 1e-6 here).

@@ -235,6 +235,64 @@ static void GGUFLoaderReadsBlockTensors() {
     std::remove(path.c_str());
 }
 
+// ---- Gemma 4 GeGLU MoE through qmoe::GeGLUMoELayer ----
+static void GeGLUConstructorRejectsSharedExpert() {
+    const qmoe_tensor r = qmoe::make_tensor(nullptr, QMOE_TYPE_F32, 2, N_EMBD, N_EXPERTS);
+    const qmoe_tensor gu = qmoe::make_tensor(nullptr, QMOE_TYPE_Q8_0, 3, N_EMBD, 2 * FFN_DIM, N_EXPERTS);
+    const qmoe_tensor d = qmoe::make_tensor(nullptr, QMOE_TYPE_Q8_0, 3, FFN_DIM, N_EMBD, N_EXPERTS);
+    bool threw = false;
+    try {
+        qmoe::GeGLUMoELayer layer(&r, &gu, &d, hparams(true));
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("has_shared_expert") != std::string::npos;
+    }
+    EXPECT(threw, "shared expert rejected");
+}
+
+// Constant weights (router 0.1, gate/up 0.05, down 0.05, input 0.5 as the
+// reference's MoE tests): the Gemma 4 one-call slice equals its two inputs fed
+// to forward(expert_in, router_in), and the output is finite and non-zero.
+static void GeGLUGemma4SliceMatchesRoutedForward() {
+    std::vector<float> router((size_t)N_EMBD * N_EXPERTS, 0.1f);
+    std::vector<uint8_t> gu = q8_const(0.05f, (size_t)N_EXPERTS * 2 * FFN_DIM * N_EMBD);
+    std::vector<uint8_t> dn = q8_const(0.05f, (size_t)N_EXPERTS * N_EMBD * FFN_DIM);
+    std::vector<float> x((size_t)N_TOKENS * N_EMBD), ones(N_EMBD, 1.0f);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = 0.5f + 0.001f * (float)(i % 7);
+    void *d_r, *d_gu, *d_dn, *d_x, *d_w, *d_ei, *d_ri, *d_y0, *d_y1;
+    HIP_OK(hipMalloc(&d_r, router.size() * 4));
+    HIP_OK(hipMalloc(&d_gu, gu.size()));
+    HIP_OK(hipMalloc(&d_dn, dn.size()));
+    for (void** p : {&d_x, &d_ei, &d_ri, &d_y0, &d_y1}) HIP_OK(hipMalloc(p, x.size() * 4));
+    HIP_OK(hipMalloc(&d_w, N_EMBD * 4));
+    HIP_OK(hipMemcpy(d_r, router.data(), router.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_gu, gu.data(), gu.size(), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_dn, dn.data(), dn.size(), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_x, x.data(), x.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_w, ones.data(), N_EMBD * 4, hipMemcpyHostToDevice));
+    const qmoe_tensor r = qmoe::make_tensor(d_r, QMOE_TYPE_F32, 2, N_EMBD, N_EXPERTS);
+    const qmoe_tensor tgu = qmoe::make_tensor(d_gu, QMOE_TYPE_Q8_0, 3, N_EMBD, 2 * FFN_DIM, N_EXPERTS);
+    const qmoe_tensor tdn = qmoe::make_tensor(d_dn, QMOE_TYPE_Q8_0, 3, FFN_DIM, N_EMBD, N_EXPERTS);
+    {
+        qmoe::GeGLUMoELayer layer(&r, &tgu, &tdn, hparams(false));
+        layer.forward_gemma4((const float*)d_x, (const float*)d_w, (const float*)d_w, 1e-6f, N_TOKENS, (float*)d_y0);
+        qmoe::check(qmoe_gemma4_moe_inputs((const float*)d_x, (const float*)d_w, (const float*)d_w, 1e-6f, N_TOKENS,
+                                           N_EMBD, (float*)d_ei, (float*)d_ri, nullptr));
+        layer.forward((const float*)d_ei, (const float*)d_ri, N_TOKENS, (float*)d_y1);
+        HIP_OK(hipDeviceSynchronize());
+        std::vector<float> y0(x.size()), y1(x.size());
+        HIP_OK(hipMemcpy(y0.data(), d_y0, y0.size() * 4, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(y1.data(), d_y1, y1.size() * 4, hipMemcpyDeviceToHost));
+        EXPECT(std::memcmp(y0.data(), y1.data(), y0.size() * 4) == 0, "one-call slice == inputs + routed forward");
+        bool finite = true, nonzero = false;
+        for (float v : y0) {
+            finite = finite && std::isfinite(v);
+            nonzero = nonzero || v != 0.0f;
+        }
+        EXPECT(finite && nonzero, "finite, non-zero output");
+    }
+    for (void* p : {d_r, d_gu, d_dn, d_x, d_w, d_ei, d_ri, d_y0, d_y1}) HIP_OK(hipFree(p));
+}
+
 // ---- MoEResidencyTracker: the reference's cases (tests/unit/test_moe_residency.cpp:17-182) ----
 template <class F>
 static bool throws_runtime(F f, const char* needle) {
@@ -354,6 +412,8 @@ int main(int argc, char** argv) {
     struct Case { const char* name; void (*fn)(); bool gpu; } cases[] = {
         {"ConstructorThrowsWithoutSharedWeights", ConstructorThrowsWithoutSharedWeights, false},
         {"GGUFLoaderReadsBlockTensors", GGUFLoaderReadsBlockTensors, false},
+        {"GeGLUConstructorRejectsSharedExpert", GeGLUConstructorRejectsSharedExpert, false},
+        {"GeGLUGemma4SliceMatchesRoutedForward", GeGLUGemma4SliceMatchesRoutedForward, true},
         {"ResConstructionSucceeds", ResConstructionSucceeds, false},
         {"ResFrequenciesStartAtZero", ResFrequenciesStartAtZero, false},
         {"ResInvalidNExpertsThrows", ResInvalidNExpertsThrows, false},

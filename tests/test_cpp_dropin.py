@@ -17,7 +17,7 @@ def binary():
 def test_cpp_dropin_host_only():
     res = subprocess.run([binary(), "--host-only"], capture_output=True, text=True, timeout=120)
     assert res.returncode == 0, res.stdout + res.stderr
-    assert "18 tests, 0 failures" in res.stdout
+    assert "19 tests, 0 failures" in res.stdout
 
 
 @pytest.mark.gpu
@@ -25,4 +25,4 @@ def test_cpp_dropin_gpu(gpu):
     res = subprocess.run([binary()], capture_output=True, text=True, timeout=120)
     print(res.stdout)
     assert res.returncode == 0, res.stdout + res.stderr
-    assert "25 tests, 0 failures" in res.stdout
+    assert "27 tests, 0 failures" in res.stdout

@@ -255,3 +255,40 @@ def test_gguf_layer_matches_in_memory_layer(gpu, tmp_path, which):
                 assert torch.equal(yg, ym), (blk, T)
             w = f.ffn_norm(blk)
             assert torch.equal(w, S.make_norm_weight(spec, 3, blk))
+
+
+@pytest.mark.gpu
+def test_gguf_gemma4_layer_matches_in_memory_layer(gpu, tmp_path):
+    """A Gemma 4 block (fused ffn_gate_up_exps, gemma4.* hparams, the MoE-branch
+    norms) read from a file gives the bits of the in-memory layer."""
+    import torch
+
+    from qwenium_amd import Workspace
+    from qwenium_amd import synthetic as S
+
+    spec = S.LayerSpec(512, 16, 4, 128, False, TYPE_Q4_0, geglu=True)
+    kv = [("general.architecture", W.STR, "gemma4"), ("gemma4.expert_count", W.U32, spec.n_experts),
+          ("gemma4.expert_used_count", W.U32, spec.top_k),
+          ("gemma4.expert_feed_forward_length", W.U32, spec.ffn_dim)]
+    t = S.make_layer_tensors(spec, 5)
+    pre, rs = S.make_gemma4_norms(spec, 5, 0)
+    tens = [(f"blk.0.{suffix}", t[slot].type, tuple(t[slot].ne), t[slot].data.cpu().numpy().tobytes())
+            for slot, suffix in G.GEMMA4_MOE_SLOTS]
+    tens += [(f"blk.0.{G.GEMMA4_PRE_NORM}", TYPE_F32, (spec.n_embd,), pre.cpu().numpy().tobytes()),
+             (f"blk.0.{G.GEMMA4_ROUTER_SCALE}", TYPE_F32, (spec.n_embd,), rs.cpu().numpy().tobytes())]
+    p = str(tmp_path / "gemma4.gguf")
+    W.write_gguf(p, kv, tens)
+    lm = S.make_layer(spec, 5, tensors=t)
+    with G.GGUFFile(p) as f:
+        lg = f.gemma4_moe_layer(0)
+        pg, rg = f.gemma4_moe_norms(0)
+        assert torch.equal(pg, pre) and torch.equal(rg, rs)
+        for T in (1, 10, 200):
+            x = S.make_x(spec, T, seed=5, batch=T)
+            ws = Workspace(lg, T)
+            yg = lg.forward_gemma4(x, pg, rg, 1e-6, workspace=ws)
+            ym = lm.forward_gemma4(x, pre, rs, 1e-6, workspace=ws)
+            torch.cuda.synchronize()
+            assert torch.equal(yg, ym), T
+        with pytest.raises(ValueError, match="gemma4: missing tensor 'blk.1.ffn_gate_inp.weight'"):
+            f.gemma4_moe_layer(1)
