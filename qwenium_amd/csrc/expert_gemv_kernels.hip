@@ -619,8 +619,16 @@ __global__ __launch_bounds__(256) void k_down_combine_tok(DownCombineArgs a) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
     extern __shared__ __align__(16) uint8_t s_dyn[];
-    const int rg = blockIdx.x / a.T;
-    const int t = blockIdx.x - rg * a.T;  // tokens fastest: neighbouring blocks share experts' rows in L2
+    // Workgroups are dealt round-robin to the 8 XCDs (block b to XCD b % 8), each
+    // with its own L2.  Logical block g = (b % 8) * (G / 8) + b / 8 gives every
+    // XCD a contiguous run of row groups with all their tokens, dispatched
+    // together: the tokens of a row group read the same expert rows (shared
+    // expert always, routed experts often) through one L2.
+    const int G = gridDim.x;
+    const int b = blockIdx.x;
+    const int g = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+    const int rg = g / a.T;
+    const int t = g - rg * a.T;  // tokens fastest within an XCD's run
     const int nj = a.K + a.S;
     // the token's steps (wave-uniform: scalar loads); steps past nj repeat the last one
     int se[NJ], sp[NJ];

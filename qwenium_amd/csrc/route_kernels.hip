@@ -319,6 +319,7 @@ struct TopkArgs {
     int4* slot_info;      // [E+1] {expert, first row, rows, token of first row}
     int4* dslots;         // [E+2] decode slot list (fused decode routing only, else null)
     unsigned long long* expert_counts;  // optional [E]: per-expert dispatch counts accumulated
+    int defer_softmax;    // 1: the selection leaves the softmax to the caller (token_softmax)
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
@@ -428,6 +429,44 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// Whole-wave maximum of a u32 (one DPP max per step), returned to every lane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#define QMOE_MAXU32_STEP(CTRL, RM) \
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, RM, 0xF, false))
+    QMOE_MAXU32_STEP(kDppQuadXor1, 0xF);
+    QMOE_MAXU32_STEP(kDppQuadXor2, 0xF);
+    QMOE_MAXU32_STEP(kDppRowHalfMirror, 0xF);
+    QMOE_MAXU32_STEP(kDppRowMirror, 0xF);
+    QMOE_MAXU32_STEP(kDppRowBcast15, 0xA);
+    QMOE_MAXU32_STEP(kDppRowBcast31, 0xC);
+#undef QMOE_MAXU32_STEP
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Softmax over a token's selected logits (s_val_row[0..K-1], slot 0 holds the
+// maximum): exps in parallel lanes, the sum in slot order, the divisions in
+// parallel lanes; and the shared-expert gate.  One wave.
+__device__ void token_softmax(const TopkArgs& a, int t, int lane, const float* s_val_row, double* s_ex_row,
+                              float sg_logit) {
+#pragma clang fp contract(off)
+    const double m = (double)s_val_row[0];
+    double ex = 0.0;
+    if (lane < a.K) {
+        ex = exp_det((double)s_val_row[lane] - m);
+        s_ex_row[lane] = ex;
+    }
+    if (lane == a.K && a.S) a.sh_gate[t] = sigmoid_det(sg_logit);
+    wave_lds_sync();
+    double sum = 0.0;
+    if (lane == 0) {
+        for (int j = 0; j < a.K; ++j) sum = sum + s_ex_row[j];
+        s_ex_row[kMaxTopK] = sum;
+    }
+    wave_lds_sync();
+    sum = s_ex_row[kMaxTopK];
+    if (lane < a.K) a.topk_w[(uint64_t)t * a.K + lane] = (float)(ex / sum);
+}
+
 // Top-k of one token from per-lane candidates (expert e = i*64 + lane in
 // v[i]/id[i], id INT_MAX for none), softmax over the selected logits and the
 // shared-expert gate.  One wave.  Each lane sorts its keys (compare-exchange
@@ -435,7 +474,7 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
 // winning lane pops its head.
 template <int EPL>
 __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EPL], int (&id)[EPL], float sg_logit,
-                               int32_t* s_idx_row, float* s_val_row, double* s_ex_row) {
+                               int32_t* s_idx_row, float* s_val_row, double* s_ex_row, float* s_sg) {
     uint64_t key[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) key[i] = id[i] == 0x7fffffff ? 0ull : sel_key(v[i], id[i]);
@@ -449,7 +488,18 @@ __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EP
             key[j] = lo;
         }
     for (int j = 0; j < a.K; ++j) {
-        const uint64_t best = wave_max_key(key[0]);
+        // the largest head: the value word's maximum first; the full keys (lowest
+        // expert id among equal values) only when several lanes hold that value
+        const uint32_t hi = (uint32_t)(key[0] >> 32);
+        const uint32_t mh = wave_max_u32(hi);
+        const uint64_t at = __ballot(hi == mh);
+        uint64_t best;
+        if ((at & (at - 1)) == 0) {
+            const int wl = __builtin_ctzll(at);
+            best = ((uint64_t)mh << 32) | (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], wl);
+        } else {
+            best = wave_max_key(hi == mh ? key[0] : 0ull);
+        }
         const bool pop = key[0] == best;  // exactly one lane: keys are distinct
 #pragma unroll
         for (int i = 0; i + 1 < EPL; ++i) key[i] = pop ? key[i + 1] : key[i];
@@ -463,33 +513,17 @@ __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EP
     }
     // lanes below read what lane 0 wrote to LDS: order the wave's LDS accesses
     wave_lds_sync();
-    // softmax over the selected logits (slot 0 holds the maximum): exps in
-    // parallel lanes, the sum in slot order, the divisions in parallel lanes
-    {
-#pragma clang fp contract(off)
-        const double m = (double)s_val_row[0];
-        double ex = 0.0;
-        if (lane < a.K) {
-            ex = exp_det((double)s_val_row[lane] - m);
-            s_ex_row[lane] = ex;
-        }
-        if (lane == a.K && a.S) a.sh_gate[t] = sigmoid_det(sg_logit);
-        wave_lds_sync();
-        double sum = 0.0;
-        if (lane == 0) {
-            for (int j = 0; j < a.K; ++j) sum = sum + s_ex_row[j];
-            s_ex_row[kMaxTopK] = sum;
-        }
-        wave_lds_sync();
-        sum = s_ex_row[kMaxTopK];
-        if (lane < a.K) a.topk_w[(uint64_t)t * a.K + lane] = (float)(ex / sum);
+    if (a.defer_softmax) {
+        if (lane == 0 && s_sg) *s_sg = sg_logit;
+        return;
     }
+    token_softmax(a, t, lane, s_val_row, s_ex_row, sg_logit);
 }
 
 // Top-k from exact logits.
 template <int EPL>
 __device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_idx_row, float* s_val_row,
-                               double* s_ex_row) {
+                               double* s_ex_row, float* s_sg) {
     const float* l = a.logits + (uint64_t)t * (a.E + 1);
     float v[EPL];
     int id[EPL];
@@ -500,7 +534,7 @@ __device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_id
         v[i] = e < a.E ? lv : -__builtin_huge_valf();
         id[i] = e < a.E ? e : 0x7fffffff;
     }
-    select_softmax<EPL>(a, t, lane, v, id, a.S ? l[a.E] : 0.0f, s_idx_row, s_val_row, s_ex_row);
+    select_softmax<EPL>(a, t, lane, v, id, a.S ? l[a.E] : 0.0f, s_idx_row, s_val_row, s_ex_row, s_sg);
 }
 
 // Top-k from approximate logits L~ with bounds d (|L~ - L| <= d): thr = the
@@ -572,16 +606,17 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
         float sg2;
         exact_dot2(a.w_sh_norm, a.w_sh_norm, xr, a.H, lane, sg, sg2);
     }
-    select_softmax<EPL>(a, t, lane, v, id, sg, s_idx_row, s_val_row, s_ex_row);
+    select_softmax<EPL>(a, t, lane, v, id, sg, s_idx_row, s_val_row, s_ex_row, nullptr);
 }
 
+// s_sg (deferred softmax only): where the shared-gate logit is kept for token_softmax.
 template <bool REFINE>
 __device__ __forceinline__ void topk_dispatch(const TopkArgs& a, int t, int lane, int32_t* s_idx_row,
-                                              float* s_val_row, double* s_ex_row) {
+                                              float* s_val_row, double* s_ex_row, float* s_sg = nullptr) {
     const int epl = (a.E + 63) >> 6;
 #define QMOE_TOPK_CASE(N)                                                   \
     if (REFINE) topk_refine_token<N>(a, t, lane, s_idx_row, s_val_row, s_ex_row); \
-    else topk_one_token<N>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+    else topk_one_token<N>(a, t, lane, s_idx_row, s_val_row, s_ex_row, s_sg);
     if (epl <= 1) { QMOE_TOPK_CASE(1) }
     else if (epl <= 2) { QMOE_TOPK_CASE(2) }
     else if (epl <= 4) { QMOE_TOPK_CASE(4) }
@@ -695,6 +730,7 @@ struct SmallRouteLds {
     int32_t idx[kTopkTokensPerBlock][kMaxTopK];
     float val[kTopkTokensPerBlock][kMaxTopK];
     double ex[kTopkTokensPerBlock][kMaxTopK + 1];
+    float sg[kTopkTokensPerBlock];  // shared-gate logits (deferred softmax)
     uint32_t mask[1024];
     int32_t cnt[1024];
     int32_t off[1024];
@@ -707,7 +743,7 @@ __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
     for (int e = tid; e < a.E; e += blockDim.x) L.mask[e] = 0;
     __syncthreads();
     if (wave < a.T) {
-        topk_dispatch<false>(a, wave, lane, L.idx[wave], L.val[wave], L.ex[wave]);
+        topk_dispatch<false>(a, wave, lane, L.idx[wave], L.val[wave], L.ex[wave], &L.sg[wave]);
         if (lane < a.K) atomicOr(&L.mask[L.idx[wave][lane]], 1u << wave);
     }
     __syncthreads();
@@ -726,6 +762,13 @@ __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
     if (a.S && tid < a.T) {
         a.rows[A + tid] = -1;
         a.row_token[A + tid] = tid;
+    }
+    if (a.defer_softmax) {
+        // the softmax of every token, on the waves the scatter above leaves idle:
+        // off the path from the top-k to the end of the routing
+        const int w0 = (A + 63) >> 6 < 16 ? (A + 63) >> 6 : 0;
+        for (int t = wave - w0; t >= 0 && t < a.T; t += 16 - w0)
+            token_softmax(a, t, lane, L.val[t], L.ex[t], L.sg[t]);
     }
 }
 
@@ -769,7 +812,8 @@ struct SharedGuArgs {
 };
 
 template <int WT, int LPR>
-__device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const SharedGuArgs& sg, int j, uint8_t* s_dyn) {
+__device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const SharedGuArgs& sg, int j, uint8_t* s_dyn,
+                                                    int8_t* xq_qs, float2* xq_ds) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
     constexpr int RPW = RPI > 2 ? RPI : 2;  // ffn rows per wave
@@ -797,6 +841,19 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
     if (wave < nt) quant_x_row(a.xe + (uint64_t)(t0 + wave) * a.H, a.H, lane, lq + (size_t)wave * a.H,
                                ld + (size_t)wave * (a.H >> 5));
     __syncthreads();
+    if (fb == 0) {
+        // the workspace copy of these tokens' Q8_0 rows (the routed experts read it),
+        // so the router blocks raise their flags without quantizing
+        const int cq = a.H >> 4, cd = a.H >> 6;  // 16-byte chunks per row: quants, {d, sum} pairs
+        for (int i = tid; i < nt * (cq + cd); i += blockDim.x) {
+            const int c = i / (cq + cd), k = i - c * (cq + cd);
+            if (k < cq)
+                ((u32x4*)(xq_qs + (uint64_t)(t0 + c) * a.H))[k] = ((const u32x4*)(lq + (size_t)c * a.H))[k];
+            else
+                ((u32x4*)(xq_ds + (uint64_t)(t0 + c) * (a.H >> 5)))[k - cq] =
+                    ((const u32x4*)(ld + (size_t)c * (a.H >> 5)))[k - cq];
+        }
+    }
     if (wave < NWA) {
         for (int c = 0; c < nt; ++c) {
             XPair x;
@@ -828,7 +885,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     const int nb = gridDim.x - sg.n_blocks;  // router blocks
     if constexpr (SWT != 0) {
         if ((int)blockIdx.x >= nb) {
-            shared_gateup_block<SWT, SLPR>(a, sg, blockIdx.x - nb, s_dyn);
+            shared_gateup_block<SWT, SLPR>(a, sg, blockIdx.x - nb, s_dyn, xq_qs, xq_ds);
             return;
         }
     }
@@ -906,9 +963,11 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
                                __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    // activation quantization: token t by block t % nb, wave (t / nb) % 16
-    for (int t = blockIdx.x; t < a.T; t += nb)
-        if (wave == (t / nb) % 16) quant_token_row(a.xe, a.H, t, lane, xq_qs, xq_ds);
+    // activation quantization (the shared-expert blocks do it when there are
+    // any): token t by block t % nb, wave (t / nb) % 16
+    if (SWT == 0)
+        for (int t = blockIdx.x; t < a.T; t += nb)
+            if (wave == (t / nb) % 16) quant_token_row(a.xe, a.H, t, lane, xq_qs, xq_ds);
     // each wave's write-through logit stores complete before the block's flag (a
     // release fence would write back the whole L2 once per wave)
     __builtin_amdgcn_s_waitcnt(0);
@@ -1071,6 +1130,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     ta.slot_info = ws.slot_info;
     ta.dslots = nullptr;
     ta.expert_counts = L.expert_counts;
+    ta.defer_softmax = 0;
     ta.counters = ws.counters;
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
@@ -1105,6 +1165,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
         // decode: one launch; it also writes the decode slot list and, when the
         // fused gate/up runs next, computes the shared expert's h on idle CUs
         ta.dslots = ws.dslots;
+        ta.defer_softmax = 1;
         const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
         const int nslab = L.H / kRdSlab;
         SharedGuArgs sg{};
