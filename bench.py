@@ -389,6 +389,11 @@ def main() -> int:
             yr, dr = host_layer(0).forward(g4_in[0][0].cpu().numpy()[:n_chk], debug=True,
                                            router_in=g4_in[0][1].cpu().numpy()[:n_chk])
             checks.append((0, yl.cpu().numpy()[:n_chk], yr, dbg["topk_idx"].cpu().numpy()[:n_chk], dr["topk_idx"]))
+        else:
+            yl, dbg = layers[0].forward(xs[0], workspace=ws, debug=True)
+            torch.cuda.synchronize()
+            yr, dr = host_layer(0).forward(xs[0].cpu().numpy()[:n_chk], debug=True)
+            checks.append((0, yl.cpu().numpy()[:n_chk], yr, dbg["topk_idx"].cpu().numpy()[:n_chk], dr["topk_idx"]))
         result_parity = {"tokens_checked": n_chk, "layers_checked": [c[0] for c in checks]}
         for (l, yg, yr, ig, ir) in checks:
             rms = float(np.sqrt(np.mean(yr.astype(np.float64) ** 2)))
