@@ -785,14 +785,18 @@ constexpr int kRdRows = 2;          // router rows per block
 constexpr int kRdParts = 8;         // waves per row
 constexpr int kRdSlab = 256;        // columns per lane-float4 sweep
 constexpr int kMaxRdSlabs = 16;     // fused decode routing for H <= 4096
-constexpr int kRdXBytes = 96 * 1024;
+constexpr int kRdXBytes = 96 * 1024;  // x staging window (H <= 2048: all of x at T <= 12)
+// H > 2048 (two slabs per wave): a wider window keeps more tokens in one staging round
+template <int NSW> constexpr int kRdXBytesFor = NSW == 1 ? kRdXBytes : 128 * 1024;
 constexpr int kMaxSpins = 1 << 22;  // bounded wait: a flag that never comes raises the error word
 constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
 
+template <int XB>
 union RouteDecodeLds {
-    float x[kRdXBytes / 4];
+    float x[XB / 4];
     SmallRouteLds route;
 };
+static_assert(sizeof(SmallRouteLds) <= kRdXBytes, "the routing tables fit the smallest staging window");
 
 // Shared expert at decode: its gate/up, SwiGLU and Q8_0 of h do not depend on
 // the routing, so blocks after the router blocks compute them meanwhile on
@@ -879,7 +883,8 @@ template <int NSW, int SWT, int SLPR>  // NSW: router slabs per wave (ceil(H/256
 __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits, int8_t* xq_qs, float2* xq_ds,
                                                        int32_t* sync, SharedGuArgs sg) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
-    RouteDecodeLds& S = *(RouteDecodeLds*)s_dyn;
+    constexpr int XB = kRdXBytesFor<NSW>;
+    RouteDecodeLds<XB>& S = *(RouteDecodeLds<XB>*)s_dyn;
     __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nb = gridDim.x - sg.n_blocks;  // router blocks
@@ -903,10 +908,10 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     double acc[kTopkTokensPerBlock];
 #pragma unroll
     for (int t = 0; t < kTopkTokensPerBlock; ++t) acc[t] = 0.0;
-    // chunk = as many slabs as fit: T * chunk * 4 bytes <= kRdXBytes
-    const int cslabs = max(1, min(nslab, kRdXBytes / (a.T * kRdSlab * 4)));
+    // chunk = as many slabs as fit: T * chunk * 4 bytes <= XB
+    const int cslabs = max(1, min(nslab, XB / (a.T * kRdSlab * 4)));
     const int ccols = cslabs * kRdSlab;
-    constexpr int kStagePerThread = kRdXBytes / 16 / 1024;  // float4 moves per thread per chunk
+    constexpr int kStagePerThread = XB / 16 / 1024;  // float4 moves per thread per chunk
     for (int s0 = 0; s0 < nslab; s0 += cslabs) {
         const int ns = min(cslabs, nslab - s0);
         const int q4 = ns * kRdSlab / 4;  // float4 per token in this chunk
@@ -1181,7 +1186,8 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
             sg.act = L.act; sg.gelu_tab = L.gelu_tab;
         }
         const dim3 g(nb + sg.n_blocks), b(64 * kTopkTokensPerBlock);
-        const size_t lds = sizeof(RouteDecodeLds);  // above the 64 KiB default window: raise it
+        // above the 64 KiB default window: raise it
+        const size_t lds = nslab <= kRdParts ? sizeof(RouteDecodeLds<kRdXBytesFor<1>>) : sizeof(RouteDecodeLds<kRdXBytesFor<2>>);
         const int lpr = L.H <= 1024 ? 16 : (L.H <= 2048 ? 32 : 64);
         const void* kern;
         if (nslab <= kRdParts) {
