@@ -285,7 +285,9 @@ template <> constexpr int kGqWaves<kTypeQ8_0> = 8;
 
 __host__ __device__ constexpr size_t gq_lds_bytes(int T, int H) { return (size_t)T * H + (size_t)T * (H / 32) * 8; }
 
-template <int WT, int LPR, int NW>
+// PPL: Q8_0 block pairs per lane of a row (pairs lp, lp + LPR, ...): LPR * PPL >= H / 64.
+// Each pair's contribution is exact in f64, so any split sums to the same bits.
+template <int WT, int LPR, int NW, int PPL>
 __global__ __launch_bounds__(NW * 64, GQ_MIN_WAVES) void k_gateup_q(ExpertArgs a, const int4* dslots) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
@@ -304,8 +306,14 @@ __global__ __launch_bounds__(NW * 64, GQ_MIN_WAVES) void k_gateup_q(ExpertArgs a
     const uint32_t mask = (uint32_t)si.w;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int sub = lane / LPR, lp = lane % LPR;
-    const int pair = min(lp, (a.H >> 6) - 1);  // lanes past the row re-read the last pair; their sums are dropped
-    const bool live = lp < (a.H >> 6);
+    // lanes past the row re-read the last pair; their sums are dropped
+    int pairk[PPL];
+    bool livek[PPL];
+#pragma unroll
+    for (int k = 0; k < PPL; ++k) {
+        livek[k] = lp + k * LPR < (a.H >> 6);
+        pairk[k] = min(lp + k * LPR, (a.H >> 6) - 1);
+    }
     // token rows of the slot -> LDS: quants [nrows][H], then {d, sum} [nrows][H/32]
     int8_t* lq = (int8_t*)s_dyn;
     float2* ld = (float2*)(lq + (size_t)nrows * a.H);
@@ -342,12 +350,15 @@ __global__ __launch_bounds__(NW * 64, GQ_MIN_WAVES) void k_gateup_q(ExpertArgs a
     const uint64_t gnb1 = sh ? a.sh_gate_nb1 : a.gate_nb1;
     const uint64_t unb1 = sh ? a.sh_up_nb1 : a.up_nb1;
     const int fw = fb * 32 + wave * RPW;
-    WPair<WT> wg[NI], wu[NI];
+    WPair<WT> wg[NI][PPL], wu[NI][PPL];
 #pragma unroll
     for (int m = 0; m < NI; ++m) {
         const int f = fw + m * RPI + sub;
-        wg[m].load(gb + (uint64_t)f * gnb1, pair);
-        wu[m].load(ub + (uint64_t)f * unb1, pair);
+#pragma unroll
+        for (int k = 0; k < PPL; ++k) {
+            wg[m][k].load(gb + (uint64_t)f * gnb1, pairk[k]);
+            wu[m][k].load(ub + (uint64_t)f * unb1, pairk[k]);
+        }
     }
     stage_store(0);
     for (int base = kStage * NT; base < nc; base += kStage * NT) {  // rows past the first round
@@ -361,32 +372,48 @@ __global__ __launch_bounds__(NW * 64, GQ_MIN_WAVES) void k_gateup_q(ExpertArgs a
 #pragma unroll
         for (int m = 0; m < NI; ++m) {
 #pragma unroll
-            for (int k = 0; k < (int)(sizeof(wg[m].w) / 4); ++k) {
-                asm volatile("" : "+v"(wg[m].w[k]));
-                asm volatile("" : "+v"(wu[m].w[k]));
+            for (int k = 0; k < PPL; ++k) {
+#pragma unroll
+                for (int i = 0; i < (int)(sizeof(wg[m][k].w) / 4); ++i) {
+                    asm volatile("" : "+v"(wg[m][k].w[i]));
+                    asm volatile("" : "+v"(wu[m][k].w[i]));
+                }
             }
         }
         // activations stream through 4 registers, one 16-byte chunk at a time,
         // re-read from LDS for each row group so its weights die after use
-        const u32x4* xq = (const u32x4*)(lq + (size_t)c * a.H + 64 * pair);
-        const u32x4 xd = *(const u32x4*)(ld + (size_t)c * (a.H >> 5) + 2 * pair);  // {dA, sumA, dB, sumB}
-        const int za = -WPair<WT>::kZero * (int)xd.y, zb = -WPair<WT>::kZero * (int)xd.w;
-        const float dxa = __builtin_bit_cast(float, (uint32_t)xd.x), dxb = __builtin_bit_cast(float, (uint32_t)xd.z);
 #pragma unroll
         for (int m = 0; m < NI; ++m) {
-            u32x4 xc = xq[0];
-            int ga = wg[m].template dot_chunk<0>(xc, za), ua = wu[m].template dot_chunk<0>(xc, za);
-            xc = xq[1];
-            ga = wg[m].template dot_chunk<1>(xc, ga); ua = wu[m].template dot_chunk<1>(xc, ua);
-            xc = xq[2];
-            int gb = wg[m].template dot_chunk<2>(xc, zb), ub = wu[m].template dot_chunk<2>(xc, zb);
-            xc = xq[3];
-            gb = wg[m].template dot_chunk<3>(xc, gb); ub = wu[m].template dot_chunk<3>(xc, ub);
-            const double pg = __builtin_fma((double)(wg[m].dA() * dxa), (double)ga, (double)(wg[m].dB() * dxb) * (double)gb);
-            const double pu = __builtin_fma((double)(wu[m].dA() * dxa), (double)ua, (double)(wu[m].dB() * dxb) * (double)ub);
-            const double g = dpp_sum_f64<LPR>(live ? pg : 0.0);
-            const double u = dpp_sum_f64<LPR>(live ? pu : 0.0);
-            if (lp == LPR - 1) s_gu[c][wave * RPW + m * RPI + sub] = make_float2((float)g, (float)u);
+            double pg = 0.0, pu = 0.0;
+#pragma unroll
+            for (int k = 0; k < PPL; ++k) {
+                const u32x4* xq = (const u32x4*)(lq + (size_t)c * a.H + 64 * pairk[k]);
+                const u32x4 xd = *(const u32x4*)(ld + (size_t)c * (a.H >> 5) + 2 * pairk[k]);  // {dA, sumA, dB, sumB}
+                const int za = -WPair<WT>::kZero * (int)xd.y, zb = -WPair<WT>::kZero * (int)xd.w;
+                const float dxa = __builtin_bit_cast(float, (uint32_t)xd.x), dxb = __builtin_bit_cast(float, (uint32_t)xd.z);
+                const WPair<WT>& g = wg[m][k];
+                const WPair<WT>& u = wu[m][k];
+                u32x4 xc = xq[0];
+                int ga = g.template dot_chunk<0>(xc, za), ua = u.template dot_chunk<0>(xc, za);
+                xc = xq[1];
+                ga = g.template dot_chunk<1>(xc, ga); ua = u.template dot_chunk<1>(xc, ua);
+                xc = xq[2];
+                int gbs = g.template dot_chunk<2>(xc, zb), ubs = u.template dot_chunk<2>(xc, zb);
+                xc = xq[3];
+                gbs = g.template dot_chunk<3>(xc, gbs); ubs = u.template dot_chunk<3>(xc, ubs);
+                const double tg = __builtin_fma((double)(g.dA() * dxa), (double)ga, (double)(g.dB() * dxb) * (double)gbs);
+                const double tu = __builtin_fma((double)(u.dA() * dxa), (double)ua, (double)(u.dB() * dxb) * (double)ubs);
+                if (k == 0) {  // dead lanes contribute +0.0, as a single-pair lane always did
+                    pg = livek[0] ? tg : 0.0;
+                    pu = livek[0] ? tu : 0.0;
+                } else if (livek[k]) {
+                    pg = pg + tg;
+                    pu = pu + tu;
+                }
+            }
+            const double gs = dpp_sum_f64<LPR>(pg);
+            const double us = dpp_sum_f64<LPR>(pu);
+            if (lp == LPR - 1) s_gu[c][wave * RPW + m * RPI + sub] = make_float2((float)gs, (float)us);
         }
     }
     __syncthreads();
@@ -847,9 +874,11 @@ static hipError_t launch_gateup_q_t(const ExpertArgs& a, const int4* dslots, int
     const dim3 g(max_v * (a.F / 32));
     const size_t lds = gq_lds_bytes(a.T, a.H);
     constexpr int NW = kGqWaves<WT>;
-    if (npairs <= 16) launch_timed(k_gateup_q<WT, 16, NW>, g, dim3(NW * 64), lds, stream, e0, e1, a, dslots);
-    else if (npairs <= 32) launch_timed(k_gateup_q<WT, 32, NW>, g, dim3(NW * 64), lds, stream, e0, e1, a, dslots);
-    else launch_timed(k_gateup_q<WT, 64, 8>, g, dim3(512), lds, stream, e0, e1, a, dslots);
+    // lanes x pairs per row: 16 x 1, 32 x 1, 16 x 3 (H = 2816: 44 of 48 slots live), 64 x 1
+    if (npairs <= 16) launch_timed(k_gateup_q<WT, 16, NW, 1>, g, dim3(NW * 64), lds, stream, e0, e1, a, dslots);
+    else if (npairs <= 32) launch_timed(k_gateup_q<WT, 32, NW, 1>, g, dim3(NW * 64), lds, stream, e0, e1, a, dslots);
+    else if (npairs <= 48) launch_timed(k_gateup_q<WT, 16, NW, 3>, g, dim3(NW * 64), lds, stream, e0, e1, a, dslots);
+    else launch_timed(k_gateup_q<WT, 64, 8, 1>, g, dim3(512), lds, stream, e0, e1, a, dslots);
     return hipGetLastError();
 }
 
