@@ -775,9 +775,11 @@ __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
 // Fused decode routing (T <= kTopkTokensPerBlock): block b computes router
 // rows 2b, 2b+1 (row E is the shared-expert gate) for all tokens, eight waves
 // per row (wave p takes the 256-column slabs p, p+8; the eight partial sums
-// are added in order), with x staged through LDS in column chunks as wide as
-// 96 KiB allows (all of H for T <= 12 at H = 2048), and quantizes tokens
-// t = b (mod gridDim.x); then raises its flag.  Block 0 waits for every other
+// are added in order).  With one slab per wave (H <= 2048) each wave loads its
+// x columns straight from memory; wider rows stage x through LDS in column
+// chunks as wide as the staging window allows.  Without a shared expert the
+// router blocks also quantize tokens t = b (mod gridDim.x).  Then the block
+// raises its flag.  Block 0 waits for every other
 // block's flag (it waits on nothing else, and the other blocks wait on
 // nothing), then runs the whole routing on the exact logits.  Flags carry the
 // forward's generation number, so nothing is reset between forwards.
@@ -908,6 +910,31 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     double acc[kTopkTokensPerBlock];
 #pragma unroll
     for (int t = 0; t < kTopkTokensPerBlock; ++t) acc[t] = 0.0;
+    if constexpr (NSW == 1) {
+        // one slab per wave: its x columns come straight from memory (L2), eight
+        // tokens' float4 in flight at a time, no LDS round trip or barrier
+        if (has_row && part < nslab) {
+            const float* xs = a.x + part * kRdSlab + 4 * lane;
+            for (int t0 = 0; t0 < a.T; t0 += 8) {
+                f32x4 xv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) xv[u] = *(const f32x4*)(xs + (uint64_t)min(t0 + u, a.T - 1) * a.H);
+                const double w0 = w[0].x, w1 = w[0].y, w2 = w[0].z, w3 = w[0].w;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+#pragma unroll
+                    for (int t = 0; t < kTopkTokensPerBlock; ++t) {
+                        if (t == t0 + u && t < a.T) {
+                            acc[t] = __builtin_fma(w0, (double)xv[u].x, acc[t]);
+                            acc[t] = __builtin_fma(w1, (double)xv[u].y, acc[t]);
+                            acc[t] = __builtin_fma(w2, (double)xv[u].z, acc[t]);
+                            acc[t] = __builtin_fma(w3, (double)xv[u].w, acc[t]);
+                        }
+                    }
+                }
+            }
+        }
+    } else {
     // chunk = as many slabs as fit: T * chunk * 4 bytes <= XB
     const int cslabs = max(1, min(nslab, XB / (a.T * kRdSlab * 4)));
     const int ccols = cslabs * kRdSlab;
@@ -947,6 +974,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
                 }
             }
         }
+    }
     }
 #pragma unroll
     for (int t = 0; t < kTopkTokensPerBlock; ++t) {
