@@ -793,6 +793,37 @@ template <int NSW> constexpr int kRdXBytesFor = NSW == 1 ? kRdXBytes : 128 * 102
 constexpr int kMaxSpins = 1 << 22;  // bounded wait: a flag that never comes raises the error word
 constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
 
+// One reduce-scatter step over an f64 pair (x, y): the 32-lane swap (W = 32)
+// leaves lanes 0..31 with x[l] + x[l + 32] and lanes 32..63 with y[l - 32] + y[l];
+// the 16-lane swap (W = 16) does the same between the even and odd rows of 16.
+template <int W>
+__device__ __forceinline__ double swap_add_f64(double x, double y) {
+    const uint64_t bx = __builtin_bit_cast(uint64_t, x), by = __builtin_bit_cast(uint64_t, y);
+    uint32_t a_lo, a_hi, b_lo, b_hi;
+    if constexpr (W == 32) {
+        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)bx, (uint32_t)by, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(bx >> 32), (uint32_t)(by >> 32), false, false);
+        a_lo = lo[0]; b_lo = lo[1]; a_hi = hi[0]; b_hi = hi[1];
+    } else {
+        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)bx, (uint32_t)by, false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(bx >> 32), (uint32_t)(by >> 32), false, false);
+        a_lo = lo[0]; b_lo = lo[1]; a_hi = hi[0]; b_hi = hi[1];
+    }
+    return __builtin_bit_cast(double, ((uint64_t)a_hi << 32) | a_lo) +
+           __builtin_bit_cast(double, ((uint64_t)b_hi << 32) | b_lo);
+}
+
+// Wave sums of 16 per-lane f64 values at once: after the 32- and 16-lane
+// swap steps every lane holds four values of slots j + 4 * (lane >> 4), and a
+// 16-lane tree completes them (every lane of the row ends with the sums).
+__device__ __forceinline__ void wave_sum16_f64(const double (&v)[16], double (&out)[4]) {
+    double h[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = swap_add_f64<32>(v[i], v[i + 8]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = dpp_sum_f64<16>(swap_add_f64<16>(h[i], h[i + 4]));
+}
+
 template <int XB>
 union RouteDecodeLds {
     float x[XB / 4];
@@ -976,11 +1007,21 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
         }
     }
     }
+    static_assert(kTopkTokensPerBlock == 16, "wave_sum16_f64 covers 16 token slots");
+    // one-slab waves: a reduce-scatter, a fixed cost below T wave trees of 6
+    // steps (the two-slab instance is at its register limit: trees there)
+    if (NSW == 1 && a.T > 4) {
+        double sums[4];
+        wave_sum16_f64(acc, sums);
+        const int j = lane & 15, t = j + 4 * (lane >> 4);
+        if (j < 4 && t < a.T) s_part[r][part][t] = j == 0 ? sums[0] : j == 1 ? sums[1] : j == 2 ? sums[2] : sums[3];
+    } else {
 #pragma unroll
-    for (int t = 0; t < kTopkTokensPerBlock; ++t) {
-        if (t < a.T) {
-            const double sum = dpp_sum_f64<64>(acc[t]);
-            if (lane == 63) s_part[r][part][t] = sum;
+        for (int t = 0; t < kTopkTokensPerBlock; ++t) {
+            if (t < a.T) {
+                const double sum = dpp_sum_f64<64>(acc[t]);
+                if (lane == 63) s_part[r][part][t] = sum;
+            }
         }
     }
     __syncthreads();
