@@ -431,8 +431,9 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
 
 // Whole-wave maximum of a u32 (one DPP max per step), returned to every lane.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    // old = 0 (the identity of the maximum): the DPP move folds into the max
 #define QMOE_MAXU32_STEP(CTRL, RM) \
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, RM, 0xF, false))
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, 0xF, false))
     QMOE_MAXU32_STEP(kDppQuadXor1, 0xF);
     QMOE_MAXU32_STEP(kDppQuadXor2, 0xF);
     QMOE_MAXU32_STEP(kDppRowHalfMirror, 0xF);
@@ -501,9 +502,18 @@ __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EP
             best = wave_max_key(hi == mh ? key[0] : 0ull);
         }
         const bool pop = key[0] == best;  // exactly one lane: keys are distinct
+        // the pop as one select per key word (element-wise selects of an array
+        // get rewritten into an indexed access, a chain of selects per key)
+        typedef uint64_t KeyVec __attribute__((ext_vector_type(EPL)));
+        KeyVec cur, nxt;
 #pragma unroll
-        for (int i = 0; i + 1 < EPL; ++i) key[i] = pop ? key[i + 1] : key[i];
-        key[EPL - 1] = pop ? 0ull : key[EPL - 1];
+        for (int i = 0; i < EPL; ++i) {
+            cur[i] = key[i];
+            nxt[i] = i + 1 < EPL ? key[i + 1 < EPL ? i + 1 : i] : 0ull;
+        }
+        cur = pop ? nxt : cur;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) key[i] = cur[i];
         if (lane == 0) {
             const int bi = sel_id(best);
             s_idx_row[j] = bi;
