@@ -128,9 +128,15 @@ __device__ __forceinline__ void gu_compute(const ExpertArgs& a, const XSrc& xs, 
         }
 #pragma unroll
         for (int m = 0; m < NI; ++m) {
-            const double g = dpp_sum_f64<LPR>(live ? pair_dot<WT>(it.wg[m], x) : 0.0);
-            const double u = dpp_sum_f64<LPR>(live ? pair_dot<WT>(it.wu[m], x) : 0.0);
-            if (lp == LPR - 1) a.gubuf[(uint64_t)(it.p0 + c) * a.F + it.f0 + m * RPI + sub] = make_float2((float)g, (float)u);
+            double g, u;
+            group_sum2_f64<LPR>(live ? pair_dot<WT>(it.wg[m], x) : 0.0, live ? pair_dot<WT>(it.wu[m], x) : 0.0, g, u);
+            float2& o = a.gubuf[(uint64_t)(it.p0 + c) * a.F + it.f0 + m * RPI + sub];
+            if constexpr (LPR >= 32) {
+                if (lp == LPR / 2 - 1) o.x = (float)g;
+                if (lp == LPR - 1) o.y = (float)u;
+            } else {
+                if (lp == LPR - 1) o = make_float2((float)g, (float)u);
+            }
         }
     }
 }
@@ -411,9 +417,15 @@ __global__ __launch_bounds__(NW * 64, GQ_MIN_WAVES) void k_gateup_q(ExpertArgs a
                     pu = pu + tu;
                 }
             }
-            const double gs = dpp_sum_f64<LPR>(pg);
-            const double us = dpp_sum_f64<LPR>(pu);
-            if (lp == LPR - 1) s_gu[c][wave * RPW + m * RPI + sub] = make_float2((float)gs, (float)us);
+            double gs, us;
+            group_sum2_f64<LPR>(pg, pu, gs, us);
+            float2& o = s_gu[c][wave * RPW + m * RPI + sub];
+            if constexpr (LPR >= 32) {
+                if (lp == LPR / 2 - 1) o.x = (float)gs;
+                if (lp == LPR - 1) o.y = (float)us;
+            } else {
+                if (lp == LPR - 1) o = make_float2((float)gs, (float)us);
+            }
         }
     }
     __syncthreads();

@@ -214,6 +214,43 @@ __device__ __forceinline__ double dpp_sum_f64(double v) {
     return v;
 }
 
+// One reduce-scatter step over an f64 pair (x, y): the 32-lane swap (W = 32)
+// leaves lanes 0..31 with x[l] + x[l + 32] and lanes 32..63 with y[l - 32] + y[l];
+// the 16-lane swap (W = 16) does the same between the even and odd rows of 16.
+template <int W>
+__device__ __forceinline__ double swap_add_f64(double x, double y) {
+    const uint64_t bx = __builtin_bit_cast(uint64_t, x), by = __builtin_bit_cast(uint64_t, y);
+    uint32_t a_lo, a_hi, b_lo, b_hi;
+    if constexpr (W == 32) {
+        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)bx, (uint32_t)by, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(bx >> 32), (uint32_t)(by >> 32), false, false);
+        a_lo = lo[0]; b_lo = lo[1]; a_hi = hi[0]; b_hi = hi[1];
+    } else {
+        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)bx, (uint32_t)by, false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(bx >> 32), (uint32_t)(by >> 32), false, false);
+        a_lo = lo[0]; b_lo = lo[1]; a_hi = hi[0]; b_hi = hi[1];
+    }
+    return __builtin_bit_cast(double, ((uint64_t)a_hi << 32) | a_lo) +
+           __builtin_bit_cast(double, ((uint64_t)b_hi << 32) | b_lo);
+}
+
+// Sums of two per-lane f64 values g and u over aligned groups of LPR lanes.
+// LPR >= 32: one swap step folds u into the upper half of each group and g
+// into the lower, then one tree of LPR/2 lanes finishes both; the sum of g is
+// then in lane LPR/2 - 1 of the group and the sum of u in lane LPR - 1 (returned
+// by those lanes).  Narrower groups: two trees, g and u both in lane LPR - 1.
+template <int LPR>
+__device__ __forceinline__ void group_sum2_f64(double g, double u, double& gs, double& us) {
+    if constexpr (LPR >= 32) {
+        const double s = dpp_sum_f64<LPR / 2>(swap_add_f64<LPR / 2>(g, u));
+        gs = s;
+        us = s;
+    } else {
+        gs = dpp_sum_f64<LPR>(g);
+        us = dpp_sum_f64<LPR>(u);
+    }
+}
+
 // (value, index) arg-max step: keep the better of own and the DPP source
 // (larger value; ties to the lower index).  Masked rows keep their own pair.
 template <int CTRL, int ROW_MASK>

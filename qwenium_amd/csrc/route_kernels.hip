@@ -803,26 +803,6 @@ template <int NSW> constexpr int kRdXBytesFor = NSW == 1 ? kRdXBytes : 128 * 102
 constexpr int kMaxSpins = 1 << 22;  // bounded wait: a flag that never comes raises the error word
 constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
 
-// One reduce-scatter step over an f64 pair (x, y): the 32-lane swap (W = 32)
-// leaves lanes 0..31 with x[l] + x[l + 32] and lanes 32..63 with y[l - 32] + y[l];
-// the 16-lane swap (W = 16) does the same between the even and odd rows of 16.
-template <int W>
-__device__ __forceinline__ double swap_add_f64(double x, double y) {
-    const uint64_t bx = __builtin_bit_cast(uint64_t, x), by = __builtin_bit_cast(uint64_t, y);
-    uint32_t a_lo, a_hi, b_lo, b_hi;
-    if constexpr (W == 32) {
-        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)bx, (uint32_t)by, false, false);
-        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(bx >> 32), (uint32_t)(by >> 32), false, false);
-        a_lo = lo[0]; b_lo = lo[1]; a_hi = hi[0]; b_hi = hi[1];
-    } else {
-        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)bx, (uint32_t)by, false, false);
-        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(bx >> 32), (uint32_t)(by >> 32), false, false);
-        a_lo = lo[0]; b_lo = lo[1]; a_hi = hi[0]; b_hi = hi[1];
-    }
-    return __builtin_bit_cast(double, ((uint64_t)a_hi << 32) | a_lo) +
-           __builtin_bit_cast(double, ((uint64_t)b_hi << 32) | b_lo);
-}
-
 // Wave sums of 16 per-lane f64 values at once: after the 32- and 16-lane
 // swap steps every lane holds four values of slots j + 4 * (lane >> 4), and a
 // 16-lane tree completes them (every lane of the row ends with the sums).
@@ -907,9 +887,15 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
             x.load(lq + (size_t)c * a.H, ld + (size_t)c * (a.H >> 5), pair);
 #pragma unroll
             for (int m = 0; m < NI; ++m) {
-                const double g = dpp_sum_f64<LPR>(live ? pair_dot<WT>(wg[m], x) : 0.0);
-                const double u = dpp_sum_f64<LPR>(live ? pair_dot<WT>(wu[m], x) : 0.0);
-                if (lp == LPR - 1) lgu[c * 32 + wave * RPW + m * RPI + sub] = make_float2((float)g, (float)u);
+                double g, u;
+                group_sum2_f64<LPR>(live ? pair_dot<WT>(wg[m], x) : 0.0, live ? pair_dot<WT>(wu[m], x) : 0.0, g, u);
+                float2& o = lgu[c * 32 + wave * RPW + m * RPI + sub];
+                if constexpr (LPR >= 32) {
+                    if (lp == LPR / 2 - 1) o.x = (float)g;
+                    if (lp == LPR - 1) o.y = (float)u;
+                } else {
+                    if (lp == LPR - 1) o = make_float2((float)g, (float)u);
+                }
             }
         }
     }
