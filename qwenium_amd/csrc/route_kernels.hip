@@ -783,23 +783,21 @@ __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
 }
 
 // Fused decode routing (T <= kTopkTokensPerBlock): block b computes router
-// rows 2b, 2b+1 (row E is the shared-expert gate) for all tokens, eight waves
-// per row (wave p takes the 256-column slabs p, p+8; the eight partial sums
-// are added in order).  With one slab per wave (H <= 2048) each wave loads its
-// x columns straight from memory; wider rows stage x through LDS in column
-// chunks as wide as the staging window allows.  Without a shared expert the
-// router blocks also quantize tokens t = b (mod gridDim.x).  Then the block
-// raises its flag.  Block 0 waits for every other
-// block's flag (it waits on nothing else, and the other blocks wait on
-// nothing), then runs the whole routing on the exact logits.  Flags carry the
-// forward's generation number, so nothing is reset between forwards.
+// rows 2b, 2b+1 (row E is the shared-expert gate) for all tokens.  Wave
+// (g, p) takes the 256-column slabs p, p+8 of both rows for the tokens
+// t = g (mod 2), loading its x columns straight from memory (each x column
+// once per block); the eight partial sums of a (row, token) are added in
+// order.  Without a shared expert the router blocks also quantize tokens
+// t = b (mod gridDim.x).  Then the block raises its flag.  Block 0 waits for
+// every other block's flag (it waits on nothing else, and the other blocks
+// wait on nothing), then runs the whole routing on the exact logits.  Flags
+// carry the forward's generation number, so nothing is reset between forwards.
 constexpr int kRdRows = 2;          // router rows per block
-constexpr int kRdParts = 8;         // waves per row
+constexpr int kRdParts = 8;         // waves per token group
 constexpr int kRdSlab = 256;        // columns per lane-float4 sweep
 constexpr int kMaxRdSlabs = 16;     // fused decode routing for H <= 4096
-constexpr int kRdXBytes = 96 * 1024;  // x staging window (H <= 2048: all of x at T <= 12)
-// H > 2048 (two slabs per wave): a wider window keeps more tokens in one staging round
-template <int NSW> constexpr int kRdXBytesFor = NSW == 1 ? kRdXBytes : 128 * 1024;
+// dynamic LDS: block 0's routing tables, the shared-expert blocks' token rows
+constexpr int kRdLdsBytes = 96 * 1024;
 constexpr int kMaxSpins = 1 << 22;  // bounded wait: a flag that never comes raises the error word
 constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
 
@@ -814,12 +812,9 @@ __device__ __forceinline__ void wave_sum16_f64(const double (&v)[16], double (&o
     for (int i = 0; i < 4; ++i) out[i] = dpp_sum_f64<16>(swap_add_f64<16>(h[i], h[i + 4]));
 }
 
-template <int XB>
-union RouteDecodeLds {
-    float x[XB / 4];
-    SmallRouteLds route;
-};
-static_assert(sizeof(SmallRouteLds) <= kRdXBytes, "the routing tables fit the smallest staging window");
+static_assert(sizeof(SmallRouteLds) <= kRdLdsBytes, "the routing tables fit the dynamic LDS");
+static_assert(kTopkTokensPerBlock * (kMaxRdSlabs * kRdSlab * 5 / 4 + 32 * 8) <= kRdLdsBytes,
+              "the shared-expert blocks' token rows fit the dynamic LDS");
 
 // Shared expert at decode: its gate/up, SwiGLU and Q8_0 of h do not depend on
 // the routing, so blocks after the router blocks compute them meanwhile on
@@ -912,8 +907,6 @@ template <int NSW, int SWT, int SLPR>  // NSW: router slabs per wave (ceil(H/256
 __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits, int8_t* xq_qs, float2* xq_ds,
                                                        int32_t* sync, SharedGuArgs sg) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
-    constexpr int XB = kRdXBytesFor<NSW>;
-    RouteDecodeLds<XB>& S = *(RouteDecodeLds<XB>*)s_dyn;
     __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nb = gridDim.x - sg.n_blocks;  // router blocks
@@ -925,98 +918,61 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     }
     const int gen = __hip_atomic_load(sync + kSyncGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
     const int E1 = a.E + a.S;
-    const int r = wave / kRdParts, part = wave % kRdParts;
-    const int e = blockIdx.x * kRdRows + r;
-    const bool has_row = e < E1;
-    const float* wrow = e < a.E ? a.w_router + (uint64_t)min(e, a.E - 1) * a.router_ld : (a.S ? a.w_sh_norm : a.w_router);
     const int nslab = a.H / kRdSlab;
-    f32x4 w[NSW];
-#pragma unroll
-    for (int i = 0; i < NSW; ++i)
-        w[i] = *(const f32x4*)(wrow + min(part + kRdParts * i, nslab - 1) * kRdSlab + 4 * lane);
-    double acc[kTopkTokensPerBlock];
-#pragma unroll
-    for (int t = 0; t < kTopkTokensPerBlock; ++t) acc[t] = 0.0;
-    if constexpr (NSW == 1) {
-        // one slab per wave: its x columns come straight from memory (L2), eight
-        // tokens' float4 in flight at a time, no LDS round trip or barrier
-        if (has_row && part < nslab) {
-            const float* xs = a.x + part * kRdSlab + 4 * lane;
-            for (int t0 = 0; t0 < a.T; t0 += 8) {
-                f32x4 xv[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) xv[u] = *(const f32x4*)(xs + (uint64_t)min(t0 + u, a.T - 1) * a.H);
-                const double w0 = w[0].x, w1 = w[0].y, w2 = w[0].z, w3 = w[0].w;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-#pragma unroll
-                    for (int t = 0; t < kTopkTokensPerBlock; ++t) {
-                        if (t == t0 + u && t < a.T) {
-                            acc[t] = __builtin_fma(w0, (double)xv[u].x, acc[t]);
-                            acc[t] = __builtin_fma(w1, (double)xv[u].y, acc[t]);
-                            acc[t] = __builtin_fma(w2, (double)xv[u].z, acc[t]);
-                            acc[t] = __builtin_fma(w3, (double)xv[u].w, acc[t]);
-                        }
-                    }
-                }
-            }
-        }
-    } else {
-    // chunk = as many slabs as fit: T * chunk * 4 bytes <= XB
-    const int cslabs = max(1, min(nslab, XB / (a.T * kRdSlab * 4)));
-    const int ccols = cslabs * kRdSlab;
-    constexpr int kStagePerThread = XB / 16 / 1024;  // float4 moves per thread per chunk
-    for (int s0 = 0; s0 < nslab; s0 += cslabs) {
-        const int ns = min(cslabs, nslab - s0);
-        const int q4 = ns * kRdSlab / 4;  // float4 per token in this chunk
-        __syncthreads();                  // the previous chunk's reads are done
-        f32x4 v[kStagePerThread];
-#pragma unroll
-        for (int j = 0; j < kStagePerThread; ++j) {
-            const int i = tid + 1024 * j;
-            const int t = min(i / q4, a.T - 1), q = i % q4;
-            v[j] = *(const f32x4*)(a.x + (uint64_t)t * a.H + s0 * kRdSlab + 4 * q);
-        }
-#pragma unroll
-        for (int j = 0; j < kStagePerThread; ++j) {
-            const int i = tid + 1024 * j;
-            if (i < a.T * q4) *(f32x4*)(&S.x[(i / q4) * ccols + 4 * (i % q4)]) = v[j];
-        }
-        __syncthreads();
-        if (has_row) {
-#pragma unroll
-            for (int i = 0; i < NSW; ++i) {
-                const int c = part + kRdParts * i;
-                if (c < s0 || c >= s0 + ns) continue;  // uniform per wave; w[] keeps static indices
-                const double w0 = w[i].x, w1 = w[i].y, w2 = w[i].z, w3 = w[i].w;
-#pragma unroll
-                for (int t = 0; t < kTopkTokensPerBlock; ++t) {
-                    if (t < a.T) {
-                        const f32x4 xv = *(const f32x4*)(&S.x[t * ccols + (c - s0) * kRdSlab + 4 * lane]);
-                        acc[t] = __builtin_fma(w0, (double)xv.x, acc[t]);
-                        acc[t] = __builtin_fma(w1, (double)xv.y, acc[t]);
-                        acc[t] = __builtin_fma(w2, (double)xv.z, acc[t]);
-                        acc[t] = __builtin_fma(w3, (double)xv.w, acc[t]);
-                    }
-                }
-            }
-        }
-    }
-    }
+    const int part = wave % kRdParts;
+    auto router_row = [&](int e) {
+        return e < a.E ? a.w_router + (uint64_t)min(e, a.E - 1) * a.router_ld : (a.S ? a.w_sh_norm : a.w_router);
+    };
     static_assert(kTopkTokensPerBlock == 16, "wave_sum16_f64 covers 16 token slots");
-    // one-slab waves: a reduce-scatter, a fixed cost below T wave trees of 6
-    // steps (the two-slab instance is at its register limit: trees there)
-    if (NSW == 1 && a.T > 4) {
+    const int grp = wave / kRdParts;
+    const int e0 = blockIdx.x * kRdRows;
+    double acc[kRdRows * 8];  // [row q][i]: token 2 i + grp
+#pragma unroll
+    for (int k = 0; k < kRdRows * 8; ++k) acc[k] = 0.0;
+#pragma unroll
+    for (int sl = 0; sl < NSW; ++sl) {
+        const int c = part + kRdParts * sl;  // this wave's slab
+        f32x4 w[kRdRows];
+#pragma unroll
+        for (int q = 0; q < kRdRows; ++q)
+            w[q] = *(const f32x4*)(router_row(e0 + q) + min(c, nslab - 1) * kRdSlab + 4 * lane);
+        if (e0 < E1 && c < nslab) {
+            const float* xs = a.x + c * kRdSlab + 4 * lane;
+            f32x4 xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (2 * i + grp < a.T) xv[i] = *(const f32x4*)(xs + (uint64_t)(2 * i + grp) * a.H);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (2 * i + grp < a.T) {
+                    const double x0 = xv[i].x, x1 = xv[i].y, x2 = xv[i].z, x3 = xv[i].w;
+#pragma unroll
+                    for (int q = 0; q < kRdRows; ++q) {
+                        double& d = acc[q * 8 + i];
+                        d = __builtin_fma((double)w[q].x, x0, d);
+                        d = __builtin_fma((double)w[q].y, x1, d);
+                        d = __builtin_fma((double)w[q].z, x2, d);
+                        d = __builtin_fma((double)w[q].w, x3, d);
+                    }
+                }
+            }
+        }
+    }
+    // wave sums of the 16 (row, token) values: one reduce-scatter, a fixed
+    // cost below the trees of 6 steps per value from T = 5 up
+    if (a.T > 4) {
         double sums[4];
         wave_sum16_f64(acc, sums);
-        const int j = lane & 15, t = j + 4 * (lane >> 4);
-        if (j < 4 && t < a.T) s_part[r][part][t] = j == 0 ? sums[0] : j == 1 ? sums[1] : j == 2 ? sums[2] : sums[3];
+        const int j = lane & 15, k = j + 4 * (lane >> 4), t = 2 * (k & 7) + grp;
+        if (j < 4 && t < a.T)
+            s_part[k >> 3][part][t] = j == 0 ? sums[0] : j == 1 ? sums[1] : j == 2 ? sums[2] : sums[3];
     } else {
 #pragma unroll
-        for (int t = 0; t < kTopkTokensPerBlock; ++t) {
+        for (int k = 0; k < kRdRows * 8; ++k) {
+            const int t = 2 * (k & 7) + grp;
             if (t < a.T) {
-                const double sum = dpp_sum_f64<64>(acc[t]);
-                if (lane == 63) s_part[r][part][t] = sum;
+                const double sum = dpp_sum_f64<64>(acc[k]);
+                if (lane == 63) s_part[k >> 3][part][t] = sum;
             }
         }
     }
@@ -1060,7 +1016,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // drop stale cached logits (L1 and this XCD's L2)
     }
     __syncthreads();
-    route_small_body(a, S.route);
+    route_small_body(a, *(SmallRouteLds*)s_dyn);
     if (tid == 0) __hip_atomic_store(sync + kSyncGen, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1252,7 +1208,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
         }
         const dim3 g(nb + sg.n_blocks), b(64 * kTopkTokensPerBlock);
         // above the 64 KiB default window: raise it
-        const size_t lds = nslab <= kRdParts ? sizeof(RouteDecodeLds<kRdXBytesFor<1>>) : sizeof(RouteDecodeLds<kRdXBytesFor<2>>);
+        const size_t lds = kRdLdsBytes;
         const int lpr = L.H <= 1024 ? 16 : (L.H <= 2048 ? 32 : 64);
         const void* kern;
         if (nslab <= kRdParts) {
