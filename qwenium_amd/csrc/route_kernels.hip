@@ -784,16 +784,19 @@ __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
 
 // Fused decode routing (T <= kTopkTokensPerBlock): block b computes router
 // rows 2b, 2b+1 (row E is the shared-expert gate) for all tokens.  Wave
-// (g, p) takes the 256-column slabs p, p+8 of both rows for the tokens
-// t = g (mod 2), loading its x columns straight from memory (each x column
-// once per block); the eight partial sums of a (row, token) are added in
+// (g, p) takes the 256-column slabs p, p+4, ... of both rows for the tokens
+// t = g (mod 4), loading its x columns straight from memory (each x column
+// once per block); the four partial sums of a (row, token) are added in
 // order.  Without a shared expert the router blocks also quantize tokens
 // t = b (mod gridDim.x).  Then the block raises its flag.  Block 0 waits for
 // every other block's flag (it waits on nothing else, and the other blocks
 // wait on nothing), then runs the whole routing on the exact logits.  Flags
 // carry the forward's generation number, so nothing is reset between forwards.
-constexpr int kRdRows = 2;          // router rows per block
-constexpr int kRdParts = 8;         // waves per token group
+constexpr int kRdRows = 2;                                     // router rows per block
+constexpr int kRdGroups = 4;                                   // token groups (t = g mod kRdGroups)
+constexpr int kRdParts = 16 / kRdGroups;                       // waves per token group
+constexpr int kRdTokSlots = kTopkTokensPerBlock / kRdGroups;   // token slots per wave
+constexpr int kRdVals = kRdRows * kRdTokSlots;                 // (row, token) sums per wave
 constexpr int kRdSlab = 256;        // columns per lane-float4 sweep
 constexpr int kMaxRdSlabs = 16;     // fused decode routing for H <= 4096
 // dynamic LDS: block 0's routing tables, the shared-expert blocks' token rows
@@ -801,15 +804,18 @@ constexpr int kRdLdsBytes = 96 * 1024;
 constexpr int kMaxSpins = 1 << 22;  // bounded wait: a flag that never comes raises the error word
 constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
 
-// Wave sums of 16 per-lane f64 values at once: after the 32- and 16-lane
-// swap steps every lane holds four values of slots j + 4 * (lane >> 4), and a
-// 16-lane tree completes them (every lane of the row ends with the sums).
-__device__ __forceinline__ void wave_sum16_f64(const double (&v)[16], double (&out)[4]) {
-    double h[8];
+// Wave sums of N per-lane f64 values at once (reduce-scatter): after the 32-
+// and 16-lane swap steps every lane holds N/4 values, of slots
+// j + (N/4) * (lane >> 4), and a 16-lane tree completes them (every lane of
+// the row ends with the sums).
+template <int N>
+__device__ __forceinline__ void wave_sum_rs_f64(const double (&v)[N], double (&out)[N / 4]) {
+    static_assert(N >= 4 && N % 4 == 0, "slots");
+    double h[N / 2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = swap_add_f64<32>(v[i], v[i + 8]);
+    for (int i = 0; i < N / 2; ++i) h[i] = swap_add_f64<32>(v[i], v[i + N / 2]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = dpp_sum_f64<16>(swap_add_f64<16>(h[i], h[i + 4]));
+    for (int i = 0; i < N / 4; ++i) out[i] = dpp_sum_f64<16>(swap_add_f64<16>(h[i], h[i + N / 4]));
 }
 
 static_assert(sizeof(SmallRouteLds) <= kRdLdsBytes, "the routing tables fit the dynamic LDS");
@@ -903,7 +909,7 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
     }
 }
 
-template <int NSW, int SWT, int SLPR>  // NSW: router slabs per wave (ceil(H/256/8)); SWT: shared type (0: none)
+template <int NSW, int SWT, int SLPR>  // NSW: router slabs per wave (ceil(H/256/4)); SWT: shared type (0: none)
 __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits, int8_t* xq_qs, float2* xq_ds,
                                                        int32_t* sync, SharedGuArgs sg) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
@@ -923,56 +929,65 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     auto router_row = [&](int e) {
         return e < a.E ? a.w_router + (uint64_t)min(e, a.E - 1) * a.router_ld : (a.S ? a.w_sh_norm : a.w_router);
     };
-    static_assert(kTopkTokensPerBlock == 16, "wave_sum16_f64 covers 16 token slots");
     const int grp = wave / kRdParts;
     const int e0 = blockIdx.x * kRdRows;
-    double acc[kRdRows * 8];  // [row q][i]: token 2 i + grp
+    double acc[kRdVals];  // [row q][i]: token kRdGroups * i + grp
 #pragma unroll
-    for (int k = 0; k < kRdRows * 8; ++k) acc[k] = 0.0;
+    for (int k = 0; k < kRdVals; ++k) acc[k] = 0.0;
+    // two slabs at a time: every load of the pair issued before its FMAs
 #pragma unroll
-    for (int sl = 0; sl < NSW; ++sl) {
-        const int c = part + kRdParts * sl;  // this wave's slab
-        f32x4 w[kRdRows];
+    for (int s0 = 0; s0 < NSW; s0 += 2) {
+        constexpr int kPair = NSW > 1 ? 2 : 1;
+        if (s0 > 0 && part + kRdParts * s0 >= nslab) break;  // uniform: no slab left for this wave
+        f32x4 w[kPair][kRdRows], xv[kPair][kRdTokSlots];
 #pragma unroll
-        for (int q = 0; q < kRdRows; ++q)
-            w[q] = *(const f32x4*)(router_row(e0 + q) + min(c, nslab - 1) * kRdSlab + 4 * lane);
-        if (e0 < E1 && c < nslab) {
-            const float* xs = a.x + c * kRdSlab + 4 * lane;
-            f32x4 xv[8];
+        for (int u = 0; u < kPair; ++u) {
+            const int c = min(part + kRdParts * (s0 + u), nslab - 1);  // this wave's slab (clamped)
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (2 * i + grp < a.T) xv[i] = *(const f32x4*)(xs + (uint64_t)(2 * i + grp) * a.H);
+            for (int q = 0; q < kRdRows; ++q)
+                w[u][q] = *(const f32x4*)(router_row(e0 + q) + c * kRdSlab + 4 * lane);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                if (2 * i + grp < a.T) {
-                    const double x0 = xv[i].x, x1 = xv[i].y, x2 = xv[i].z, x3 = xv[i].w;
+            for (int i = 0; i < kRdTokSlots; ++i)
+                if (kRdGroups * i + grp < a.T)
+                    xv[u][i] = *(const f32x4*)(a.x + (uint64_t)(kRdGroups * i + grp) * a.H + c * kRdSlab + 4 * lane);
+        }
+#pragma unroll
+        for (int u = 0; u < kPair; ++u) {
+            if (s0 + u >= NSW || e0 >= E1 || part + kRdParts * (s0 + u) >= nslab) continue;  // uniform
+#pragma unroll
+            for (int i = 0; i < kRdTokSlots; ++i) {
+                if (kRdGroups * i + grp < a.T) {
+                    const double x0 = xv[u][i].x, x1 = xv[u][i].y, x2 = xv[u][i].z, x3 = xv[u][i].w;
 #pragma unroll
                     for (int q = 0; q < kRdRows; ++q) {
-                        double& d = acc[q * 8 + i];
-                        d = __builtin_fma((double)w[q].x, x0, d);
-                        d = __builtin_fma((double)w[q].y, x1, d);
-                        d = __builtin_fma((double)w[q].z, x2, d);
-                        d = __builtin_fma((double)w[q].w, x3, d);
+                        double& d = acc[q * kRdTokSlots + i];
+                        d = __builtin_fma((double)w[u][q].x, x0, d);
+                        d = __builtin_fma((double)w[u][q].y, x1, d);
+                        d = __builtin_fma((double)w[u][q].z, x2, d);
+                        d = __builtin_fma((double)w[u][q].w, x3, d);
                     }
                 }
             }
         }
     }
-    // wave sums of the 16 (row, token) values: one reduce-scatter, a fixed
-    // cost below the trees of 6 steps per value from T = 5 up
-    if (a.T > 4) {
-        double sums[4];
-        wave_sum16_f64(acc, sums);
-        const int j = lane & 15, k = j + 4 * (lane >> 4), t = 2 * (k & 7) + grp;
-        if (j < 4 && t < a.T)
-            s_part[k >> 3][part][t] = j == 0 ? sums[0] : j == 1 ? sums[1] : j == 2 ? sums[2] : sums[3];
+    // wave sums of the (row, token) values: one reduce-scatter, a fixed cost
+    // below the trees of 6 steps per live value
+    if (kRdVals <= 8 || a.T > 4) {
+        double sums[kRdVals / 4];
+        wave_sum_rs_f64<kRdVals>(acc, sums);
+        const int j = lane & 15, k = j + (kRdVals / 4) * (lane >> 4);
+        const int t = kRdGroups * (k % kRdTokSlots) + grp;
+        double v = sums[0];
+#pragma unroll
+        for (int m = 1; m < kRdVals / 4; ++m) v = j == m ? sums[m] : v;
+        if (j < kRdVals / 4 && t < a.T) s_part[k / kRdTokSlots][part][t] = v;
     } else {
 #pragma unroll
-        for (int k = 0; k < kRdRows * 8; ++k) {
-            const int t = 2 * (k & 7) + grp;
+        for (int k = 0; k < kRdVals; ++k) {
+            const int t = kRdGroups * (k % kRdTokSlots) + grp;
             if (t < a.T) {
                 const double sum = dpp_sum_f64<64>(acc[k]);
-                if (lane == 63) s_part[k >> 3][part][t] = sum;
+                if (lane == 63) s_part[k / kRdTokSlots][part][t] = sum;
             }
         }
     }
@@ -1108,6 +1123,24 @@ bool route_decode_fused(const LayerDesc& L, int T) {
            (L.E + L.S + kRdRows - 1) / kRdRows <= kMaxRdBlocks;
 }
 
+// The fused decode routing instance for nsw slabs per wave, shared-expert
+// type swt (0 none, 1 Q4_0, 2 Q8_0) and the shared blocks' lanes per row
+// (16 for H <= 1024, 32 for H <= 2048, else 64).
+template <int NSW, int SLPR>
+static const void* route_decode_for(int swt) {
+    return swt == 0 ? (const void*)k_route_decode<NSW, 0, SLPR>
+                    : swt == 1 ? (const void*)k_route_decode<NSW, kTypeQ4_0, SLPR>
+                               : (const void*)k_route_decode<NSW, kTypeQ8_0, SLPR>;
+}
+static const void* route_decode_kernel(int nsw, int swt, int lpr) {
+    static_assert(kRdParts == 4, "slabs per wave: 1 at H <= 1024, 2 at H <= 2048, 3-4 at H <= 4096");
+    if (nsw == 1 && lpr == 16) return route_decode_for<1, 16>(swt);
+    if (nsw == 2 && lpr == 32) return route_decode_for<2, 32>(swt);
+    if (nsw == 3 && lpr == 64) return route_decode_for<3, 64>(swt);
+    if (nsw == 4 && lpr == 64) return route_decode_for<4, 64>(swt);
+    return nullptr;
+}
+
 static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, const float* xr, const float* xe, int T,
                                       bool quant, hipStream_t stream) {
     RouterArgs ra;
@@ -1210,18 +1243,10 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
         // above the 64 KiB default window: raise it
         const size_t lds = kRdLdsBytes;
         const int lpr = L.H <= 1024 ? 16 : (L.H <= 2048 ? 32 : 64);
-        const void* kern;
-        if (nslab <= kRdParts) {
-            if (!sg.n_blocks) kern = (const void*)k_route_decode<1, 0, 32>;
-            else if (L.gu_type == kTypeQ4_0) kern = lpr == 16 ? (const void*)k_route_decode<1, kTypeQ4_0, 16>
-                                                              : (const void*)k_route_decode<1, kTypeQ4_0, 32>;
-            else kern = lpr == 16 ? (const void*)k_route_decode<1, kTypeQ8_0, 16>
-                                  : (const void*)k_route_decode<1, kTypeQ8_0, 32>;
-        } else {
-            if (!sg.n_blocks) kern = (const void*)k_route_decode<2, 0, 64>;
-            else kern = L.gu_type == kTypeQ4_0 ? (const void*)k_route_decode<2, kTypeQ4_0, 64>
-                                               : (const void*)k_route_decode<2, kTypeQ8_0, 64>;
-        }
+        const int nsw = (nslab + kRdParts - 1) / kRdParts;  // slabs per wave
+        const int swt = !sg.n_blocks ? 0 : (L.gu_type == kTypeQ4_0 ? 1 : 2);
+        const void* kern = route_decode_kernel(nsw, swt, lpr);
+        if (!kern) return hipErrorInvalidValue;
         if ((err = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
             return err;
         int32_t* sync = ws.sync;
