@@ -197,8 +197,15 @@ constexpr int kDppRowBcast31 = 0x143;
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ double dpp_f64_or_zero(double v) {
     const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xF, false);
+    uint32_t lo, hi;
+    if constexpr (ROW_MASK == 0xF) {
+        // every lane is written from a lane of its own row: no old value needed
+        lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+        hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+    } else {
+        lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xF, false);
+        hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xF, false);
+    }
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 

@@ -429,6 +429,22 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// Whole-wave maximum of a u32 in every lane: four in-row DPP steps (the DPP
+// moves fold into the maximum), then the 16- and 32-lane swaps; no scalar
+// round trip.
+__device__ __forceinline__ uint32_t wave_allmax_u32(uint32_t v) {
+#define QMOE_MAXU32_STEP(CTRL) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false))
+    QMOE_MAXU32_STEP(kDppQuadXor1);
+    QMOE_MAXU32_STEP(kDppQuadXor2);
+    QMOE_MAXU32_STEP(kDppRowHalfMirror);
+    QMOE_MAXU32_STEP(kDppRowMirror);
+#undef QMOE_MAXU32_STEP
+    const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max((uint32_t)r16[0], (uint32_t)r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max((uint32_t)r32[0], (uint32_t)r32[1]);
+}
+
 // Whole-wave maximum of a u32 (one DPP max per step), returned to every lane.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     // old = 0 (the identity of the maximum): the DPP move folds into the max
@@ -492,16 +508,15 @@ __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EP
         // the largest head: the value word's maximum first; the full keys (lowest
         // expert id among equal values) only when several lanes hold that value
         const uint32_t hi = (uint32_t)(key[0] >> 32);
-        const uint32_t mh = wave_max_u32(hi);
-        const uint64_t at = __ballot(hi == mh);
-        uint64_t best;
-        if ((at & (at - 1)) == 0) {
-            const int wl = __builtin_ctzll(at);
-            best = ((uint64_t)mh << 32) | (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], wl);
-        } else {
-            best = wave_max_key(hi == mh ? key[0] : 0ull);
+        bool pop = hi == wave_allmax_u32(hi);
+        const uint64_t at = __ballot(pop);
+        if (at & (at - 1)) pop = key[0] == wave_max_key(pop ? key[0] : 0ull);  // a value tie: keys are distinct
+        if (pop) {  // the winning lane records its head
+            const int bi = sel_id(key[0]);
+            s_idx_row[j] = bi;
+            s_val_row[j] = sel_val(key[0]);
+            a.topk_idx[(uint64_t)t * a.K + j] = bi;
         }
-        const bool pop = key[0] == best;  // exactly one lane: keys are distinct
         // the pop as one select per key word (element-wise selects of an array
         // get rewritten into an indexed access, a chain of selects per key)
         typedef uint64_t KeyVec __attribute__((ext_vector_type(EPL)));
@@ -514,14 +529,8 @@ __device__ void select_softmax(const TopkArgs& a, int t, int lane, float (&v)[EP
         cur = pop ? nxt : cur;
 #pragma unroll
         for (int i = 0; i < EPL; ++i) key[i] = cur[i];
-        if (lane == 0) {
-            const int bi = sel_id(best);
-            s_idx_row[j] = bi;
-            s_val_row[j] = sel_val(best);
-            a.topk_idx[(uint64_t)t * a.K + j] = bi;
-        }
     }
-    // lanes below read what lane 0 wrote to LDS: order the wave's LDS accesses
+    // every lane reads what the winning lanes wrote to LDS: order the wave's LDS accesses
     wave_lds_sync();
     if (a.defer_softmax) {
         if (lane == 0 && s_sg) *s_sg = sg_logit;
