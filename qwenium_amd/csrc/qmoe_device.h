@@ -467,16 +467,27 @@ struct XPair {
     }
 };
 
-// Within-8-lane (and wider) reductions for the h quantization.
+// Within-row reductions for the h quantization (CTRL moves within a row of 16
+// lanes, so every lane has a source and no old value is needed), and the step
+// between the two rows of a 32-lane group: the 16-lane swap hands each lane its
+// partner's value, the pair is combined in both lanes.
 template <int CTRL>
 __device__ __forceinline__ float dpp8_max(float v) {
-    const float o = __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    const float o = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
     return fmaxf(v, o);
 }
 template <int CTRL>
 __device__ __forceinline__ int dpp8_add(int v) {
-    return v + __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+    return v + __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ int xor16_add(int v) {
+    const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    return (int)r[0] + (int)r[1];
 }
 
 // h = silu(g)*u (or gelu(g)*u) of one value per lane and the Q8_0 quantization of the 32-value
@@ -491,7 +502,7 @@ __device__ __forceinline__ void swiglu_q8_block32(float g, float u, int fl, int8
     amax = dpp8_max<kDppQuadXor2>(amax);
     amax = dpp8_max<kDppRowHalfMirror>(amax);
     amax = dpp8_max<kDppRowMirror>(amax);
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = xor16_max(amax);
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     const int qv = (int)__builtin_rintf(h * id);
@@ -500,7 +511,7 @@ __device__ __forceinline__ void swiglu_q8_block32(float g, float u, int fl, int8
     sum = dpp8_add<kDppQuadXor2>(sum);
     sum = dpp8_add<kDppRowHalfMirror>(sum);
     sum = dpp8_add<kDppRowMirror>(sum);
-    sum += __shfl_xor(sum, 16);
+    sum = xor16_add(sum);
     qs[fl] = (int8_t)qv;
     if (fl == 0) *ds = make_float2(fp16_to_f32(f32_to_fp16(d)), __builtin_bit_cast(float, sum));
 }
