@@ -310,8 +310,11 @@ def main() -> int:
     if not mfma_path:
         if T <= 16:
             # k_gateup_q: routed experts' gate+up rows, the token rows of x (Q8_0), h written as
-            # Q8_0 (the shared expert's gate/up runs inside the routing launch)
+            # Q8_0 (the shared expert's gate/up runs inside the routing launch); with a shared
+            # expert of F = 512, also its down rows, its h rows and the f32 rows ysh it writes
             gu_bytes = D_prof * 2 * F * rb_h + T * (H + H // 32 * 8) + T * K * (F + F // 32 * 8)
+            if S and F == 512:
+                gu_bytes += H * rb_f + T * (F + F // 32 * 8) + T * H * 4
             gu_kernel = (f"k_gateup_q (routed gate+up expert GEMV with {'GeGLU' if geglu else 'SwiGLU'} and Q8_0 of h, "
                          "one Q8_0 block per workgroup)")
         else:

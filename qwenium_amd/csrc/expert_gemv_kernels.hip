@@ -33,6 +33,8 @@ struct ExpertArgs {
     float* ybuf;                               // [R][H] down outputs (unweighted)
     int act;                                   // kActSilu or kActGeluTanh
     const uint16_t* gelu_tab;                  // [65536] fp16 gelu table (GeGLU layers)
+    float* ysh;                                // [T][H] the shared expert's down rows (fused decode)
+    int sd_blocks;                             // fused decode gate/up: leading workgroups computing ysh
 };
 
 // Loads the slot table into LDS (all E+1 entries; those past n_active are
@@ -291,6 +293,42 @@ template <> constexpr int kGqWaves<kTypeQ8_0> = 8;
 
 __host__ __device__ constexpr size_t gq_lds_bytes(int T, int H) { return (size_t)T * H + (size_t)T * (H / 32) * 8; }
 
+// The shared expert's down projection in the fused decode gate/up launch (its h
+// rows were written by the routing launch): ysh[t][n] = the dot of down row n
+// with token t's Q8_0 h over 8 lanes of one block pair each (F = 512) and the
+// same f64 tree as the down+combine kernel's shared step, so the same f32 value.
+// Wave gw of these workgroups takes the 8 rows of group gw / kSdSplit and the
+// tokens t = gw (mod kSdSplit), two tokens' h rows in flight.
+constexpr int kSdLanes = 8;
+constexpr int kSdSplit = 2;
+template <int WT, int NW>
+__device__ void gu_shared_down(const ExpertArgs& a, int j) {
+#pragma clang fp contract(off)
+    constexpr int RPI = 64 / kSdLanes;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / kSdLanes, lp = lane % kSdLanes;
+    const int gw = j * NW + wave;
+    const int g = gw / kSdSplit;
+    if (g >= a.H / RPI) return;
+    const int n = g * RPI + sub;
+    WPair<WT> w;
+    w.load(a.w_sh_down + (uint64_t)n * a.sh_down_nb1, lp);
+    const int nfb = a.F >> 5;
+    for (int t = gw % kSdSplit; t < a.T; t += 2 * kSdSplit) {
+        const uint64_t p0 = (uint64_t)a.T * a.K + t, p1 = p0 + kSdSplit;  // the shared expert's h rows
+        const bool has1 = t + kSdSplit < a.T;
+        XPair x0, x1;
+        x0.load(a.hq_qs + p0 * a.F, a.hq_ds + p0 * nfb, lp);
+        if (has1) x1.load(a.hq_qs + p1 * a.F, a.hq_ds + p1 * nfb, lp);
+        const double y0 = dpp_sum_f64<kSdLanes>(pair_dot<WT>(w, x0));
+        if (lp == kSdLanes - 1) a.ysh[(uint64_t)t * a.H + n] = (float)y0;
+        if (has1) {
+            const double y1 = dpp_sum_f64<kSdLanes>(pair_dot<WT>(w, x1));
+            if (lp == kSdLanes - 1) a.ysh[(uint64_t)(t + kSdSplit) * a.H + n] = (float)y1;
+        }
+    }
+}
+
 // PPL: Q8_0 block pairs per lane of a row (pairs lp, lp + LPR, ...): LPR * PPL >= H / 64.
 // Each pair's contribution is exact in f64, so any split sums to the same bits.
 template <int WT, int LPR, int NW, int PPL>
@@ -303,9 +341,14 @@ __global__ __launch_bounds__(NW * 64, GQ_MIN_WAVES) void k_gateup_q(ExpertArgs a
     static_assert(NI >= 1 && NI * RPI == RPW, "rows per wave");
     extern __shared__ __align__(16) uint8_t s_dyn[];
     __shared__ float2 s_gu[kTopkTokensPerBlock][32];
+    if ((int)blockIdx.x < a.sd_blocks) {  // dispatched first: no dependence on the slot list
+        gu_shared_down<WT, NW>(a, blockIdx.x);
+        return;
+    }
+    const int bid = (int)blockIdx.x - a.sd_blocks;
     const int nfb = a.F >> 5;
-    const int v = blockIdx.x / nfb;
-    const int fb = blockIdx.x - v * nfb;
+    const int v = bid / nfb;
+    const int fb = bid - v * nfb;
     const int4 si = dslots[v];
     if (si.x < 0) return;  // past the forward's active slots (whole block)
     const int e = si.x, p0 = si.y, nrows = si.z;
@@ -562,6 +605,7 @@ struct DownCombineArgs {
     const int32_t* topk_idx; const float* topk_w; const int32_t* pos; const float* sh_gate;
     const int8_t* hq_qs; const float2* hq_ds;
     const float* residual; float* y;
+    const float* ysh;  // [T][H] the shared expert's down rows, computed by the gate/up launch (or null)
 };
 
 template <int WT>
@@ -668,7 +712,7 @@ __global__ __launch_bounds__(256) void k_down_combine_tok(DownCombineArgs a) {
     const int g = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
     const int rg = g / a.T;
     const int t = g - rg * a.T;  // tokens fastest within an XCD's run
-    const int nj = a.K + a.S;
+    const int nj = a.K + (a.ysh ? 0 : a.S);  // steps with weights here (the shared one may come precomputed)
     // the token's steps (wave-uniform: scalar loads); steps past nj repeat the last one
     int se[NJ], sp[NJ];
     float sw[NJ];
@@ -686,6 +730,7 @@ __global__ __launch_bounds__(256) void k_down_combine_tok(DownCombineArgs a) {
     const int n = min(n_raw, a.H - 1);
     const int pair = min(lp, (a.F >> 6) - 1);
     const bool live = lp < (a.F >> 6);
+    const float ysh = a.ysh ? a.ysh[(uint64_t)t * a.H + n] : 0.0f;
     // staging loads (chunks past nc re-read the last one; only chunks < nc are stored)
     int8_t* lq = (int8_t*)s_dyn;
     float2* ld = (float2*)(lq + (size_t)nj * a.F);
@@ -726,10 +771,20 @@ __global__ __launch_bounds__(256) void k_down_combine_tok(DownCombineArgs a) {
             dc_combine(acc, j, a.K, sw[j], dpp_sum_f64<LPR>(live ? pair_dot<WT>(w[j], x) : 0.0));
         }
     }
+    if (a.ysh) acc = acc + ysh * a.sh_gate[t];  // the shared step, last (as dc_combine orders it)
     if (lp == LPR - 1 && n_raw < a.H) {
         if (a.residual) acc = acc + a.residual[(uint64_t)t * a.H + n];
         a.y[(uint64_t)t * a.H + n] = acc;
     }
+}
+
+bool shared_down_in_gateup(const LayerDesc& L, int T) {
+    return L.S && gateup_q_fused(L, T) && L.F == 64 * kSdLanes && L.dn_type == L.gu_type && down_combine_tok_fits(L);
+}
+
+bool down_combine_tok_fits(const LayerDesc& L) {
+    const int nj = L.K + L.S;
+    return nj <= 9 && dc_lds_bytes(L.F, nj) <= 64 * 1024 && dc_stage_chunks(L.F, nj) <= 1024 && L.dc_ahead <= 2;
 }
 
 bool down_combine_fused(const LayerDesc& L, int T) {
@@ -742,7 +797,7 @@ bool down_combine_fused(const LayerDesc& L, int T) {
 template <int WT, int LPR>
 static hipError_t launch_down_combine_v(const DownCombineArgs& a, int ahead, hipStream_t stream) {
     constexpr int RPI = 64 / LPR;
-    const int nj = a.K + a.S;
+    const int nj = a.K + (a.ysh ? 0 : a.S);
     const int nc = dc_stage_chunks(a.F, nj);
     if (nj <= 9 && dc_lds_bytes(a.F, nj) <= 64 * 1024 && nc <= 1024 && ahead <= 2) {
         const dim3 g(a.T * ((a.H + 4 * RPI - 1) / (4 * RPI))), b(256);
@@ -751,6 +806,7 @@ static hipError_t launch_down_combine_v(const DownCombineArgs& a, int ahead, hip
         else hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 9, 4>), g, b, lds, stream, a);
         return hipGetLastError();
     }
+    if (a.ysh) return hipErrorInvalidValue;  // only the token-per-workgroup kernel takes a precomputed shared step
     const int n_items = a.T * (a.H / RPI);
     const dim3 g((n_items + 3) / 4), b(256);
     if (ahead <= 2) hipLaunchKernelGGL((k_down_combine<WT, LPR, 2>), g, b, 0, stream, a);
@@ -777,6 +833,7 @@ hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, f
     a.topk_idx = ws.topk_idx; a.topk_w = ws.topk_w; a.pos = ws.pos; a.sh_gate = ws.sh_gate;
     a.hq_qs = ws.hq_qs; a.hq_ds = ws.hq_ds;
     a.residual = residual; a.y = y;
+    a.ysh = shared_down_in_gateup(L, T) ? ws.ysh : nullptr;
     return (L.dn_type == kTypeQ4_0) ? launch_down_combine_t<kTypeQ4_0>(a, L.dc_ahead, stream)
                                     : launch_down_combine_t<kTypeQ8_0>(a, L.dc_ahead, stream);
 }
@@ -861,6 +918,8 @@ static ExpertArgs make_expert_args(const LayerDesc& L, const Workspace& ws, int 
     a.ybuf = ws.ybuf;
     a.act = L.act;
     a.gelu_tab = L.gelu_tab;
+    a.ysh = ws.ysh;
+    a.sd_blocks = 0;
     return a;
 }
 
@@ -883,7 +942,7 @@ template <int WT>
 static hipError_t launch_gateup_q_t(const ExpertArgs& a, const int4* dslots, int max_v, hipStream_t stream,
                                     hipEvent_t e0, hipEvent_t e1) {
     const int npairs = a.H / 64;
-    const dim3 g(max_v * (a.F / 32));
+    const dim3 g(a.sd_blocks + max_v * (a.F / 32));
     const size_t lds = gq_lds_bytes(a.T, a.H);
     constexpr int NW = kGqWaves<WT>;
     // lanes x pairs per row: 16 x 1, 32 x 1, 16 x 3 (H = 2816: 44 of 48 slots live), 64 x 1
@@ -896,8 +955,13 @@ static hipError_t launch_gateup_q_t(const ExpertArgs& a, const int4* dslots, int
 
 hipError_t launch_gateup_q(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream, hipEvent_t ev_start,
                            hipEvent_t ev_stop) {
-    const ExpertArgs a = make_expert_args(L, ws, T);
-    const int max_v = min(L.E, T * L.K);  // routed slots; the routing launch does the shared expert
+    ExpertArgs a = make_expert_args(L, ws, T);
+    const int max_v = min(L.E, T * L.K);  // routed slots; the routing launch does the shared expert's h
+    if (shared_down_in_gateup(L, T)) {
+        constexpr int NW = 8;  // waves per workgroup of the Q4_0 and Q8_0 instances
+        static_assert(kGqWaves<kTypeQ4_0> == NW && kGqWaves<kTypeQ8_0> == NW, "shared-down workgroup size");
+        a.sd_blocks = ((L.H / (64 / kSdLanes)) * kSdSplit + NW - 1) / NW;
+    }
     return (L.gu_type == kTypeQ4_0) ? launch_gateup_q_t<kTypeQ4_0>(a, ws.dslots, max_v, stream, ev_start, ev_stop)
                                     : launch_gateup_q_t<kTypeQ8_0>(a, ws.dslots, max_v, stream, ev_start, ev_stop);
 }

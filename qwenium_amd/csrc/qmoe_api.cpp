@@ -158,6 +158,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.hq_qs = (int8_t*)take(R * F);
     ws.hq_ds = (float2*)take(R * (F / 32) * sizeof(float2));
     ws.ybuf = (float*)take(R * H * sizeof(float));
+    ws.ysh = (float*)take((size_t)T * H * sizeof(float));
     ws.xn = (float*)take((size_t)T * H * sizeof(float));
     ws.xr = (float*)take((size_t)T * H * sizeof(float));
     ws.max_tiles = max_tiles;

@@ -81,6 +81,7 @@ struct Workspace {
     float* xn = nullptr;          // [T][H] RMSNorm(x)*w for fused-norm forwards (the experts' input)
     float* xr = nullptr;          // [T][H] the router's own input when it differs (Gemma 4 slice)
     float* ybuf = nullptr;        // [R][H] down outputs (unweighted)
+    float* ysh = nullptr;         // [T][H] the shared expert's down rows (fused decode)
     int max_tiles = 0;
 };
 
@@ -137,6 +138,13 @@ hipError_t launch_combine(const LayerDesc& L, const Workspace& ws, int T, float*
 // Decode sizes: token-major down projection with the combine in its epilogue
 // (replaces launch_experts_down + launch_combine when down_combine_fused()).
 bool down_combine_fused(const LayerDesc& L, int T);
+// The token-per-workgroup down+combine kernel takes the layer's K + S steps.
+bool down_combine_tok_fits(const LayerDesc& L);
+// Fused decode with a shared expert of F = 512 (down rows of the gate/up type):
+// its down projection runs in the gate/up launch, on workgroups of their own,
+// into ws.ysh; the down+combine kernel adds ysh * sh_gate as its last step
+// instead of computing it.
+bool shared_down_in_gateup(const LayerDesc& L, int T);
 hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
                                hipStream_t stream);
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream);
