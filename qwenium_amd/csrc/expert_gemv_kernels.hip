@@ -802,7 +802,9 @@ static hipError_t launch_down_combine_v(const DownCombineArgs& a, int ahead, hip
     if (nj <= 9 && dc_lds_bytes(a.F, nj) <= 64 * 1024 && nc <= 1024 && ahead <= 2) {
         const dim3 g(a.T * ((a.H + 4 * RPI - 1) / (4 * RPI))), b(256);
         const size_t lds = dc_lds_bytes(a.F, nj);
-        if (nc <= 512) hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 9, 2>), g, b, lds, stream, a);
+        // 8 steps (top-8 with the shared row precomputed): no ninth weight pair in registers
+        if (nj <= 8 && nc <= 512) hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 8, 2>), g, b, lds, stream, a);
+        else if (nc <= 512) hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 9, 2>), g, b, lds, stream, a);
         else hipLaunchKernelGGL((k_down_combine_tok<WT, LPR, 9, 4>), g, b, lds, stream, a);
         return hipGetLastError();
     }
