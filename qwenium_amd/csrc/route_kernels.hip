@@ -1031,8 +1031,8 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
         bool done = false;
         for (int it = 0; it < kMaxSpins && !done; ++it) {
             bool mine = true;
-            for (int bb = 1 + lane; bb < nb; bb += 64)
-                mine = mine && __hip_atomic_load(sync + kSyncFlags + bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen;
+            for (int bb = 1 + lane; bb < nb; bb += 64)  // every watched flag loaded in each pass, independently
+                mine &= __hip_atomic_load(sync + kSyncFlags + bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen;
             done = __all(mine);
             if (!done) __builtin_amdgcn_s_sleep(2);
         }
