@@ -87,6 +87,16 @@ def test_decode_35b_q4_0_t10(gpu):
     assert 40 <= distinct <= 80
 
 
+@pytest.mark.parametrize("spec,T", [(synthetic.QWEN35B, 1), (synthetic.QWEN35B, 3), (synthetic.QWEN35B, 16),
+                                    (synthetic.QWEN35B_Q8, 5)])
+def test_decode_35b_token_counts(gpu, spec, T):
+    """35B shape (shared expert of ffn 512) at decode sizes: the shared expert's down projection
+    runs in the gate/up launch (odd and even tokens on separate waves) and enters the down+combine
+    kernel as its last step; routing and outputs match the oracle as on every other path."""
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=200 + T)
+    assert_parity(y, got, y_ref, d_ref, spec)
+
+
 @pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 33, 64])
 def test_token_counts_small_layer(gpu, T):
     """Edge token counts: single token, block boundaries of the top-k sort (16 per block)."""
