@@ -97,6 +97,16 @@ def test_decode_35b_token_counts(gpu, spec, T):
     assert_parity(y, got, y_ref, d_ref, spec)
 
 
+@pytest.mark.parametrize("spec,T", [(LayerSpec(4096, 64, 4, 256, True, TYPE_Q8_0), 7),
+                                    (LayerSpec(3072, 96, 6, 512, True, TYPE_Q4_0), 12),
+                                    (LayerSpec(1280, 40, 4, 512, False, TYPE_Q4_0), 9)])
+def test_decode_hidden_sizes(gpu, spec, T):
+    """Decode routing at hidden 4096 / 3072 / 1280: four, three and two 256-column slabs per
+    router wave (the last two waves of 3072 and the last of 1280 with one slab fewer)."""
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=300 + T)
+    assert_parity(y, got, y_ref, d_ref, spec)
+
+
 @pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 33, 64])
 def test_token_counts_small_layer(gpu, T):
     """Edge token counts: single token, block boundaries of the top-k sort (16 per block)."""
