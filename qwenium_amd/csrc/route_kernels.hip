@@ -445,21 +445,6 @@ __device__ __forceinline__ uint32_t wave_allmax_u32(uint32_t v) {
     return max((uint32_t)r32[0], (uint32_t)r32[1]);
 }
 
-// Whole-wave maximum of a u32 (one DPP max per step), returned to every lane.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    // old = 0 (the identity of the maximum): the DPP move folds into the max
-#define QMOE_MAXU32_STEP(CTRL, RM) \
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, 0xF, false))
-    QMOE_MAXU32_STEP(kDppQuadXor1, 0xF);
-    QMOE_MAXU32_STEP(kDppQuadXor2, 0xF);
-    QMOE_MAXU32_STEP(kDppRowHalfMirror, 0xF);
-    QMOE_MAXU32_STEP(kDppRowMirror, 0xF);
-    QMOE_MAXU32_STEP(kDppRowBcast15, 0xA);
-    QMOE_MAXU32_STEP(kDppRowBcast31, 0xC);
-#undef QMOE_MAXU32_STEP
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
 // Softmax over a token's selected logits (s_val_row[0..K-1], slot 0 holds the
 // maximum): exps in parallel lanes, the sum in slot order, the divisions in
 // parallel lanes; and the shared-expert gate.  One wave.
