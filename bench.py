@@ -5,7 +5,7 @@ Workloads (Qwen3.6-35B-A3B MoE layer shape: hidden 2048, 256 experts, top-8 +
 1 shared expert, ffn 512, SwiGLU; synthetic seeded weights N(0,0.02) in GGUF
 block layout, f32 router N(0,0.02), f32 activations N(0,1)):
 
-  decode  (default)  10 tokens, Q4_0 experts.  HBM-bound.  Steps rotate over
+  decode             10 tokens, Q4_0 experts.  HBM-bound.  Steps rotate over
                      --layers distinct layers (8 x 0.45 GB by default, far above
                      the 256 MB Infinity Cache) and --batches input batches.
   prefill            4096 tokens, Q4_0 experts.  int8-MFMA path.
@@ -18,12 +18,16 @@ block layout, f32 router N(0,0.02), f32 activations N(0,1)):
                      tokens, Q4_0; a step is build_moe_geglu(expert_in, router_in)
                      on inputs prepared from the residual rows beforehand.
 
-A step is one layer forward over one batch (stack: one pass over all 40
-layers).  Output: ONE JSON line with value = tokens/s, the roofline of the
-dominant kernel (per-launch duration from HIP events the library records on its
-own stream; HBM traffic per launch from the committed rocprofv3 counter
-summary, when one exists for the workload) and the CPU oracle timed on the
-host cores over a bounded sample.
+Without --workload the run is the decode line (the headline: value, roofline,
+cpu_baseline) with the 4096-token prefill measured in the same process under
+"prefill" (its own MFMA roofline and CPU baseline).  A step is one layer
+forward over one batch (stack: one pass over all 40 layers); exactly --steps
+steps are timed.  The roofline's per-launch duration comes from HIP events the
+library records around the dominant kernel on its own stream; HBM traffic per
+launch from the committed rocprofv3 counter summary, when one exists.  The CPU
+oracle is timed on the host cores over a bounded sample: the median of >= 10
+forwards after 3 warm-ups, on all cores of the process's share and on 4
+threads (ggml's default thread count).
 """
 from __future__ import annotations
 
@@ -51,6 +55,9 @@ WORKLOADS = {
     "gemma4-prefill": (4096, "GEMMA4", 4, 2, 64, 8),
 }
 STACK_LAYERS = 40
+CPU_MIN_FORWARDS = 10
+CPU_WARMUP = 3
+GGML_DEFAULT_THREADS = 4
 
 
 def log(msg: str) -> None:
@@ -71,7 +78,8 @@ def cpu_model() -> str:
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", default="decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default=None, choices=sorted(WORKLOADS),
+                    help="one workload only (default: decode, plus the prefill leg)")
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--tokens", type=int, default=None)
@@ -80,7 +88,8 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of HIP graph replays")
     ap.add_argument("--profile-steps", type=int, default=None)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="per CPU leg: keep timing forwards (beyond the first 10) until this much time has passed")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, os.cpu_count())")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -126,41 +135,71 @@ class PhaseEvents:
             self.hip.hipEventDestroy(e)
 
 
-def main() -> int:
-    args = parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the MoE layer on one MI355X); "
-              f"--gpus {args.gpus} is not supported: expert-parallel sharding across GPUs is not built.",
-              file=sys.stderr, flush=True)
-        return 2
+class LayerPool:
+    """Synthetic layers generated on the GPU once and shared by the legs of a run."""
 
+    def __init__(self, seed: int, dev):
+        self.seed, self.dev = seed, dev
+        self.cache = {}
+
+    def get(self, spec_name: str, n: int, norms: bool = False):
+        from qwenium_amd import synthetic
+
+        spec = getattr(synthetic, spec_name)
+        have = self.cache.setdefault(spec_name, {"layers": [], "tensors": [], "norms": []})
+        while len(have["layers"]) < n:
+            l = len(have["layers"])
+            t = synthetic.make_layer_tensors(spec, self.seed, layer=l, device=self.dev)
+            have["tensors"].append(t)
+            have["layers"].append(synthetic.make_layer(spec, self.seed, layer=l, tensors=t))
+        while norms and len(have["norms"]) < n:
+            have["norms"].append(synthetic.make_norm_weight(spec, self.seed, len(have["norms"]), device=self.dev))
+        return spec, have["layers"][:n], have["tensors"][:n], have["norms"][:n]
+
+
+def cpu_legs(run, n_tok: int, threads_all: int, seconds: float, divide: int = 1) -> dict:
+    """Median tokens/s of the CPU oracle over >= CPU_MIN_FORWARDS forwards after
+    CPU_WARMUP warm-ups, on all threads of the share and on ggml's default 4."""
+    import numpy as np
+
+    legs = []
+    for threads in sorted({threads_all, GGML_DEFAULT_THREADS}, reverse=True):
+        for _ in range(CPU_WARMUP):
+            run(threads)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < CPU_MIN_FORWARDS or (time.perf_counter() - t_start < seconds and len(times) < 200):
+            t0 = time.perf_counter()
+            run(threads)
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        legs.append({"threads": threads, "forwards": len(times), "median_s": med,
+                     "tok_per_s": n_tok / med / divide})
+        log(f"cpu leg: {threads} threads, median {med * 1e3:.1f} ms per forward of {n_tok} tokens "
+            f"-> {n_tok / med / divide:.4g} tok/s")
+    return {leg["threads"]: leg for leg in legs}
+
+
+def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
     import numpy as np
     import torch
 
     from qwenium_amd import TYPE_Q4_0, Workspace, gemma4_moe_inputs, lib, rms_norm, synthetic
     from qwenium_amd._lib import check, row_bytes
 
-    T0, spec_name, L0, B0, S0, W0 = WORKLOADS[args.workload]
-    spec = getattr(synthetic, spec_name)
-    stack = args.workload == "stack"
-    T = args.tokens or T0
-    L = STACK_LAYERS if stack else (args.layers or L0)
-    B = args.batches or B0
-    steps_req = args.steps or S0
+    T0, spec_name, L0, B0, S0, W0 = WORKLOADS[workload]
+    stack = workload == "stack"
+    # --tokens / --layers / --batches shape the selected workload only
+    T = (args.tokens if headline and args.tokens else None) or T0
+    L = STACK_LAYERS if stack else ((args.layers if headline and args.layers else None) or L0)
+    B = (args.batches if headline and args.batches else None) or B0
+    steps = args.steps or S0
     warmup = args.warmup if args.warmup is not None else W0
+    dev = pool.dev
+    log(f"workload {workload}: T={T}, {L} layers, {B} input batches (generated on the GPU)")
+    spec, layers, tensors, norms = pool.get(spec_name, L, norms=stack)
     H, E, K, F = spec.n_embd, spec.n_experts, spec.top_k, spec.ffn_dim
     wname = "Q4_0" if spec.wtype == TYPE_Q4_0 else "Q8_0"
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-
-    log(f"workload {args.workload}: T={T}, generating {L} layers ({wname}) and {B} input batches on the GPU")
-    layers, tensors, norms = [], [], []
-    for l in range(L):
-        t = synthetic.make_layer_tensors(spec, args.seed, layer=l, device=dev)
-        tensors.append(t)
-        layers.append(synthetic.make_layer(spec, args.seed, layer=l, tensors=t))
-        if stack:
-            norms.append(synthetic.make_norm_weight(spec, args.seed, l, device=dev))
     xs = [synthetic.make_x(spec, T, args.seed, batch=b, device=dev) for b in range(B)]
     geglu = spec.geglu
     if geglu:
@@ -244,28 +283,34 @@ def main() -> int:
         run_step(i)
     torch.cuda.synchronize()
 
-    steps = steps_req
-    graph = None
+    # exactly `steps` steps: whole graphs of `period` steps, then a graph of the remainder
+    graphs = []
     if not args.eager:
         stream = torch.cuda.Stream()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(period):
-                run_step(i)
-        for _ in range(2):
-            graph.replay()
+        full, rem = steps // period, steps % period
+        for n, reps in ((period, full), (rem, 1)):
+            if n == 0 or reps == 0:
+                continue
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(n):
+                    run_step(i)
+            graphs.append((g, reps))
+        for g, _ in graphs:
+            g.replay()
         torch.cuda.synchronize()
-        steps = max(period, (steps_req // period) * period)
-
-    log(f"timing {steps} steps ({'eager' if args.eager else f'graph of {period} steps'})")
+    timing = "eager" if args.eager else (
+        f"hip graph of {period} steps x {steps // period}" + (f" + graph of {steps % period}" if steps % period else ""))
+    log(f"timing {steps} steps ({timing})")
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record()
-    if graph is not None:
-        for _ in range(steps // period):
-            graph.replay()
+    if graphs:
+        for g, reps in graphs:
+            for _ in range(reps):
+                g.replay()
     else:
         for i in range(steps):
             run_step(i)
@@ -284,10 +329,8 @@ def main() -> int:
     pe = PhaseEvents(n_prof)
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2.4e9 * 0.05))  # ~50 ms at 2.4 GHz
-    prof_layers = []
     for i in range(n_prof):
         l, b = (i % L, 0) if stack else sched[i % period]
-        prof_layers.append(l)
         check(lib().qmoe_layer_set_phase_events(layers[l]._handle, pe.arr(i)))
         layer_forward(l, b)
         check(lib().qmoe_layer_set_phase_events(layers[l]._handle, None))
@@ -295,14 +338,20 @@ def main() -> int:
     phase = pe.phases_us(n_prof)
     pe.close()
     phase_us = phase.mean(axis=0)
-    log("phase us: route %.2f gate/up %.2f h-quant+down %.2f combine %.2f" % tuple(phase_us))
     D_prof = D_mean if stack else float(np.mean([distinct[i % period] for i in range(n_prof)]))
     gu_us = float(phase_us[1])
+    fused_combine = T <= 16
+    if fused_combine:
+        # the combine runs in the down kernel: events [3] and [4] are back to back
+        phases = {"route": phase_us[0], "gate_up": phase_us[1], "down_combine": phase_us[2] + phase_us[3]}
+    else:
+        phases = {"route": phase_us[0], "gate_up": phase_us[1], "hquant_down": phase_us[2], "combine": phase_us[3]}
+    log("phase us: " + ", ".join(f"{k} {v:.2f}" for k, v in phases.items()))
 
     # HBM traffic per launch of the dominant kernel, measured by rocprofv3 FETCH_SIZE /
     # WRITE_SIZE passes and scaled by a known-size copy (summary committed under profiles/)
     traffic = None
-    tpath = os.path.join(REPO, "profiles", f"traffic_{args.workload}.json")
+    tpath = os.path.join(REPO, "profiles", f"traffic_{workload}.json")
     if os.path.exists(tpath) and not stack:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -329,7 +378,7 @@ def main() -> int:
     else:
         achieved = ops_gu / (gu_us * 1e-6) / 1e12
         roofline = {
-            "bound": "mfma", "kernel": "k_expert_mfma<gate/up> (int8 MFMA grouped GEMM, f64-exact block epilogue)",
+            "bound": "mfma", "kernel": "k_expert_mfma<gate/up> (int8 MFMA grouped GEMM)",
             "achieved": achieved, "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s", "frac": achieved / MFMA_I8_PEAK_TOPS,
             "traffic": traffic, "ops_per_launch": ops_gu, "avg_launch_us": gu_us,
         }
@@ -352,9 +401,9 @@ def main() -> int:
     elif geglu:
         metric = (f"MoE-layer tokens/s at Gemma 4 26B-A4B shape (GeGLU, "
                   f"{'decode batch' if T <= 64 else 'prefill'} {T}{'' if T <= 64 else ' tokens'}, {wname})")
-    elif args.workload == "decode":
+    elif workload == "decode":
         metric = f"MoE-layer tokens/s at 35B-A3B shape (decode batch {T}, {wname})"
-    elif args.workload == "skewed":
+    elif workload == "skewed":
         metric = f"MoE-layer tokens/s at 35B-A3B shape (Zipf-skewed routing, {T} tokens, {wname})"
     else:
         metric = f"MoE-layer tokens/s at 35B-A3B shape (prefill {T} tokens, {wname})"
@@ -405,26 +454,71 @@ def main() -> int:
                 "max_abs_err_over_rms": float(np.max(np.abs(yg - yr)) / rms),
                 "bit_identical_frac": float(np.mean(yg.view(np.int32) == yr.view(np.int32))),
             }
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads_all = args.cpu_threads or min(16, os.cpu_count() or 1)
         ref = host_layer(0)
         n_cpu_tok = min(T, 10 if T <= 64 else 256)
         xc = (g4_in[0][0] if geglu else xs[0]).cpu().numpy()[:n_cpu_tok]
         xrc = g4_in[0][1].cpu().numpy()[:n_cpu_tok] if geglu else None
-        ref.forward(xc, nthreads=threads, router_in=xrc)  # warm
-        iters, t_cpu = 0, 0.0
-        t_start = time.perf_counter()
-        while t_cpu < args.cpu_seconds:
-            ref.forward(xc, nthreads=threads, router_in=xrc)
-            iters += 1
-            t_cpu = time.perf_counter() - t_start
-        layer_tok_s = iters * n_cpu_tok / t_cpu
+        legs = cpu_legs(lambda th: ref.forward(xc, nthreads=th, router_in=xrc), n_cpu_tok, threads_all,
+                        args.cpu_seconds, divide=L if stack else 1)
+        main_leg = legs[threads_all]
         cpu = {
-            "value": layer_tok_s / (L if stack else 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{iters} forwards of layer 0 on {n_cpu_tok} tokens of batch 0 in {t_cpu:.1f}s"
-                      + (f", divided by the {L} layers of the stack" if stack else "")
-                      + f"; ggml-semantics CPU restatement (oracle/liboracle.so, OpenMP) on {cpu_model()}",
+            "value": main_leg["tok_per_s"], "unit": "tokens/s", "cores": threads_all, "kind": "port",
+            "sample": (f"median of {main_leg['forwards']} forwards (after {CPU_WARMUP} warm-ups) of layer 0 on "
+                       f"{n_cpu_tok} tokens of batch 0" + (f", divided by the {L} layers of the stack" if stack else "")
+                       + f"; ggml-semantics CPU restatement (oracle/liboracle.so, OpenMP, exact f64 block sums) "
+                       f"on {cpu_model()}"),
+            "legs": [{"threads": th, "tok_per_s": lg["tok_per_s"], "median_ms_per_forward": lg["median_s"] * 1e3,
+                      "forwards": lg["forwards"]} for th, lg in sorted(legs.items())],
         }
-        log(f"cpu baseline {cpu['value']:.4g} tok/s on {threads} threads")
+
+    fault = ws.check()
+    if fault:
+        raise RuntimeError(f"workload {workload}: a decode routing wait gave up during the run (outputs are NaN)")
+    return {
+        "metric": metric,
+        "value": tok_per_s,
+        "unit": "tokens/s",
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms_per_step,
+        "dtype": f"{wname.lower()} x q8_0 int8 dot, f32 activations",
+        "config": {
+            "workload": (f"{L} x Qwen3.6-35B-A3B MoE block (RMSNorm + MoE + residual), {T} tokens" if stack else
+                         f"Gemma 4 26B-A4B GeGLU MoE layer, {workload} {T} tokens" if geglu else
+                         f"Qwen3.6-35B-A3B MoE layer, {workload} {T} tokens") +
+                        f": hidden {H}, {E} experts, top-{K}{' + shared' if spec.shared else ''}, ffn {F}, {wname}" +
+                        (f"; {D_mean:.1f} distinct routed experts per forward on average" if T <= 64 else ""),
+            "tokens": T, "hidden": H, "experts": E, "top_k": K, "ffn": F, "shared_expert": spec.shared,
+            "weight_type": wname, "layers": L, "distinct_batches": B, "timing": timing,
+        },
+        "layer": layer_rate,
+        "phase_us": {"note": "eager forwards with events between phases (event overhead included)", **phases},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "parity": result_parity,
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the MoE layer on one MI355X); "
+              f"--gpus {args.gpus} is not supported: expert-parallel sharding across GPUs is not built.",
+              file=sys.stderr, flush=True)
+        return 2
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    pool = LayerPool(args.seed, dev)
+    head_name = args.workload or "decode"
+    head = run_leg(args, pool, head_name, headline=True)
+    extra = {}
+    if args.workload is None:
+        # the prefill part of the metric, in the same process on the same layers
+        extra["prefill"] = run_leg(args, pool, "prefill", headline=False)
 
     if args.copy_mib > 0:
         n = args.copy_mib << 20
@@ -438,35 +532,27 @@ def main() -> int:
         del src, dst
 
     out = {
-        "metric": metric,
-        "value": tok_per_s,
+        "metric": head["metric"],
+        "value": head["value"],
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
-        "ms_per_step": ms_per_step,
+        "steps": head["steps"],
+        "warmup": head["warmup"],
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": f"{wname.lower()} x q8_0 int8 dot, f64-exact accumulation, f32 activations",
+        "dtype": head["dtype"],
         "data": ("synthetic (seeded, generated on device; random-init weights of the "
-                 f"{'Gemma 4 26B-A4B' if geglu else '35B-A3B'} MoE layer shape)"),
-        "config": {
-            "workload": (f"{L} x Qwen3.6-35B-A3B MoE block (RMSNorm + MoE + residual), {T} tokens" if stack else
-                         f"Gemma 4 26B-A4B GeGLU MoE layer, {args.workload} {T} tokens" if geglu else
-                         f"Qwen3.6-35B-A3B MoE layer, {args.workload} {T} tokens") +
-                        f": hidden {H}, {E} experts, top-{K}{' + shared' if spec.shared else ''}, ffn {F}, {wname}",
-            "tokens": T, "hidden": H, "experts": E, "top_k": K, "ffn": F, "shared_expert": spec.shared,
-            "weight_type": wname, "layers": L, "distinct_batches": B,
-            "timing": "eager" if args.eager else f"hip graph of {period} steps",
-        },
-        "layer": layer_rate,
-        "phase_us": {"route": phase_us[0], "gate_up": phase_us[1], "hquant_down": phase_us[2],
-                     "combine": phase_us[3]},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "parity": result_parity,
+                 f"{'Gemma 4 26B-A4B' if head_name.startswith('gemma4') else '35B-A3B'} MoE layer shape)"),
+        "config": head["config"],
+        "layer": head["layer"],
+        "phase_us": head["phase_us"],
+        "roofline": head["roofline"],
+        "cpu_baseline": head["cpu_baseline"],
+        "parity": head["parity"],
     }
+    out.update(extra)
     print(json.dumps(out), flush=True)
     return 0
 

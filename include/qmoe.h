@@ -44,7 +44,9 @@ enum qmoe_status {
     QMOE_ERR_TYPE     = 3,  /* unsupported or mismatched ggml type */
     QMOE_ERR_VALUE    = 4,  /* bad hparam / argument value */
     QMOE_ERR_CAPACITY = 5,  /* n_tokens above the workspace capacity */
-    QMOE_ERR_HIP      = 6   /* a HIP runtime call failed */
+    QMOE_ERR_HIP      = 6,  /* a HIP runtime call failed */
+    QMOE_ERR_SYNC     = 7   /* an earlier forward on the workspace gave up a bounded
+                               cross-block wait; qmoe_workspace_check clears it */
 };
 
 /* A borrowed ggml tensor view: device data + ggml type + ne/nb (ne[0] contiguous).
@@ -119,8 +121,12 @@ int qmoe_workspace_destroy(qmoe_workspace* ws);
 int32_t qmoe_workspace_capacity(const qmoe_workspace* ws);
 /* Synchronizes the device and reports, in *fault, whether any forward on this
  * workspace gave up a bounded cross-block wait (1) or not (0); clears the
- * word.  A raised word means that forward's routing is not to be trusted.  No
- * counterpart in the reference (ggml runs ops one after another). */
+ * word and restarts the workspace's signalling area.  A give-up is loud
+ * without this call: the forward that gave up, and every forward queued on the
+ * workspace behind it, writes NaN outputs, and every qmoe_layer_forward* call
+ * on the workspace returns QMOE_ERR_SYNC (read from host-mapped memory, no
+ * synchronisation) until this call clears it.  No counterpart in the
+ * reference (ggml runs ops one after another). */
 int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault);
 
 /* Replaces MoELayer::build (moe.h:58-63, moe.cpp:55-177):
@@ -128,7 +134,9 @@ int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault);
  *   the caller's ggml_add(cur, ffn_inp) of qwen36.cpp:304).
  * x, y, residual: device f32, token-major (ggml [n_embd, n_tokens]).  y may
  * alias residual but not x.  ws == NULL uses a workspace owned by the layer,
- * allocated (synchronously) on first use and grown when n_tokens exceeds it.
+ * allocated on first use and grown when n_tokens exceeds it; growing it
+ * synchronises the device, and on a stream that is being captured into a HIP
+ * graph it fails with QMOE_ERR_CAPACITY instead (pass a workspace there).
  * n_tokens == 0 is a no-op.  dbg may be NULL. */
 int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
                        const float* x, int32_t n_tokens, float* y,

@@ -22,6 +22,7 @@ QMOE_ERR_TYPE = 3
 QMOE_ERR_VALUE = 4
 QMOE_ERR_CAPACITY = 5
 QMOE_ERR_HIP = 6
+QMOE_ERR_SYNC = 7
 
 # every function declared in include/qmoe.h
 EXPORTED = (

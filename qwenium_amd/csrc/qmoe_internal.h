@@ -43,6 +43,7 @@ struct LayerDesc {
     int mfma_min_tokens = 128;              // token count from which the int8-MFMA path runs
     int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs
     int dc_ahead = 2;                       // decode down+combine: steps with loads in flight (2 or 4)
+    int max_spins = 1 << 22;                // decode routing: polling passes before its bounded wait gives up
     unsigned long long* expert_counts = nullptr;  // optional device [E]: += each forward's per-expert dispatches
     int act = 0;                            // 0 SwiGLU (silu(g)*u), 1 GeGLU-tanh (gelu(g)*u, ggml's fp16 table)
     const uint16_t* gelu_tab = nullptr;     // device [65536] fp16 gelu table of the layer's device (GeGLU)
@@ -74,6 +75,7 @@ struct Workspace {
                                   // active routed experts, then expert -1 up to min(E, T*K)
     int32_t* counters = nullptr;  // [16] n_active, n_tiles, ...
     int32_t* sync = nullptr;      // [kSyncWords] zeroed at creation: generation, error flag, block flags
+    int32_t* host_err = nullptr;  // host-mapped word (device address): raised with sync[kSyncErr]
     int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
     float2* gubuf = nullptr;      // [R][F] (gate, up) projections
     int8_t* hq_qs = nullptr;      // [R][F]   Q8_0 quants of h = silu(g)*u

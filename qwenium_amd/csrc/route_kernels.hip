@@ -324,6 +324,8 @@ struct TopkArgs {
     int4* tiles;
     int max_tiles;
     int nblk;
+    int max_spins;        // fused decode routing: polling passes before the bounded wait gives up
+    int32_t* host_err;    // fused decode routing: host-mapped error word (raised on a give-up)
 };
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
@@ -795,7 +797,6 @@ constexpr int kRdSlab = 256;        // columns per lane-float4 sweep
 constexpr int kMaxRdSlabs = 16;     // fused decode routing for H <= 4096
 // dynamic LDS: block 0's routing tables, the shared-expert blocks' token rows
 constexpr int kRdLdsBytes = 96 * 1024;
-constexpr int kMaxSpins = 1 << 22;  // bounded wait: a flag that never comes raises the error word
 constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
 
 // Wave sums of N per-lane f64 values at once (reduce-scatter): after the 32-
@@ -1011,21 +1012,40 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
         if (tid == 0) __hip_atomic_store(sync + kSyncFlags + blockIdx.x, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    // block 0: wait for the other blocks' flags (lane l watches blocks 1 + l + 64 i)
+    // block 0: wait for the other blocks' flags (lane l watches blocks 1 + l + 64 i).
+    // The wait is bounded.  A give-up raises the workspace's error word, which
+    // stays raised (every later forward on the workspace sees it here) until the
+    // host clears the whole signalling area after a device synchronisation; the
+    // host-mapped copy lets the next host call fail without one.  A forward that
+    // sees the word routes as usual (every table stays in range) and then sets
+    // its softmax weights and shared gates to NaN, so its outputs are NaN.
+    __shared__ int s_fault;
     if (wave == 0) {
-        bool done = false;
-        for (int it = 0; it < kMaxSpins && !done; ++it) {
+        bool done = nb <= 1;
+        for (int it = 0; it < a.max_spins && !done; ++it) {
             bool mine = true;
             for (int bb = 1 + lane; bb < nb; bb += 64)  // every watched flag loaded in each pass, independently
                 mine &= __hip_atomic_load(sync + kSyncFlags + bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen;
             done = __all(mine);
             if (!done) __builtin_amdgcn_s_sleep(2);
         }
-        if (!done && lane == 0) __hip_atomic_store(sync + kSyncErr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool fault = !done || __hip_atomic_load(sync + kSyncErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+        if (fault && lane == 0) {
+            __hip_atomic_store(sync + kSyncErr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.host_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        if (lane == 0) s_fault = fault ? 1 : 0;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // drop stale cached logits (L1 and this XCD's L2)
     }
     __syncthreads();
     route_small_body(a, *(SmallRouteLds*)s_dyn);
+    if (s_fault) {
+        __syncthreads();  // after the softmax writes of route_small_body
+        const float nan = __builtin_nanf("");
+        for (int i = tid; i < a.T * a.K; i += blockDim.x) a.topk_w[i] = nan;
+        if (a.S)
+            for (int t = tid; t < a.T; t += blockDim.x) a.sh_gate[t] = nan;
+    }
     if (tid == 0) __hip_atomic_store(sync + kSyncGen, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1188,6 +1208,8 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
     ta.nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
+    ta.max_spins = L.max_spins;
+    ta.host_err = ws.host_err;
     hipError_t err;
     if (route_uses_mfma(L, T)) {
         RouterMfmaArgs ma;

@@ -12,6 +12,7 @@ computation runs in libqmoe's HIP kernels.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import dataclasses
 from typing import Optional
@@ -54,6 +55,51 @@ def _stream_ptr(stream) -> Optional[int]:
     if stream is None:
         stream = torch.cuda.current_stream()
     return stream.cuda_stream
+
+
+def _on(stream):
+    """Makes `stream` current while the arguments of a launch are prepared, so
+    contiguous copies and output allocations are ordered on the stream the
+    kernels run on (and return to its pool when freed)."""
+    return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+
+
+def _rows_in(name: str, t: torch.Tensor, T: int, H: int, device) -> torch.Tensor:
+    """A read-only [T, H] f32 operand on `device` (the input rows' device, a
+    cuda device once x has been checked): checked, then made contiguous."""
+    if (not isinstance(t, torch.Tensor) or t.dim() != 2 or tuple(t.shape) != (T, H) or t.dtype != torch.float32
+            or t.device != device):
+        raise ValueError(f"{name} expected a cuda float32 [{T}, {H}] tensor on {device}, got "
+                         f"{_describe(t)}")
+    return t.contiguous()
+
+
+def _rows_out(name: str, t: Optional[torch.Tensor], T: int, H: int, device, like: torch.Tensor) -> torch.Tensor:
+    """The [T, H] f32 output: a new tensor, or the caller's, which must be
+    contiguous (the kernels write T*H floats from its first element)."""
+    if t is None:
+        return torch.empty((T, H), dtype=torch.float32, device=device)
+    if (not isinstance(t, torch.Tensor) or t.dim() != 2 or tuple(t.shape) != (T, H) or t.dtype != torch.float32
+            or t.device != device or not t.is_contiguous()):
+        raise ValueError(f"{name} expected a contiguous cuda float32 [{T}, {H}] tensor on {device}, got "
+                         f"{_describe(t)}")
+    if t.data_ptr() == like.data_ptr():
+        raise ValueError(f"{name} expected a buffer distinct from the input rows, got the same storage")
+    return t
+
+
+def _vec_in(name: str, t: torch.Tensor, H: int, device) -> torch.Tensor:
+    """A per-feature f32 weight [H] on `device`."""
+    if (not isinstance(t, torch.Tensor) or t.dim() != 1 or t.shape[0] != H or t.dtype != torch.float32
+            or t.device != device):
+        raise ValueError(f"{name} expected a cuda float32 [{H}] tensor on {device}, got {_describe(t)}")
+    return t.contiguous()
+
+
+def _describe(t) -> str:
+    if not isinstance(t, torch.Tensor):
+        return type(t).__name__
+    return f"{tuple(t.shape)} {t.dtype} on {t.device}{'' if t.is_contiguous() else ' (non-contiguous)'}"
 
 
 class Workspace:
@@ -135,74 +181,56 @@ class MoELayer:
         routing intermediates (logits, topk_idx, topk_w, sh_gate, offsets, rows, and
         router_approx/router_bound, left NaN unless the batched MFMA router ran)."""
         del phase, il  # MoE has one topology (moe.h:55-57); il only names tensors in ggml
-        if x.dim() != 2 or x.shape[1] != self.n_embd or x.dtype != torch.float32 or not x.is_cuda:
-            raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got "
-                             f"{tuple(x.shape)} {x.dtype} on {x.device}")
-        x = x.contiguous()
-        T = x.shape[0]
-        y = out if out is not None else torch.empty_like(x)
-        dbg = None
-        dbg_tensors = None
-        if debug:
-            E, k = self.hp.n_experts, self.hp.top_k
-            dev = x.device
-            dbg_tensors = {
-                "logits": torch.empty((T, E), dtype=torch.float32, device=dev),
-                "topk_idx": torch.empty((T, k), dtype=torch.int32, device=dev),
-                "topk_w": torch.empty((T, k), dtype=torch.float32, device=dev),
-                "sh_gate": torch.empty((T,), dtype=torch.float32, device=dev),
-                "offsets": torch.empty((E + 1,), dtype=torch.int32, device=dev),
-                "rows": torch.empty((T * k,), dtype=torch.int32, device=dev),
-                "router_approx": torch.full((T, E), float("nan"), dtype=torch.float32, device=dev),
-                "router_bound": torch.full((T, E), float("nan"), dtype=torch.float32, device=dev),
-            }
-            dbg = QmoeDebug(*(dbg_tensors[n].data_ptr() for n in
-                              ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows",
-                               "router_approx", "router_bound")))
-        check(lib().qmoe_layer_forward(
-            self._handle, workspace._handle if workspace is not None else None,
-            x.data_ptr(), int(T), y.data_ptr(),
-            residual.contiguous().data_ptr() if residual is not None else None,
-            ctypes.byref(dbg) if dbg is not None else None, _stream_ptr(stream)))
-        if debug:
-            return y, dbg_tensors
-        return y
+        with _on(stream):
+            x = self._check_x(x)
+            T = x.shape[0]
+            res = _rows_in("residual", residual, T, self.n_embd, x.device) if residual is not None else None
+            y = _rows_out("out", out, T, self.n_embd, x.device, x)
+            dbg, dbg_tensors = self._debug(T, x.device) if debug else (None, None)
+            check(lib().qmoe_layer_forward(
+                self._handle, workspace._handle if workspace is not None else None,
+                x.data_ptr(), int(T), y.data_ptr(), res.data_ptr() if res is not None else None,
+                ctypes.byref(dbg) if dbg is not None else None, _stream_ptr(stream)))
+        return (y, dbg_tensors) if debug else y
 
     def forward_norm(self, x: torch.Tensor, norm_weight: torch.Tensor, eps: float, *,
-                     out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None, stream=None):
+                     out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None,
+                     debug: bool = False, stream=None):
         """The block's caller slice in one call (qwen36.cpp:297-304):
         y = x + MoE(RMSNorm(x) * norm_weight).  Same bits as
         forward(rms_norm(x, norm_weight, eps), residual=x)."""
-        if x.dim() != 2 or x.shape[1] != self.n_embd or x.dtype != torch.float32 or not x.is_cuda:
-            raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got "
-                             f"{tuple(x.shape)} {x.dtype} on {x.device}")
-        x = x.contiguous()
-        w = norm_weight.contiguous()
-        y = out if out is not None else torch.empty_like(x)
-        check(lib().qmoe_layer_forward_norm(
-            self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), w.data_ptr(),
-            float(eps), int(x.shape[0]), y.data_ptr(), None, _stream_ptr(stream)))
-        return y
+        with _on(stream):
+            x = self._check_x(x)
+            w = _vec_in("norm_weight", norm_weight, self.n_embd, x.device)
+            y = _rows_out("out", out, x.shape[0], self.n_embd, x.device, x)
+            dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
+            check(lib().qmoe_layer_forward_norm(
+                self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), w.data_ptr(),
+                float(eps), int(x.shape[0]), y.data_ptr(), ctypes.byref(dbg) if dbg is not None else None,
+                _stream_ptr(stream)))
+        return (y, dbg_tensors) if debug else y
 
     def forward_routed(self, expert_in: torch.Tensor, router_in: torch.Tensor, *, out: Optional[torch.Tensor] = None,
                        workspace: Optional[Workspace] = None, debug: bool = False, stream=None):
         """y = MoE(expert_in) routed on router_in (build_moe_geglu's two inputs,
         gemma4.cpp:367-380); the shared expert's gate, if any, reads router_in."""
-        x = self._check_x(expert_in)
-        xr = self._check_x(router_in)
-        if xr.shape != x.shape:
-            raise ValueError(f"router_in expected shape {tuple(x.shape)}, got {tuple(xr.shape)}")
-        y = out if out is not None else torch.empty_like(x)
-        dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
-        check(lib().qmoe_layer_forward_routed(
-            self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), xr.data_ptr(),
-            int(x.shape[0]), y.data_ptr(), ctypes.byref(dbg) if dbg is not None else None, _stream_ptr(stream)))
+        with _on(stream):
+            x = self._check_x(expert_in)
+            xr = _rows_in("router_in", router_in, x.shape[0], self.n_embd, x.device)
+            y = _rows_out("out", out, x.shape[0], self.n_embd, x.device, x)
+            if y.data_ptr() == xr.data_ptr():
+                raise ValueError("out expected a buffer distinct from router_in, got the same storage")
+            dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
+            check(lib().qmoe_layer_forward_routed(
+                self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), xr.data_ptr(),
+                int(x.shape[0]), y.data_ptr(), ctypes.byref(dbg) if dbg is not None else None,
+                _stream_ptr(stream)))
         return (y, dbg_tensors) if debug else y
 
     def _check_x(self, x: torch.Tensor) -> torch.Tensor:
-        if x.dim() != 2 or x.shape[1] != self.n_embd or x.dtype != torch.float32 or not x.is_cuda:
-            raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got "
-                             f"{tuple(x.shape)} {x.dtype} on {x.device}")
+        if (not isinstance(x, torch.Tensor) or x.dim() != 2 or x.shape[1] != self.n_embd
+                or x.dtype != torch.float32 or not x.is_cuda):
+            raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got {_describe(x)}")
         return x.contiguous()
 
     def _debug(self, T: int, dev):
@@ -247,25 +275,31 @@ class GeGLUMoELayer(MoELayer):
                        debug: bool = False, stream=None):
         """The Gemma 4 MoE branch from the residual rows x (gemma4.cpp:555-565):
         build_moe_geglu(rms_norm(x)*pre_norm_weight, (rms_norm(x)/sqrt(n_embd))*router_scale)."""
-        x = self._check_x(x)
-        w, rs = pre_norm_weight.contiguous(), router_scale.contiguous()
-        y = out if out is not None else torch.empty_like(x)
-        dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
-        check(lib().qmoe_layer_forward_gemma4(
-            self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), w.data_ptr(),
-            rs.data_ptr(), float(eps), int(x.shape[0]), y.data_ptr(), ctypes.byref(dbg) if dbg is not None else None,
-            _stream_ptr(stream)))
+        with _on(stream):
+            x = self._check_x(x)
+            w = _vec_in("pre_norm_weight", pre_norm_weight, self.n_embd, x.device)
+            rs = _vec_in("router_scale", router_scale, self.n_embd, x.device)
+            y = _rows_out("out", out, x.shape[0], self.n_embd, x.device, x)
+            dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
+            check(lib().qmoe_layer_forward_gemma4(
+                self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), w.data_ptr(),
+                rs.data_ptr(), float(eps), int(x.shape[0]), y.data_ptr(),
+                ctypes.byref(dbg) if dbg is not None else None, _stream_ptr(stream)))
         return (y, dbg_tensors) if debug else y
 
 
 def gemma4_moe_inputs(x: torch.Tensor, pre_norm_weight: torch.Tensor, router_scale: torch.Tensor, eps: float,
                       stream=None):
     """(expert_in, router_in) of the Gemma 4 MoE branch (gemma4.cpp:555-563)."""
-    x = x.contiguous()
-    ei, ri = torch.empty_like(x), torch.empty_like(x)
-    check(lib().qmoe_gemma4_moe_inputs(x.data_ptr(), pre_norm_weight.contiguous().data_ptr(),
-                                       router_scale.contiguous().data_ptr(), float(eps), int(x.shape[0]),
-                                       int(x.shape[1]), ei.data_ptr(), ri.data_ptr(), _stream_ptr(stream)))
+    with _on(stream):
+        if not isinstance(x, torch.Tensor) or x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda:
+            raise ValueError(f"x expected a cuda float32 [T, n_embd] tensor, got {_describe(x)}")
+        x = x.contiguous()
+        w = _vec_in("pre_norm_weight", pre_norm_weight, x.shape[1], x.device)
+        rs = _vec_in("router_scale", router_scale, x.shape[1], x.device)
+        ei, ri = torch.empty_like(x), torch.empty_like(x)
+        check(lib().qmoe_gemma4_moe_inputs(x.data_ptr(), w.data_ptr(), rs.data_ptr(), float(eps), int(x.shape[0]),
+                                           int(x.shape[1]), ei.data_ptr(), ri.data_ptr(), _stream_ptr(stream)))
     return ei, ri
 
 
@@ -281,10 +315,15 @@ def gelu_f16_table():
 def rms_norm(x: torch.Tensor, w: Optional[torch.Tensor], eps: float, out: Optional[torch.Tensor] = None,
              stream=None) -> torch.Tensor:
     """build_rms_norm (norm.cpp:15-26): x / sqrt(mean(x^2) + eps) * w, per token."""
-    x = x.contiguous()
-    y = out if out is not None else torch.empty_like(x)
-    check(lib().qmoe_rms_norm(x.data_ptr(), w.data_ptr() if w is not None else None, int(x.shape[0]),
-                              int(x.shape[1]), float(eps), y.data_ptr(), _stream_ptr(stream)))
+    with _on(stream):
+        if not isinstance(x, torch.Tensor) or x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda:
+            raise ValueError(f"x expected a cuda float32 [T, n_embd] tensor, got {_describe(x)}")
+        x = x.contiguous()
+        T, H = x.shape
+        wc = _vec_in("w", w, H, x.device) if w is not None else None
+        y = _rows_out("out", out, T, H, x.device, x) if out is not None else torch.empty_like(x)
+        check(lib().qmoe_rms_norm(x.data_ptr(), wc.data_ptr() if wc is not None else None, int(T), int(H),
+                                  float(eps), y.data_ptr(), _stream_ptr(stream)))
     return y
 
 

@@ -168,3 +168,50 @@ def test_python_wrapper_raises_with_message():
     from qwenium_amd import QmoeError
     with pytest.raises(QmoeError, match="has_shared_expert=true"):
         _lib.check(create({**layer_descs(), "sh_gate": None}, QmoeHparams(256, 8, 512, 1))[0])
+
+
+# ---- the Python mirror's argument checks (no GPU: the checks run before any launch) ----
+
+def test_python_row_and_vector_checks():
+    import torch
+
+    from qwenium_amd import moe
+
+    dev = torch.device("cpu")
+    x = torch.zeros(4, 8)
+    ok = torch.zeros(4, 8)
+    assert moe._rows_out("out", ok, 4, 8, dev, x) is ok
+    for bad in (torch.zeros(3, 8), torch.zeros(4, 8, dtype=torch.float64), torch.zeros(8, 4).t(),
+                torch.zeros(4 * 8), "not a tensor"):
+        with pytest.raises(ValueError, match="out expected a contiguous"):
+            moe._rows_out("out", bad, 4, 8, dev, x)
+    with pytest.raises(ValueError, match="distinct from the input rows"):
+        moe._rows_out("out", x, 4, 8, dev, x)
+    # a read-only operand is copied when strided, rejected when the shape or type is wrong
+    strided = torch.zeros(8, 4).t()
+    assert moe._rows_in("residual", strided, 4, 8, dev).is_contiguous()
+    for bad in (torch.zeros(4, 7), torch.zeros(4, 8, dtype=torch.float16), None):
+        with pytest.raises(ValueError, match="residual expected"):
+            moe._rows_in("residual", bad, 4, 8, dev)
+    assert moe._vec_in("norm_weight", torch.zeros(8), 8, dev).shape == (8,)
+    for bad in (torch.zeros(7), torch.zeros(1, 8), torch.zeros(8, dtype=torch.int32)):
+        with pytest.raises(ValueError, match="norm_weight expected"):
+            moe._vec_in("norm_weight", bad, 8, dev)
+    # another device than the input rows'
+    with pytest.raises(ValueError, match="on meta"):
+        moe._rows_in("residual", torch.zeros(4, 8), 4, 8, torch.device("meta"))
+
+
+def test_python_forward_rejects_host_input():
+    import torch
+
+    from qwenium_amd import moe
+
+    layer = moe.MoELayer.__new__(moe.MoELayer)  # no handle: the checks fail before any call into the library
+    layer.n_embd = 8
+    with pytest.raises(ValueError, match="x expected a cuda float32"):
+        layer.forward(torch.zeros(2, 8))
+    with pytest.raises(ValueError, match="x expected a cuda float32"):
+        layer.forward_norm(torch.zeros(2, 8), torch.ones(8), 1e-6)
+    with pytest.raises(ValueError, match="x expected a cuda float32"):
+        moe.rms_norm(torch.zeros(2, 8), None, 1e-6)

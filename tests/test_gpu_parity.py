@@ -399,14 +399,17 @@ def test_skewed_q8_0_t2048(gpu):
     assert np.mean(yg.view(np.int32) == y_ref.view(np.int32)) >= 0.999
 
 
-def test_stack_40_layers_t10(gpu):
-    """40 consecutive blocks x <- x + MoE_l(RMSNorm(x) * w_l) at decode batch 10 through the
-    fused-norm call; layers 0 and 39 checked against the oracle on their actual inputs (and
-    against the unfused rms_norm + forward)."""
+@pytest.mark.parametrize("T", [1, 10, 64, 8192])
+def test_stack_40_layers(gpu, T):
+    """Config 5: 40 consecutive blocks x <- x + MoE_l(RMSNorm(x) * w_l) (qwen36.cpp:297-304 at
+    prefill, :427-432 at decode) through the fused-norm call, at decode batches 1, 10 and 64
+    and at 8192-token prefill.  Layers 0 and 39 are checked against the oracle on their actual
+    inputs (and against the unfused rms_norm + forward): routing bit-exact on every token,
+    outputs within tolerance (all tokens up to 64, a sample of 48 at 8192)."""
     from qwenium_amd import Workspace, rms_norm
 
     spec = synthetic.QWEN35B
-    T, L, seed = 10, 40, 11
+    L, seed = 40, 11
     ws = None
     x = synthetic.make_x(spec, T, seed)
     h = torch.empty_like(x)
@@ -423,21 +426,31 @@ def test_stack_40_layers_t10(gpu):
             y_fused = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws)
             torch.cuda.synchronize()
             assert torch.equal(y, y_fused), f"layer {l}: fused RMSNorm path"
-            keep[l] = (x.cpu().numpy(), wn.cpu().numpy(), t, y.cpu().numpy(), dbg["topk_idx"].cpu().numpy())
+            keep[l] = (x.cpu().numpy(), wn.cpu().numpy(), t, y.cpu().numpy(),
+                       {k: dbg[k].cpu().numpy() for k in ("topk_idx", "offsets", "rows")})
         else:
             y = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws)
         x = y
         del t, layer
     torch.cuda.synchronize()
     assert np.isfinite(x.cpu().numpy()).all()
-    for l, (xin, wn, t, yg, ig) in keep.items():
+    assert ws.check() == 0
+    for l, (xin, wn, t, yg, got) in keep.items():
         hh = po.rms_norm(xin, wn, synthetic.NORM_EPS)
-        yr, dr = host_layer(spec, t).forward(hh, debug=True)
-        yr = yr + xin
-        np.testing.assert_array_equal(ig, dr["topk_idx"])
+        ref = host_layer(spec, t)
+        # routing of every token
+        idx, _ = po.topk_softmax(po.router_logits(ref.t["router"], hh), spec.top_k)
+        off, rows, _ = po.sort_assignments(idx, spec.n_experts)
+        np.testing.assert_array_equal(got["topk_idx"], idx, err_msg=f"layer {l}")
+        np.testing.assert_array_equal(got["offsets"], off, err_msg=f"layer {l}")
+        np.testing.assert_array_equal(got["rows"], rows, err_msg=f"layer {l}")
+        sample = np.arange(T) if T <= 64 else np.concatenate(
+            [np.arange(8), np.random.default_rng(l).choice(T, 40, replace=False)])
+        yr = ref.forward(hh[sample]) + xin[sample]
+        ys = yg[sample]
         rms = float(np.sqrt(np.mean(yr.astype(np.float64) ** 2)))
-        assert np.max(np.abs(yg - yr)) <= TOL * rms, f"layer {l}"
-        assert np.mean(yg.view(np.int32) == yr.view(np.int32)) >= 0.999, f"layer {l}"
+        assert np.max(np.abs(ys - yr)) <= TOL * rms, f"layer {l}"
+        assert np.mean(ys.view(np.int32) == yr.view(np.int32)) >= 0.999, f"layer {l}"
 
 
 @pytest.mark.parametrize("n_experts,T", [(256, 10), (1024, 16), (16, 3)])
@@ -482,3 +495,82 @@ def test_forward_norm_matches_unfused(gpu, which, T):
     torch.cuda.synchronize()
     assert ws.check() == 0
     assert torch.equal(y_fused, y_ref)
+
+
+def test_decode_wait_give_up_is_loud(gpu, monkeypatch):
+    """The decode routing's bounded wait forced to give up from the host (a layer created
+    with no polling passes): every kernel exits normally, the outputs are NaN, the next
+    forward call on the workspace fails with QMOE_ERR_SYNC (read from host-mapped memory,
+    no synchronisation), Workspace.check() reports and clears it, and forwards after that
+    match the oracle again."""
+    from qwenium_amd import Workspace
+    from qwenium_amd._lib import QMOE_ERR_SYNC, QmoeError
+
+    spec = synthetic.QWEN35B
+    T, seed = 10, 5
+    tensors = synthetic.make_layer_tensors(spec, seed)
+    monkeypatch.setenv("QMOE_MAX_SPINS", "0")
+    bad = synthetic.make_layer(spec, seed, tensors=tensors)
+    monkeypatch.delenv("QMOE_MAX_SPINS")
+    good = synthetic.make_layer(spec, seed, tensors=tensors)
+    ws = Workspace(good, 16)
+    x = synthetic.make_x(spec, T, seed)
+    y_bad = bad.forward(x, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.isnan(y_bad).all()
+    with pytest.raises(QmoeError) as ei:
+        good.forward(x, workspace=ws)
+    assert ei.value.code == QMOE_ERR_SYNC
+    assert ws.check() == 1
+    assert ws.check() == 0
+    # a forward queued right behind a give-up, before the host could see it, is NaN too
+    y_bad = bad.forward(x, workspace=ws)
+    try:
+        y_next = good.forward(x, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.isnan(y_next).all()
+    except QmoeError as e:
+        assert e.code == QMOE_ERR_SYNC
+    torch.cuda.synchronize()
+    assert torch.isnan(y_bad).all()
+    assert ws.check() == 1
+    # cleared: the same workspace routes correctly again, forward after forward
+    ref = host_layer(spec, tensors)
+    for batch in range(3):
+        xb = synthetic.make_x(spec, T, seed, batch=batch)
+        y, dbg = good.forward(xb, workspace=ws, debug=True)
+        torch.cuda.synchronize()
+        y_ref, d_ref = ref.forward(xb.cpu().numpy(), debug=True)
+        assert_parity(y.cpu().numpy(), {k: v.cpu().numpy() for k, v in dbg.items()}, y_ref, d_ref, spec,
+                      min_identical=1.0)
+    assert ws.check() == 0
+
+
+def test_python_checks_on_device_operands(gpu):
+    """out, residual and the norm weights are checked before any launch (a short or
+    strided out would make the kernels write past it)."""
+    from qwenium_amd import Workspace
+
+    spec = synthetic.CONFIG1
+    layer = synthetic.make_layer(spec, 3)
+    x = synthetic.make_x(spec, 4, 3)
+    H = spec.n_embd
+    for bad in (torch.empty(3, H, device=gpu), torch.empty(H, 4, device=gpu).t(),
+                torch.empty(4, H, dtype=torch.float16, device=gpu), torch.empty(4, H)):
+        with pytest.raises(ValueError, match="out expected"):
+            layer.forward(x, out=bad)
+    with pytest.raises(ValueError, match="residual expected"):
+        layer.forward(x, residual=torch.empty(4, H - 32, device=gpu))
+    with pytest.raises(ValueError, match="norm_weight expected"):
+        layer.forward_norm(x, torch.ones(H - 1, device=gpu), 1e-6)
+    with pytest.raises(ValueError, match="distinct"):
+        layer.forward(x, out=x)
+    # a strided residual is copied on the launch stream; an explicit stream works end to end
+    ws = Workspace(layer, 4)
+    s = torch.cuda.Stream()
+    res = torch.randn(H, 4, device=gpu).t()
+    want = layer.forward(x, residual=res.contiguous(), workspace=ws)
+    torch.cuda.synchronize()
+    got = layer.forward(x, residual=res, workspace=ws, stream=s)
+    s.synchronize()
+    assert torch.equal(got, want)

@@ -217,13 +217,19 @@ def test_record_counts_shape_and_sign_checked():
 @pytest.mark.parametrize("spec_name,Ts", [("CONFIG1", (1, 7, 300)), ("QWEN35B", (10, 1, 16, 257)),
                                           ("QWEN35B_SKEW", (10, 600))])
 def test_device_histogram_equals_topk_bincount(gpu, spec_name, Ts):
+    """The device histogram against a bincount of the ORACLE's top-k ids on the same
+    inputs (so a routing bug that also corrupted the histogram cannot pass), the GPU's
+    own top-k equal to the oracle's, and the host tracker fed from it."""
     import torch
 
+    from oracle import pyoracle as po
     from qwenium_amd import synthetic
 
     spec = getattr(synthetic, spec_name)
-    layer = synthetic.make_layer(spec, 17)
+    tensors = synthetic.make_layer_tensors(spec, 17)
+    layer = synthetic.make_layer(spec, 17, tensors=tensors)
     E = spec.n_experts
+    router = tensors["router"].data.cpu().numpy().reshape(E, spec.n_embd)
     counts = torch.zeros(E, dtype=torch.int64, device=gpu)
     layer.set_expert_counts(counts)
     want = np.zeros(E, np.int64)
@@ -233,8 +239,10 @@ def test_device_histogram_equals_topk_bincount(gpu, spec_name, Ts):
         before = counts.cpu().numpy().copy()
         _, dbg = layer.forward(x, debug=True)
         torch.cuda.synchronize()
+        idx_ref, _ = po.topk_softmax(po.router_logits(router, x.cpu().numpy()), spec.top_k)
         idx = dbg["topk_idx"].cpu().numpy()
-        want += np.bincount(idx.reshape(-1), minlength=E)
+        np.testing.assert_array_equal(idx, idx_ref)
+        want += np.bincount(idx_ref.reshape(-1), minlength=E)
         got = counts.cpu().numpy()
         assert np.array_equal(got, want), f"T={T}"
         tracker.record_counts(got - before)
