@@ -143,6 +143,24 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
                        const float* residual, const qmoe_debug* dbg,
                        void* hip_stream);
 
+/* Allocation-free forward.  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same result as
+ * qmoe_layer_forward(layer, ws, x, n_tokens, y, residual, NULL, stream) on a
+ * workspace of its own, but the scratch is a file-scope device array of
+ * QMOE_STATIC_SCRATCH_BYTES per GPU (held until the process ends), so no call
+ * allocates or frees.  Its first call on a GPU (with that GPU current) looks
+ * the array up and clears its signalling area on `hip_stream`.  Sizes whose
+ * scratch exceeds the maximum (at the 35B-A3B shape: above about 100 tokens)
+ * fail with QMOE_ERR_CAPACITY.  Every call on one GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (other streams, other threads)
+ * race and must not be issued; calls ordered on one stream are fine.  A
+ * decode routing wait that gives up is reported by NaN outputs only (there is
+ * no workspace to check). */
+#define QMOE_STATIC_SCRATCH_BYTES (16u << 20)
+int qmoe_layer_forward_static(qmoe_layer* layer, const float* x, int32_t n_tokens, float* y,
+                              const float* residual, void* hip_stream);
+
 /* Optional per-phase timing for benchmarks and profilers.  events points to
  * QMOE_N_PHASE_EVENTS hipEvent_t created by the caller (or is NULL to disable).
  * While set, each qmoe_layer_forward records them on its stream: [0] before

@@ -36,6 +36,7 @@ EXPORTED = (
     "qmoe_workspace_check",
     "qmoe_layer_forward",
     "qmoe_layer_forward_norm",
+    "qmoe_layer_forward_static",
     "qmoe_layer_set_phase_events",
     "qmoe_rms_norm",
     "qmoe_synth_f32",
@@ -154,6 +155,8 @@ def lib() -> ctypes.CDLL:
     L.qmoe_workspace_check.argtypes = [vp, ctypes.POINTER(ctypes.c_int32)]
     L.qmoe_layer_forward.restype = ctypes.c_int
     L.qmoe_layer_forward.argtypes = [vp, vp, vp, ctypes.c_int32, vp, vp, P(QmoeDebug), vp]
+    L.qmoe_layer_forward_static.restype = ctypes.c_int
+    L.qmoe_layer_forward_static.argtypes = [vp, vp, ctypes.c_int32, vp, vp, vp]
     L.qmoe_layer_forward_norm.restype = ctypes.c_int
     L.qmoe_layer_forward_norm.argtypes = [vp, vp, vp, vp, ctypes.c_float, ctypes.c_int32, vp, P(QmoeDebug), vp]
     L.qmoe_layer_set_phase_events.restype = ctypes.c_int

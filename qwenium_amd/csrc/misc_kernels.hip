@@ -138,6 +138,19 @@ hipError_t launch_gemma4_inputs(const float* x, const float* w_pre, const float*
 // Synthetic data: N(mean, sigma) from (seed, stream, index); quantized rows
 // use ggml's reference quantizers (quantize_row_q4_0_ref / _q8_0_ref).
 // ---------------------------------------------------------------------------
+// Plain fill of n words (clears flags and counters; unlike hipMemsetAsync it
+// records as an ordinary kernel node when a caller captures the stream).
+__global__ __launch_bounds__(256) void k_fill_i32(int32_t* dst, int n, int32_t v) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = v;
+}
+
+hipError_t launch_fill_i32(int32_t* dst, int n, int32_t v, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_i32, dim3((n + 255) / 256), dim3(256), 0, stream, dst, n, v);
+    return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void k_synth_f32(float* dst, int64_t n, uint64_t key, double mean, double sigma) {
 #pragma clang fp contract(off)
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)

@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -423,6 +424,43 @@ int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault) {
     return QMOE_OK;
 }
 
+// Scratch of the allocation-free forward: one copy of this array per GPU, held
+// until the process ends.  Host code never passes `scratch` itself to a kernel
+// (in host code the name is a stand-in, not a device address): it uses the
+// address hipGetSymbolAddress returns on each device, kept in g_scratch.
+static __device__ __align__(256) uint8_t scratch[QMOE_STATIC_SCRATCH_BYTES];
+// The decode routing's signalling area sits at the start of the array.
+constexpr size_t kStaticSyncBytes = 4096;
+static_assert(kStaticSyncBytes >= qmoe::kSyncWords * sizeof(int32_t), "signalling area fits");
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// The device address of this GPU's scratch (dev current), set up on first use:
+// the symbol lookup, then a fill kernel on `stream` that zeroes the signalling
+// area (a kernel node, never a memset, in case the caller is capturing).
+int static_scratch(int dev, hipStream_t stream, void** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(QMOE_ERR_VALUE, "qmoe: device expected 0.." + std::to_string(kMaxDevices - 1) + ", got " +
+                                        std::to_string(dev));
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
+        err = qmoe::launch_fill_i32((int32_t*)p, (int)(kStaticSyncBytes / sizeof(int32_t)), 0, stream);
+        if (err != hipSuccess) return hip_fail(err, "scratch signalling area clear");
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return QMOE_OK;
+}
+
+}  // namespace
+
 // What feeds one forward: x and optional residual, or x as the residual row of
 // a fused caller slice (norm_w: the Qwen pre-MoE RMSNorm; g4_pre_w + g4_rs_w:
 // the Gemma 4 expert and router inputs), or a separate router input xr.
@@ -574,6 +612,40 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws, const float* x, in
     in.x = x;
     in.residual = residual;
     return forward_impl(layer, ws, in, n_tokens, y, dbg, hip_stream);
+}
+
+int qmoe_layer_forward_static(qmoe_layer* layer, const float* x, int32_t n_tokens, float* y, const float* residual,
+                              void* hip_stream) {
+    g_last_error.clear();
+    if (!layer) return fail(QMOE_ERR_NULL, "qmoe: layer expected non-null, got null");
+    if (n_tokens < 0) return fail(QMOE_ERR_VALUE, "qmoe: n_tokens expected >= 0, got " + std::to_string(n_tokens));
+    if (n_tokens == 0) return QMOE_OK;
+    const LayerDesc& d = layer->d;
+    const size_t need = kStaticSyncBytes + qmoe::workspace_bytes(n_tokens, d.H, d.E, d.K, d.F, nullptr, nullptr);
+    if (need > QMOE_STATIC_SCRATCH_BYTES)
+        return fail(QMOE_ERR_CAPACITY, "qmoe: n_tokens expected a scratch of at most " +
+                                           std::to_string(QMOE_STATIC_SCRATCH_BYTES) + " bytes (the static scratch), got " +
+                                           std::to_string(n_tokens) + " tokens needing " + std::to_string(need));
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+    if (dev != layer->device)
+        return fail(QMOE_ERR_VALUE, "qmoe: current device expected the layer's device " + std::to_string(layer->device) +
+                                        ", got " + std::to_string(dev));
+    void* base = nullptr;
+    int rc = static_scratch(dev, (hipStream_t)hip_stream, &base);
+    if (rc) return rc;
+    // the signalling area keeps its place at the start of the array from call to
+    // call; the rest is carved for this call's token count
+    qmoe_workspace ws;
+    ws.device = dev;
+    qmoe::workspace_bytes(n_tokens, d.H, d.E, d.K, d.F, &ws.w, (char*)base + kStaticSyncBytes);
+    ws.w.sync = (int32_t*)base;
+    ws.w.host_err = nullptr;
+    ForwardIn in;
+    in.x = x;
+    in.residual = residual;
+    return forward_impl(layer, &ws, in, n_tokens, y, nullptr, hip_stream);
 }
 
 int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* norm_w, float eps,

@@ -150,6 +150,8 @@ bool shared_down_in_gateup(const LayerDesc& L, int T);
 hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
                                hipStream_t stream);
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream);
+// dst[0..n) = v on `stream` (a kernel, never a memset node).
+hipError_t launch_fill_i32(int32_t* dst, int n, int32_t v, hipStream_t stream);
 // Gemma 4 MoE inputs from one pass over x (H <= 4096): expert_in = (x*scale)*w_pre,
 // router_in = ((x*scale)*s)*w_rs with scale = 1/sqrtf(mean(x^2) + eps).
 hipError_t launch_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps, float s,

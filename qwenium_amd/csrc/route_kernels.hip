@@ -325,7 +325,7 @@ struct TopkArgs {
     int max_tiles;
     int nblk;
     int max_spins;        // fused decode routing: polling passes before the bounded wait gives up
-    int32_t* host_err;    // fused decode routing: host-mapped error word (raised on a give-up)
+    int32_t* host_err;    // fused decode routing: host-mapped error word (raised on a give-up), or null
 };
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
@@ -1032,7 +1032,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
         const bool fault = !done || __hip_atomic_load(sync + kSyncErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
         if (fault && lane == 0) {
             __hip_atomic_store(sync + kSyncErr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.host_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (a.host_err) __hip_atomic_store(a.host_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
         if (lane == 0) s_fault = fault ? 1 : 0;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // drop stale cached logits (L1 and this XCD's L2)
