@@ -20,7 +20,7 @@ LIB_PATH = os.path.join(PKG_DIR, "libqmoe.so")
 SOURCES = [
     "route_kernels.hip",
     "expert_gemv_kernels.hip",
-    "expert_mfma_kernels.hip",
+    "expert_f16_kernels.hip",
     "misc_kernels.hip",
     "qmoe_api.cpp",
     "gguf.cpp",

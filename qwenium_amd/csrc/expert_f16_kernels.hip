@@ -1,0 +1,752 @@
+// expert_f16_kernels.hip -- grouped expert GEMMs for large token counts
+// (prefill) on f16 MFMA (gfx950), plus the exact fixup of h's quantization.
+//
+// Semantics as the reference's mul_mat_id with Q8_0 activations
+// (src/layers/moe.cpp:105-127, shared expert :161-165): per 32-value quant
+// block b, y[p][n] += fp32(dw[n][b]) * fp32(dx[p][b]) * isum_b[p][n], with
+// isum_b the exact integer dot of the block's quants.
+//
+// Per block and 32x32 output tile, on the MFMA pipe:
+//   isum: two v_mfma_f32_32x32x16_f16 over the quants as f16 (the activation
+//         quants q in [-127, 127] and the weights' q - 8 (Q4_0) or q (Q8_0) are
+//         exact in f16, and so is every partial sum, < 2^24), exact in f32;
+//   scale: one v_mfma_f32_32x32x16_f16 outer product dx (rows) x dw (columns),
+//         exact in f32 (two 11-bit significands);
+// then one FMA per output, acc += scale * isum, in f32 (as ggml's CPU dot
+// accumulates its block terms in f32).  VALU and MFMA instructions do not
+// overlap on this pipe (measured), so the work per tile is 3 MFMAs + ~24 VALU
+// instructions, the weight unpack shared by four row tiles.
+//
+// Tiles come from the routing: tiles[i] = {expert, first row, rows <= 128}.
+// A workgroup (4 waves) computes 128 rows x 128 weight columns of one tile;
+// each wave owns all 128 rows (four 32-row MFMA tiles) and 32 columns:
+//   gate/up: wave w takes gate (w < 2) or up (w >= 2) rows f = 64 y + 32 (w & 1) + lane % 32;
+//   down:    output columns n = 128 y + 32 w + lane % 32.
+// Activation rows (f16 quants and f16 block scales) are staged in LDS by
+// direct global->LDS loads, 128 k values per chunk, double buffered; weights
+// are read per lane straight from the GGUF blocks, one chunk ahead.
+//
+// Gate/up epilogue: h = act(g) * u in f32 and the Q8_0 of h per 32-wide block
+// (ggml's activation quantizer: d = fp16(amax / 127), q = rint(h * 127 / amax)),
+// written as the down GEMM's f16 quants and scales.  The f32 sums differ from
+// the exact ones by rounding errors proportional to the partial sums, not to
+// the result: each value gets an error estimate from max(|g|, rms of the
+// block's 32 g) (likewise u), carried through the activation and the scaling
+// by 127 / amax.  A value whose quant is not settled by it (h * 127 / amax
+// within the error of a rounding tie; for GeGLU, g within it of an fp16 tie,
+// which selects the table entry; a candidate for the block's largest |h| when
+// the top two are not clear of each other or amax / 127 is near an fp16 tie)
+// is listed with the block's amax candidates, and k_fix_h recomputes them
+// exactly (the f64 block sum, rounded once, and the deterministic activation,
+// as the CPU restatement does) and requantizes the block with the exact amax
+// before the down GEMM reads it.
+// Down epilogue: the unweighted expert rows into ybuf for the k-ordered combine.
+#include "qmoe_device.h"
+#include "qmoe_internal.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace qmoe {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+// 4-byte aligned (block pairs are only dword aligned): dwordx3 / dwordx2 loads, nothing wider
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3), aligned(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
+
+constexpr int kTM = kMfmaTileM;             // 128 rows per tile
+constexpr int kKC = kF16ChunkK;             // 128 k values per LDS chunk (4 quant blocks)
+constexpr int kLd = kKC + 8;                // LDS row stride in f16 (272 bytes: conflict-free 16-byte reads)
+constexpr int kSlotsPerRow = kLd / 8;       // 17 sixteen-byte slots, the last one padding
+constexpr int kASlots = kTM * kSlotsPerRow;
+constexpr int kAHalfs = kASlots * 8;
+constexpr int kDmaIters = (kASlots + 255) / 256;
+constexpr int kSinkBytes = (kDmaIters * 256 - kASlots) * 16;  // the last round's spare lanes land here
+constexpr int kScaleBytes = kTM * 16;       // per row and chunk: 4 f16 block scales + 8 zero bytes
+constexpr int kStageBytes = kAHalfs * 2 + kScaleBytes;
+constexpr int kHLd = 64 + 4;                // gate/up epilogue: g and u rows in LDS, f32
+constexpr size_t kF16LdsBytes = 2 * (size_t)kStageBytes + kSinkBytes + kTM * 8;
+static_assert(2 * (size_t)kTM * kHLd * 4 <= 2 * (size_t)kStageBytes, "g and u rows fit the stage buffers");
+// Error model of the gate/up epilogue's f32 values.  The accumulation error of
+// g (n block terms summed by fma in f32) relative to max(|g|, rms of the
+// block's g) is at most 1.2e-6 over 0.5M emulated values at n = 64; it is
+// charged as kAccErr * sqrt(n) (3e-6 at n = 64).  The activation's slope is
+// below kActSlope (SiLU 1.10, GELU 1.13); the f32 SiLU and product are within
+// kActRel * (1 + |g|) * |h| of the exact ones.
+constexpr float kAccErr = 3.75e-7f;
+constexpr float kActSlope = 1.13f;
+constexpr float kActRel = 2.5e-7f;
+
+struct F16Args {
+    int H, F, E;
+    const uint8_t* w0; uint64_t w0_nb1, w0_nb2;  // gate (gate/up) or down
+    const uint8_t* w1; uint64_t w1_nb1, w1_nb2;  // up (gate/up)
+    const uint8_t* sh0; uint64_t sh0_nb1;        // shared gate or shared down
+    const uint8_t* sh1; uint64_t sh1_nb1;        // shared up
+    const int32_t* counters;                     // [1] n_tiles
+    const int4* tiles;
+    const int32_t* row_token;                    // gate/up: the token of each output row
+    const _Float16* a_q;                         // A quants [rows][K] as f16
+    const uint16_t* a_d;                         // A block scales [rows][K/32] (fp16 bits)
+    int K;                                       // reduction length (H or F)
+    int n_y;                                     // column chunks per tile
+    // gate/up: h's quants and scales, the fixup list
+    _Float16* h_q; uint16_t* h_d;
+    int4* fix;                                   // [max] {row, f block, expert, mask of uncertain values}
+    float* fix_h;                                // [max][32] the block's f32 h values
+    int32_t* fix_count;
+    int fix_max;
+    float acc_err;                               // kAccErr * sqrt(K / 32)
+    int act; const uint16_t* gelu_tab;
+    // down
+    float* ybuf;
+};
+
+// The bytes of a GGUF block pair (two consecutive 32-value blocks of one
+// weight row; pairs start 4-byte aligned) that one lane needs: its k half kh
+// of each block's quants and both block scales.
+//   Q4_0 (36 bytes): w[0..2] = bytes 8kh .. 8kh+11 (block 0: d0 for kh = 0,
+//     quants at 2 + 8kh), w[3] = bytes 16 (kh = 0: d1) or 0 (kh = 1: d0),
+//     w[4..5] = bytes 20 + 8kh .. (block 1 quants); kh = 1 finds d1 in w[2].
+//   Q8_0 (68 bytes): w[0..2] = bytes 8kh .. (d0 / first quant half of block 0),
+//     w[3..5] = bytes 16 + 8kh .. (second half; kh = 1 also d1 at bytes 34-35),
+//     w[6] = bytes 32 (kh = 0: d1) or 0 (kh = 1: d0), w[7..8] = bytes 36 + 8kh,
+//     w[9..10] = bytes 52 + 8kh (block 1's quant halves).
+template <int WT> struct RawPair;
+template <> struct RawPair<kTypeQ4_0> {
+    uint32_t w[6];
+    __device__ __forceinline__ void load(const uint8_t* base, uint32_t off, bool kh) {
+        const uint8_t* p = base + off;
+        const uint32_t h8 = kh ? 8u : 0u;
+        const u32x3 a = *(const u32x3*)(p + h8);
+        const u32x2 b = *(const u32x2*)(p + 20 + h8);
+        w[0] = a.x; w[1] = a.y; w[2] = a.z;
+        w[3] = *(const uint32_t*)(p + (kh ? 0 : 16));
+        w[4] = b.x; w[5] = b.y;
+    }
+};
+template <> struct RawPair<kTypeQ8_0> {
+    uint32_t w[11];
+    __device__ __forceinline__ void load(const uint8_t* base, uint32_t off, bool kh) {
+        const uint8_t* p = base + off;
+        const uint32_t h8 = kh ? 8u : 0u;
+        const u32x3 a = *(const u32x3*)(p + h8);
+        const u32x3 b = *(const u32x3*)(p + 16 + h8);
+        const u32x2 c = *(const u32x2*)(p + 36 + h8);
+        const u32x2 d = *(const u32x2*)(p + 52 + h8);
+        w[0] = a.x; w[1] = a.y; w[2] = a.z;
+        w[3] = b.x; w[4] = b.y; w[5] = b.z;
+        w[6] = *(const uint32_t*)(p + (kh ? 0 : 32));
+        w[7] = c.x; w[8] = c.y;
+        w[9] = d.x; w[10] = d.y;
+    }
+};
+
+// Two f16 (1024 + byte) values from two bytes of u (v_perm: 0x64 = the f16
+// exponent bits of 1024 in the high byte of each half).
+__device__ __forceinline__ uint32_t bytes_1024(uint32_t u, uint32_t sel) {
+    return __builtin_amdgcn_perm(0x64646464u, u, sel);
+}
+constexpr uint32_t kSelB01 = 0x04010400u;  // [b0, 0x64, b1, 0x64]
+constexpr uint32_t kSelB23 = 0x04030402u;  // [b2, 0x64, b3, 0x64]
+
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Q4_0 quants of this lane as exact f16 q - 8 (8 bytes u0, u1 = qs[8kh..8kh+7]):
+// half 0 = low nibbles (k = 8kh + i), half 1 = high nibbles (k = 16 + 8kh + i).
+__device__ __forceinline__ void quants_q4(uint32_t u0, uint32_t u1, v8h (&b)[2]) {
+#pragma clang fp contract(off)
+    const h2 c1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const h2 c72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    const h2 c16th = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const uint32_t p[4] = {bytes_1024(u0, kSelB01), bytes_1024(u0, kSelB23), bytes_1024(u1, kSelB01),
+                           bytes_1024(u1, kSelB23)};
+    u32x4 lo, hi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // (1024 + lo) - 1032 = lo - 8; (1024 + 16 hi) / 16 - 72 = hi - 8: both exact
+        lo[i] = as_u32(as_h2(p[i] & 0xFF0FFF0Fu) + c1032);
+        hi[i] = as_u32(__builtin_elementwise_fma(as_h2(p[i] & 0xFFF0FFF0u), c16th, c72));
+    }
+    b[0] = __builtin_bit_cast(v8h, lo);
+    b[1] = __builtin_bit_cast(v8h, hi);
+}
+
+// Q8_0 quants (8 signed bytes) as exact f16: (1024 + (q ^ 0x80)) - 1152 = q.
+__device__ __forceinline__ v8h quants_q8(uint32_t u0, uint32_t u1) {
+#pragma clang fp contract(off)
+    const h2 c1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t a = u0 ^ 0x80808080u, b = u1 ^ 0x80808080u;
+    const uint32_t p[4] = {bytes_1024(a, kSelB01), bytes_1024(a, kSelB23), bytes_1024(b, kSelB01),
+                           bytes_1024(b, kSelB23)};
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = as_u32(as_h2(p[i]) + c1152);
+    return __builtin_bit_cast(v8h, r);
+}
+
+// Quants (two MFMA halves) and the fp16 scale bits of block j (0/1) of a raw pair.
+template <int WT>
+__device__ __forceinline__ uint32_t block_quants(const RawPair<WT>& r, int j, bool kh, v8h (&b)[2]);
+
+template <>
+__device__ __forceinline__ uint32_t block_quants<kTypeQ4_0>(const RawPair<kTypeQ4_0>& r, int j, bool kh, v8h (&b)[2]) {
+    if (j == 0) {
+        // block 0: quants at bytes 2 + 8kh .. 9 + 8kh = bytes 2..9 of w[0..2]
+        quants_q4(__builtin_amdgcn_alignbyte(r.w[1], r.w[0], 2), __builtin_amdgcn_alignbyte(r.w[2], r.w[1], 2), b);
+        return (kh ? r.w[3] : r.w[0]) & 0xffffu;
+    }
+    quants_q4(r.w[4], r.w[5], b);
+    return (kh ? r.w[2] : r.w[3]) >> 16;
+}
+
+template <>
+__device__ __forceinline__ uint32_t block_quants<kTypeQ8_0>(const RawPair<kTypeQ8_0>& r, int j, bool kh, v8h (&b)[2]) {
+    if (j == 0) {
+        b[0] = quants_q8(__builtin_amdgcn_alignbyte(r.w[1], r.w[0], 2), __builtin_amdgcn_alignbyte(r.w[2], r.w[1], 2));
+        b[1] = quants_q8(__builtin_amdgcn_alignbyte(r.w[4], r.w[3], 2), __builtin_amdgcn_alignbyte(r.w[5], r.w[4], 2));
+        return (kh ? r.w[6] : r.w[0]) & 0xffffu;
+    }
+    b[0] = quants_q8(r.w[7], r.w[8]);
+    b[1] = quants_q8(r.w[9], r.w[10]);
+    return (kh ? r.w[5] : r.w[6]) >> 16;
+}
+
+__device__ __forceinline__ v16f mfma16(v8h a, v8h b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// silu(g) (moe.cpp:117) or ggml's tabled gelu(g) (gemma4.cpp:423) in f32.
+__device__ __forceinline__ float act_f32(int act, const uint16_t* tab, float g) {
+    if (act == kActGeluTanh) {
+        if (g <= -10.0f) return 0.0f;
+        if (g >= 10.0f) return g;
+        return fp16_to_f32(tab[f32_to_fp16(g) & 0xffffu]);
+    }
+    return g / (1.0f + __expf(-g));
+}
+
+template <int WT, bool GATEUP>
+__global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    // [2 stages] {A quants [128][kLd] f16, block scale records [128][8] f16 (4
+    // scales, 4 zeros)}, the sink, A row offsets [128], scale row offsets [128]
+    uint8_t* s_stage = s_dyn;
+    uint32_t* s_rowoff = (uint32_t*)(s_dyn + 2 * kStageBytes + kSinkBytes);
+    uint32_t* s_doff = s_rowoff + kTM;
+    // XCD-aware mapping (workgroups are dealt to the 8 XCDs round-robin): XCD x
+    // takes tiles x, x + 8, ... and all column chunks of each, so a tile's
+    // activation rows are read into one L2 and the XCDs get statistically
+    // equal shares of the (unequal) tiles
+    const int jb = (int)(blockIdx.x >> 3);
+    const int tile_local = jb / a.n_y, y = jb - tile_local * a.n_y;
+    const int tile_id = (int)(blockIdx.x & 7) + 8 * tile_local;
+    if (tile_id >= a.counters[1]) return;
+    const int4 tile = a.tiles[tile_id];
+    const int e = tile.x, p0 = tile.y, nr = tile.z;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int col = lane & 31;
+    const bool kh = lane >= 32;
+    const bool sh = e >= a.E;
+    const int nm = (nr + 31) >> 5;  // 32-row MFMA tiles with rows (wave-uniform)
+    const int nblk = a.K >> 5;
+
+    if (tid < kTM) {
+        const int pr = p0 + min(tid, nr - 1);
+        const int arow = GATEUP ? a.row_token[pr] : pr;
+        s_rowoff[tid] = (uint32_t)arow * (uint32_t)a.K;
+        s_doff[tid] = (uint32_t)arow * (uint32_t)nblk;
+    }
+    // the zero halves of the scale records (never written by the staging)
+    for (int i = tid; i < 2 * kTM; i += 256)
+        *(uint64_t*)(s_stage + (i / kTM) * kStageBytes + kAHalfs * 2 + (i % kTM) * 16 + 8) = 0;
+    __syncthreads();
+
+    // this lane's weight row (wave-uniform slab base + 32-bit row offset: an
+    // expert's slab is far below 4 GiB)
+    const uint8_t* wbase;
+    uint32_t woff;
+    int out_col;
+    if (GATEUP) {
+        const bool up = wave >= 2;
+        const int f = y * 64 + 32 * (wave & 1) + col;
+        wbase = up ? (sh ? a.sh1 : a.w1 + (uint64_t)e * a.w1_nb2) : (sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2);
+        woff = (uint32_t)(f * (up ? (sh ? a.sh1_nb1 : a.w1_nb1) : (sh ? a.sh0_nb1 : a.w0_nb1)));
+        out_col = f;
+    } else {
+        out_col = y * 128 + 32 * wave + col;
+        wbase = sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2;
+        woff = (uint32_t)(out_col * (sh ? a.sh0_nb1 : a.w0_nb1));
+    }
+    constexpr uint32_t kPairBytes = 2 * BlockTraits<WT>::kBytes;
+    const int npairs = nblk >> 1;
+    const int nchunk = (nblk + 3) >> 2;
+
+    // direct global->LDS staging of chunk c.  Quants: slot s = row * 17 + unit
+    // (unit 16 is the row's padding); every wave issues exactly kDmaIters
+    // unconditional loads (a count the wait counters can track): slots past
+    // the buffer land in the sink, the padding unit reloads the chunk's first
+    // 16 bytes of the row into a slot that is never read.  K is a multiple of
+    // 64, so a last chunk holds 2 or 4 blocks; a 2-block one reads up to 128
+    // bytes of quants and 4 bytes of scales past a row (the A buffers end in
+    // padding) into slots that are never read.  This lane's source offsets
+    // (row offset + 8 unit) are computed once.
+    uint32_t soff[kDmaIters];
+#pragma unroll
+    for (int it = 0; it < kDmaIters; ++it) {
+        const int s = min(it * 256 + wave * 64 + lane, kASlots - 1);
+        const int r = s / kSlotsPerRow;
+        const int u = s - r * kSlotsPerRow;
+        soff[it] = s_rowoff[r] + (u < 16 ? 8 * u : 0);
+    }
+    // Scales: one dword (two blocks) into the first 8 bytes of each row's
+    // 16-byte record; lane slot sl = (row, dword) = (sl / 4, sl % 4), two
+    // rounds of 64 slots per wave, dwords 2-3 (the zeros) not loaded.
+    uint32_t doff[2];
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+        const int sl = wave * 128 + 64 * rd + lane;
+        doff[rd] = s_doff[sl >> 2] + 2 * (sl & 1);
+    }
+    const bool dlane = (lane & 2) == 0;  // dwords 0, 1 of a record
+    auto stage = [&](int c) {
+        uint8_t* st = s_stage + (c & 1) * kStageBytes;
+        const uint32_t k0 = (uint32_t)(c * kKC);
+#pragma unroll
+        for (int it = 0; it < kDmaIters; ++it) {
+            const int s0 = it * 256 + wave * 64;
+            void* dst = s0 < kASlots ? (void*)(st + s0 * 16) : (void*)(s_stage + 2 * kStageBytes);  // wave-uniform
+            __builtin_amdgcn_global_load_lds((const void*)(a.a_q + soff[it] + k0),
+                                             (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+        }
+#pragma unroll
+        for (int rd = 0; rd < 2; ++rd) {
+            if (dlane)
+                __builtin_amdgcn_global_load_lds(
+                    (const void*)(a.a_d + doff[rd] + (uint32_t)(4 * c)),
+                    (__attribute__((address_space(3))) void*)(st + kAHalfs * 2 + (wave * 128 + 64 * rd) * 4), 4, 0, 0);
+        }
+    };
+
+    v16f acc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = v16f{};
+
+    // weights one whole chunk ahead: chunk c's two pairs live in wa (c even) or
+    // wb (c odd), so nothing inside a chunk waits on memory.  The second pair
+    // of a 2-block last chunk reloads the first (never used).
+    RawPair<WT> wa[2], wb[2];  // [pair of the chunk]
+    auto fetch = [&](int c, RawPair<WT>(&dst)[2]) {
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+            const int pair = min(2 * c + pp, npairs - 1);
+            dst[pp].load(wbase, woff + (uint32_t)pair * kPairBytes, kh);
+        }
+    };
+    // this lane's A fragment: row col of each 32-row tile, k offset 8 kh (+ 16 for half 1)
+    const int arow0 = col * kLd + (kh ? 8 : 0);
+    // the main loop for NM row tiles with rows (a wave-uniform count)
+    auto run = [&](auto nm_c) {
+        constexpr int NM = decltype(nm_c)::value;
+        auto chunk = [&](int c, const RawPair<WT>(&cur)[2], RawPair<WT>(&nxt)[2]) {
+            __builtin_amdgcn_s_waitcnt(0);  // chunk c's LDS loads and weights (issued a chunk ago) have landed
+            __syncthreads();                // ... for every wave; stage (c + 1) & 1 is no longer read
+            if (c + 1 < nchunk) {
+                fetch(c + 1, nxt);
+                stage(c + 1);
+            }
+            const uint8_t* st = s_stage + (c & 1) * kStageBytes;
+            const _Float16* aq = (const _Float16*)st;
+            const uint8_t* srec = st + kAHalfs * 2 + col * 16;  // this lane's row (32 m + col) scale record
+            const int np = min(2, npairs - 2 * c);
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                if (pp >= np) break;  // uniform
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int bl = 2 * pp + j;  // block within the chunk
+                    v8h bq[2];
+                    const uint32_t dw = block_quants<WT>(cur[pp], j, kh, bq);
+                    // the outer product's B: dw at element bl of lanes 0..31 (k = bl),
+                    // zero elsewhere; its A is the row's record {dx0..dx3, 0 x4}:
+                    // D = dx_bl * dw, exact
+                    const uint32_t dwl = kh ? 0u : dw;
+                    u32x4 bsw = {0u, 0u, 0u, 0u};
+                    bsw[bl >> 1] = (bl & 1) ? (dwl << 16) : dwl;
+                    const v8h bs = __builtin_bit_cast(v8h, bsw);
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) {
+                        const int o = arow0 + 32 * m * kLd + 32 * bl;
+                        const v8h aq0 = *(const v8h*)(aq + o);
+                        const v8h aq1 = *(const v8h*)(aq + o + 16);
+                        const v8h as = *(const v8h*)(srec + 32 * m * 16);
+                        const v16f sc = mfma16(as, bs, v16f{});
+                        v16f P = mfma16(aq0, bq[0], v16f{});
+                        P = mfma16(aq1, bq[1], P);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[m][r] = __builtin_fmaf(sc[r], P[r], acc[m][r]);
+                    }
+                }
+            }
+        };
+        for (int c = 0; c < nchunk; c += 2) {
+            chunk(c, wa, wb);
+            if (c + 1 < nchunk) chunk(c + 1, wb, wa);
+        }
+    };
+    fetch(0, wa);
+    stage(0);
+    switch (nm) {
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        case 3: run(std::integral_constant<int, 3>{}); break;
+        default: run(std::integral_constant<int, 4>{}); break;
+    }
+
+    if (!GATEUP) {
+        // unweighted expert rows (lane: column out_col, rows 32 m + 8 (r / 4) + 4 kh + r % 4)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 32 * m + 8 * (r >> 2) + (kh ? 4 : 0) + (r & 3);
+                if (row < nr) a.ybuf[(uint64_t)(p0 + row) * a.H + out_col] = acc[m][r];
+            }
+        return;
+    }
+
+    // gate/up epilogue.  1) g (waves 0, 1) and u (waves 2, 3) into LDS rows
+    // [128][64] each (the stage buffers are free once every wave is done)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    float* s_g = (float*)s_dyn;
+    float* s_u = s_g + kTM * kHLd;
+    {
+        float* dst = wave >= 2 ? s_u : s_g;
+        const int fl = 32 * (wave & 1) + col;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 32 * m + 8 * (r >> 2) + (kh ? 4 : 0) + (r & 3);
+                dst[row * kHLd + fl] = acc[m][r];
+            }
+    }
+    __syncthreads();
+    // 2) one thread per (row, 32-wide f block): rows tid % 128, f block 2 y + tid / 128
+    const int row = tid & (kTM - 1), jb2 = tid >> 7;
+    const int fb = y * 2 + jb2;  // f block of h
+    const int nfb = a.F >> 5;
+    if (row >= nr || fb >= nfb) return;
+    float vg[32], vu[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 gv = *(const f32x4*)(s_g + row * kHLd + 32 * jb2 + 4 * i);
+        const f32x4 uv = *(const f32x4*)(s_u + row * kHLd + 32 * jb2 + 4 * i);
+        vg[4 * i] = gv.x; vg[4 * i + 1] = gv.y; vg[4 * i + 2] = gv.z; vg[4 * i + 3] = gv.w;
+        vu[4 * i] = uv.x; vu[4 * i + 1] = uv.y; vu[4 * i + 2] = uv.z; vu[4 * i + 3] = uv.w;
+    }
+    float sg = 0.0f, su = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        sg = __builtin_fmaf(vg[i], vg[i], sg);
+        su = __builtin_fmaf(vu[i], vu[i], su);
+    }
+    const float rg = __builtin_sqrtf(sg * (1.0f / 32.0f)), ru = __builtin_sqrtf(su * (1.0f / 32.0f));
+    // h and its error estimate (vg[] and vu[] are overwritten with them); GeGLU:
+    // the table entry is picked by fp16(g) (and |g| >= 10 by a threshold)
+    float amax = 0.0f, ea = 0.0f;
+    uint32_t unsure = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const float gv = vg[i], uv = vu[i];
+        const float av = act_f32(a.act, a.gelu_tab, gv);
+        const float h = av * uv;
+        const float eg = a.acc_err * fmaxf(__builtin_fabsf(gv), rg);
+        const float eu = a.acc_err * fmaxf(__builtin_fabsf(uv), ru);
+        const float eh = kActSlope * __builtin_fabsf(uv) * eg + __builtin_fabsf(av) * eu +
+                         kActRel * (1.0f + __builtin_fabsf(gv)) * __builtin_fabsf(h);
+        if (a.act == kActGeluTanh) {
+            const float lo = gv - eg, hi = gv + eg;
+            if (f32_to_fp16(lo) != f32_to_fp16(hi) || (lo <= -10.0f) != (hi <= -10.0f) ||
+                (lo >= 10.0f) != (hi >= 10.0f))
+                unsure |= 1u << i;
+        }
+        vg[i] = h;
+        vu[i] = eh;
+        amax = fmaxf(amax, __builtin_fabsf(h));
+        ea = fmaxf(ea, eh);
+    }
+    float sec = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const float ah = __builtin_fabsf(vg[i]);
+        sec = fmaxf(sec, ah < amax ? ah : 0.0f);
+    }
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    // quants; a value whose t = h * 127 / amax lies within its error (amax's
+    // own error included) of a rounding tie is uncertain
+    uint32_t cand = 0, packed[16];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const float t = vg[i] * id;
+        const float q = __builtin_rintf(t);
+        const float at = __builtin_fabsf(t);
+        const float et = (vu[i] + at * ea * (1.0f / 127.0f)) * id + at * 2.5e-7f;
+        if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << i;
+        if (__builtin_fabsf(vg[i]) >= amax - 2.0f * ea) cand |= 1u << i;  // could be the exact largest |h|
+        const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
+        packed[i >> 1] = (i & 1) ? (packed[i >> 1] | (qb << 16)) : qb;
+    }
+    const uint64_t p = (uint64_t)(p0 + row);
+    u32x4* hq = (u32x4*)(a.h_q + p * a.F + 32 * fb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hq[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
+    a.h_d[p * nfb + fb] = (uint16_t)f32_to_fp16(d);
+    // the block's largest |h|: the runner-up not clear of it, or amax / 127
+    // near an fp16 tie; a listed block's requantization needs the exact amax,
+    // so its candidates are listed with it
+    const bool amax_open = amax - sec <= 2.0f * ea ||
+                           f32_to_fp16((amax - ea) * (1.0f / 127.0f)) != f32_to_fp16((amax + ea) * (1.0f / 127.0f));
+    uint32_t mask = unsure | (amax_open ? cand : 0u);
+    if (mask) {
+        mask |= cand;
+        const int slot = atomicAdd(a.fix_count, 1);
+        if (slot < a.fix_max) {
+            f32x4* fh = (f32x4*)(a.fix_h + (uint64_t)slot * 32);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) fh[i] = f32x4{vg[4 * i], vg[4 * i + 1], vg[4 * i + 2], vg[4 * i + 3]};
+            a.fix[slot] = make_int4((int)p, fb, e, (int)mask);
+        }
+    }
+}
+
+// Exact recomputation of listed h blocks (one wave per block): each uncertain
+// value gets g and u as the exact f64 sum of its block terms fp32(dw) *
+// fp32(dx) * isum rounded once to f32 and the deterministic activation (the
+// CPU restatement's values); the block is then requantized from its 32 values.
+struct FixArgs {
+    int H, F, E;
+    const uint8_t* wg; uint64_t wg_nb1, wg_nb2;
+    const uint8_t* wu; uint64_t wu_nb1, wu_nb2;
+    const uint8_t* sg; uint64_t sg_nb1;
+    const uint8_t* su; uint64_t su_nb1;
+    const int32_t* row_token;
+    const _Float16* x_q; const uint16_t* x_d;  // x quants [T][H] f16, scales [T][H/32]
+    const int4* fix; const float* fix_h; const int32_t* fix_count; int fix_max;
+    _Float16* h_q; uint16_t* h_d;
+    int act; const uint16_t* gelu_tab;
+};
+
+// Integer dots of one quant block of the gate row and of the up row with the
+// same 32 activation quants (exact f16 integers); dw: the two block scales.
+template <int WT>
+__device__ __forceinline__ void block_isum2(const uint8_t* bg, const uint8_t* bu, const int (&xv)[32], int& ig, int& iu,
+                                            float& dg, float& du) {
+    // blocks are 2-byte aligned (18 / 34 bytes): halfword loads
+    const uint16_t* g16 = (const uint16_t*)bg;
+    const uint16_t* u16 = (const uint16_t*)bu;
+    dg = fp16_to_f32(g16[0]);
+    du = fp16_to_f32(u16[0]);
+    ig = 0;
+    iu = 0;
+    if (WT == kTypeQ4_0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t wg = g16[1 + j], wu = u16[1 + j];  // quant bytes 2j, 2j + 1
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int k = 2 * j + h;
+                const uint32_t cg = (wg >> (8 * h)) & 0xffu, cu = (wu >> (8 * h)) & 0xffu;
+                ig += ((int)(cg & 15u) - 8) * xv[k] + ((int)(cg >> 4) - 8) * xv[k + 16];
+                iu += ((int)(cu & 15u) - 8) * xv[k] + ((int)(cu >> 4) - 8) * xv[k + 16];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t wg = g16[1 + j], wu = u16[1 + j];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int k = 2 * j + h;
+                ig += (int)(int8_t)(uint8_t)(wg >> (8 * h)) * xv[k];
+                iu += (int)(int8_t)(uint8_t)(wu >> (8 * h)) * xv[k];
+            }
+        }
+    }
+}
+
+// The exact gate and up dots of weight rows rg, ru with one x row over the
+// lanes of a 32-lane half (lane l32 takes blocks l32, l32 + 32, ...): each
+// block term fp32(dw) * fp32(dx) * isum is exact in f64 (a 22-bit scale
+// product times a 19-bit integer); the caller sums them over the half.
+template <int WT>
+__device__ void exact_gu_part(const uint8_t* rg, const uint8_t* ru, const _Float16* xq, const uint16_t* xd, int nblk,
+                              int l32, double& g, double& u) {
+    g = 0.0;
+    u = 0.0;
+    for (int b = l32; b < nblk; b += 32) {
+        int xv[32];
+        const u32x4* xs = (const u32x4*)(xq + 32 * b);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 w = xs[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xv[8 * i + 2 * j] = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffffu));
+                xv[8 * i + 2 * j + 1] = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
+            }
+        }
+        const float dx = fp16_to_f32(xd[b]);
+        int ig, iu;
+        float dg, du;
+        block_isum2<WT>(rg + (uint64_t)b * BlockTraits<WT>::kBytes, ru + (uint64_t)b * BlockTraits<WT>::kBytes, xv, ig, iu,
+                        dg, du);
+        g += (double)(dg * dx) * (double)ig;  // fp32(dw) * fp32(dx) is exact in f32
+        u += (double)(du * dx) * (double)iu;
+    }
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// One wave per listed block; its uncertain values two at a time (one per
+// 32-lane half), each from the exact f64 gate and up sums rounded once to f32
+// and the deterministic activation; then the block is requantized.
+template <int WT>
+__global__ __launch_bounds__(256) void k_fix_h(FixArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int l32 = lane & 31;
+    const bool upper = lane >= 32;
+    const int n = min(*a.fix_count, a.fix_max);
+    const int nblk = a.H >> 5;
+    for (int i = blockIdx.x * 4 + (int)(threadIdx.x >> 6); i < n; i += gridDim.x * 4) {
+        const int4 ent = a.fix[i];
+        const int p = ent.x, fb = ent.y, e = ent.z;
+        uint32_t todo = (uint32_t)ent.w;  // the uncertain values of the block
+        const bool sh = e >= a.E;
+        const int t = a.row_token[p];
+        const _Float16* xq = a.x_q + (uint64_t)t * a.H;
+        const uint16_t* xd = a.x_d + (uint64_t)t * nblk;
+        float h = a.fix_h[(uint64_t)i * 32 + l32];  // value l32 of the block (both halves)
+        while (todo) {
+            const int v0 = __builtin_ctz(todo);
+            todo &= todo - 1;
+            const int v1 = todo ? __builtin_ctz(todo) : -1;
+            if (todo) todo &= todo - 1;
+            const int v = upper ? v1 : v0;
+            double gd = 0.0, ud = 0.0;
+            if (v >= 0) {
+                const int f = 32 * fb + v;
+                const uint8_t* rg =
+                    sh ? a.sg + (uint64_t)f * a.sg_nb1 : a.wg + (uint64_t)e * a.wg_nb2 + (uint64_t)f * a.wg_nb1;
+                const uint8_t* ru =
+                    sh ? a.su + (uint64_t)f * a.su_nb1 : a.wu + (uint64_t)e * a.wu_nb2 + (uint64_t)f * a.wu_nb1;
+                exact_gu_part<WT>(rg, ru, xq, xd, nblk, l32, gd, ud);
+            }
+            gd = dpp_sum_f64<32>(gd);  // half sums in lanes 31 and 63
+            ud = dpp_sum_f64<32>(ud);
+            const float h0 = act_mul(a.act, a.gelu_tab, (float)readlane_f64(gd, 31), (float)readlane_f64(ud, 31));
+            if (l32 == v0) h = h0;
+            if (v1 >= 0) {
+                const float h1 = act_mul(a.act, a.gelu_tab, (float)readlane_f64(gd, 63), (float)readlane_f64(ud, 63));
+                if (l32 == v1) h = h1;
+            }
+        }
+        // requantize the block from its 32 values (lanes 0..31; 32..63 mirror them)
+        float amax = __builtin_fabsf(h);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        if (lane < 32) a.h_q[(uint64_t)p * a.F + 32 * fb + lane] = (_Float16)__builtin_rintf(h * id);
+        if (lane == 0) a.h_d[(uint64_t)p * (a.F >> 5) + fb] = (uint16_t)f32_to_fp16(d);
+    }
+}
+
+static F16Args base_f16_args(const LayerDesc& L, const Workspace& ws) {
+    F16Args a{};
+    a.H = L.H; a.F = L.F; a.E = L.E;
+    a.counters = ws.counters;
+    a.tiles = ws.tiles;
+    a.row_token = ws.row_token;
+    a.h_q = ws.h_q; a.h_d = ws.h_d;
+    a.fix = ws.fix; a.fix_h = ws.fix_h; a.fix_count = ws.counters + kCounterFix; a.fix_max = ws.fix_max;
+    a.acc_err = kAccErr * sqrtf((float)(L.H / 32));
+    a.ybuf = ws.ybuf;
+    a.act = L.act;
+    a.gelu_tab = L.gelu_tab;
+    return a;
+}
+
+static int f16_max_tiles(const LayerDesc& L, const Workspace& ws, int T) {
+    return min(ws.max_tiles, (T * L.K + kTM - 1) / kTM + min(L.E, T * L.K) + (L.S ? (T + kTM - 1) / kTM : 0));
+}
+
+template <typename Kern>
+static hipError_t launch_f16(Kern kern, dim3 grid, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop,
+                             const F16Args& a) {
+    // above the 64 KiB default dynamic LDS window: raise it (idempotent)
+    hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kF16LdsBytes);
+    if (err != hipSuccess) return err;
+    launch_timed(kern, grid, dim3(256), kF16LdsBytes, stream, ev_start, ev_stop, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
+                              hipEvent_t ev_start, hipEvent_t ev_stop) {
+    F16Args a = base_f16_args(L, ws);
+    a.w0 = L.w_gate; a.w0_nb1 = L.gate_nb1; a.w0_nb2 = L.gate_nb2;
+    a.w1 = L.w_up; a.w1_nb1 = L.up_nb1; a.w1_nb2 = L.up_nb2;
+    a.sh0 = L.w_sh_gate; a.sh0_nb1 = L.sh_gate_nb1;
+    a.sh1 = L.w_sh_up; a.sh1_nb1 = L.sh_up_nb1;
+    a.a_q = ws.x_q; a.a_d = ws.x_d;
+    a.K = L.H;
+    a.n_y = L.F / 64;
+    // the fixup list starts empty (a kernel node, not a memset, under capture)
+    hipError_t err = launch_fill_i32(ws.counters + kCounterFix, 1, 0, stream);
+    if (err != hipSuccess) return err;
+    const dim3 grid(8 * ((f16_max_tiles(L, ws, T) + 7) / 8) * a.n_y);
+    err = L.gu_type == kTypeQ4_0 ? launch_f16(k_expert_f16<kTypeQ4_0, true>, grid, stream, ev_start, ev_stop, a)
+                                 : launch_f16(k_expert_f16<kTypeQ8_0, true>, grid, stream, ev_start, ev_stop, a);
+    if (err != hipSuccess) return err;
+    FixArgs f{};
+    f.H = L.H; f.F = L.F; f.E = L.E;
+    f.wg = L.w_gate; f.wg_nb1 = L.gate_nb1; f.wg_nb2 = L.gate_nb2;
+    f.wu = L.w_up; f.wu_nb1 = L.up_nb1; f.wu_nb2 = L.up_nb2;
+    f.sg = L.w_sh_gate; f.sg_nb1 = L.sh_gate_nb1;
+    f.su = L.w_sh_up; f.su_nb1 = L.sh_up_nb1;
+    f.row_token = ws.row_token;
+    f.x_q = ws.x_q; f.x_d = ws.x_d;
+    f.fix = ws.fix; f.fix_h = ws.fix_h; f.fix_count = ws.counters + kCounterFix; f.fix_max = ws.fix_max;
+    f.h_q = ws.h_q; f.h_d = ws.h_d;
+    f.act = L.act; f.gelu_tab = L.gelu_tab;
+    // one wave per listed block, enough waves in flight to hide the row reads
+    const dim3 fgrid(std::max(1, std::min(8 * L.n_cu, (ws.fix_max + 3) / 4)));
+    if (L.gu_type == kTypeQ4_0) hipLaunchKernelGGL(k_fix_h<kTypeQ4_0>, fgrid, dim3(256), 0, stream, f);
+    else hipLaunchKernelGGL(k_fix_h<kTypeQ8_0>, fgrid, dim3(256), 0, stream, f);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
+    F16Args a = base_f16_args(L, ws);
+    a.w0 = L.w_down; a.w0_nb1 = L.down_nb1; a.w0_nb2 = L.down_nb2;
+    a.sh0 = L.w_sh_down; a.sh0_nb1 = L.sh_down_nb1;
+    a.a_q = ws.h_q; a.a_d = ws.h_d;
+    a.K = L.F;
+    a.n_y = L.H / 128;
+    const dim3 grid(8 * ((f16_max_tiles(L, ws, T) + 7) / 8) * a.n_y);
+    return L.dn_type == kTypeQ4_0 ? launch_f16(k_expert_f16<kTypeQ4_0, false>, grid, stream, nullptr, nullptr, a)
+                                  : launch_f16(k_expert_f16<kTypeQ8_0, false>, grid, stream, nullptr, nullptr, a);
+}
+
+}  // namespace qmoe

@@ -156,6 +156,16 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.sync = (int32_t*)take(kSyncWords * sizeof(int32_t));
     ws.tiles = (int4*)take((size_t)max_tiles * sizeof(int4));
     ws.gubuf = (float2*)take(R * F * sizeof(float2));
+    ws.h_q = (_Float16*)ws.gubuf;  // R*F*2 bytes of the R*F*8 (the rest is its padding)
+    // the prefill GEMMs stage whole 128-wide k chunks: a 64-wide last chunk
+    // reads up to 128 bytes of quants and 4 bytes of scales past a row, so the
+    // four A buffers end in 256 bytes of padding
+    ws.h_d = (uint16_t*)take(R * (F / 32) * sizeof(uint16_t) + 256);
+    ws.x_q = (_Float16*)take((size_t)T * H * sizeof(_Float16) + 256);
+    ws.x_d = (uint16_t*)take((size_t)T * (H / 32) * sizeof(uint16_t) + 256);
+    ws.fix_max = (int)std::min<size_t>(R * (F / 32), (size_t)1 << 30);  // every h block, at worst
+    ws.fix = (int4*)take((size_t)ws.fix_max * sizeof(int4));
+    ws.fix_h = (float*)take((size_t)ws.fix_max * 32 * sizeof(float));
     ws.hq_qs = (int8_t*)take(R * F);
     ws.hq_ds = (float2*)take(R * (F / 32) * sizeof(float2));
     ws.ybuf = (float*)take(R * H * sizeof(float));
@@ -552,9 +562,9 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         xin = v.xn;
         xr = v.xr;
     }
-    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, xr, n_tokens, rdbg, stream);
+    const bool mfma = n_tokens >= d.mfma_min_tokens && !qmoe::gateup_q_fused(d, n_tokens);
+    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, xr, n_tokens, rdbg, mfma, stream);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
-    const bool mfma = n_tokens >= d.mfma_min_tokens;
     // events [1] and [2] are taken by the gate/up launch itself (its own start and end)
     hipEvent_t e1 = layer->record_phases ? layer->phase_events[1] : nullptr;
     hipEvent_t e2 = layer->record_phases ? layer->phase_events[2] : nullptr;
@@ -562,9 +572,12 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         // decode: SwiGLU and the Q8_0 of h run in the gate/up kernel
         err = qmoe::launch_gateup_q(d, v, n_tokens, stream, e1, e2);
         if (err != hipSuccess) return hip_fail(err, "gate/up+quant expert kernel");
+    } else if (mfma) {
+        // prefill: SwiGLU and the Q8_0 of h (as the down GEMM's f16 planes) run in the gate/up epilogue
+        err = qmoe::launch_gateup_mfma(d, v, n_tokens, stream, e1, e2);
+        if (err != hipSuccess) return hip_fail(err, "gate/up expert kernel");
     } else {
-        err = mfma ? qmoe::launch_gateup_mfma(d, v, n_tokens, stream, e1, e2)
-                   : qmoe::launch_experts_gateup(d, v, n_tokens, stream, e1, e2);
+        err = qmoe::launch_experts_gateup(d, v, n_tokens, stream, e1, e2);
         if (err != hipSuccess) return hip_fail(err, "gate/up expert kernel");
         err = qmoe::launch_quant_h(d, v, n_tokens, stream);
     }

@@ -221,6 +221,15 @@ __device__ __forceinline__ double dpp_sum_f64(double v) {
     return v;
 }
 
+// The whole wave's f64 sum in every lane (dpp_sum_f64<64> leaves it in lane 63).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v = dpp_sum_f64<64>(v);
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
 // One reduce-scatter step over an f64 pair (x, y): the 32-lane swap (W = 32)
 // leaves lanes 0..31 with x[l] + x[l + 32] and lanes 32..63 with y[l - 32] + y[l];
 // the 16-lane swap (W = 16) does the same between the even and odd rows of 16.

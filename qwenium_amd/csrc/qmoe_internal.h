@@ -19,7 +19,11 @@ constexpr int kSyncGen = 0;
 constexpr int kSyncErr = 1;
 constexpr int kSyncFlags = 64;     // flags start here (448 router blocks max)
 // Row tile of the prefill grouped GEMM (rows of one expert per tile).
-constexpr int kMfmaTileM = 64;
+constexpr int kMfmaTileM = 128;
+// k values per LDS chunk of the prefill GEMMs.
+constexpr int kF16ChunkK = 128;
+// Workspace counters: [0] active slots, [1] tiles, [kCounterFix] listed h blocks.
+constexpr int kCounterFix = 4;
 // Expert activations: SwiGLU (moe.cpp:117) or GeGLU-tanh (gemma4.cpp:423).
 constexpr int kActSilu = 0;
 constexpr int kActGeluTanh = 1;
@@ -80,6 +84,14 @@ struct Workspace {
     float2* gubuf = nullptr;      // [R][F] (gate, up) projections
     int8_t* hq_qs = nullptr;      // [R][F]   Q8_0 quants of h = silu(g)*u
     float2* hq_ds = nullptr;      // [R][F/32] {d, bitcast(sum q)}
+    // prefill GEMM operands: Q8_0 quants as exact f16 values and fp16 block scales
+    _Float16* x_q = nullptr;      // [T][H] x (the experts' input)
+    uint16_t* x_d = nullptr;      // [T][H/32]
+    _Float16* h_q = nullptr;      // [R][F] h (aliases gubuf: the prefill path writes no (g, u))
+    uint16_t* h_d = nullptr;      // [R][F/32]
+    int4* fix = nullptr;          // [fix_max] h blocks whose rounding the f32 values do not settle
+    float* fix_h = nullptr;       // [fix_max][32] their f32 h values
+    int fix_max = 0;
     float* xn = nullptr;          // [T][H] RMSNorm(x)*w for fused-norm forwards (the experts' input)
     float* xr = nullptr;          // [T][H] the router's own input when it differs (Gemma 4 slice)
     float* ybuf = nullptr;        // [R][H] down outputs (unweighted)
@@ -118,8 +130,11 @@ bool route_uses_mfma(const LayerDesc& L, int T);
 bool route_decode_fused(const LayerDesc& L, int T);
 // x: the experts' input (quantized to Q8_0); xr: the router's input (x for
 // the Qwen layer; the scaled norm for Gemma 4); the shared gate reads xr.
+// x_f16: also write x's Q8_0 quants as f16 and its fp16 block scales (ws.x_q,
+// ws.x_d), the prefill GEMMs' A operand (inside the batched router's launch,
+// else a launch of its own).
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
-                        const RouteDebug& dbg, hipStream_t stream);
+                        const RouteDebug& dbg, bool x_f16, hipStream_t stream);
 // ev_start / ev_stop (optional): events recorded at the kernel's own start and
 // end (profiling of the dominant kernel without marker overhead).
 hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,

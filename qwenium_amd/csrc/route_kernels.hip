@@ -130,6 +130,43 @@ __device__ __forceinline__ void quant_token_row(const float* x, int H, int t, in
     quant_x_row(x + (uint64_t)t * H, H, lane, xq_qs + (uint64_t)t * H, xq_ds + (uint64_t)t * (H >> 5));
 }
 
+// The same Q8_0 quantization of one token row (one wave; lane b handles blocks
+// b, b+64, ...), written as the prefill GEMMs' A operand: the quants as exact
+// f16 values and the block scales as fp16 bits.
+__device__ void quant_x_row_f16(const float* xr, int H, int lane, _Float16* q, uint16_t* d) {
+    const int nb = H >> 5;
+    for (int b = lane; b < nb; b += 64) {
+        const f32x4* src = (const f32x4*)(xr + 32 * b);
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const f32x4 x = src[i];
+            v[4 * i + 0] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        uint32_t w[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const _Float16 q0 = (_Float16)__builtin_rintf(v[2 * i] * id), q1 = (_Float16)__builtin_rintf(v[2 * i + 1] * id);
+            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, q0) | ((uint32_t)__builtin_bit_cast(uint16_t, q1) << 16);
+        }
+        u32x4* dst = (u32x4*)(q + 32 * b);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+        d[b] = (uint16_t)f32_to_fp16(amax / 127.0f);
+    }
+}
+
+// x's f16 quants and scales for the prefill GEMMs, four tokens per block (one wave each).
+__global__ __launch_bounds__(256) void k_x_f16(const float* x, int T, int H, _Float16* q, uint16_t* d) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t < T)
+        quant_x_row_f16(x + (uint64_t)t * H, H, threadIdx.x & 63, q + (uint64_t)t * H, d + (uint64_t)t * (H >> 5));
+}
+
 // Blocks [0, n_router_blocks) compute router rows; any further blocks
 // quantize x, four tokens per block.
 template <int NCH>
@@ -181,6 +218,8 @@ struct RouterMfmaArgs {
     float* bound;           // [T][E]
     int8_t* xq_qs;
     float2* xq_ds;
+    _Float16* x_q;          // non-null: the quantizing blocks write x's f16 quants and scales instead of xq
+    uint16_t* x_d;
 };
 
 __device__ __forceinline__ void split_store(const f32x4 v, __bf16* hi_dst, __bf16* lo_dst) {
@@ -200,7 +239,13 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if ((int)blockIdx.x >= a.n_tiles) {
         const int t = ((int)blockIdx.x - a.n_tiles) * 4 + wave;
-        if (t < a.T) quant_token_row(a.xe, a.H, t, lane, a.xq_qs, a.xq_ds);
+        if (t < a.T) {
+            if (a.x_q)
+                quant_x_row_f16(a.xe + (uint64_t)t * a.H, a.H, lane, a.x_q + (uint64_t)t * a.H,
+                                a.x_d + (uint64_t)t * (a.H >> 5));
+            else
+                quant_token_row(a.xe, a.H, t, lane, a.xq_qs, a.xq_ds);
+        }
         return;
     }
     // XCD-aware order: blocks are dealt round-robin to the 8 XCDs, so block b
@@ -350,13 +395,6 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-__device__ __forceinline__ double wave_sum_f64(double v) {
-    v = dpp_sum_f64<64>(v);
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
 
 __device__ __forceinline__ double dot4_f64(const f32x4 w, const f32x4 v, double acc) {
     acc = __builtin_fma((double)w.x, (double)v.x, acc);
@@ -1178,8 +1216,8 @@ static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, c
     return hipGetLastError();
 }
 
-hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
-                        const RouteDebug& dbg, hipStream_t stream) {
+static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
+                                      const RouteDebug& dbg, bool& x_f16, hipStream_t stream) {
     TopkArgs ta;
     ta.logits = ws.logits;
     ta.logit_bound = ws.logit_bound;
@@ -1224,6 +1262,9 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
         ma.bound = ws.logit_bound;
         ma.xq_qs = ws.xq_qs;
         ma.xq_ds = ws.xq_ds;
+        ma.x_q = x_f16 ? ws.x_q : nullptr;
+        ma.x_d = ws.x_d;
+        x_f16 = false;  // written by the router launch
         hipLaunchKernelGGL(k_router_mfma, dim3(ma.n_tiles + (T + 3) / 4), dim3(256), 0, stream, ma);
         if ((err = hipGetLastError()) != hipSuccess) return err;
         hipLaunchKernelGGL(k_topk<true>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
@@ -1277,6 +1318,15 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, stream, ta);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL(k_scatter, dim3((T * L.K + L.S * T + 255) / 256), dim3(256), 0, stream, ta);
+    return hipGetLastError();
+}
+
+hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
+                        const RouteDebug& dbg, bool x_f16, hipStream_t stream) {
+    hipError_t err = launch_route_tables(L, ws, x, xr, T, dbg, x_f16, stream);
+    if (err != hipSuccess || !x_f16) return err;
+    // the routing launch did not write x's f16 quants (only the batched router's does)
+    hipLaunchKernelGGL(k_x_f16, dim3((T + 3) / 4), dim3(256), 0, stream, x, T, L.H, ws.x_q, ws.x_d);
     return hipGetLastError();
 }
 

@@ -2,10 +2,15 @@
 same seeded inputs.
 
 Bar: top-k expert ids, per-expert offsets and row lists bit-exact (ties to the
-lowest expert id); layer outputs within max-abs 2e-3 x output RMS.  Because the
-kernels accumulate quantized block dots exactly (f64) and use the same
-deterministic exp, outputs are in practice bit-identical; that is asserted
-separately as a fraction so a rare router rounding flip does not hide behind it.
+lowest expert id); layer outputs within max-abs 2e-3 x output RMS.  Below 128
+tokens the kernels accumulate quantized block dots exactly (f64) and use the
+same deterministic exp, so outputs are in practice bit-identical; that is
+asserted separately as a fraction so a rare router rounding flip does not hide
+behind it.  From 128 tokens (or when forced) the grouped GEMMs run f16 MFMAs:
+the block dots are exact, their scaled sum is accumulated in f32, and every h
+value whose Q8_0 rounding that error could change is recomputed exactly, so the
+h quants match the oracle's; outputs differ by f32 rounding of the sums (about
+1e-6 x RMS), held to MFMA_TOL, a hundred times tighter than the bar.
 """
 import numpy as np
 import pytest
@@ -18,6 +23,10 @@ from qwenium_amd.synthetic import LayerSpec
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
+# bound on the f16-MFMA prefill path's error (max |y - y_ref| / rms of y_ref;
+# measured <= 1.6e-6 at 35B-A3B prefill shapes); one h quant off by one would
+# exceed it
+MFMA_TOL = 2e-5
 
 
 def host_layer(spec: LayerSpec, tensors: dict) -> po.Layer:
@@ -43,7 +52,7 @@ def run_pair(spec: LayerSpec, T: int, seed: int, batch: int = 0, x=None):
     return y.cpu().numpy(), got, y_ref, d_ref, layer, tensors, ref
 
 
-def assert_parity(y, got, y_ref, d_ref, spec: LayerSpec, min_identical=0.999):
+def assert_parity(y, got, y_ref, d_ref, spec: LayerSpec, min_identical=0.999, mfma=False):
     np.testing.assert_array_equal(got["topk_idx"], d_ref["topk_idx"])
     np.testing.assert_array_equal(got["offsets"], d_ref["offsets"])
     np.testing.assert_array_equal(got["rows"], d_ref["rows"])
@@ -57,7 +66,10 @@ def assert_parity(y, got, y_ref, d_ref, spec: LayerSpec, min_identical=0.999):
     err = float(np.max(np.abs(y - y_ref)))
     assert err <= TOL * rms, f"max |y - y_ref| = {err:.3e} > {TOL} * rms ({rms:.3e})"
     identical = float(np.mean(y.view(np.int32) == y_ref.view(np.int32)))
-    assert identical >= min_identical, f"only {identical:.5f} of outputs bit-identical"
+    if mfma:
+        assert err <= MFMA_TOL * rms, f"f16-MFMA path: max |y - y_ref| = {err / rms:.2e} x rms > {MFMA_TOL}"
+    else:
+        assert identical >= min_identical, f"only {identical:.5f} of outputs bit-identical"
     return err, rms, identical
 
 
@@ -258,7 +270,7 @@ def test_graph_replay_matches_eager(gpu):
         torch.cuda.synchronize()
 
 
-# ---- int8-MFMA grouped GEMM path (prefill) -------------------------------------------------
+# ---- f16-MFMA grouped GEMM path (prefill) -------------------------------------------------
 @pytest.mark.parametrize("wtype", [TYPE_Q4_0, TYPE_Q8_0])
 @pytest.mark.parametrize("T", [1, 17, 64, 65, 130])
 def test_mfma_path_small_layer(gpu, monkeypatch, wtype, T):
@@ -266,20 +278,20 @@ def test_mfma_path_small_layer(gpu, monkeypatch, wtype, T):
     monkeypatch.setenv("QMOE_MFMA_MIN_TOKENS", "1")
     spec = LayerSpec(256, 16, 4, 128, True, wtype)
     y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=200 + T)
-    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=True)
 
 
 def test_mfma_config1_forced(gpu, monkeypatch):
     monkeypatch.setenv("QMOE_MFMA_MIN_TOKENS", "1")
     spec = synthetic.CONFIG1
     y, got, y_ref, d_ref, *_ = run_pair(spec, 32, seed=0)
-    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=True)
 
 
 def test_mfma_35b_q4_0_t256(gpu):
     spec = synthetic.QWEN35B
     y, got, y_ref, d_ref, *_ = run_pair(spec, 256, seed=9)
-    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=True)
 
 
 def check_router_bound(got, exact_logits):
@@ -300,7 +312,7 @@ def test_batched_router_forced_small_layer(gpu, monkeypatch, T):
     monkeypatch.setenv("QMOE_BIG_ROUTER_MIN_TOKENS", "1")
     spec = LayerSpec(256, 16, 4, 128, True, TYPE_Q4_0)
     y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=300 + T)
-    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0, mfma=T >= 128)
     check_router_bound(got, d_ref["logits"])
 
 
@@ -308,7 +320,7 @@ def test_batched_router_35b_t300(gpu):
     """The default threshold (256 tokens) selects the batched router."""
     spec = synthetic.QWEN35B
     y, got, y_ref, d_ref, *_ = run_pair(spec, 300, seed=31)
-    assert_parity(y, got, y_ref, d_ref, spec, min_identical=1.0)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=True)
     assert check_router_bound(got, d_ref["logits"]) < 0.5
 
 
@@ -363,8 +375,7 @@ def test_prefill_35b_q4_0_t4096(gpu):
     y_ref = ref.forward(xh[sample])
     yg = y.cpu().numpy()[sample]
     rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
-    assert np.max(np.abs(yg - y_ref)) <= TOL * rms
-    assert np.mean(yg.view(np.int32) == y_ref.view(np.int32)) >= 0.999
+    assert np.max(np.abs(yg - y_ref)) <= MFMA_TOL * rms
 
 
 def test_skewed_q8_0_t2048(gpu):
@@ -395,8 +406,7 @@ def test_skewed_q8_0_t2048(gpu):
     y_ref = ref.forward(xh[sample])
     yg = y.cpu().numpy()[sample]
     rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
-    assert np.max(np.abs(yg - y_ref)) <= TOL * rms
-    assert np.mean(yg.view(np.int32) == y_ref.view(np.int32)) >= 0.999
+    assert np.max(np.abs(yg - y_ref)) <= MFMA_TOL * rms
 
 
 @pytest.mark.parametrize("T", [1, 10, 64, 8192])
@@ -450,7 +460,10 @@ def test_stack_40_layers(gpu, T):
         ys = yg[sample]
         rms = float(np.sqrt(np.mean(yr.astype(np.float64) ** 2)))
         assert np.max(np.abs(ys - yr)) <= TOL * rms, f"layer {l}"
-        assert np.mean(ys.view(np.int32) == yr.view(np.int32)) >= 0.999, f"layer {l}"
+        if T >= 128:  # the f16-MFMA prefill path
+            assert np.max(np.abs(ys - yr)) <= MFMA_TOL * rms, f"layer {l}"
+        else:
+            assert np.mean(ys.view(np.int32) == yr.view(np.int32)) >= 0.999, f"layer {l}"
 
 
 @pytest.mark.parametrize("n_experts,T", [(256, 10), (1024, 16), (16, 3)])
