@@ -64,7 +64,7 @@ constexpr int kASlots = kTM * kSlotsPerRow;
 constexpr int kAHalfs = kASlots * 8;
 constexpr int kDmaIters = (kASlots + 255) / 256;
 constexpr int kSinkBytes = (kDmaIters * 256 - kASlots) * 16;  // the last round's spare lanes land here
-constexpr int kScaleBytes = kTM * 16;       // per row and chunk: 4 f16 block scales + 8 zero bytes
+constexpr int kScaleBytes = kTM * 16;       // per row and chunk: its 4 f16 block scales, twice
 constexpr int kStageBytes = kAHalfs * 2 + kScaleBytes;
 constexpr int kHLd = 64 + 4;                // gate/up epilogue: g and u rows in LDS, f32
 constexpr size_t kF16LdsBytes = 2 * (size_t)kStageBytes + kSinkBytes + kTM * 8;
@@ -94,8 +94,8 @@ struct F16Args {
     int n_y;                                     // column chunks per tile
     // gate/up: h's quants and scales, the fixup list
     _Float16* h_q; uint16_t* h_d;
-    int4* fix;                                   // [max] {row, f block, expert, mask of uncertain values}
-    float* fix_h;                                // [max][32] the block's f32 h values
+    int4* fix;                                   // [max] {row, f block | expert << 16, uncertain values, amax candidates}
+    float* fix_h;                                // [max][kFixStride] the block's f32 h values, amax's error
     int32_t* fix_count;
     int fix_max;
     float acc_err;                               // kAccErr * sqrt(K / 32)
@@ -215,6 +215,24 @@ __device__ __forceinline__ uint32_t block_quants<kTypeQ8_0>(const RawPair<kTypeQ
     return (kh ? r.w[5] : r.w[6]) >> 16;
 }
 
+// Direct global->LDS loads (lane i's 16 or 4 bytes to LDS byte address
+// lds + 16 i or + 4 i; lds wave-uniform).  Issued as assembly so that the
+// compiler does not order every later LDS read after them: the kernel waits
+// for them itself (s_waitcnt vmcnt at the chunk boundary, then a barrier).
+// M0 takes the LDS base; the LDS-DMA read of M0 needs one wait state.
+// Source: a wave-uniform base plus this lane's 32-bit byte offset.
+__device__ __forceinline__ void dma_lds16(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 __device__ __forceinline__ v16f mfma16(v8h a, v8h b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -232,8 +250,8 @@ __device__ __forceinline__ float act_f32(int act, const uint16_t* tab, float g) 
 template <int WT, bool GATEUP>
 __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
-    // [2 stages] {A quants [128][kLd] f16, block scale records [128][8] f16 (4
-    // scales, 4 zeros)}, the sink, A row offsets [128], scale row offsets [128]
+    // [2 stages] {A quants [128][kLd] f16, block scale records [128][8] f16 (the
+    // 4 scales twice)}, the sink, A row offsets [128], scale row offsets [128]
     uint8_t* s_stage = s_dyn;
     uint32_t* s_rowoff = (uint32_t*)(s_dyn + 2 * kStageBytes + kSinkBytes);
     uint32_t* s_doff = s_rowoff + kTM;
@@ -248,7 +266,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
     const int4 tile = a.tiles[tile_id];
     const int e = tile.x, p0 = tile.y, nr = tile.z;
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // wave: scalar
     const int col = lane & 31;
     const bool kh = lane >= 32;
     const bool sh = e >= a.E;
@@ -261,9 +279,6 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         s_rowoff[tid] = (uint32_t)arow * (uint32_t)a.K;
         s_doff[tid] = (uint32_t)arow * (uint32_t)nblk;
     }
-    // the zero halves of the scale records (never written by the staging)
-    for (int i = tid; i < 2 * kTM; i += 256)
-        *(uint64_t*)(s_stage + (i / kTM) * kStageBytes + kAHalfs * 2 + (i % kTM) * 16 + 8) = 0;
     __syncthreads();
 
     // this lane's weight row (wave-uniform slab base + 32-bit row offset: an
@@ -303,33 +318,29 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         const int u = s - r * kSlotsPerRow;
         soff[it] = s_rowoff[r] + (u < 16 ? 8 * u : 0);
     }
-    // Scales: one dword (two blocks) into the first 8 bytes of each row's
-    // 16-byte record; lane slot sl = (row, dword) = (sl / 4, sl % 4), two
-    // rounds of 64 slots per wave, dwords 2-3 (the zeros) not loaded.
+    // Scales: each row's 16-byte record holds the chunk's 4 block scales twice
+    // (dword d = blocks 2 (d & 1), + 1); lane slot sl = (row, dword) = (sl / 4,
+    // sl % 4), two rounds of 64 slots per wave.  The scale MFMA's B operand is
+    // zero at k >= 4, so the copy in halves 4..7 (finite) adds nothing.
     uint32_t doff[2];
 #pragma unroll
     for (int rd = 0; rd < 2; ++rd) {
         const int sl = wave * 128 + 64 * rd + lane;
         doff[rd] = s_doff[sl >> 2] + 2 * (sl & 1);
     }
-    const bool dlane = (lane & 2) == 0;  // dwords 0, 1 of a record
-    auto stage = [&](int c) {
-        uint8_t* st = s_stage + (c & 1) * kStageBytes;
+    auto stage = [&](int c, int buf) {
+        uint8_t* st = s_stage + buf * kStageBytes;
         const uint32_t k0 = (uint32_t)(c * kKC);
 #pragma unroll
         for (int it = 0; it < kDmaIters; ++it) {
             const int s0 = it * 256 + wave * 64;
-            void* dst = s0 < kASlots ? (void*)(st + s0 * 16) : (void*)(s_stage + 2 * kStageBytes);  // wave-uniform
-            __builtin_amdgcn_global_load_lds((const void*)(a.a_q + soff[it] + k0),
-                                             (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+            const void* dst = s0 < kASlots ? (const void*)(st + s0 * 16) : (const void*)(s_stage + 2 * kStageBytes);
+            dma_lds16(a.a_q + k0, 2u * soff[it], __builtin_amdgcn_readfirstlane(lds_addr(dst)));  // wave-uniform
         }
 #pragma unroll
-        for (int rd = 0; rd < 2; ++rd) {
-            if (dlane)
-                __builtin_amdgcn_global_load_lds(
-                    (const void*)(a.a_d + doff[rd] + (uint32_t)(4 * c)),
-                    (__attribute__((address_space(3))) void*)(st + kAHalfs * 2 + (wave * 128 + 64 * rd) * 4), 4, 0, 0);
-        }
+        for (int rd = 0; rd < 2; ++rd)
+            dma_lds4(a.a_d + 4 * c, 2u * doff[rd],
+                     __builtin_amdgcn_readfirstlane(lds_addr(st + kAHalfs * 2 + (wave * 128 + 64 * rd) * 4)));
     };
 
     v16f acc[4];
@@ -357,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
             __syncthreads();                // ... for every wave; stage (c + 1) & 1 is no longer read
             if (c + 1 < nchunk) {
                 fetch(c + 1, nxt);
-                stage(c + 1);
+                stage(c + 1, (c + 1) & 1);
             }
             const uint8_t* st = s_stage + (c & 1) * kStageBytes;
             const _Float16* aq = (const _Float16*)st;
@@ -372,7 +383,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
                     v8h bq[2];
                     const uint32_t dw = block_quants<WT>(cur[pp], j, kh, bq);
                     // the outer product's B: dw at element bl of lanes 0..31 (k = bl),
-                    // zero elsewhere; its A is the row's record {dx0..dx3, 0 x4}:
+                    // zero elsewhere; its A is the row's record {dx0..dx3, dx0..dx3}:
                     // D = dx_bl * dw, exact
                     const uint32_t dwl = kh ? 0u : dw;
                     u32x4 bsw = {0u, 0u, 0u, 0u};
@@ -399,7 +410,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         }
     };
     fetch(0, wa);
-    stage(0);
+    stage(0, 0);
     switch (nm) {
         case 1: run(std::integral_constant<int, 1>{}); break;
         case 2: run(std::integral_constant<int, 2>{}); break;
@@ -459,7 +470,8 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
     const float rg = __builtin_sqrtf(sg * (1.0f / 32.0f)), ru = __builtin_sqrtf(su * (1.0f / 32.0f));
     // h and its error estimate (vg[] and vu[] are overwritten with them); GeGLU:
     // the table entry is picked by fp16(g) (and |g| >= 10 by a threshold)
-    float amax = 0.0f, ea = 0.0f;
+    // amax_lo, amax_hi: bounds on the exact block amax (the largest |h| - eh and |h| + eh)
+    float amax = 0.0f, amax_lo = 0.0f, amax_hi = 0.0f;
     uint32_t unsure = 0;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
@@ -468,29 +480,31 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         const float h = av * uv;
         const float eg = a.acc_err * fmaxf(__builtin_fabsf(gv), rg);
         const float eu = a.acc_err * fmaxf(__builtin_fabsf(uv), ru);
-        const float eh = kActSlope * __builtin_fabsf(uv) * eg + __builtin_fabsf(av) * eu +
-                         kActRel * (1.0f + __builtin_fabsf(gv)) * __builtin_fabsf(h);
+        const float ah = __builtin_fabsf(h);
+        // the activation's error: SiLU from g's error through its slope; GeGLU's
+        // table entry is exact for a settled fp16(g) (and |g| >= 10 threshold),
+        // else it may be any entry of the range, within the slope bound of it
+        float eav = kActSlope * eg;
         if (a.act == kActGeluTanh) {
             const float lo = gv - eg, hi = gv + eg;
-            if (f32_to_fp16(lo) != f32_to_fp16(hi) || (lo <= -10.0f) != (hi <= -10.0f) ||
-                (lo >= 10.0f) != (hi >= 10.0f))
-                unsure |= 1u << i;
+            const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
+            eav = (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
+                      ? 0.0f
+                      : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
         }
+        const float eh = __builtin_fabsf(uv) * eav + __builtin_fabsf(av) * eu + kActRel * (1.0f + __builtin_fabsf(gv)) * ah;
         vg[i] = h;
         vu[i] = eh;
-        amax = fmaxf(amax, __builtin_fabsf(h));
-        ea = fmaxf(ea, eh);
+        amax = fmaxf(amax, ah);
+        amax_lo = fmaxf(amax_lo, ah - eh);
+        amax_hi = fmaxf(amax_hi, ah + eh);
     }
-    float sec = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float ah = __builtin_fabsf(vg[i]);
-        sec = fmaxf(sec, ah < amax ? ah : 0.0f);
-    }
+    const float ea = fmaxf(amax_hi - amax, amax - amax_lo);  // error of the f32 amax
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     // quants; a value whose t = h * 127 / amax lies within its error (amax's
-    // own error included) of a rounding tie is uncertain
+    // own error included) of a rounding tie is uncertain; a value whose range
+    // reaches amax_lo could be the exact largest |h|
     uint32_t cand = 0, packed[16];
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
@@ -499,7 +513,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         const float at = __builtin_fabsf(t);
         const float et = (vu[i] + at * ea * (1.0f / 127.0f)) * id + at * 2.5e-7f;
         if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << i;
-        if (__builtin_fabsf(vg[i]) >= amax - 2.0f * ea) cand |= 1u << i;  // could be the exact largest |h|
+        if (__builtin_fabsf(vg[i]) + vu[i] >= amax_lo) cand |= 1u << i;
         const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
         packed[i >> 1] = (i & 1) ? (packed[i >> 1] | (qb << 16)) : qb;
     }
@@ -508,20 +522,19 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) hq[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
     a.h_d[p * nfb + fb] = (uint16_t)f32_to_fp16(d);
-    // the block's largest |h|: the runner-up not clear of it, or amax / 127
-    // near an fp16 tie; a listed block's requantization needs the exact amax,
-    // so its candidates are listed with it
-    const bool amax_open = amax - sec <= 2.0f * ea ||
-                           f32_to_fp16((amax - ea) * (1.0f / 127.0f)) != f32_to_fp16((amax + ea) * (1.0f / 127.0f));
-    uint32_t mask = unsure | (amax_open ? cand : 0u);
+    // the block's largest |h| is open when several values could be it or
+    // amax / 127 is near an fp16 tie (then its candidates are uncertain values too)
+    const bool amax_open = __builtin_popcount(cand) > 1 ||
+                           f32_to_fp16(amax_lo / 127.0f) != f32_to_fp16(amax_hi / 127.0f);
+    const uint32_t mask = unsure | (amax_open ? cand : 0u);
     if (mask) {
-        mask |= cand;
         const int slot = atomicAdd(a.fix_count, 1);
         if (slot < a.fix_max) {
-            f32x4* fh = (f32x4*)(a.fix_h + (uint64_t)slot * 32);
+            f32x4* fh = (f32x4*)(a.fix_h + (uint64_t)slot * kFixStride);
 #pragma unroll
             for (int i = 0; i < 8; ++i) fh[i] = f32x4{vg[4 * i], vg[4 * i + 1], vg[4 * i + 2], vg[4 * i + 3]};
-            a.fix[slot] = make_int4((int)p, fb, e, (int)mask);
+            fh[8] = f32x4{ea, 0.0f, 0.0f, 0.0f};
+            a.fix[slot] = make_int4((int)p, fb | (e << 16), (int)mask, (int)cand);
         }
     }
 }
@@ -537,78 +550,33 @@ struct FixArgs {
     const uint8_t* sg; uint64_t sg_nb1;
     const uint8_t* su; uint64_t su_nb1;
     const int32_t* row_token;
-    const _Float16* x_q; const uint16_t* x_d;  // x quants [T][H] f16, scales [T][H/32]
+    const int8_t* xq_qs; const float2* xq_ds;  // x's Q8_0 quants [T][H], {scale, quant sum} [T][H/32]
     const int4* fix; const float* fix_h; const int32_t* fix_count; int fix_max;
     _Float16* h_q; uint16_t* h_d;
     int act; const uint16_t* gelu_tab;
 };
 
-// Integer dots of one quant block of the gate row and of the up row with the
-// same 32 activation quants (exact f16 integers); dw: the two block scales.
+// The exact gate and up dots of weight rows rg, ru with one token's int8
+// quants over the lanes of a 32-lane half (lane l32 takes block pairs l32,
+// l32 + 32, ...): each block term fp32(dw) * fp32(dx) * isum is exact in f64
+// (a 22-bit scale product times a 19-bit integer); the caller sums them over
+// the half.
 template <int WT>
-__device__ __forceinline__ void block_isum2(const uint8_t* bg, const uint8_t* bu, const int (&xv)[32], int& ig, int& iu,
-                                            float& dg, float& du) {
-    // blocks are 2-byte aligned (18 / 34 bytes): halfword loads
-    const uint16_t* g16 = (const uint16_t*)bg;
-    const uint16_t* u16 = (const uint16_t*)bu;
-    dg = fp16_to_f32(g16[0]);
-    du = fp16_to_f32(u16[0]);
-    ig = 0;
-    iu = 0;
-    if (WT == kTypeQ4_0) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t wg = g16[1 + j], wu = u16[1 + j];  // quant bytes 2j, 2j + 1
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int k = 2 * j + h;
-                const uint32_t cg = (wg >> (8 * h)) & 0xffu, cu = (wu >> (8 * h)) & 0xffu;
-                ig += ((int)(cg & 15u) - 8) * xv[k] + ((int)(cg >> 4) - 8) * xv[k + 16];
-                iu += ((int)(cu & 15u) - 8) * xv[k] + ((int)(cu >> 4) - 8) * xv[k + 16];
-            }
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint32_t wg = g16[1 + j], wu = u16[1 + j];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int k = 2 * j + h;
-                ig += (int)(int8_t)(uint8_t)(wg >> (8 * h)) * xv[k];
-                iu += (int)(int8_t)(uint8_t)(wu >> (8 * h)) * xv[k];
-            }
-        }
-    }
-}
-
-// The exact gate and up dots of weight rows rg, ru with one x row over the
-// lanes of a 32-lane half (lane l32 takes blocks l32, l32 + 32, ...): each
-// block term fp32(dw) * fp32(dx) * isum is exact in f64 (a 22-bit scale
-// product times a 19-bit integer); the caller sums them over the half.
-template <int WT>
-__device__ void exact_gu_part(const uint8_t* rg, const uint8_t* ru, const _Float16* xq, const uint16_t* xd, int nblk,
+__device__ void exact_gu_part(const uint8_t* rg, const uint8_t* ru, const int8_t* xqs, const float2* xds, int npairs,
                               int l32, double& g, double& u) {
     g = 0.0;
     u = 0.0;
-    for (int b = l32; b < nblk; b += 32) {
-        int xv[32];
-        const u32x4* xs = (const u32x4*)(xq + 32 * b);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4 w = xs[i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                xv[8 * i + 2 * j] = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffffu));
-                xv[8 * i + 2 * j + 1] = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
-            }
-        }
-        const float dx = fp16_to_f32(xd[b]);
-        int ig, iu;
-        float dg, du;
-        block_isum2<WT>(rg + (uint64_t)b * BlockTraits<WT>::kBytes, ru + (uint64_t)b * BlockTraits<WT>::kBytes, xv, ig, iu,
-                        dg, du);
-        g += (double)(dg * dx) * (double)ig;  // fp32(dw) * fp32(dx) is exact in f32
-        u += (double)(du * dx) * (double)iu;
+    for (int pr = l32; pr < npairs; pr += 32) {
+        WPair<WT> wg, wu;
+        wg.load(rg, pr);
+        wu.load(ru, pr);
+        XPair xp;
+        xp.load(xqs, xds, pr);
+        // fp32(dw) * fp32(dx) is exact in f32
+        g += (double)(wg.dA() * xp.dA) * (double)wg.dotA(xp.xs, xp.sA) +
+             (double)(wg.dB() * xp.dB) * (double)wg.dotB(xp.xs + 8, xp.sB);
+        u += (double)(wu.dA() * xp.dA) * (double)wu.dotA(xp.xs, xp.sA) +
+             (double)(wu.dB() * xp.dB) * (double)wu.dotB(xp.xs + 8, xp.sB);
     }
 }
 
@@ -619,57 +587,79 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-// One wave per listed block; its uncertain values two at a time (one per
-// 32-lane half), each from the exact f64 gate and up sums rounded once to f32
-// and the deterministic activation; then the block is requantized.
+// One 32-lane half per listed block, its uncertain values one at a time (lane
+// l takes weight block pairs l, l + 32, ...), each from the exact f64 gate and
+// up sums rounded once to f32 and the deterministic activation.  The block is
+// then requantized with the f32 amax if every recomputed value's quant is
+// settled despite amax's error, else with the exact amax (its candidates
+// recomputed as well).
+template <int WT>
+__device__ __forceinline__ void fix_values(const FixArgs& a, uint32_t todo, int fb, int e, bool sh, const int8_t* xqs,
+                                           const float2* xds, float& h) {
+    const int l32 = threadIdx.x & 31;
+    const bool upper = (threadIdx.x & 63) >= 32;
+    while (todo) {
+        const int v = __builtin_ctz(todo);
+        todo &= todo - 1;
+        const int f = 32 * fb + v;
+        const uint8_t* rg = sh ? a.sg + (uint64_t)f * a.sg_nb1 : a.wg + (uint64_t)e * a.wg_nb2 + (uint64_t)f * a.wg_nb1;
+        const uint8_t* ru = sh ? a.su + (uint64_t)f * a.su_nb1 : a.wu + (uint64_t)e * a.wu_nb2 + (uint64_t)f * a.wu_nb1;
+        double gd, ud;
+        exact_gu_part<WT>(rg, ru, xqs, xds, a.H >> 6, l32, gd, ud);
+        gd = dpp_sum_f64<32>(gd);  // half sums in lanes 31 and 63
+        ud = dpp_sum_f64<32>(ud);
+        const double g = upper ? readlane_f64(gd, 63) : readlane_f64(gd, 31);
+        const double u = upper ? readlane_f64(ud, 63) : readlane_f64(ud, 31);
+        const float hv = act_mul(a.act, a.gelu_tab, (float)g, (float)u);
+        if (l32 == v) h = hv;
+    }
+}
+
+__device__ __forceinline__ float half_max(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
 template <int WT>
 __global__ __launch_bounds__(256) void k_fix_h(FixArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int l32 = lane & 31;
-    const bool upper = lane >= 32;
+    const int l32 = threadIdx.x & 31;
+    const bool upper = (threadIdx.x & 63) >= 32;
     const int n = min(*a.fix_count, a.fix_max);
     const int nblk = a.H >> 5;
-    for (int i = blockIdx.x * 4 + (int)(threadIdx.x >> 6); i < n; i += gridDim.x * 4) {
+    for (int i = blockIdx.x * 8 + (int)(threadIdx.x >> 5); i < n; i += gridDim.x * 8) {
         const int4 ent = a.fix[i];
-        const int p = ent.x, fb = ent.y, e = ent.z;
-        uint32_t todo = (uint32_t)ent.w;  // the uncertain values of the block
+        const int p = ent.x, fb = ent.y & 0xffff, e = ent.y >> 16;
+        const uint32_t unsure = (uint32_t)ent.z, cand = (uint32_t)ent.w;
         const bool sh = e >= a.E;
         const int t = a.row_token[p];
-        const _Float16* xq = a.x_q + (uint64_t)t * a.H;
-        const uint16_t* xd = a.x_d + (uint64_t)t * nblk;
-        float h = a.fix_h[(uint64_t)i * 32 + l32];  // value l32 of the block (both halves)
-        while (todo) {
-            const int v0 = __builtin_ctz(todo);
-            todo &= todo - 1;
-            const int v1 = todo ? __builtin_ctz(todo) : -1;
-            if (todo) todo &= todo - 1;
-            const int v = upper ? v1 : v0;
-            double gd = 0.0, ud = 0.0;
-            if (v >= 0) {
-                const int f = 32 * fb + v;
-                const uint8_t* rg =
-                    sh ? a.sg + (uint64_t)f * a.sg_nb1 : a.wg + (uint64_t)e * a.wg_nb2 + (uint64_t)f * a.wg_nb1;
-                const uint8_t* ru =
-                    sh ? a.su + (uint64_t)f * a.su_nb1 : a.wu + (uint64_t)e * a.wu_nb2 + (uint64_t)f * a.wu_nb1;
-                exact_gu_part<WT>(rg, ru, xq, xd, nblk, l32, gd, ud);
-            }
-            gd = dpp_sum_f64<32>(gd);  // half sums in lanes 31 and 63
-            ud = dpp_sum_f64<32>(ud);
-            const float h0 = act_mul(a.act, a.gelu_tab, (float)readlane_f64(gd, 31), (float)readlane_f64(ud, 31));
-            if (l32 == v0) h = h0;
-            if (v1 >= 0) {
-                const float h1 = act_mul(a.act, a.gelu_tab, (float)readlane_f64(gd, 63), (float)readlane_f64(ud, 63));
-                if (l32 == v1) h = h1;
+        const int8_t* xqs = a.xq_qs + (uint64_t)t * a.H;
+        const float2* xds = a.xq_ds + (uint64_t)t * nblk;
+        const float* fh = a.fix_h + (uint64_t)i * kFixStride;
+        float h = fh[l32];  // value l32 of the block
+        const float ea = fh[32];
+        fix_values<WT>(a, unsure, fb, e, sh, xqs, xds, h);
+        float amax = half_max(__builtin_fabsf(h));
+        const uint32_t rest = cand & ~unsure;
+        if (rest) {
+            // amax is one of the f32 candidates: is every recomputed quant settled
+            // under amax's error?
+            const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+            const float tv = h * id, at = __builtin_fabsf(tv);
+            const bool open = ((unsure >> l32) & 1u) &&
+                              __builtin_fabsf(__builtin_fabsf(tv - __builtin_rintf(tv)) - 0.5f) <=
+                                  at * (ea * 1.01f / amax + 2.5e-7f);
+            const uint64_t ball = __ballot(open);
+            if ((upper ? (ball >> 32) : (ball & 0xffffffffull)) != 0) {
+                fix_values<WT>(a, rest, fb, e, sh, xqs, xds, h);
+                amax = half_max(__builtin_fabsf(h));
             }
         }
-        // requantize the block from its 32 values (lanes 0..31; 32..63 mirror them)
-        float amax = __builtin_fabsf(h);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        // requantize the block from its 32 values
         const float d = amax / 127.0f;
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-        if (lane < 32) a.h_q[(uint64_t)p * a.F + 32 * fb + lane] = (_Float16)__builtin_rintf(h * id);
-        if (lane == 0) a.h_d[(uint64_t)p * (a.F >> 5) + fb] = (uint16_t)f32_to_fp16(d);
+        a.h_q[(uint64_t)p * a.F + 32 * fb + l32] = (_Float16)__builtin_rintf(h * id);
+        if (l32 == 0) a.h_d[(uint64_t)p * (a.F >> 5) + fb] = (uint16_t)f32_to_fp16(d);
     }
 }
 
@@ -726,12 +716,12 @@ hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hi
     f.sg = L.w_sh_gate; f.sg_nb1 = L.sh_gate_nb1;
     f.su = L.w_sh_up; f.su_nb1 = L.sh_up_nb1;
     f.row_token = ws.row_token;
-    f.x_q = ws.x_q; f.x_d = ws.x_d;
+    f.xq_qs = ws.xq_qs; f.xq_ds = ws.xq_ds;
     f.fix = ws.fix; f.fix_h = ws.fix_h; f.fix_count = ws.counters + kCounterFix; f.fix_max = ws.fix_max;
     f.h_q = ws.h_q; f.h_d = ws.h_d;
     f.act = L.act; f.gelu_tab = L.gelu_tab;
-    // one wave per listed block, enough waves in flight to hide the row reads
-    const dim3 fgrid(std::max(1, std::min(8 * L.n_cu, (ws.fix_max + 3) / 4)));
+    // one 32-lane half per listed block, enough waves in flight to hide the row reads
+    const dim3 fgrid(std::max(1, std::min(8 * L.n_cu, (ws.fix_max + 7) / 8)));
     if (L.gu_type == kTypeQ4_0) hipLaunchKernelGGL(k_fix_h<kTypeQ4_0>, fgrid, dim3(256), 0, stream, f);
     else hipLaunchKernelGGL(k_fix_h<kTypeQ8_0>, fgrid, dim3(256), 0, stream, f);
     return hipGetLastError();

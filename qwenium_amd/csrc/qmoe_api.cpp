@@ -165,7 +165,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.x_d = (uint16_t*)take((size_t)T * (H / 32) * sizeof(uint16_t) + 256);
     ws.fix_max = (int)std::min<size_t>(R * (F / 32), (size_t)1 << 30);  // every h block, at worst
     ws.fix = (int4*)take((size_t)ws.fix_max * sizeof(int4));
-    ws.fix_h = (float*)take((size_t)ws.fix_max * 32 * sizeof(float));
+    ws.fix_h = (float*)take((size_t)ws.fix_max * kFixStride * sizeof(float));
     ws.hq_qs = (int8_t*)take(R * F);
     ws.hq_ds = (float2*)take(R * (F / 32) * sizeof(float2));
     ws.ybuf = (float*)take(R * H * sizeof(float));
@@ -562,7 +562,11 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         xin = v.xn;
         xr = v.xr;
     }
-    const bool mfma = n_tokens >= d.mfma_min_tokens && !qmoe::gateup_q_fused(d, n_tokens);
+    // the prefill GEMMs address their A operands (x and h quants as f16) with
+    // 32-bit byte offsets
+    const uint64_t R = (uint64_t)n_tokens * (d.K + d.S);
+    const bool mfma = n_tokens >= d.mfma_min_tokens && !qmoe::gateup_q_fused(d, n_tokens) &&
+                      R * d.F * 2 + 256 < (1ull << 32) && (uint64_t)n_tokens * d.H * 2 + 256 < (1ull << 32);
     if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, xr, n_tokens, rdbg, mfma, stream);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
     // events [1] and [2] are taken by the gate/up launch itself (its own start and end)

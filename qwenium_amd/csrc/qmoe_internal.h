@@ -24,6 +24,7 @@ constexpr int kMfmaTileM = 128;
 constexpr int kF16ChunkK = 128;
 // Workspace counters: [0] active slots, [1] tiles, [kCounterFix] listed h blocks.
 constexpr int kCounterFix = 4;
+constexpr int kFixStride = 36;  // floats per listed h block: 32 values, amax's error estimate, padding
 // Expert activations: SwiGLU (moe.cpp:117) or GeGLU-tanh (gemma4.cpp:423).
 constexpr int kActSilu = 0;
 constexpr int kActGeluTanh = 1;
@@ -90,7 +91,7 @@ struct Workspace {
     _Float16* h_q = nullptr;      // [R][F] h (aliases gubuf: the prefill path writes no (g, u))
     uint16_t* h_d = nullptr;      // [R][F/32]
     int4* fix = nullptr;          // [fix_max] h blocks whose rounding the f32 values do not settle
-    float* fix_h = nullptr;       // [fix_max][32] their f32 h values
+    float* fix_h = nullptr;       // [fix_max][kFixStride] their 32 f32 h values and amax's error estimate
     int fix_max = 0;
     float* xn = nullptr;          // [T][H] RMSNorm(x)*w for fused-norm forwards (the experts' input)
     float* xr = nullptr;          // [T][H] the router's own input when it differs (Gemma 4 slice)

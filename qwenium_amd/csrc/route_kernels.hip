@@ -131,9 +131,10 @@ __device__ __forceinline__ void quant_token_row(const float* x, int H, int t, in
 }
 
 // The same Q8_0 quantization of one token row (one wave; lane b handles blocks
-// b, b+64, ...), written as the prefill GEMMs' A operand: the quants as exact
-// f16 values and the block scales as fp16 bits.
-__device__ void quant_x_row_f16(const float* xr, int H, int lane, _Float16* q, uint16_t* d) {
+// b, b+64, ...), written as the prefill GEMMs' A operand (the quants as exact
+// f16 values, the block scales as fp16 bits) and in the int8 layout above (for
+// the exact recomputation of uncertain h values).
+__device__ void quant_x_row_f16(const float* xr, int H, int lane, _Float16* q, uint16_t* d, int8_t* qs, float2* ds) {
     const int nb = H >> 5;
     for (int b = lane; b < nb; b += 64) {
         const f32x4* src = (const f32x4*)(xr + 32 * b);
@@ -147,24 +148,36 @@ __device__ void quant_x_row_f16(const float* xr, int H, int lane, _Float16* q, u
 #pragma unroll
         for (int i = 0; i < 32; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-        uint32_t w[16];
+        uint32_t w[16], packed[8] = {};
+        int sum = 0;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const _Float16 q0 = (_Float16)__builtin_rintf(v[2 * i] * id), q1 = (_Float16)__builtin_rintf(v[2 * i + 1] * id);
-            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, q0) | ((uint32_t)__builtin_bit_cast(uint16_t, q1) << 16);
+            const float r0 = __builtin_rintf(v[2 * i] * id), r1 = __builtin_rintf(v[2 * i + 1] * id);
+            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)r0) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)r1) << 16);
+            const int i0 = (int)r0, i1 = (int)r1;
+            sum += i0 + i1;
+            packed[i >> 1] |= (((uint32_t)(i0 & 0xff)) | ((uint32_t)(i1 & 0xff) << 8)) << (16 * (i & 1));
         }
         u32x4* dst = (u32x4*)(q + 32 * b);
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
-        d[b] = (uint16_t)f32_to_fp16(amax / 127.0f);
+        const uint32_t dh = f32_to_fp16(amax / 127.0f);
+        d[b] = (uint16_t)dh;
+        u32x4* qdst = (u32x4*)(qs + 32 * b);
+        qdst[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+        qdst[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+        ds[b] = make_float2(fp16_to_f32(dh), __builtin_bit_cast(float, sum));
     }
 }
 
 // x's f16 quants and scales for the prefill GEMMs, four tokens per block (one wave each).
-__global__ __launch_bounds__(256) void k_x_f16(const float* x, int T, int H, _Float16* q, uint16_t* d) {
+__global__ __launch_bounds__(256) void k_x_f16(const float* x, int T, int H, _Float16* q, uint16_t* d, int8_t* qs,
+                                               float2* ds) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t < T)
-        quant_x_row_f16(x + (uint64_t)t * H, H, threadIdx.x & 63, q + (uint64_t)t * H, d + (uint64_t)t * (H >> 5));
+        quant_x_row_f16(x + (uint64_t)t * H, H, threadIdx.x & 63, q + (uint64_t)t * H, d + (uint64_t)t * (H >> 5),
+                        qs + (uint64_t)t * H, ds + (uint64_t)t * (H >> 5));
 }
 
 // Blocks [0, n_router_blocks) compute router rows; any further blocks
@@ -218,7 +231,7 @@ struct RouterMfmaArgs {
     float* bound;           // [T][E]
     int8_t* xq_qs;
     float2* xq_ds;
-    _Float16* x_q;          // non-null: the quantizing blocks write x's f16 quants and scales instead of xq
+    _Float16* x_q;          // non-null: the quantizing blocks also write x's f16 quants and scales
     uint16_t* x_d;
 };
 
@@ -242,7 +255,8 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
         if (t < a.T) {
             if (a.x_q)
                 quant_x_row_f16(a.xe + (uint64_t)t * a.H, a.H, lane, a.x_q + (uint64_t)t * a.H,
-                                a.x_d + (uint64_t)t * (a.H >> 5));
+                                a.x_d + (uint64_t)t * (a.H >> 5), a.xq_qs + (uint64_t)t * a.H,
+                                a.xq_ds + (uint64_t)t * (a.H >> 5));
             else
                 quant_token_row(a.xe, a.H, t, lane, a.xq_qs, a.xq_ds);
         }
@@ -1326,7 +1340,7 @@ hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x,
     hipError_t err = launch_route_tables(L, ws, x, xr, T, dbg, x_f16, stream);
     if (err != hipSuccess || !x_f16) return err;
     // the routing launch did not write x's f16 quants (only the batched router's does)
-    hipLaunchKernelGGL(k_x_f16, dim3((T + 3) / 4), dim3(256), 0, stream, x, T, L.H, ws.x_q, ws.x_d);
+    hipLaunchKernelGGL(k_x_f16, dim3((T + 3) / 4), dim3(256), 0, stream, x, T, L.H, ws.x_q, ws.x_d, ws.xq_qs, ws.xq_ds);
     return hipGetLastError();
 }
 
