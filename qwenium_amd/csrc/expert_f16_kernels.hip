@@ -57,13 +57,18 @@ typedef uint32_t u32x3 __attribute__((ext_vector_type(3), aligned(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
 
 constexpr int kTM = kMfmaTileM;             // 128 rows per tile
+constexpr int kNM = kTM / 32;               // 32-row MFMA tiles per tile
 constexpr int kKC = kF16ChunkK;             // 128 k values per LDS chunk (4 quant blocks)
 constexpr int kLd = kKC + 8;                // LDS row stride in f16 (272 bytes: conflict-free 16-byte reads)
 constexpr int kSlotsPerRow = kLd / 8;       // 17 sixteen-byte slots, the last one padding
 constexpr int kASlots = kTM * kSlotsPerRow;
 constexpr int kAHalfs = kASlots * 8;
 constexpr int kDmaIters = (kASlots + 255) / 256;
-constexpr int kSinkBytes = (kDmaIters * 256 - kASlots) * 16;  // the last round's spare lanes land here
+constexpr int kSinkBytes = 64 * 16;        // the last round's spare waves all land here
+static_assert(kASlots % 64 == 0, "a wave's staging slots are all real or all spare");
+constexpr int kScaleRounds = kTM * 4 / 256;  // scale dword slots per thread
+static_assert(kTM * 4 % 256 == 0, "scale slots");
+static_assert(kNM == 4, "the main loop instantiates 1..4 row tiles");
 constexpr int kScaleBytes = kTM * 16;       // per row and chunk: its 4 f16 block scales, twice
 constexpr int kStageBytes = kAHalfs * 2 + kScaleBytes;
 constexpr int kHLd = 64 + 4;                // gate/up epilogue: g and u rows in LDS, f32
@@ -322,10 +327,10 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
     // (dword d = blocks 2 (d & 1), + 1); lane slot sl = (row, dword) = (sl / 4,
     // sl % 4), two rounds of 64 slots per wave.  The scale MFMA's B operand is
     // zero at k >= 4, so the copy in halves 4..7 (finite) adds nothing.
-    uint32_t doff[2];
+    uint32_t doff[kScaleRounds];
 #pragma unroll
-    for (int rd = 0; rd < 2; ++rd) {
-        const int sl = wave * 128 + 64 * rd + lane;
+    for (int rd = 0; rd < kScaleRounds; ++rd) {
+        const int sl = 256 * rd + wave * 64 + lane;
         doff[rd] = s_doff[sl >> 2] + 2 * (sl & 1);
     }
     auto stage = [&](int c, int buf) {
@@ -337,15 +342,18 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
             const void* dst = s0 < kASlots ? (const void*)(st + s0 * 16) : (const void*)(s_stage + 2 * kStageBytes);
             dma_lds16(a.a_q + k0, 2u * soff[it], __builtin_amdgcn_readfirstlane(lds_addr(dst)));  // wave-uniform
         }
+        // a 2-block last chunk: the odd dwords (blocks 2, 3, past the row) reload
+        // blocks 0, 1, so every scale the MFMA multiplies (by 0 or not) is finite
+        const uint32_t back = (4 * c + 4 > nblk && (lane & 1)) ? 4u : 0u;
 #pragma unroll
-        for (int rd = 0; rd < 2; ++rd)
-            dma_lds4(a.a_d + 4 * c, 2u * doff[rd],
-                     __builtin_amdgcn_readfirstlane(lds_addr(st + kAHalfs * 2 + (wave * 128 + 64 * rd) * 4)));
+        for (int rd = 0; rd < kScaleRounds; ++rd)
+            dma_lds4(a.a_d + 4 * c, 2u * doff[rd] - back,
+                     __builtin_amdgcn_readfirstlane(lds_addr(st + kAHalfs * 2 + (256 * rd + wave * 64) * 4)));
     };
 
-    v16f acc[4];
+    v16f acc[kNM];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc[m] = v16f{};
+    for (int m = 0; m < kNM; ++m) acc[m] = v16f{};
 
     // weights one whole chunk ahead: chunk c's two pairs live in wa (c even) or
     // wb (c odd), so nothing inside a chunk waits on memory.  The second pair
@@ -421,7 +429,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
     if (!GATEUP) {
         // unweighted expert rows (lane: column out_col, rows 32 m + 8 (r / 4) + 4 kh + r % 4)
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int m = 0; m < kNM; ++m)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = 32 * m + 8 * (r >> 2) + (kh ? 4 : 0) + (r & 3);
@@ -440,7 +448,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         float* dst = wave >= 2 ? s_u : s_g;
         const int fl = 32 * (wave & 1) + col;
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int m = 0; m < kNM; ++m)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = 32 * m + 8 * (r >> 2) + (kh ? 4 : 0) + (r & 3);
@@ -448,56 +456,64 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
             }
     }
     __syncthreads();
-    // 2) one thread per (row, 32-wide f block): rows tid % 128, f block 2 y + tid / 128
-    const int row = tid & (kTM - 1), jb2 = tid >> 7;
+    // 2) one thread per (row, 32-wide f block): rows tid % kTM, f block 2 y + tid / kTM.
+    // The thread's 32 g and u values stay in LDS; h and its error estimate
+    // overwrite them there (three passes of 16-byte reads, few registers).
+    if (tid >= 2 * kTM) return;
+    const int row = tid & (kTM - 1), jb2 = tid / kTM;
     const int fb = y * 2 + jb2;  // f block of h
     const int nfb = a.F >> 5;
     if (row >= nr || fb >= nfb) return;
-    float vg[32], vu[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const f32x4 gv = *(const f32x4*)(s_g + row * kHLd + 32 * jb2 + 4 * i);
-        const f32x4 uv = *(const f32x4*)(s_u + row * kHLd + 32 * jb2 + 4 * i);
-        vg[4 * i] = gv.x; vg[4 * i + 1] = gv.y; vg[4 * i + 2] = gv.z; vg[4 * i + 3] = gv.w;
-        vu[4 * i] = uv.x; vu[4 * i + 1] = uv.y; vu[4 * i + 2] = uv.z; vu[4 * i + 3] = uv.w;
-    }
+    f32x4* pg = (f32x4*)(s_g + row * kHLd + 32 * jb2);
+    f32x4* pu = (f32x4*)(s_u + row * kHLd + 32 * jb2);
     float sg = 0.0f, su = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        sg = __builtin_fmaf(vg[i], vg[i], sg);
-        su = __builtin_fmaf(vu[i], vu[i], su);
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 g4 = pg[i], u4 = pu[i];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            sg = __builtin_fmaf(g4[k], g4[k], sg);
+            su = __builtin_fmaf(u4[k], u4[k], su);
+        }
     }
     const float rg = __builtin_sqrtf(sg * (1.0f / 32.0f)), ru = __builtin_sqrtf(su * (1.0f / 32.0f));
-    // h and its error estimate (vg[] and vu[] are overwritten with them); GeGLU:
-    // the table entry is picked by fp16(g) (and |g| >= 10 by a threshold)
-    // amax_lo, amax_hi: bounds on the exact block amax (the largest |h| - eh and |h| + eh)
+    // h and its error estimate eh; amax_lo, amax_hi: bounds on the exact block
+    // amax (the largest |h| - eh and |h| + eh)
     float amax = 0.0f, amax_lo = 0.0f, amax_hi = 0.0f;
     uint32_t unsure = 0;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float gv = vg[i], uv = vu[i];
-        const float av = act_f32(a.act, a.gelu_tab, gv);
-        const float h = av * uv;
-        const float eg = a.acc_err * fmaxf(__builtin_fabsf(gv), rg);
-        const float eu = a.acc_err * fmaxf(__builtin_fabsf(uv), ru);
-        const float ah = __builtin_fabsf(h);
-        // the activation's error: SiLU from g's error through its slope; GeGLU's
-        // table entry is exact for a settled fp16(g) (and |g| >= 10 threshold),
-        // else it may be any entry of the range, within the slope bound of it
-        float eav = kActSlope * eg;
-        if (a.act == kActGeluTanh) {
-            const float lo = gv - eg, hi = gv + eg;
-            const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
-            eav = (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
-                      ? 0.0f
-                      : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 g4 = pg[i], u4 = pu[i];
+        f32x4 h4, e4;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float gv = g4[k], uv = u4[k];
+            const float av = act_f32(a.act, a.gelu_tab, gv);
+            const float h = av * uv;
+            const float eg = a.acc_err * fmaxf(__builtin_fabsf(gv), rg);
+            const float eu = a.acc_err * fmaxf(__builtin_fabsf(uv), ru);
+            const float ah = __builtin_fabsf(h);
+            // the activation's error: SiLU from g's error through its slope; GeGLU's
+            // table entry is exact for a settled fp16(g) (and |g| >= 10 threshold),
+            // else it may be any entry of the range, within the slope bound of it
+            float eav = kActSlope * eg;
+            if (a.act == kActGeluTanh) {
+                const float lo = gv - eg, hi = gv + eg;
+                const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
+                eav = (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
+                          ? 0.0f
+                          : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
+            }
+            const float eh =
+                __builtin_fabsf(uv) * eav + __builtin_fabsf(av) * eu + kActRel * (1.0f + __builtin_fabsf(gv)) * ah;
+            h4[k] = h;
+            e4[k] = eh;
+            amax = fmaxf(amax, ah);
+            amax_lo = fmaxf(amax_lo, ah - eh);
+            amax_hi = fmaxf(amax_hi, ah + eh);
         }
-        const float eh = __builtin_fabsf(uv) * eav + __builtin_fabsf(av) * eu + kActRel * (1.0f + __builtin_fabsf(gv)) * ah;
-        vg[i] = h;
-        vu[i] = eh;
-        amax = fmaxf(amax, ah);
-        amax_lo = fmaxf(amax_lo, ah - eh);
-        amax_hi = fmaxf(amax_hi, ah + eh);
+        pg[i] = h4;
+        pu[i] = e4;
     }
     const float ea = fmaxf(amax_hi - amax, amax - amax_lo);  // error of the f32 amax
     const float d = amax / 127.0f;
@@ -505,22 +521,30 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
     // quants; a value whose t = h * 127 / amax lies within its error (amax's
     // own error included) of a rounding tie is uncertain; a value whose range
     // reaches amax_lo could be the exact largest |h|
-    uint32_t cand = 0, packed[16];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float t = vg[i] * id;
-        const float q = __builtin_rintf(t);
-        const float at = __builtin_fabsf(t);
-        const float et = (vu[i] + at * ea * (1.0f / 127.0f)) * id + at * 2.5e-7f;
-        if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << i;
-        if (__builtin_fabsf(vg[i]) + vu[i] >= amax_lo) cand |= 1u << i;
-        const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
-        packed[i >> 1] = (i & 1) ? (packed[i >> 1] | (qb << 16)) : qb;
-    }
+    uint32_t cand = 0;
     const uint64_t p = (uint64_t)(p0 + row);
     u32x4* hq = (u32x4*)(a.h_q + p * a.F + 32 * fb);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hq[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
+    for (int i = 0; i < 8; i += 2) {
+        uint32_t packed[4];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const f32x4 h4 = pg[i + ii], e4 = pu[i + ii];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int v = 4 * (i + ii) + k;
+                const float t = h4[k] * id;
+                const float q = __builtin_rintf(t);
+                const float at = __builtin_fabsf(t);
+                const float et = (e4[k] + at * ea * (1.0f / 127.0f)) * id + at * 2.5e-7f;
+                if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << v;
+                if (__builtin_fabsf(h4[k]) + e4[k] >= amax_lo) cand |= 1u << v;
+                const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
+                packed[2 * ii + (k >> 1)] = (k & 1) ? (packed[2 * ii + (k >> 1)] | (qb << 16)) : qb;
+            }
+        }
+        hq[i >> 1] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    }
     a.h_d[p * nfb + fb] = (uint16_t)f32_to_fp16(d);
     // the block's largest |h| is open when several values could be it or
     // amax / 127 is near an fp16 tie (then its candidates are uncertain values too)
@@ -532,7 +556,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         if (slot < a.fix_max) {
             f32x4* fh = (f32x4*)(a.fix_h + (uint64_t)slot * kFixStride);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) fh[i] = f32x4{vg[4 * i], vg[4 * i + 1], vg[4 * i + 2], vg[4 * i + 3]};
+            for (int i = 0; i < 8; ++i) fh[i] = pg[i];
             fh[8] = f32x4{ea, 0.0f, 0.0f, 0.0f};
             a.fix[slot] = make_int4((int)p, fb | (e << 16), (int)mask, (int)cand);
         }
