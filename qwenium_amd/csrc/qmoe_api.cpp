@@ -143,7 +143,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.topk_w = (float*)take(A * sizeof(float));
     ws.sh_gate = (float*)take((size_t)T * sizeof(float));
     ws.local_rank = (int32_t*)take(A * sizeof(int32_t));
-    ws.hist = (int32_t*)take((size_t)nblk * E * sizeof(int32_t));
+    ws.hist = (int32_t*)take((size_t)(nblk + 1) * E * sizeof(int32_t));  // + a row of per-expert totals
     ws.offsets = (int32_t*)take((size_t)(E + 2) * sizeof(int32_t));
     ws.rows = (int32_t*)take(R * sizeof(int32_t));
     ws.row_token = (int32_t*)take(R * sizeof(int32_t));

@@ -17,6 +17,7 @@ constexpr int kTopkTokensPerBlock = 16;
 constexpr int kSyncWords = 512;
 constexpr int kSyncGen = 0;
 constexpr int kSyncErr = 1;
+constexpr int kSyncScan = 2;      // the expert-count scan's finished-workgroup counter (back to 0 after each scan)
 constexpr int kSyncFlags = 64;     // flags start here (448 router blocks max)
 // Row tile of the prefill grouped GEMM (rows of one expert per tile).
 constexpr int kMfmaTileM = 128;

@@ -1103,57 +1103,60 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
 
 // Per-expert exclusive prefix of the per-block histograms (in place: hist
 // becomes each block's base inside its expert), then the expert scans.  One
-// block of 1024 threads: thread (q, e) owns a contiguous range of blocks of
-// expert e and keeps up to kScanChunk counts in registers, so each pass is
-// one round of independent loads.
-constexpr int kScanChunk = 32;
+// workgroup per 64 experts (lane = expert), its 16 waves each owning a
+// contiguous range of blocks (all of a range's loads in flight at once); the
+// workgroups publish their experts' totals (row nblk of hist, written
+// through), and the last one to finish runs the expert scans.
+constexpr int kScanPer = 16;  // blocks per wave and pass (one pass for nblk <= 256, i.e. T <= 4096)
 
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_scan(TopkArgs a) {
-    __shared__ int32_t s_part[1024];
+__global__ __launch_bounds__(1024) void k_scan(TopkArgs a, int32_t* sync) {
+    __shared__ int32_t s_part[16][64];
     __shared__ int32_t s_cnt[1024];
     __shared__ int32_t s_misc[64];
-    const int tid = threadIdx.x;
-    const int Q = min(16, 1024 / a.E);
-    const int q = tid / a.E, e = tid - q * a.E;
-    const bool mine = q < Q;
-    const int per = (a.nblk + Q - 1) / Q;
-    const int b0 = min(a.nblk, q * per), b1 = min(a.nblk, b0 + per);
-    int vals[kScanChunk];
+    __shared__ int s_last;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int e = blockIdx.x * 64 + lane;
+    const bool live = e < a.E;
+    const int per = (a.nblk + 15) / 16;
+    const int b0 = min(a.nblk, wave * per), b1 = min(a.nblk, b0 + per);
+    int32_t* col = a.hist + min(e, a.E - 1);
     int sum = 0;
-    if (mine) {
-        // 32-bit element offsets (hist holds nblk*E < 2^31 counts): cheap
-        // addresses let all of a chunk's loads issue before the first wait
-        const int32_t* col = a.hist + e;
-        for (int bb = b0; bb < b1; bb += kScanChunk) {
-            const int last = (b1 - 1) * a.E;
+    for (int bb = b0; bb < b1; bb += kScanPer) {
+        int vals[kScanPer];
 #pragma unroll
-            for (int i = 0; i < kScanChunk; ++i) vals[i] = col[min((bb + i) * a.E, last)];
+        for (int i = 0; i < kScanPer; ++i) vals[i] = col[(uint32_t)min(bb + i, b1 - 1) * (uint32_t)a.E];
 #pragma unroll
-            for (int i = 0; i < kScanChunk; ++i) sum += bb + i < b1 ? vals[i] : 0;
-        }
-        s_part[tid] = sum;
+        for (int i = 0; i < kScanPer; ++i) sum += bb + i < b1 ? vals[i] : 0;
     }
+    s_part[wave][lane] = sum;
     __syncthreads();
-    if (mine) {
-        int run = 0;
-        for (int qq = 0; qq < q; ++qq) run += s_part[qq * a.E + e];
-        if (q == Q - 1) s_cnt[e] = run + sum;
-        if (b1 - b0 <= kScanChunk) {
-            int32_t* colw = a.hist + e;
+    int run = 0;
+    for (int q = 0; q < wave; ++q) run += s_part[q][lane];
+    if (live) {
+        for (int bb = b0; bb < b1; bb += kScanPer) {
+            int vals[kScanPer];
 #pragma unroll
-            for (int i = 0; i < kScanChunk; ++i)
-                if (b0 + i < b1) {
-                    colw[(b0 + i) * a.E] = run;
+            for (int i = 0; i < kScanPer; ++i) vals[i] = col[(uint32_t)min(bb + i, b1 - 1) * (uint32_t)a.E];
+#pragma unroll
+            for (int i = 0; i < kScanPer; ++i)
+                if (bb + i < b1) {
+                    col[(uint32_t)(bb + i) * (uint32_t)a.E] = run;
                     run += vals[i];
                 }
-        } else {
-            for (int b = b0; b < b1; ++b) {
-                const int c = a.hist[(uint64_t)b * a.E + e];
-                a.hist[(uint64_t)b * a.E + e] = run;
-                run += c;
-            }
         }
+        if (wave == 15)  // written through: the last workgroup reads it
+            __hip_atomic_store(a.hist + (uint64_t)a.nblk * a.E + e, run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(sync + kSyncScan, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (int)gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(sync + kSyncScan, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = tid; i < a.E; i += 1024)
+        s_cnt[i] = __hip_atomic_load(a.hist + (uint64_t)a.nblk * a.E + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     scan_experts(a, s_cnt, nullptr, nullptr, s_misc);
 }
@@ -1329,7 +1332,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         hipLaunchKernelGGL(k_topk<false>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
         if ((err = hipGetLastError()) != hipSuccess) return err;
     }
-    hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, stream, ta);
+    hipLaunchKernelGGL(k_scan, dim3((L.E + 63) / 64), dim3(1024), 0, stream, ta, ws.sync);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL(k_scatter, dim3((T * L.K + L.S * T + 255) / 256), dim3(256), 0, stream, ta);
     return hipGetLastError();
