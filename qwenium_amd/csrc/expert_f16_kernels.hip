@@ -220,24 +220,6 @@ __device__ __forceinline__ uint32_t block_quants<kTypeQ8_0>(const RawPair<kTypeQ
     return (kh ? r.w[5] : r.w[6]) >> 16;
 }
 
-// Direct global->LDS loads (lane i's 16 or 4 bytes to LDS byte address
-// lds + 16 i or + 4 i; lds wave-uniform).  Issued as assembly so that the
-// compiler does not order every later LDS read after them: the kernel waits
-// for them itself (s_waitcnt vmcnt at the chunk boundary, then a barrier).
-// M0 takes the LDS base; the LDS-DMA read of M0 needs one wait state.
-// Source: a wave-uniform base plus this lane's 32-bit byte offset.
-__device__ __forceinline__ void dma_lds16(const void* base, uint32_t off, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma_lds4(const void* base, uint32_t off, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
 __device__ __forceinline__ v16f mfma16(v8h a, v8h b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }

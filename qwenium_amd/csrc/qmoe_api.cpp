@@ -163,6 +163,9 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.h_d = (uint16_t*)take(R * (F / 32) * sizeof(uint16_t) + 256);
     ws.x_q = (_Float16*)take((size_t)T * H * sizeof(_Float16) + 256);
     ws.x_d = (uint16_t*)take((size_t)T * (H / 32) * sizeof(uint16_t) + 256);
+    ws.rx_split = (uint16_t*)take((size_t)2 * T * H * sizeof(uint16_t));
+    ws.rw_split = (uint16_t*)take((size_t)2 * E * H * sizeof(uint16_t));
+    ws.rnorm = (float*)take((size_t)(T + E) * sizeof(float));
     ws.fix_max = (int)std::min<size_t>(R * (F / 32), (size_t)1 << 30);  // every h block, at worst
     ws.fix = (int4*)take((size_t)ws.fix_max * sizeof(int4));
     ws.fix_h = (float*)take((size_t)ws.fix_max * kFixStride * sizeof(float));

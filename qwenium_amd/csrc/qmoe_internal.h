@@ -91,6 +91,10 @@ struct Workspace {
     uint16_t* x_d = nullptr;      // [T][H/32]
     _Float16* h_q = nullptr;      // [R][F] h (aliases gubuf: the prefill path writes no (g, u))
     uint16_t* h_d = nullptr;      // [R][F/32]
+    // batched router operands: bf16 hi/lo splits of the router input and weights, row norms
+    uint16_t* rx_split = nullptr; // [2][T][H] (hi, lo)
+    uint16_t* rw_split = nullptr; // [2][E][H]
+    float* rnorm = nullptr;       // [T + E] |x_t|, |w_e|
     int4* fix = nullptr;          // [fix_max] h blocks whose rounding the f32 values do not settle
     float* fix_h = nullptr;       // [fix_max][kFixStride] their 32 f32 h values and amax's error estimate
     int fix_max = 0;

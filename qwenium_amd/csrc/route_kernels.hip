@@ -222,46 +222,164 @@ constexpr float kRouterBoundRel = 8.0e-5f;
 
 struct RouterMfmaArgs {
     const float* x;         // [T][H] router input
-    const float* xe;        // [T][H] expert input (quantized to Q8_0 here)
+    const float* xe;        // [T][H] expert input (quantized to Q8_0 by the preparation)
     const float* w;         // [E][ld]
     uint64_t ld;
     int T, H, E;
-    int n_etiles, n_tiles;  // router tiles; blocks beyond n_tiles quantize x
+    int n_etiles, n_tiles;  // router tiles
     float* logits;          // [T][E+1] approximate logits (column E untouched)
     float* bound;           // [T][E]
     int8_t* xq_qs;
     float2* xq_ds;
-    _Float16* x_q;          // non-null: the quantizing blocks also write x's f16 quants and scales
+    _Float16* x_q;          // non-null: the preparation also writes x's f16 quants and scales
     uint16_t* x_d;
+    uint16_t* rx;           // [2][T][H] bf16 hi, lo of the router input
+    uint16_t* rw;           // [2][E][H] bf16 hi, lo of the router weights
+    float* rnorm;           // [T + E]
 };
 
-__device__ __forceinline__ void split_store(const f32x4 v, __bf16* hi_dst, __bf16* lo_dst) {
-    const bf16x4 h = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
-    const bf16x4 l = {(__bf16)(v.x - (float)h.x), (__bf16)(v.y - (float)h.y), (__bf16)(v.z - (float)h.z),
-                      (__bf16)(v.w - (float)h.w)};
-    *(bf16x4*)hi_dst = h;
-    *(bf16x4*)lo_dst = l;
+// bf16 split of 8 floats (round to nearest both times): hi = bf16(v), lo = bf16(v - hi);
+// returns their sum of squares
+__device__ float split8(const f32x4 a, const f32x4 b, u32x4& hi, u32x4& lo) {
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const __bf16 h0 = (__bf16)v[2 * i], h1 = (__bf16)v[2 * i + 1];
+        const __bf16 l0 = (__bf16)(v[2 * i] - (float)h0), l1 = (__bf16)(v[2 * i + 1] - (float)h1);
+        h[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        l[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+    }
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = u32x4{l[0], l[1], l[2], l[3]};
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sq += v[i] * v[i];
+    return sq;
 }
 
-__global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
-    __shared__ __attribute__((aligned(16))) __bf16 s_xh[kRtTile * kRtLd];
-    __shared__ __attribute__((aligned(16))) __bf16 s_xl[kRtTile * kRtLd];
-    __shared__ __attribute__((aligned(16))) __bf16 s_wh[kRtTile * kRtLd];
-    __shared__ __attribute__((aligned(16))) __bf16 s_wl[kRtTile * kRtLd];
-    __shared__ float s_nx[kRtTile], s_nw[kRtTile];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if ((int)blockIdx.x >= a.n_tiles) {
-        const int t = ((int)blockIdx.x - a.n_tiles) * 4 + wave;
-        if (t < a.T) {
-            if (a.x_q)
-                quant_x_row_f16(a.xe + (uint64_t)t * a.H, a.H, lane, a.x_q + (uint64_t)t * a.H,
-                                a.x_d + (uint64_t)t * (a.H >> 5), a.xq_qs + (uint64_t)t * a.H,
-                                a.xq_ds + (uint64_t)t * (a.H >> 5));
-            else
-                quant_token_row(a.xe, a.H, t, lane, a.xq_qs, a.xq_ds);
+// The split of one row (one wave; lane l takes 8-float groups l, l + 64, ...)
+// and its f32 norm.
+__device__ __forceinline__ float split_row(const float* src, int H, int lane, uint16_t* hi, uint16_t* lo) {
+    float sq = 0.0f;
+    for (int c = lane; c < (H >> 3); c += 64) {
+        const f32x4 a = *(const f32x4*)(src + 8 * c), b = *(const f32x4*)(src + 8 * c + 4);
+        u32x4 h, l;
+        sq += split8(a, b, h, l);
+        *(u32x4*)(hi + 8 * c) = h;
+        *(u32x4*)(lo + 8 * c) = l;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    return __builtin_sqrtf(sq);
+}
+
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+// The Q8_0 of one row (as quant_x_row / quant_x_row_f16: the same quants,
+// scales and sums) with coalesced accesses: lanes 8j..8j+7 take block
+// 8 i + j, four values each, the block's amax and quant sum over the 8 lanes.
+// Writes the f16 quants when q is non-null; with hi non-null also the row's
+// bf16 hi/lo split and returns this lane's sum of squares.
+__device__ float quant_split_row(const float* xr, int H, int lane, _Float16* q, uint16_t* d, int8_t* qs, float2* ds,
+                                 uint16_t* hi, uint16_t* lo) {
+    const int nb = H >> 5;
+    const int sub = lane & 7;
+    float sq = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+        const int b = b0 + (lane >> 3);
+        const int o = 32 * b + 4 * sub;
+        const f32x4 v = *(const f32x4*)(xr + o);
+        float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)), fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+        amax = dpp8_max<kDppQuadXor1>(amax);
+        amax = dpp8_max<kDppQuadXor2>(amax);
+        amax = dpp8_max<kDppRowHalfMirror>(amax);
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        const float r0 = __builtin_rintf(v.x * id), r1 = __builtin_rintf(v.y * id), r2 = __builtin_rintf(v.z * id),
+                    r3 = __builtin_rintf(v.w * id);
+        const int i0 = (int)r0, i1 = (int)r1, i2 = (int)r2, i3 = (int)r3;
+        int sum = i0 + i1 + i2 + i3;
+        sum = dpp8_add<kDppQuadXor1>(sum);
+        sum = dpp8_add<kDppQuadXor2>(sum);
+        sum = dpp8_add<kDppRowHalfMirror>(sum);
+        if (q) {
+            const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)r0) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)r1) << 16);
+            const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)r2) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)r3) << 16);
+            *(u32x2v*)(q + o) = u32x2v{w0, w1};
+        }
+        *(uint32_t*)(qs + o) = ((uint32_t)(i0 & 0xff)) | ((uint32_t)(i1 & 0xff) << 8) | ((uint32_t)(i2 & 0xff) << 16) |
+                               ((uint32_t)(i3 & 0xff) << 24);
+        if (sub == 0) {
+            const uint32_t dh = f32_to_fp16(amax / 127.0f);
+            if (q) d[b] = (uint16_t)dh;
+            ds[b] = make_float2(fp16_to_f32(dh), __builtin_bit_cast(float, sum));
+        }
+        if (hi) {
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            uint32_t hw[2], lw[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const __bf16 h0 = (__bf16)vv[2 * i], h1 = (__bf16)vv[2 * i + 1];
+                const __bf16 l0 = (__bf16)(vv[2 * i] - (float)h0), l1 = (__bf16)(vv[2 * i + 1] - (float)h1);
+                hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            *(u32x2v*)(hi + o) = u32x2v{hw[0], hw[1]};
+            *(u32x2v*)(lo + o) = u32x2v{lw[0], lw[1]};
+            sq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    }
+    return sq;
+}
+
+// Batched-router preparation, one wave per row: blocks [0, ceil(T/4)) take
+// tokens (the experts' Q8_0 of x, the router input's split and norm), the
+// rest take router rows (split and norm).
+__global__ __launch_bounds__(256) void k_router_prep(RouterMfmaArgs a) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ntb = (a.T + 3) / 4;
+    if ((int)blockIdx.x < ntb) {
+        const int t = (int)blockIdx.x * 4 + wave;
+        if (t >= a.T) return;
+        uint16_t* hi = a.rx + (uint64_t)t * a.H;
+        uint16_t* lo = a.rx + ((uint64_t)a.T + t) * a.H;
+        const bool same = a.x == a.xe;  // one pass over the row: quants and the router operand
+        float sq = quant_split_row(a.xe + (uint64_t)t * a.H, a.H, lane, a.x_q ? a.x_q + (uint64_t)t * a.H : nullptr,
+                                   a.x_d + (uint64_t)t * (a.H >> 5), a.xq_qs + (uint64_t)t * a.H,
+                                   a.xq_ds + (uint64_t)t * (a.H >> 5), same ? hi : nullptr, same ? lo : nullptr);
+        if (same) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+            if (lane == 0) a.rnorm[t] = __builtin_sqrtf(sq);
+        } else {
+            const float n = split_row(a.x + (uint64_t)t * a.H, a.H, lane, hi, lo);
+            if (lane == 0) a.rnorm[t] = n;
         }
         return;
     }
+    const int e = ((int)blockIdx.x - ntb) * 4 + wave;
+    if (e >= a.E) return;
+    const float n = split_row(a.w + (uint64_t)e * a.ld, a.H, lane, a.rw + (uint64_t)e * a.H,
+                              a.rw + ((uint64_t)a.E + e) * a.H);
+    if (lane == 0) a.rnorm[a.T + e] = n;
+}
+
+// Router tiles of 64 tokens x 64 experts, one 32x32 MFMA tile per wave.  The
+// four split operands of each 64-wide k step are loaded straight into LDS
+// (three buffers, issued two steps ahead: a fixed 9 loads per wave and step).
+constexpr int kRtStages = 3;
+constexpr int kRtRowUnits = kRtLd / 8;                   // 16-byte units per LDS row (8 + 1 padding)
+constexpr int kRtSlots = 4 * kRtTile * kRtRowUnits;      // per stage
+constexpr int kRtDma = kRtSlots / 256;                   // loads per thread and step
+static_assert(kRtSlots % 256 == 0 && (kRtTile * kRtRowUnits) % 64 == 0, "router staging slots");
+constexpr int kRtStageHalfs = 4 * kRtTile * kRtLd;
+
+__global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    __bf16* s_op = (__bf16*)s_dyn;  // [stage][xh, xl, wh, wl][64][kRtLd]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // XCD-aware order: blocks are dealt round-robin to the 8 XCDs, so block b
     // takes logical tile (b % 8) * (n/8) + b / 8 and the expert tiles of one
     // token tile run on one XCD and share its L2.
@@ -269,50 +387,60 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
     const int g = (a.n_tiles & 7) == 0 ? (b & 7) * (a.n_tiles >> 3) + (b >> 3) : b;
     const int t0 = (g / a.n_etiles) * kRtTile;
     const int e0 = (g % a.n_etiles) * kRtTile;
-    // loader: float4 f = tid + 256 i -> tile row (tid >> 4) + 16 i, k (tid & 15) * 4
-    const int lrow = tid >> 4, lk = (tid & 15) * 4;
-    const float* xp[4];
-    const float* wp[4];
+    // this thread's staging slots: slot s = (array, row, unit); unit 8 (the
+    // padding) reloads unit 0 into a slot that is never read
+    uint32_t soff[kRtDma];       // byte offset of the slot's source from its array base (k step 0)
+    const uint16_t* sbase[kRtDma];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        xp[i] = a.x + (uint64_t)min(t0 + lrow + 16 * i, a.T - 1) * a.H + lk;
-        wp[i] = a.w + (uint64_t)min(e0 + lrow + 16 * i, a.E - 1) * a.ld + lk;
+    for (int i = 0; i < kRtDma; ++i) {
+        const int sl = i * 256 + tid;
+        const int arr = sl / (kRtTile * kRtRowUnits);
+        const int rem = sl - arr * (kRtTile * kRtRowUnits);
+        const int r = rem / kRtRowUnits, u = rem - r * kRtRowUnits;
+        const bool isx = arr < 2;
+        const int row = isx ? min(t0 + r, a.T - 1) : min(e0 + r, a.E - 1);
+        // the array is wave-uniform (576 slots per array, a multiple of 64): scalar base
+        const uint64_t base =
+            (uint64_t)(isx ? a.rx + (uint64_t)(arr & 1) * a.T * a.H : a.rw + (uint64_t)(arr & 1) * a.E * a.H);
+        sbase[i] = (const uint16_t*)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32)) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base));
+        soff[i] = (uint32_t)row * (uint32_t)a.H * 2u + (u < 8 ? 16u * u : 0u);
     }
-    f32x4 xv[4], wv[4];
+    const int nstep = a.H / kRtK;
+    auto stage = [&](int st) {
+        const int stc = min(st, nstep - 1);  // past the end: a repeat into a buffer that is not read
+        __bf16* dst = s_op + (st % kRtStages) * kRtStageHalfs;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { xv[i] = *(const f32x4*)xp[i]; wv[i] = *(const f32x4*)wp[i]; }
-    float sqx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sqw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < kRtDma; ++i) {
+            // the wave's 64 slots are contiguous in LDS: base = the first slot of the wave
+            const uint32_t lds = lds_addr(dst) + (uint32_t)(i * 256 + wave * 64) * 16u;
+            dma_lds16(sbase[i], soff[i] + (uint32_t)stc * kRtK * 2u, __builtin_amdgcn_readfirstlane(lds));
+        }
+    };
     double acc64[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc64[r] = 0.0;
     const int ms = wave & 1, ns = wave >> 1;
     const int arow = (ms * 32 + (lane & 31)) * kRtLd + (lane >> 5) * 8;
     const int brow = (ns * 32 + (lane & 31)) * kRtLd + (lane >> 5) * 8;
-    for (int k0 = 0; k0 < a.H; k0 += kRtK) {
-        __syncthreads();  // the previous step's operand reads are done
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sqx[i] += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
-            sqw[i] += wv[i].x * wv[i].x + wv[i].y * wv[i].y + wv[i].z * wv[i].z + wv[i].w * wv[i].w;
-            const int o = (lrow + 16 * i) * kRtLd + lk;
-            split_store(xv[i], s_xh + o, s_xl + o);
-            split_store(wv[i], s_wh + o, s_wl + o);
-        }
-        __syncthreads();
-        if (k0 + kRtK < a.H) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xv[i] = *(const f32x4*)(xp[i] + k0 + kRtK);
-                wv[i] = *(const f32x4*)(wp[i] + k0 + kRtK);
-            }
-        }
+    stage(0);
+    stage(1);
+    for (int st = 0; st < nstep; ++st) {
+        __builtin_amdgcn_s_waitcnt(kRtDma);  // vmcnt(step st + 1's loads): step st's have landed
+        __syncthreads();                     // ... for every wave; buffer (st + 2) % 3 (read at st - 1) is free
+        stage(st + 2);
+        const __bf16* op = s_op + (st % kRtStages) * kRtStageHalfs;
+        const __bf16* xh = op;
+        const __bf16* xl = op + kRtTile * kRtLd;
+        const __bf16* wh = op + 2 * kRtTile * kRtLd;
+        const __bf16* wl = op + 3 * kRtTile * kRtLd;
         f32x16 acc = {};
 #pragma unroll
-        for (int s = 0; s < kRtK / 16; ++s) {
-            const bf16x8 ah = *(const bf16x8*)(s_xh + arow + 16 * s);
-            const bf16x8 al = *(const bf16x8*)(s_xl + arow + 16 * s);
-            const bf16x8 bh = *(const bf16x8*)(s_wh + brow + 16 * s);
-            const bf16x8 bl = *(const bf16x8*)(s_wl + brow + 16 * s);
+        for (int s16 = 0; s16 < kRtK / 16; ++s16) {
+            const bf16x8 ah = *(const bf16x8*)(xh + arow + 16 * s16);
+            const bf16x8 al = *(const bf16x8*)(xl + arow + 16 * s16);
+            const bf16x8 bh = *(const bf16x8*)(wh + brow + 16 * s16);
+            const bf16x8 bl = *(const bf16x8*)(wl + brow + 16 * s16);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
@@ -320,31 +448,18 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc64[r] += (double)acc[r];
     }
-    // row norms: the 16 lanes of a loader row hold its partial sums
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float sx = sqx[i], sw = sqw[i];
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) {
-            sx += __shfl_xor(sx, o, 64);
-            sw += __shfl_xor(sw, o, 64);
-        }
-        if ((tid & 15) == 0) {
-            s_nx[lrow + 16 * i] = __builtin_sqrtf(sx);
-            s_nw[lrow + 16 * i] = __builtin_sqrtf(sw);
-        }
-    }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);  // the repeated loads past the end have landed
     // D[row][col]: row = 8 (r / 4) + 4 (lane / 32) + r % 4, col = lane % 32
     const int col = ns * 32 + (lane & 31);
     const int e = e0 + col;
+    const float nw = a.rnorm[a.T + min(e, a.E - 1)];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int row = ms * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int t = t0 + row;
         if (t < a.T && e < a.E) {
             const float L = (float)acc64[r];
-            const float d = kRouterBoundRel * s_nx[row] * s_nw[col] + 0x1p-21f * __builtin_fabsf(L) + 1e-30f;
+            const float d = kRouterBoundRel * a.rnorm[t] * nw + 0x1p-21f * __builtin_fabsf(L) + 1e-30f;
             a.logits[(uint64_t)t * (a.E + 1) + e] = L;
             a.bound[(uint64_t)t * a.E + e] = d;
         }
@@ -1281,8 +1396,17 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         ma.xq_ds = ws.xq_ds;
         ma.x_q = x_f16 ? ws.x_q : nullptr;
         ma.x_d = ws.x_d;
-        x_f16 = false;  // written by the router launch
-        hipLaunchKernelGGL(k_router_mfma, dim3(ma.n_tiles + (T + 3) / 4), dim3(256), 0, stream, ma);
+        ma.rx = ws.rx_split;
+        ma.rw = ws.rw_split;
+        ma.rnorm = ws.rnorm;
+        x_f16 = false;  // written by the preparation
+        hipLaunchKernelGGL(k_router_prep, dim3((T + 3) / 4 + (L.E + 3) / 4), dim3(256), 0, stream, ma);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+        const size_t lds = (size_t)kRtStages * kRtStageHalfs * 2;
+        if ((err = hipFuncSetAttribute((const void*)k_router_mfma, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds)) != hipSuccess)
+            return err;
+        hipLaunchKernelGGL(k_router_mfma, dim3(ma.n_tiles), dim3(256), lds, stream, ma);
         if ((err = hipGetLastError()) != hipSuccess) return err;
         hipLaunchKernelGGL(k_topk<true>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
         if ((err = hipGetLastError()) != hipSuccess) return err;
