@@ -109,6 +109,15 @@ def test_router_width_rules():
     assert rc == QMOE_ERR_SHAPE and '"w_router"' in msg
 
 
+@pytest.mark.parametrize("H,F,slot", [(1056, 512, '"w_router"'), (2048, 96, '"ffn_dim"')])
+def test_widths_outside_the_limits_rejected(H, F, slot):
+    """Widths the reference's Q4_0/Q8_0 rows allow (multiples of 32) but this
+    build does not: rejected before any launch, naming the slot and the limit."""
+    rc, msg = create(layer_descs(H=H, F=F), QmoeHparams(256, 8, F, 1))
+    assert rc in (QMOE_ERR_SHAPE, QMOE_ERR_VALUE)
+    assert slot in msg and "multiple of" in msg and "got" in msg
+
+
 def test_null_data_and_misaligned():
     d = layer_descs()
     d["gate"] = make_tensor(0, TYPE_Q4_0, (2048, 512, 256))
