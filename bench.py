@@ -8,7 +8,7 @@ block layout, f32 router N(0,0.02), f32 activations N(0,1)):
   decode             10 tokens, Q4_0 experts.  HBM-bound.  Steps rotate over
                      --layers distinct layers (8 x 0.45 GB by default, far above
                      the 256 MB Infinity Cache) and --batches input batches.
-  prefill            4096 tokens, Q4_0 experts.  int8-MFMA path.
+  prefill            4096 tokens, Q4_0 experts.  f16-MFMA path (exact block dots).
   skewed             2048 tokens, Q8_0 experts, Zipf(1.2)-skewed routing: ~50% of
                      assignments on 8 hot experts, ~46 experts empty.
   stack              40 consecutive layers, each x <- x + MoE(RMSNorm(x) * w):
@@ -44,6 +44,7 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_I8_PEAK_TOPS = 5000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA (the instruction the prefill GEMMs run)
 
 WORKLOADS = {
     # name: (tokens, layer spec name, default layers, default batches, default steps, warmup)
@@ -273,10 +274,10 @@ def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
     router_bytes = E * H * 4 + S * H * 4
     R = T * K + S * T
     layer_bytes = (D_mean + S) * expert_bytes + router_bytes + (3 if geglu else 2) * T * H * 4
-    ops_gu = 2.0 * R * 2 * F * H      # int8 multiply-adds x2, gate + up
+    ops_gu = 2.0 * R * 2 * F * H      # the GEMMs' multiply-adds x2 (quant x quant), gate + up
     ops_dn = 2.0 * R * H * F
     layer_ops = ops_gu + ops_dn
-    mfma_path = T >= 128               # the library's default switch to the grouped int8-MFMA GEMMs
+    mfma_path = T >= 128               # the library's default switch to the grouped f16-MFMA GEMMs
 
     log(f"warmup {warmup} steps")
     for i in range(warmup):
@@ -345,7 +346,10 @@ def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
         # the combine runs in the down kernel: events [3] and [4] are back to back
         phases = {"route": phase_us[0], "gate_up": phase_us[1], "down_combine": phase_us[2] + phase_us[3]}
     else:
-        phases = {"route": phase_us[0], "gate_up": phase_us[1], "hquant_down": phase_us[2], "combine": phase_us[3]}
+        # MFMA path: SwiGLU and the Q8_0 of h run in the gate/up kernel; the exact
+        # recomputation of uncertain h values precedes the down kernel
+        phases = {"route": phase_us[0], "gate_up": phase_us[1],
+                  ("fixup_down" if mfma_path else "hquant_down"): phase_us[2], "combine": phase_us[3]}
     log("phase us: " + ", ".join(f"{k} {v:.2f}" for k, v in phases.items()))
 
     # HBM traffic per launch of the dominant kernel, measured by rocprofv3 FETCH_SIZE /
@@ -378,8 +382,11 @@ def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
     else:
         achieved = ops_gu / (gu_us * 1e-6) / 1e12
         roofline = {
-            "bound": "mfma", "kernel": "k_expert_mfma<gate/up> (int8 MFMA grouped GEMM)",
-            "achieved": achieved, "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s", "frac": achieved / MFMA_I8_PEAK_TOPS,
+            "bound": "mfma",
+            "kernel": ("k_expert_f16<gate/up> (f16 MFMA grouped GEMM: exact integer block dots and scale "
+                       "products, f32 accumulation, SwiGLU and Q8_0 of h in the epilogue)"),
+            "achieved": achieved, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / MFMA_F16_PEAK_TFLOPS, "frac_of_int8_peak": achieved / MFMA_I8_PEAK_TOPS,
             "traffic": traffic, "ops_per_launch": ops_gu, "avg_launch_us": gu_us,
         }
     layer_us = ms_per_step * 1e3 / (L if stack else 1)
@@ -387,8 +394,9 @@ def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
         "distinct_experts_mean": D_mean, "algorithmic_bytes_per_layer": layer_bytes,
         "hbm_GBs": layer_bytes / (layer_us * 1e-6) / 1e9,
         "frac_of_hbm_peak": layer_bytes / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-        "int8_ops_per_layer": layer_ops,
-        "int8_TOPs": layer_ops / (layer_us * 1e-6) / 1e12,
+        "gemm_ops_per_layer": layer_ops,
+        "gemm_TOPs": layer_ops / (layer_us * 1e-6) / 1e12,
+        "frac_of_f16_mfma_peak": layer_ops / (layer_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS,
         "frac_of_int8_mfma_peak": layer_ops / (layer_us * 1e-6) / 1e12 / MFMA_I8_PEAK_TOPS,
         "us_per_layer": layer_us,
     }
@@ -482,7 +490,8 @@ def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": ms_per_step,
-        "dtype": f"{wname.lower()} x q8_0 int8 dot, f32 activations",
+        "dtype": (f"{wname.lower()} x q8_0 block dots on f16 MFMA (exact), f32 accumulation" if mfma_path else
+                  f"{wname.lower()} x q8_0 int8 dot (exact), f32 activations"),
         "config": {
             "workload": (f"{L} x Qwen3.6-35B-A3B MoE block (RMSNorm + MoE + residual), {T} tokens" if stack else
                          f"Gemma 4 26B-A4B GeGLU MoE layer, {workload} {T} tokens" if geglu else
