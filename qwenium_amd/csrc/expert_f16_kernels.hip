@@ -58,9 +58,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
 
 constexpr int kTM = kMfmaTileM;             // 128 rows per tile
 constexpr int kNM = kTM / 32;               // 32-row MFMA tiles per tile
-constexpr int kKC = kF16ChunkK;             // 128 k values per LDS chunk (4 quant blocks)
-constexpr int kLd = kKC + 8;                // LDS row stride in f16 (272 bytes: conflict-free 16-byte reads)
-constexpr int kSlotsPerRow = kLd / 8;       // 17 sixteen-byte slots, the last one padding
+constexpr int kKC = kF16ChunkK;             // k values per LDS chunk
+constexpr int kPPC = kKC / 64;              // quant block pairs per chunk
+static_assert(kPPC == 1 || kPPC == 2, "chunks of 64 or 128");
+constexpr int kLd = kKC + 8;                // LDS row stride in f16 (144 or 272 bytes: conflict-free 16-byte reads)
+constexpr int kSlotsPerRow = kLd / 8;       // sixteen-byte slots per row, the last one padding
 constexpr int kASlots = kTM * kSlotsPerRow;
 constexpr int kAHalfs = kASlots * 8;
 constexpr int kDmaIters = (kASlots + 255) / 256;
@@ -73,7 +75,7 @@ constexpr int kScaleBytes = kTM * 16;       // per row and chunk: its 4 f16 bloc
 constexpr int kStageBytes = kAHalfs * 2 + kScaleBytes;
 constexpr int kHLd = 64 + 4;                // gate/up epilogue: g and u rows in LDS, f32
 constexpr size_t kF16LdsBytes = 2 * (size_t)kStageBytes + kSinkBytes + kTM * 8;
-static_assert(2 * (size_t)kTM * kHLd * 4 <= 2 * (size_t)kStageBytes, "g and u rows fit the stage buffers");
+static_assert(2 * 64 * kHLd * 4 <= 2 * (size_t)kStageBytes, "an epilogue pass's g and u rows fit the stage buffers");
 // Error model of the gate/up epilogue's f32 values.  The accumulation error of
 // g (n block terms summed by fma in f32) relative to max(|g|, rms of the
 // block's g) is at most 1.2e-6 over 0.5M emulated values at n = 64; it is
@@ -235,7 +237,7 @@ __device__ __forceinline__ float act_f32(int act, const uint16_t* tab, float g) 
 }
 
 template <int WT, bool GATEUP>
-__global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
+__global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
     // [2 stages] {A quants [128][kLd] f16, block scale records [128][8] f16 (the
     // 4 scales twice)}, the sink, A row offsets [128], scale row offsets [128]
@@ -286,34 +288,35 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
     }
     constexpr uint32_t kPairBytes = 2 * BlockTraits<WT>::kBytes;
     const int npairs = nblk >> 1;
-    const int nchunk = (nblk + 3) >> 2;
+    const int nchunk = (nblk + 2 * kPPC - 1) / (2 * kPPC);
 
-    // direct global->LDS staging of chunk c.  Quants: slot s = row * 17 + unit
-    // (unit 16 is the row's padding); every wave issues exactly kDmaIters
+    // direct global->LDS staging of chunk c.  Quants: slot s = row * kSlotsPerRow
+    // + unit (the last unit is the row's padding); every wave issues exactly kDmaIters
     // unconditional loads (a count the wait counters can track): slots past
     // the buffer land in the sink, the padding unit reloads the chunk's first
     // 16 bytes of the row into a slot that is never read.  K is a multiple of
-    // 64, so a last chunk holds 2 or 4 blocks; a 2-block one reads up to 128
-    // bytes of quants and 4 bytes of scales past a row (the A buffers end in
-    // padding) into slots that are never read.  This lane's source offsets
-    // (row offset + 8 unit) are computed once.
+    // 64; with 128-wide chunks a last chunk holds 2 or 4 blocks, and a 2-block
+    // one reads up to 128 bytes of quants and 4 bytes of scales past a row (the
+    // A buffers end in padding) into slots that are never read.  This lane's
+    // source offsets (row offset + 8 unit) are computed once.
     uint32_t soff[kDmaIters];
 #pragma unroll
     for (int it = 0; it < kDmaIters; ++it) {
         const int s = min(it * 256 + wave * 64 + lane, kASlots - 1);
         const int r = s / kSlotsPerRow;
         const int u = s - r * kSlotsPerRow;
-        soff[it] = s_rowoff[r] + (u < 16 ? 8 * u : 0);
+        soff[it] = s_rowoff[r] + (u < kSlotsPerRow - 1 ? 8 * u : 0);
     }
-    // Scales: each row's 16-byte record holds the chunk's 4 block scales twice
-    // (dword d = blocks 2 (d & 1), + 1); lane slot sl = (row, dword) = (sl / 4,
-    // sl % 4), two rounds of 64 slots per wave.  The scale MFMA's B operand is
-    // zero at k >= 4, so the copy in halves 4..7 (finite) adds nothing.
+    // Scales: each row's 16-byte record holds the chunk's block scales: with
+    // 128-wide chunks its 4 scales twice (dword d = blocks 2 (d & 1), + 1), with
+    // 64-wide chunks its 2 scales four times; lane slot sl = (row, dword) =
+    // (sl / 4, sl % 4), two rounds of 64 slots per wave.  The scale MFMA's B
+    // operand is zero at k >= 2 kPPC, so the copies (finite) add nothing.
     uint32_t doff[kScaleRounds];
 #pragma unroll
     for (int rd = 0; rd < kScaleRounds; ++rd) {
         const int sl = 256 * rd + wave * 64 + lane;
-        doff[rd] = s_doff[sl >> 2] + 2 * (sl & 1);
+        doff[rd] = s_doff[sl >> 2] + (kPPC == 2 ? 2 * (sl & 1) : 0);
     }
     auto stage = [&](int c, int buf) {
         uint8_t* st = s_stage + buf * kStageBytes;
@@ -326,10 +329,10 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         }
         // a 2-block last chunk: the odd dwords (blocks 2, 3, past the row) reload
         // blocks 0, 1, so every scale the MFMA multiplies (by 0 or not) is finite
-        const uint32_t back = (4 * c + 4 > nblk && (lane & 1)) ? 4u : 0u;
+        const uint32_t back = (kPPC == 2 && 4 * c + 4 > nblk && (lane & 1)) ? 4u : 0u;
 #pragma unroll
         for (int rd = 0; rd < kScaleRounds; ++rd)
-            dma_lds4(a.a_d + 4 * c, 2u * doff[rd] - back,
+            dma_lds4(a.a_d + 2 * kPPC * c, 2u * doff[rd] - back,
                      __builtin_amdgcn_readfirstlane(lds_addr(st + kAHalfs * 2 + (256 * rd + wave * 64) * 4)));
     };
 
@@ -337,14 +340,14 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
 #pragma unroll
     for (int m = 0; m < kNM; ++m) acc[m] = v16f{};
 
-    // weights one whole chunk ahead: chunk c's two pairs live in wa (c even) or
+    // weights one whole chunk ahead: chunk c's kPPC pairs live in wa (c even) or
     // wb (c odd), so nothing inside a chunk waits on memory.  The second pair
-    // of a 2-block last chunk reloads the first (never used).
-    RawPair<WT> wa[2], wb[2];  // [pair of the chunk]
-    auto fetch = [&](int c, RawPair<WT>(&dst)[2]) {
+    // of a 2-block last 128-wide chunk reloads the first (never used).
+    RawPair<WT> wa[kPPC], wb[kPPC];  // [pair of the chunk]
+    auto fetch = [&](int c, RawPair<WT>(&dst)[kPPC]) {
 #pragma unroll
-        for (int pp = 0; pp < 2; ++pp) {
-            const int pair = min(2 * c + pp, npairs - 1);
+        for (int pp = 0; pp < kPPC; ++pp) {
+            const int pair = min(kPPC * c + pp, npairs - 1);
             dst[pp].load(wbase, woff + (uint32_t)pair * kPairBytes, kh);
         }
     };
@@ -353,7 +356,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
     // the main loop for NM row tiles with rows (a wave-uniform count)
     auto run = [&](auto nm_c) {
         constexpr int NM = decltype(nm_c)::value;
-        auto chunk = [&](int c, const RawPair<WT>(&cur)[2], RawPair<WT>(&nxt)[2]) {
+        auto chunk = [&](int c, const RawPair<WT>(&cur)[kPPC], RawPair<WT>(&nxt)[kPPC]) {
             __builtin_amdgcn_s_waitcnt(0);  // chunk c's LDS loads and weights (issued a chunk ago) have landed
             __syncthreads();                // ... for every wave; stage (c + 1) & 1 is no longer read
             if (c + 1 < nchunk) {
@@ -363,9 +366,9 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
             const uint8_t* st = s_stage + (c & 1) * kStageBytes;
             const _Float16* aq = (const _Float16*)st;
             const uint8_t* srec = st + kAHalfs * 2 + col * 16;  // this lane's row (32 m + col) scale record
-            const int np = min(2, npairs - 2 * c);
+            const int np = min(kPPC, npairs - kPPC * c);
 #pragma unroll
-            for (int pp = 0; pp < 2; ++pp) {
+            for (int pp = 0; pp < kPPC; ++pp) {
                 if (pp >= np) break;  // uniform
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
@@ -420,128 +423,134 @@ __global__ __launch_bounds__(256, 2) void k_expert_f16(F16Args a) {
         return;
     }
 
-    // gate/up epilogue.  1) g (waves 0, 1) and u (waves 2, 3) into LDS rows
-    // [128][64] each (the stage buffers are free once every wave is done)
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // gate/up epilogue, in passes of kEH rows (the g and u rows of a pass in
+    // LDS, over the stage buffers: free once every wave is done).
+    // 1) g (waves 0, 1) and u (waves 2, 3) of the pass's row tiles into LDS;
+    // 2) one thread per (row, 32-wide f block): the thread's 32 g and u values
+    //    stay in LDS, h and its error estimate overwrite them there (three
+    //    passes of 16-byte reads, few registers).
+    constexpr int kEH = 64;
     float* s_g = (float*)s_dyn;
-    float* s_u = s_g + kTM * kHLd;
-    {
-        float* dst = wave >= 2 ? s_u : s_g;
-        const int fl = 32 * (wave & 1) + col;
-#pragma unroll
-        for (int m = 0; m < kNM; ++m)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = 32 * m + 8 * (r >> 2) + (kh ? 4 : 0) + (r & 3);
-                dst[row * kHLd + fl] = acc[m][r];
-            }
-    }
-    __syncthreads();
-    // 2) one thread per (row, 32-wide f block): rows tid % kTM, f block 2 y + tid / kTM.
-    // The thread's 32 g and u values stay in LDS; h and its error estimate
-    // overwrite them there (three passes of 16-byte reads, few registers).
-    if (tid >= 2 * kTM) return;
-    const int row = tid & (kTM - 1), jb2 = tid / kTM;
-    const int fb = y * 2 + jb2;  // f block of h
+    float* s_u = s_g + kEH * kHLd;
     const int nfb = a.F >> 5;
-    if (row >= nr || fb >= nfb) return;
-    f32x4* pg = (f32x4*)(s_g + row * kHLd + 32 * jb2);
-    f32x4* pu = (f32x4*)(s_u + row * kHLd + 32 * jb2);
-    float sg = 0.0f, su = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const f32x4 g4 = pg[i], u4 = pu[i];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            sg = __builtin_fmaf(g4[k], g4[k], sg);
-            su = __builtin_fmaf(u4[k], u4[k], su);
-        }
-    }
-    const float rg = __builtin_sqrtf(sg * (1.0f / 32.0f)), ru = __builtin_sqrtf(su * (1.0f / 32.0f));
-    // h and its error estimate eh; amax_lo, amax_hi: bounds on the exact block
-    // amax (the largest |h| - eh and |h| + eh)
-    float amax = 0.0f, amax_lo = 0.0f, amax_hi = 0.0f;
-    uint32_t unsure = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const f32x4 g4 = pg[i], u4 = pu[i];
-        f32x4 h4, e4;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float gv = g4[k], uv = u4[k];
-            const float av = act_f32(a.act, a.gelu_tab, gv);
-            const float h = av * uv;
-            const float eg = a.acc_err * fmaxf(__builtin_fabsf(gv), rg);
-            const float eu = a.acc_err * fmaxf(__builtin_fabsf(uv), ru);
-            const float ah = __builtin_fabsf(h);
-            // the activation's error: SiLU from g's error through its slope; GeGLU's
-            // table entry is exact for a settled fp16(g) (and |g| >= 10 threshold),
-            // else it may be any entry of the range, within the slope bound of it
-            float eav = kActSlope * eg;
-            if (a.act == kActGeluTanh) {
-                const float lo = gv - eg, hi = gv + eg;
-                const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
-                eav = (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
-                          ? 0.0f
-                          : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
-            }
-            const float eh =
-                __builtin_fabsf(uv) * eav + __builtin_fabsf(av) * eu + kActRel * (1.0f + __builtin_fabsf(gv)) * ah;
-            h4[k] = h;
-            e4[k] = eh;
-            amax = fmaxf(amax, ah);
-            amax_lo = fmaxf(amax_lo, ah - eh);
-            amax_hi = fmaxf(amax_hi, ah + eh);
-        }
-        pg[i] = h4;
-        pu[i] = e4;
-    }
-    const float ea = fmaxf(amax_hi - amax, amax - amax_lo);  // error of the f32 amax
-    const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    // quants; a value whose t = h * 127 / amax lies within its error (amax's
-    // own error included) of a rounding tie is uncertain; a value whose range
-    // reaches amax_lo could be the exact largest |h|
-    uint32_t cand = 0;
-    const uint64_t p = (uint64_t)(p0 + row);
-    u32x4* hq = (u32x4*)(a.h_q + p * a.F + 32 * fb);
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-        uint32_t packed[4];
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-            const f32x4 h4 = pg[i + ii], e4 = pu[i + ii];
-#pragma unroll
+    auto epi = [&](int row, int lrow, int jb2) {
+        const int fb = y * 2 + jb2;  // f block of h
+        if (row >= nr || fb >= nfb) return;
+        f32x4* pg = (f32x4*)(s_g + lrow * kHLd + 32 * jb2);
+        f32x4* pu = (f32x4*)(s_u + lrow * kHLd + 32 * jb2);
+        float sg = 0.0f, su = 0.0f;
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const f32x4 g4 = pg[i], u4 = pu[i];
+    #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const int v = 4 * (i + ii) + k;
-                const float t = h4[k] * id;
-                const float q = __builtin_rintf(t);
-                const float at = __builtin_fabsf(t);
-                const float et = (e4[k] + at * ea * (1.0f / 127.0f)) * id + at * 2.5e-7f;
-                if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << v;
-                if (__builtin_fabsf(h4[k]) + e4[k] >= amax_lo) cand |= 1u << v;
-                const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
-                packed[2 * ii + (k >> 1)] = (k & 1) ? (packed[2 * ii + (k >> 1)] | (qb << 16)) : qb;
+                sg = __builtin_fmaf(g4[k], g4[k], sg);
+                su = __builtin_fmaf(u4[k], u4[k], su);
             }
         }
-        hq[i >> 1] = u32x4{packed[0], packed[1], packed[2], packed[3]};
-    }
-    a.h_d[p * nfb + fb] = (uint16_t)f32_to_fp16(d);
-    // the block's largest |h| is open when several values could be it or
-    // amax / 127 is near an fp16 tie (then its candidates are uncertain values too)
-    const bool amax_open = __builtin_popcount(cand) > 1 ||
-                           f32_to_fp16(amax_lo / 127.0f) != f32_to_fp16(amax_hi / 127.0f);
-    const uint32_t mask = unsure | (amax_open ? cand : 0u);
-    if (mask) {
-        const int slot = atomicAdd(a.fix_count, 1);
-        if (slot < a.fix_max) {
-            f32x4* fh = (f32x4*)(a.fix_h + (uint64_t)slot * kFixStride);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) fh[i] = pg[i];
-            fh[8] = f32x4{ea, 0.0f, 0.0f, 0.0f};
-            a.fix[slot] = make_int4((int)p, fb | (e << 16), (int)mask, (int)cand);
+        const float rg = __builtin_sqrtf(sg * (1.0f / 32.0f)), ru = __builtin_sqrtf(su * (1.0f / 32.0f));
+        // h and its error estimate eh; amax_lo, amax_hi: bounds on the exact block
+        // amax (the largest |h| - eh and |h| + eh)
+        float amax = 0.0f, amax_lo = 0.0f, amax_hi = 0.0f;
+        uint32_t unsure = 0;
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const f32x4 g4 = pg[i], u4 = pu[i];
+            f32x4 h4, e4;
+    #pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float gv = g4[k], uv = u4[k];
+                const float av = act_f32(a.act, a.gelu_tab, gv);
+                const float h = av * uv;
+                const float eg = a.acc_err * fmaxf(__builtin_fabsf(gv), rg);
+                const float eu = a.acc_err * fmaxf(__builtin_fabsf(uv), ru);
+                const float ah = __builtin_fabsf(h);
+                // the activation's error: SiLU from g's error through its slope; GeGLU's
+                // table entry is exact for a settled fp16(g) (and |g| >= 10 threshold),
+                // else it may be any entry of the range, within the slope bound of it
+                float eav = kActSlope * eg;
+                if (a.act == kActGeluTanh) {
+                    const float lo = gv - eg, hi = gv + eg;
+                    const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
+                    eav = (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
+                              ? 0.0f
+                              : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
+                }
+                const float eh =
+                    __builtin_fabsf(uv) * eav + __builtin_fabsf(av) * eu + kActRel * (1.0f + __builtin_fabsf(gv)) * ah;
+                h4[k] = h;
+                e4[k] = eh;
+                amax = fmaxf(amax, ah);
+                amax_lo = fmaxf(amax_lo, ah - eh);
+                amax_hi = fmaxf(amax_hi, ah + eh);
+            }
+            pg[i] = h4;
+            pu[i] = e4;
         }
+        const float ea = fmaxf(amax_hi - amax, amax - amax_lo);  // error of the f32 amax
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        // quants; a value whose t = h * 127 / amax lies within its error (amax's
+        // own error included) of a rounding tie is uncertain; a value whose range
+        // reaches amax_lo could be the exact largest |h|
+        uint32_t cand = 0;
+        const uint64_t p = (uint64_t)(p0 + row);
+        u32x4* hq = (u32x4*)(a.h_q + p * a.F + 32 * fb);
+    #pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            uint32_t packed[4];
+    #pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                const f32x4 h4 = pg[i + ii], e4 = pu[i + ii];
+    #pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int v = 4 * (i + ii) + k;
+                    const float t = h4[k] * id;
+                    const float q = __builtin_rintf(t);
+                    const float at = __builtin_fabsf(t);
+                    const float et = (e4[k] + at * ea * (1.0f / 127.0f)) * id + at * 2.5e-7f;
+                    if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << v;
+                    if (__builtin_fabsf(h4[k]) + e4[k] >= amax_lo) cand |= 1u << v;
+                    const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
+                    packed[2 * ii + (k >> 1)] = (k & 1) ? (packed[2 * ii + (k >> 1)] | (qb << 16)) : qb;
+                }
+            }
+            hq[i >> 1] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+        }
+        a.h_d[p * nfb + fb] = (uint16_t)f32_to_fp16(d);
+        // the block's largest |h| is open when several values could be it or
+        // amax / 127 is near an fp16 tie (then its candidates are uncertain values too)
+        const bool amax_open = __builtin_popcount(cand) > 1 ||
+                               f32_to_fp16(amax_lo / 127.0f) != f32_to_fp16(amax_hi / 127.0f);
+        const uint32_t mask = unsure | (amax_open ? cand : 0u);
+        if (mask) {
+            const int slot = atomicAdd(a.fix_count, 1);
+            if (slot < a.fix_max) {
+                f32x4* fh = (f32x4*)(a.fix_h + (uint64_t)slot * kFixStride);
+    #pragma unroll
+                for (int i = 0; i < 8; ++i) fh[i] = pg[i];
+                fh[8] = f32x4{ea, 0.0f, 0.0f, 0.0f};
+                a.fix[slot] = make_int4((int)p, fb | (e << 16), (int)mask, (int)cand);
+            }
+        }
+    };
+#pragma unroll
+    for (int half = 0; half < kTM / kEH; ++half) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        {
+            float* dst = wave >= 2 ? s_u : s_g;
+            const int fl = 32 * (wave & 1) + col;
+#pragma unroll
+            for (int mm = 0; mm < kEH / 32; ++mm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int lrow = 32 * mm + 8 * (r >> 2) + (kh ? 4 : 0) + (r & 3);
+                    dst[lrow * kHLd + fl] = acc[half * (kEH / 32) + mm][r];
+                }
+        }
+        __syncthreads();
+        if (tid < 2 * kEH) epi(half * kEH + (tid & (kEH - 1)), tid & (kEH - 1), tid / kEH);
     }
 }
 

@@ -22,7 +22,7 @@ constexpr int kSyncFlags = 64;     // flags start here (448 router blocks max)
 // Row tile of the prefill grouped GEMM (rows of one expert per tile).
 constexpr int kMfmaTileM = 128;
 // k values per LDS chunk of the prefill GEMMs.
-constexpr int kF16ChunkK = 128;
+constexpr int kF16ChunkK = 64;
 // Workspace counters: [0] active slots, [1] tiles, [kCounterFix] listed h blocks.
 constexpr int kCounterFix = 4;
 constexpr int kFixStride = 36;  // floats per listed h block: 32 values, amax's error estimate, padding
