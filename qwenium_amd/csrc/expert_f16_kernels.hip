@@ -80,11 +80,12 @@ static_assert(2 * 64 * kHLd * 4 <= 2 * (size_t)kStageBytes, "an epilogue pass's 
 // g (n block terms summed by fma in f32) relative to max(|g|, rms of the
 // block's g) is at most 1.2e-6 over 0.5M emulated values at n = 64; it is
 // charged as kAccErr * sqrt(n) (3e-6 at n = 64).  The activation's slope is
-// below kActSlope (SiLU 1.10, GELU 1.13); the f32 SiLU and product are within
-// kActRel * (1 + |g|) * |h| of the exact ones.
+// below kActSlope (SiLU 1.10, GELU 1.13); the f32 SiLU (within 3.6e-7 (1 + |g|)
+// relative) and the product (half an ulp) are within kActRel * (1 + |g|) * |h|
+// of the exact ones.
 constexpr float kAccErr = 3.75e-7f;
 constexpr float kActSlope = 1.13f;
-constexpr float kActRel = 2.5e-7f;
+constexpr float kActRel = 4.5e-7f;
 
 struct F16Args {
     int H, F, E;
@@ -227,16 +228,19 @@ __device__ __forceinline__ v16f mfma16(v8h a, v8h b, v16f c) {
 }
 
 // silu(g) (moe.cpp:117) or ggml's tabled gelu(g) (gemma4.cpp:423) in f32.
-__device__ __forceinline__ float act_f32(int act, const uint16_t* tab, float g) {
-    if (act == kActGeluTanh) {
+// SiLU: exp (argument error |g| 6e-8 relative, 1 ulp), 1 + e, a 1-ulp
+// reciprocal and the product: within 3.6e-7 (1 + |g|) of silu(g) relative.
+template <int ACT>
+__device__ __forceinline__ float act_f32(const uint16_t* tab, float g) {
+    if (ACT == kActGeluTanh) {
         if (g <= -10.0f) return 0.0f;
         if (g >= 10.0f) return g;
         return fp16_to_f32(tab[f32_to_fp16(g) & 0xffffu]);
     }
-    return g / (1.0f + __expf(-g));
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
-template <int WT, bool GATEUP>
+template <int WT, bool GATEUP, int ACT>
 __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
     // [2 stages] {A quants [128][kLd] f16, block scale records [128][8] f16 (the
@@ -449,10 +453,9 @@ __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
             }
         }
         const float rg = __builtin_sqrtf(sg * (1.0f / 32.0f)), ru = __builtin_sqrtf(su * (1.0f / 32.0f));
-        // h and its error estimate eh; amax_lo, amax_hi: bounds on the exact block
-        // amax (the largest |h| - eh and |h| + eh)
-        float amax = 0.0f, amax_lo = 0.0f, amax_hi = 0.0f;
-        uint32_t unsure = 0;
+        // h and its error bound eh (over g and u in LDS); the exact block amax
+        // lies within amax +- emax (emax: the block's largest eh)
+        float amax = 0.0f, emax = 0.0f;
     #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const f32x4 g4 = pg[i], u4 = pu[i];
@@ -460,40 +463,48 @@ __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
     #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float gv = g4[k], uv = u4[k];
-                const float av = act_f32(a.act, a.gelu_tab, gv);
+                const float ag = __builtin_fabsf(gv), au = __builtin_fabsf(uv);
+                const float av = act_f32<ACT>(a.gelu_tab, gv);
                 const float h = av * uv;
-                const float eg = a.acc_err * fmaxf(__builtin_fabsf(gv), rg);
-                const float eu = a.acc_err * fmaxf(__builtin_fabsf(uv), ru);
                 const float ah = __builtin_fabsf(h);
-                // the activation's error: SiLU from g's error through its slope; GeGLU's
-                // table entry is exact for a settled fp16(g) (and |g| >= 10 threshold),
-                // else it may be any entry of the range, within the slope bound of it
-                float eav = kActSlope * eg;
-                if (a.act == kActGeluTanh) {
+                // g and u are within eg = acc_err max(|g|, rg) and eu = acc_err
+                // max(|u|, ru); the activation's error: SiLU's from g's error through
+                // its slope; GeGLU's table entry is exact for a settled fp16(g) (and
+                // |g| >= 10 threshold), else it may be any entry of the range, within
+                // the slope bound of it
+                float eh;
+                if (ACT == kActGeluTanh) {
+                    const float eg = a.acc_err * fmaxf(ag, rg);
                     const float lo = gv - eg, hi = gv + eg;
                     const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
-                    eav = (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
-                              ? 0.0f
-                              : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
+                    const float eav =
+                        (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
+                            ? 0.0f
+                            : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
+                    eh = au * eav + __builtin_fabsf(av) * (a.acc_err * fmaxf(au, ru));
+                } else {
+                    // |u| kActSlope eg + |av| eu
+                    eh = a.acc_err * __builtin_fmaf(kActSlope * au, fmaxf(ag, rg), __builtin_fabsf(av) * fmaxf(au, ru));
                 }
-                const float eh =
-                    __builtin_fabsf(uv) * eav + __builtin_fabsf(av) * eu + kActRel * (1.0f + __builtin_fabsf(gv)) * ah;
+                eh = __builtin_fmaf(kActRel, __builtin_fmaf(ag, ah, ah), eh);
                 h4[k] = h;
                 e4[k] = eh;
                 amax = fmaxf(amax, ah);
-                amax_lo = fmaxf(amax_lo, ah - eh);
-                amax_hi = fmaxf(amax_hi, ah + eh);
+                emax = fmaxf(emax, eh);
             }
             pg[i] = h4;
             pu[i] = e4;
         }
-        const float ea = fmaxf(amax_hi - amax, amax - amax_lo);  // error of the f32 amax
+        const float ea = emax;  // error bound of the f32 amax
+        const float amax_lo = amax - ea;
         const float d = amax / 127.0f;
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-        // quants; a value whose t = h * 127 / amax lies within its error (amax's
-        // own error included) of a rounding tie is uncertain; a value whose range
-        // reaches amax_lo could be the exact largest |h|
-        uint32_t cand = 0;
+        // t = h * 127 / amax is within et = eh id + |t| (ea id / 127 + 2.5e-7) of
+        // the exact one (amax's own error and the product's rounding included)
+        const float c1 = __builtin_fmaf(ea * id, 1.0f / 127.0f, 2.5e-7f);
+        // quants; a value whose t lies within et of a rounding tie is uncertain;
+        // a value whose range reaches amax_lo could be the exact largest |h|
+        uint32_t unsure = 0, cand = 0;
         const uint64_t p = (uint64_t)(p0 + row);
         u32x4* hq = (u32x4*)(a.h_q + p * a.F + 32 * fb);
     #pragma unroll
@@ -507,8 +518,7 @@ __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
                     const int v = 4 * (i + ii) + k;
                     const float t = h4[k] * id;
                     const float q = __builtin_rintf(t);
-                    const float at = __builtin_fabsf(t);
-                    const float et = (e4[k] + at * ea * (1.0f / 127.0f)) * id + at * 2.5e-7f;
+                    const float et = __builtin_fmaf(e4[k], id, __builtin_fabsf(t) * c1);
                     if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << v;
                     if (__builtin_fabsf(h4[k]) + e4[k] >= amax_lo) cand |= 1u << v;
                     const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
@@ -521,7 +531,7 @@ __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
         // the block's largest |h| is open when several values could be it or
         // amax / 127 is near an fp16 tie (then its candidates are uncertain values too)
         const bool amax_open = __builtin_popcount(cand) > 1 ||
-                               f32_to_fp16(amax_lo / 127.0f) != f32_to_fp16(amax_hi / 127.0f);
+                               f32_to_fp16(amax_lo / 127.0f) != f32_to_fp16((amax + ea) / 127.0f);
         const uint32_t mask = unsure | (amax_open ? cand : 0u);
         if (mask) {
             const int slot = atomicAdd(a.fix_count, 1);
@@ -721,8 +731,13 @@ hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hi
     hipError_t err = launch_fill_i32(ws.counters + kCounterFix, 1, 0, stream);
     if (err != hipSuccess) return err;
     const dim3 grid(8 * ((f16_max_tiles(L, ws, T) + 7) / 8) * a.n_y);
-    err = L.gu_type == kTypeQ4_0 ? launch_f16(k_expert_f16<kTypeQ4_0, true>, grid, stream, ev_start, ev_stop, a)
-                                 : launch_f16(k_expert_f16<kTypeQ8_0, true>, grid, stream, ev_start, ev_stop, a);
+    const bool gelu = L.act == kActGeluTanh;
+    if (L.gu_type == kTypeQ4_0)
+        err = gelu ? launch_f16(k_expert_f16<kTypeQ4_0, true, kActGeluTanh>, grid, stream, ev_start, ev_stop, a)
+                   : launch_f16(k_expert_f16<kTypeQ4_0, true, kActSilu>, grid, stream, ev_start, ev_stop, a);
+    else
+        err = gelu ? launch_f16(k_expert_f16<kTypeQ8_0, true, kActGeluTanh>, grid, stream, ev_start, ev_stop, a)
+                   : launch_f16(k_expert_f16<kTypeQ8_0, true, kActSilu>, grid, stream, ev_start, ev_stop, a);
     if (err != hipSuccess) return err;
     FixArgs f{};
     f.H = L.H; f.F = L.F; f.E = L.E;
@@ -750,8 +765,8 @@ hipError_t launch_down_mfma(const LayerDesc& L, const Workspace& ws, int T, hipS
     a.K = L.F;
     a.n_y = L.H / 128;
     const dim3 grid(8 * ((f16_max_tiles(L, ws, T) + 7) / 8) * a.n_y);
-    return L.dn_type == kTypeQ4_0 ? launch_f16(k_expert_f16<kTypeQ4_0, false>, grid, stream, nullptr, nullptr, a)
-                                  : launch_f16(k_expert_f16<kTypeQ8_0, false>, grid, stream, nullptr, nullptr, a);
+    return L.dn_type == kTypeQ4_0 ? launch_f16(k_expert_f16<kTypeQ4_0, false, kActSilu>, grid, stream, nullptr, nullptr, a)
+                                  : launch_f16(k_expert_f16<kTypeQ8_0, false, kActSilu>, grid, stream, nullptr, nullptr, a);
 }
 
 }  // namespace qmoe
