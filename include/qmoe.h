@@ -45,8 +45,8 @@ enum qmoe_status {
     QMOE_ERR_VALUE    = 4,  /* bad hparam / argument value */
     QMOE_ERR_CAPACITY = 5,  /* n_tokens above the workspace capacity */
     QMOE_ERR_HIP      = 6,  /* a HIP runtime call failed */
-    QMOE_ERR_SYNC     = 7   /* an earlier forward on the workspace gave up a bounded
-                               cross-block wait; qmoe_workspace_check clears it */
+    QMOE_ERR_SYNC     = 7   /* reserved: no kernel waits on another workgroup, so
+                               no forward returns it */
 };
 
 /* A borrowed ggml tensor view: device data + ggml type + ne/nb (ne[0] contiguous).
@@ -119,14 +119,11 @@ int qmoe_layer_n_embd(const qmoe_layer* layer);
 int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_workspace** out);
 int qmoe_workspace_destroy(qmoe_workspace* ws);
 int32_t qmoe_workspace_capacity(const qmoe_workspace* ws);
-/* Synchronizes the device and reports, in *fault, whether any forward on this
- * workspace gave up a bounded cross-block wait (1) or not (0); clears the
- * word and restarts the workspace's signalling area.  A give-up is loud
- * without this call: the forward that gave up, and every forward queued on the
- * workspace behind it, writes NaN outputs, and every qmoe_layer_forward* call
- * on the workspace returns QMOE_ERR_SYNC (read from host-mapped memory, no
- * synchronisation) until this call clears it.  No counterpart in the
- * reference (ggml runs ops one after another). */
+/* Synchronizes the device (a device error surfaces as QMOE_ERR_HIP) and
+ * reports, in *fault, whether a forward on this workspace failed a
+ * cross-workgroup wait: always 0, since no kernel waits on another workgroup
+ * (every dependency is a launch boundary or a last-workgroup counter).  No
+ * counterpart in the reference (ggml runs ops one after another). */
 int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault);
 
 /* Replaces MoELayer::build (moe.h:58-63, moe.cpp:55-177):
@@ -154,9 +151,7 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
  * scratch exceeds the maximum (at the 35B-A3B shape: above about 100 tokens)
  * fail with QMOE_ERR_CAPACITY.  Every call on one GPU shares that GPU's
  * array: calls that overlap in time on one GPU (other streams, other threads)
- * race and must not be issued; calls ordered on one stream are fine.  A
- * decode routing wait that gives up is reported by NaN outputs only (there is
- * no workspace to check). */
+ * race and must not be issued; calls ordered on one stream are fine. */
 #define QMOE_STATIC_SCRATCH_BYTES (16u << 20)
 int qmoe_layer_forward_static(qmoe_layer* layer, const float* x, int32_t n_tokens, float* y,
                               const float* residual, void* hip_stream);

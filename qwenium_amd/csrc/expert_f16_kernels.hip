@@ -240,6 +240,115 @@ __device__ __forceinline__ float act_f32(const uint16_t* tab, float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
+// One 32-wide block of h from its 32 g and u values in LDS (pg, pu; h and its
+// error bound overwrite them): the Q8_0 of h into h_q / h_d, and the block into
+// the fixup list when a quant (or the amax) is not settled by the error bound.
+// Row p of the tile lists, f block fb, expert e.
+template <int ACT>
+__device__ __forceinline__ void h_block(const F16Args& a, f32x4* pg, f32x4* pu, uint64_t p, int fb, int e) {
+    const int nfb = a.F >> 5;
+    float sg = 0.0f, su = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 g4 = pg[i], u4 = pu[i];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            sg = __builtin_fmaf(g4[k], g4[k], sg);
+            su = __builtin_fmaf(u4[k], u4[k], su);
+        }
+    }
+    const float rg = __builtin_sqrtf(sg * (1.0f / 32.0f)), ru = __builtin_sqrtf(su * (1.0f / 32.0f));
+    // h and its error bound eh (over g and u in LDS); the exact block amax
+    // lies within amax +- emax (emax: the block's largest eh)
+    float amax = 0.0f, emax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 g4 = pg[i], u4 = pu[i];
+        f32x4 h4, e4;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float gv = g4[k], uv = u4[k];
+            const float ag = __builtin_fabsf(gv), au = __builtin_fabsf(uv);
+            const float av = act_f32<ACT>(a.gelu_tab, gv);
+            const float h = av * uv;
+            const float ah = __builtin_fabsf(h);
+            // g and u are within eg = acc_err max(|g|, rg) and eu = acc_err
+            // max(|u|, ru); the activation's error: SiLU's from g's error through
+            // its slope; GeGLU's table entry is exact for a settled fp16(g) (and
+            // |g| >= 10 threshold), else it may be any entry of the range, within
+            // the slope bound of it
+            float eh;
+            if (ACT == kActGeluTanh) {
+                const float eg = a.acc_err * fmaxf(ag, rg);
+                const float lo = gv - eg, hi = gv + eg;
+                const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
+                const float eav =
+                    (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
+                        ? 0.0f
+                        : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
+                eh = au * eav + __builtin_fabsf(av) * (a.acc_err * fmaxf(au, ru));
+            } else {
+                // |u| kActSlope eg + |av| eu
+                eh = a.acc_err * __builtin_fmaf(kActSlope * au, fmaxf(ag, rg), __builtin_fabsf(av) * fmaxf(au, ru));
+            }
+            eh = __builtin_fmaf(kActRel, __builtin_fmaf(ag, ah, ah), eh);
+            h4[k] = h;
+            e4[k] = eh;
+            amax = fmaxf(amax, ah);
+            emax = fmaxf(emax, eh);
+        }
+        pg[i] = h4;
+        pu[i] = e4;
+    }
+    const float ea = emax;  // error bound of the f32 amax
+    const float amax_lo = amax - ea;
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    // t = h * 127 / amax is within et = eh id + |t| (ea id / 127 + 2.5e-7) of
+    // the exact one (amax's own error and the product's rounding included)
+    const float c1 = __builtin_fmaf(ea * id, 1.0f / 127.0f, 2.5e-7f);
+    // quants; a value whose t lies within et of a rounding tie is uncertain;
+    // a value whose range reaches amax_lo could be the exact largest |h|
+    uint32_t unsure = 0, cand = 0;
+    u32x4* hq = (u32x4*)(a.h_q + p * a.F + 32 * fb);
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        uint32_t packed[4];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const f32x4 h4 = pg[i + ii], e4 = pu[i + ii];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int v = 4 * (i + ii) + k;
+                const float t = h4[k] * id;
+                const float q = __builtin_rintf(t);
+                const float et = __builtin_fmaf(e4[k], id, __builtin_fabsf(t) * c1);
+                if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << v;
+                if (__builtin_fabsf(h4[k]) + e4[k] >= amax_lo) cand |= 1u << v;
+                const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
+                packed[2 * ii + (k >> 1)] = (k & 1) ? (packed[2 * ii + (k >> 1)] | (qb << 16)) : qb;
+            }
+        }
+        hq[i >> 1] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    }
+    a.h_d[p * nfb + fb] = (uint16_t)f32_to_fp16(d);
+    // the block's largest |h| is open when several values could be it or
+    // amax / 127 is near an fp16 tie (then its candidates are uncertain values too)
+    const bool amax_open = __builtin_popcount(cand) > 1 ||
+                           f32_to_fp16(amax_lo / 127.0f) != f32_to_fp16((amax + ea) / 127.0f);
+    const uint32_t mask = unsure | (amax_open ? cand : 0u);
+    if (mask) {
+        const int slot = atomicAdd(a.fix_count, 1);
+        if (slot < a.fix_max) {
+            f32x4* fh = (f32x4*)(a.fix_h + (uint64_t)slot * kFixStride);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) fh[i] = pg[i];
+            fh[8] = f32x4{ea, 0.0f, 0.0f, 0.0f};
+            a.fix[slot] = make_int4((int)p, fb | (e << 16), (int)mask, (int)cand);
+        }
+    }
+}
+
 template <int WT, bool GATEUP, int ACT>
 __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
@@ -440,109 +549,8 @@ __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
     auto epi = [&](int row, int lrow, int jb2) {
         const int fb = y * 2 + jb2;  // f block of h
         if (row >= nr || fb >= nfb) return;
-        f32x4* pg = (f32x4*)(s_g + lrow * kHLd + 32 * jb2);
-        f32x4* pu = (f32x4*)(s_u + lrow * kHLd + 32 * jb2);
-        float sg = 0.0f, su = 0.0f;
-    #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const f32x4 g4 = pg[i], u4 = pu[i];
-    #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                sg = __builtin_fmaf(g4[k], g4[k], sg);
-                su = __builtin_fmaf(u4[k], u4[k], su);
-            }
-        }
-        const float rg = __builtin_sqrtf(sg * (1.0f / 32.0f)), ru = __builtin_sqrtf(su * (1.0f / 32.0f));
-        // h and its error bound eh (over g and u in LDS); the exact block amax
-        // lies within amax +- emax (emax: the block's largest eh)
-        float amax = 0.0f, emax = 0.0f;
-    #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const f32x4 g4 = pg[i], u4 = pu[i];
-            f32x4 h4, e4;
-    #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float gv = g4[k], uv = u4[k];
-                const float ag = __builtin_fabsf(gv), au = __builtin_fabsf(uv);
-                const float av = act_f32<ACT>(a.gelu_tab, gv);
-                const float h = av * uv;
-                const float ah = __builtin_fabsf(h);
-                // g and u are within eg = acc_err max(|g|, rg) and eu = acc_err
-                // max(|u|, ru); the activation's error: SiLU's from g's error through
-                // its slope; GeGLU's table entry is exact for a settled fp16(g) (and
-                // |g| >= 10 threshold), else it may be any entry of the range, within
-                // the slope bound of it
-                float eh;
-                if (ACT == kActGeluTanh) {
-                    const float eg = a.acc_err * fmaxf(ag, rg);
-                    const float lo = gv - eg, hi = gv + eg;
-                    const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
-                    const float eav =
-                        (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
-                            ? 0.0f
-                            : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
-                    eh = au * eav + __builtin_fabsf(av) * (a.acc_err * fmaxf(au, ru));
-                } else {
-                    // |u| kActSlope eg + |av| eu
-                    eh = a.acc_err * __builtin_fmaf(kActSlope * au, fmaxf(ag, rg), __builtin_fabsf(av) * fmaxf(au, ru));
-                }
-                eh = __builtin_fmaf(kActRel, __builtin_fmaf(ag, ah, ah), eh);
-                h4[k] = h;
-                e4[k] = eh;
-                amax = fmaxf(amax, ah);
-                emax = fmaxf(emax, eh);
-            }
-            pg[i] = h4;
-            pu[i] = e4;
-        }
-        const float ea = emax;  // error bound of the f32 amax
-        const float amax_lo = amax - ea;
-        const float d = amax / 127.0f;
-        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-        // t = h * 127 / amax is within et = eh id + |t| (ea id / 127 + 2.5e-7) of
-        // the exact one (amax's own error and the product's rounding included)
-        const float c1 = __builtin_fmaf(ea * id, 1.0f / 127.0f, 2.5e-7f);
-        // quants; a value whose t lies within et of a rounding tie is uncertain;
-        // a value whose range reaches amax_lo could be the exact largest |h|
-        uint32_t unsure = 0, cand = 0;
-        const uint64_t p = (uint64_t)(p0 + row);
-        u32x4* hq = (u32x4*)(a.h_q + p * a.F + 32 * fb);
-    #pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            uint32_t packed[4];
-    #pragma unroll
-            for (int ii = 0; ii < 2; ++ii) {
-                const f32x4 h4 = pg[i + ii], e4 = pu[i + ii];
-    #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int v = 4 * (i + ii) + k;
-                    const float t = h4[k] * id;
-                    const float q = __builtin_rintf(t);
-                    const float et = __builtin_fmaf(e4[k], id, __builtin_fabsf(t) * c1);
-                    if (__builtin_fabsf(__builtin_fabsf(t - q) - 0.5f) <= et) unsure |= 1u << v;
-                    if (__builtin_fabsf(h4[k]) + e4[k] >= amax_lo) cand |= 1u << v;
-                    const uint32_t qb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
-                    packed[2 * ii + (k >> 1)] = (k & 1) ? (packed[2 * ii + (k >> 1)] | (qb << 16)) : qb;
-                }
-            }
-            hq[i >> 1] = u32x4{packed[0], packed[1], packed[2], packed[3]};
-        }
-        a.h_d[p * nfb + fb] = (uint16_t)f32_to_fp16(d);
-        // the block's largest |h| is open when several values could be it or
-        // amax / 127 is near an fp16 tie (then its candidates are uncertain values too)
-        const bool amax_open = __builtin_popcount(cand) > 1 ||
-                               f32_to_fp16(amax_lo / 127.0f) != f32_to_fp16((amax + ea) / 127.0f);
-        const uint32_t mask = unsure | (amax_open ? cand : 0u);
-        if (mask) {
-            const int slot = atomicAdd(a.fix_count, 1);
-            if (slot < a.fix_max) {
-                f32x4* fh = (f32x4*)(a.fix_h + (uint64_t)slot * kFixStride);
-    #pragma unroll
-                for (int i = 0; i < 8; ++i) fh[i] = pg[i];
-                fh[8] = f32x4{ea, 0.0f, 0.0f, 0.0f};
-                a.fix[slot] = make_int4((int)p, fb | (e << 16), (int)mask, (int)cand);
-            }
-        }
+        h_block<ACT>(a, (f32x4*)(s_g + lrow * kHLd + 32 * jb2), (f32x4*)(s_u + lrow * kHLd + 32 * jb2),
+                     (uint64_t)(p0 + row), fb, e);
     };
 #pragma unroll
     for (int half = 0; half < kTM / kEH; ++half) {

@@ -933,7 +933,7 @@ hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T,
                                     : launch_gateup<kTypeQ8_0>(a, max_slots, L.n_cu, stream, ev_start, ev_stop);
 }
 
-// The fused decode gate/up needs the decode slot list (fused decode routing),
+// The fused decode gate/up needs the decode slot list (the decode routing),
 // 16..64 lanes per H row (H in (512, 4096]) and the token rows within 64 KiB of LDS.
 bool gateup_q_fused(const LayerDesc& L, int T) {
     return route_decode_fused(L, T) && down_combine_fused(L, T) && L.H > 512 && L.H <= 4096 &&

@@ -195,18 +195,7 @@ struct qmoe_layer {
 struct qmoe_workspace {
     Workspace w;
     int device = 0;
-    int32_t* host_err = nullptr;  // host view of w.host_err (pinned, mapped, coherent)
 };
-
-namespace {
-
-// The error word a decode routing raised on this workspace, read on the host
-// without a device synchronisation (the word lives in mapped host memory).
-bool workspace_faulted(const qmoe_workspace* ws) {
-    return ws->host_err && __atomic_load_n(ws->host_err, __ATOMIC_ACQUIRE) != 0;
-}
-
-}  // namespace
 
 extern "C" {
 
@@ -303,11 +292,6 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 1) d.dc_ahead = (int)std::min<long>(v, 4);
     }
-    // polling passes of the decode routing's bounded wait (0 makes every wait give up: tests)
-    if (const char* env = std::getenv("QMOE_MAX_SPINS")) {
-        const long v = std::strtol(env, nullptr, 10);
-        if (v >= 0) d.max_spins = (int)std::min<long>(v, 1 << 30);
-    }
     // token count from which routing runs the batched bf16-MFMA router
     if (const char* env = std::getenv("QMOE_BIG_ROUTER_MIN_TOKENS")) {
         const long v = std::strtol(env, nullptr, 10);
@@ -381,7 +365,7 @@ int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_works
         return hip_fail(err, "hipMalloc(workspace)");
     }
     qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, &ws->w, base);
-    // the signalling area starts at zero (generation 0, no flags raised)
+    // the signalling area (the expert scan's finished-workgroup counter) starts at zero
     err = hipMemset(ws->w.sync, 0, qmoe::kSyncWords * sizeof(int32_t));
     if (err == hipSuccess) err = hipDeviceSynchronize();
     if (err != hipSuccess) {
@@ -389,22 +373,6 @@ int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_works
         delete ws;
         return hip_fail(err, "hipMemset(workspace sync area)");
     }
-    // the host-visible copy of the error word
-    void* hp = nullptr;
-    err = hipHostMalloc(&hp, 64, hipHostMallocMapped | hipHostMallocCoherent);
-    void* dp = nullptr;
-    if (err == hipSuccess) {
-        *(volatile int32_t*)hp = 0;
-        err = hipHostGetDevicePointer(&dp, hp, 0);
-        if (err != hipSuccess) (void)hipHostFree(hp);
-    }
-    if (err != hipSuccess) {
-        (void)hipFree(base);
-        delete ws;
-        return hip_fail(err, "hipHostMalloc(workspace error word)");
-    }
-    ws->host_err = (int32_t*)hp;
-    ws->w.host_err = (int32_t*)dp;
     (void)hipGetDevice(&ws->device);
     *out = ws;
     return QMOE_OK;
@@ -413,7 +381,6 @@ int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_works
 int qmoe_workspace_destroy(qmoe_workspace* ws) {
     if (!ws) return QMOE_OK;
     if (ws->w.base) (void)hipFree(ws->w.base);
-    if (ws->host_err) (void)hipHostFree(ws->host_err);
     delete ws;
     return QMOE_OK;
 }
@@ -423,17 +390,11 @@ int32_t qmoe_workspace_capacity(const qmoe_workspace* ws) { return ws ? ws->w.ca
 int qmoe_workspace_check(qmoe_workspace* ws, int32_t* fault) {
     g_last_error.clear();
     if (!ws || !fault) return fail(QMOE_ERR_NULL, "qmoe: ws and fault expected non-null, got null");
+    // no kernel waits on another workgroup, so no forward can fail that way: the
+    // check synchronizes (surfacing any device error) and reports no fault
     hipError_t err = hipDeviceSynchronize();
-    int32_t v = 0;
-    if (err == hipSuccess) err = hipMemcpy(&v, ws->w.sync + qmoe::kSyncErr, sizeof(v), hipMemcpyDeviceToHost);
-    if (err == hipSuccess && workspace_faulted(ws)) v = 1;
-    // after the synchronisation no workgroup of an earlier forward is left: the
-    // whole signalling area starts again from zero (generation 0, no flags)
-    if (err == hipSuccess && v) err = hipMemset(ws->w.sync, 0, qmoe::kSyncWords * sizeof(int32_t));
-    if (err == hipSuccess) err = hipDeviceSynchronize();
     if (err != hipSuccess) return hip_fail(err, "workspace check");
-    if (v && ws->host_err) __atomic_store_n(ws->host_err, 0, __ATOMIC_RELEASE);
-    *fault = v;
+    *fault = 0;
     return QMOE_OK;
 }
 
@@ -525,10 +486,6 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         }
         ws = layer->own_ws;
     }
-    if (workspace_faulted(ws))
-        return fail(QMOE_ERR_SYNC, "qmoe: workspace expected no failed cross-block wait, got one raised by an earlier "
-                                   "forward (its outputs, and those of forwards queued behind it, are NaN); "
-                                   "qmoe_workspace_check clears it");
     const Workspace& w = ws->w;
     if (n_tokens > w.cap_T)
         return fail(QMOE_ERR_CAPACITY, "qmoe: n_tokens expected <= workspace capacity " + std::to_string(w.cap_T) +
@@ -661,7 +618,6 @@ int qmoe_layer_forward_static(qmoe_layer* layer, const float* x, int32_t n_token
     ws.device = dev;
     qmoe::workspace_bytes(n_tokens, d.H, d.E, d.K, d.F, &ws.w, (char*)base + kStaticSyncBytes);
     ws.w.sync = (int32_t*)base;
-    ws.w.host_err = nullptr;
     ForwardIn in;
     in.x = x;
     in.residual = residual;

@@ -12,13 +12,10 @@ namespace qmoe {
 // Tokens handled by one top-k block; the per-block histogram granularity of
 // the stable counting sort.
 constexpr int kTopkTokensPerBlock = 16;
-// Cross-block signalling area of a workspace: generation counter of the
-// fused decode routing, its error flag, and one flag per router block.
-constexpr int kSyncWords = 512;
-constexpr int kSyncGen = 0;
-constexpr int kSyncErr = 1;
-constexpr int kSyncScan = 2;      // the expert-count scan's finished-workgroup counter (back to 0 after each scan)
-constexpr int kSyncFlags = 64;     // flags start here (448 router blocks max)
+// Cross-block signalling area of a workspace: the expert-count scan's
+// finished-workgroup counter (back to 0 after each scan).
+constexpr int kSyncWords = 64;
+constexpr int kSyncScan = 0;
 // Row tile of the prefill grouped GEMM (rows of one expert per tile).
 constexpr int kMfmaTileM = 128;
 // k values per LDS chunk of the prefill GEMMs.
@@ -49,7 +46,6 @@ struct LayerDesc {
     int mfma_min_tokens = 128;              // token count from which the int8-MFMA path runs
     int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs
     int dc_ahead = 2;                       // decode down+combine: steps with loads in flight (2 or 4)
-    int max_spins = 1 << 22;                // decode routing: polling passes before its bounded wait gives up
     unsigned long long* expert_counts = nullptr;  // optional device [E]: += each forward's per-expert dispatches
     int act = 0;                            // 0 SwiGLU (silu(g)*u), 1 GeGLU-tanh (gelu(g)*u, ggml's fp16 table)
     const uint16_t* gelu_tab = nullptr;     // device [65536] fp16 gelu table of the layer's device (GeGLU)
@@ -80,8 +76,7 @@ struct Workspace {
     int4* dslots = nullptr;       // [E+2] decode slot list {expert, first row, rows, token mask}:
                                   // active routed experts, then expert -1 up to min(E, T*K)
     int32_t* counters = nullptr;  // [16] n_active, n_tiles, ...
-    int32_t* sync = nullptr;      // [kSyncWords] zeroed at creation: generation, error flag, block flags
-    int32_t* host_err = nullptr;  // host-mapped word (device address): raised with sync[kSyncErr]
+    int32_t* sync = nullptr;      // [kSyncWords] zeroed at creation: the scan's finished-workgroup counter
     int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
     float2* gubuf = nullptr;      // [R][F] (gate, up) projections
     int8_t* hq_qs = nullptr;      // [R][F]   Q8_0 quants of h = silu(g)*u

@@ -491,15 +491,13 @@ struct TopkArgs {
     int32_t* active;      // [E+1]
     int32_t* expert_slot; // [E]
     int4* slot_info;      // [E+1] {expert, first row, rows, token of first row}
-    int4* dslots;         // [E+2] decode slot list (fused decode routing only, else null)
+    int4* dslots;         // [E+2] decode slot list (decode routing only, else null)
     unsigned long long* expert_counts;  // optional [E]: per-expert dispatch counts accumulated
     int defer_softmax;    // 1: the selection leaves the softmax to the caller (token_softmax)
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
     int nblk;
-    int max_spins;        // fused decode routing: polling passes before the bounded wait gives up
-    int32_t* host_err;    // fused decode routing: host-mapped error word (raised on a give-up), or null
 };
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
@@ -945,26 +943,23 @@ __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
     }
 }
 
-// Fused decode routing (T <= kTopkTokensPerBlock): block b computes router
-// rows 2b, 2b+1 (row E is the shared-expert gate) for all tokens.  Wave
-// (g, p) takes the 256-column slabs p, p+4, ... of both rows for the tokens
-// t = g (mod 4), loading its x columns straight from memory (each x column
-// once per block); the four partial sums of a (row, token) are added in
-// order.  Without a shared expert the router blocks also quantize tokens
-// t = b (mod gridDim.x).  Then the block raises its flag.  Block 0 waits for
-// every other block's flag (it waits on nothing else, and the other blocks
-// wait on nothing), then runs the whole routing on the exact logits.  Flags
-// carry the forward's generation number, so nothing is reset between forwards.
+// Decode routing (T <= kTopkTokensPerBlock), two launches.  The router launch:
+// block b computes router rows 2b, 2b+1 (row E is the shared-expert gate) for
+// all tokens.  Wave (g, p) takes the 256-column slabs p, p+4, ... of both rows
+// for the tokens t = g (mod 4), loading its x columns straight from memory
+// (each x column once per block); the four partial sums of a (row, token) are
+// added in order.  The routing-table launch (after the launch boundary, so no
+// workgroup waits on another) runs the whole routing on the exact logits in
+// one workgroup while the others compute the shared expert's h or x's Q8_0.
 constexpr int kRdRows = 2;                                     // router rows per block
 constexpr int kRdGroups = 4;                                   // token groups (t = g mod kRdGroups)
 constexpr int kRdParts = 16 / kRdGroups;                       // waves per token group
 constexpr int kRdTokSlots = kTopkTokensPerBlock / kRdGroups;   // token slots per wave
 constexpr int kRdVals = kRdRows * kRdTokSlots;                 // (row, token) sums per wave
 constexpr int kRdSlab = 256;        // columns per lane-float4 sweep
-constexpr int kMaxRdSlabs = 16;     // fused decode routing for H <= 4096
+constexpr int kMaxRdSlabs = 16;     // decode routing for H <= 4096
 // dynamic LDS: block 0's routing tables, the shared-expert blocks' token rows
 constexpr int kRdLdsBytes = 96 * 1024;
-constexpr int kMaxRdBlocks = kSyncWords - kSyncFlags;
 
 // Wave sums of N per-lane f64 values at once (reduce-scatter): after the 32-
 // and 16-lane swap steps every lane holds N/4 values, of slots
@@ -1071,20 +1066,10 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
     }
 }
 
-template <int NSW, int SWT, int SLPR>  // NSW: router slabs per wave (ceil(H/256/4)); SWT: shared type (0: none)
-__global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits, int8_t* xq_qs, float2* xq_ds,
-                                                       int32_t* sync, SharedGuArgs sg) {
-    extern __shared__ __align__(16) uint8_t s_dyn[];
+template <int NSW>  // NSW: router slabs per wave (ceil(H/256/4))
+__global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits) {
     __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int nb = gridDim.x - sg.n_blocks;  // router blocks
-    if constexpr (SWT != 0) {
-        if ((int)blockIdx.x >= nb) {
-            shared_gateup_block<SWT, SLPR>(a, sg, blockIdx.x - nb, s_dyn, xq_qs, xq_ds);
-            return;
-        }
-    }
-    const int gen = __hip_atomic_load(sync + kSyncGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
     const int E1 = a.E + a.S;
     const int nslab = a.H / kRdSlab;
     const int part = wave % kRdParts;
@@ -1161,59 +1146,28 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
             double sum = s_part[rr][0][t];
 #pragma unroll
             for (int q = 1; q < kRdParts; ++q) sum = sum + s_part[rr][q][t];
-            // written through to memory (agent-scope store): block 0 reads it after the flags
-            __hip_atomic_store(logits + (uint64_t)t * (a.E + 1) + er, (float)sum, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            logits[(uint64_t)t * (a.E + 1) + er] = (float)sum;
         }
     }
-    // activation quantization (the shared-expert blocks do it when there are
-    // any): token t by block t % nb, wave (t / nb) % 16
-    if (SWT == 0)
-        for (int t = blockIdx.x; t < a.T; t += nb)
-            if (wave == (t / nb) % 16) quant_token_row(a.xe, a.H, t, lane, xq_qs, xq_ds);
-    // each wave's write-through logit stores complete before the block's flag (a
-    // release fence would write back the whole L2 once per wave)
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (blockIdx.x != 0) {
-        if (tid == 0) __hip_atomic_store(sync + kSyncFlags + blockIdx.x, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Decode routing on the router launch's logits (complete and visible at the
+// launch boundary): workgroup 0 runs the top-k, softmax, counts, scan and the
+// row and slot tables; the other workgroups meanwhile compute the shared
+// expert's h (SWT: its weight type) or, without one, x's Q8_0 (one wave per token).
+template <int SWT, int SLPR>
+__global__ __launch_bounds__(1024) void k_route_decode_tables(TopkArgs a, int8_t* xq_qs, float2* xq_ds, SharedGuArgs sg) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];
+    if (blockIdx.x == 0) {
+        route_small_body(a, *(SmallRouteLds*)s_dyn);
         return;
     }
-    // block 0: wait for the other blocks' flags (lane l watches blocks 1 + l + 64 i).
-    // The wait is bounded.  A give-up raises the workspace's error word, which
-    // stays raised (every later forward on the workspace sees it here) until the
-    // host clears the whole signalling area after a device synchronisation; the
-    // host-mapped copy lets the next host call fail without one.  A forward that
-    // sees the word routes as usual (every table stays in range) and then sets
-    // its softmax weights and shared gates to NaN, so its outputs are NaN.
-    __shared__ int s_fault;
-    if (wave == 0) {
-        bool done = nb <= 1;
-        for (int it = 0; it < a.max_spins && !done; ++it) {
-            bool mine = true;
-            for (int bb = 1 + lane; bb < nb; bb += 64)  // every watched flag loaded in each pass, independently
-                mine &= __hip_atomic_load(sync + kSyncFlags + bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen;
-            done = __all(mine);
-            if (!done) __builtin_amdgcn_s_sleep(2);
-        }
-        const bool fault = !done || __hip_atomic_load(sync + kSyncErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-        if (fault && lane == 0) {
-            __hip_atomic_store(sync + kSyncErr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (a.host_err) __hip_atomic_store(a.host_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
-        if (lane == 0) s_fault = fault ? 1 : 0;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // drop stale cached logits (L1 and this XCD's L2)
+    if constexpr (SWT != 0) {
+        shared_gateup_block<SWT, SLPR>(a, sg, blockIdx.x - 1, s_dyn, xq_qs, xq_ds);
+    } else {
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        if (wave < a.T) quant_token_row(a.xe, a.H, wave, lane, xq_qs, xq_ds);
     }
-    __syncthreads();
-    route_small_body(a, *(SmallRouteLds*)s_dyn);
-    if (s_fault) {
-        __syncthreads();  // after the softmax writes of route_small_body
-        const float nan = __builtin_nanf("");
-        for (int i = tid; i < a.T * a.K; i += blockDim.x) a.topk_w[i] = nan;
-        if (a.S)
-            for (int t = tid; t < a.T; t += blockDim.x) a.sh_gate[t] = nan;
-    }
-    if (tid == 0) __hip_atomic_store(sync + kSyncGen, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Per-expert exclusive prefix of the per-block histograms (in place: hist
@@ -1303,26 +1257,30 @@ bool route_uses_mfma(const LayerDesc& L, int T) {
 }
 
 bool route_decode_fused(const LayerDesc& L, int T) {
-    return !route_uses_mfma(L, T) && T <= kTopkTokensPerBlock && L.H <= kMaxRdSlabs * kRdSlab &&
-           (L.E + L.S + kRdRows - 1) / kRdRows <= kMaxRdBlocks;
+    return !route_uses_mfma(L, T) && T <= kTopkTokensPerBlock && L.H <= kMaxRdSlabs * kRdSlab;
 }
 
-// The fused decode routing instance for nsw slabs per wave, shared-expert
-// type swt (0 none, 1 Q4_0, 2 Q8_0) and the shared blocks' lanes per row
-// (16 for H <= 1024, 32 for H <= 2048, else 64).
-template <int NSW, int SLPR>
-static const void* route_decode_for(int swt) {
-    return swt == 0 ? (const void*)k_route_decode<NSW, 0, SLPR>
-                    : swt == 1 ? (const void*)k_route_decode<NSW, kTypeQ4_0, SLPR>
-                               : (const void*)k_route_decode<NSW, kTypeQ8_0, SLPR>;
-}
-static const void* route_decode_kernel(int nsw, int swt, int lpr) {
+// The decode router instance for nsw slabs per wave; the routing-table launch
+// for shared-expert type swt (0 none, 1 Q4_0, 2 Q8_0) and the shared blocks'
+// lanes per row (16 for H <= 1024, 32 for H <= 2048, else 64).
+static const void* route_decode_kernel(int nsw) {
     static_assert(kRdParts == 4, "slabs per wave: 1 at H <= 1024, 2 at H <= 2048, 3-4 at H <= 4096");
-    if (nsw == 1 && lpr == 16) return route_decode_for<1, 16>(swt);
-    if (nsw == 2 && lpr == 32) return route_decode_for<2, 32>(swt);
-    if (nsw == 3 && lpr == 64) return route_decode_for<3, 64>(swt);
-    if (nsw == 4 && lpr == 64) return route_decode_for<4, 64>(swt);
-    return nullptr;
+    switch (nsw) {
+        case 1: return (const void*)k_route_decode<1>;
+        case 2: return (const void*)k_route_decode<2>;
+        case 3: return (const void*)k_route_decode<3>;
+        case 4: return (const void*)k_route_decode<4>;
+        default: return nullptr;
+    }
+}
+template <int SLPR>
+static const void* route_tables_for(int swt) {
+    return swt == 0 ? (const void*)k_route_decode_tables<0, SLPR>
+                    : swt == 1 ? (const void*)k_route_decode_tables<kTypeQ4_0, SLPR>
+                               : (const void*)k_route_decode_tables<kTypeQ8_0, SLPR>;
+}
+static const void* route_tables_kernel(int swt, int lpr) {
+    return lpr == 16 ? route_tables_for<16>(swt) : lpr == 32 ? route_tables_for<32>(swt) : route_tables_for<64>(swt);
 }
 
 static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, const float* xr, const float* xe, int T,
@@ -1378,8 +1336,6 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
     ta.nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
-    ta.max_spins = L.max_spins;
-    ta.host_err = ws.host_err;
     hipError_t err;
     if (route_uses_mfma(L, T)) {
         RouterMfmaArgs ma;
@@ -1419,8 +1375,9 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
             return err;
         if (dbg.exact_logits && (err = launch_router_exact(L, ws, xr, x, T, false, stream)) != hipSuccess) return err;
     } else if (route_decode_fused(L, T)) {
-        // decode: one launch; it also writes the decode slot list and, when the
-        // fused gate/up runs next, computes the shared expert's h on idle CUs
+        // decode: the router launch, then the routing-table launch (it also writes
+        // the decode slot list and, when the fused gate/up runs next, computes
+        // the shared expert's h on other CUs meanwhile)
         ta.dslots = ws.dslots;
         ta.defer_softmax = 1;
         const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
@@ -1437,19 +1394,26 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
             sg.hq_qs = ws.hq_qs; sg.hq_ds = ws.hq_ds;
             sg.act = L.act; sg.gelu_tab = L.gelu_tab;
         }
-        const dim3 g(nb + sg.n_blocks), b(64 * kTopkTokensPerBlock);
         // above the 64 KiB default window: raise it
         const size_t lds = kRdLdsBytes;
         const int lpr = L.H <= 1024 ? 16 : (L.H <= 2048 ? 32 : 64);
         const int nsw = (nslab + kRdParts - 1) / kRdParts;  // slabs per wave
         const int swt = !sg.n_blocks ? 0 : (L.gu_type == kTypeQ4_0 ? 1 : 2);
-        const void* kern = route_decode_kernel(nsw, swt, lpr);
+        const void* kern = route_decode_kernel(nsw);
         if (!kern) return hipErrorInvalidValue;
-        if ((err = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
+        float* logits = ws.logits;
+        void* args[] = {&ta, &logits};
+        if ((err = hipLaunchKernel(kern, dim3(nb), dim3(64 * kTopkTokensPerBlock), args, 0, stream)) != hipSuccess)
             return err;
-        int32_t* sync = ws.sync;
-        void* args[] = {&ta, (void*)&ws.logits, (void*)&ws.xq_qs, (void*)&ws.xq_ds, &sync, &sg};
-        if ((err = hipLaunchKernel(kern, g, b, args, lds, stream)) != hipSuccess) return err;
+        const void* tk = route_tables_kernel(swt, lpr);
+        if ((err = hipFuncSetAttribute(tk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
+            return err;
+        int8_t* xq_qs = ws.xq_qs;
+        float2* xq_ds = ws.xq_ds;
+        void* targs[] = {&ta, &xq_qs, &xq_ds, &sg};
+        if ((err = hipLaunchKernel(tk, dim3(1 + (sg.n_blocks ? sg.n_blocks : 1)), dim3(1024), targs, lds, stream)) !=
+            hipSuccess)
+            return err;
         return hipGetLastError();
     } else {
         if ((err = launch_router_exact(L, ws, xr, x, T, true, stream)) != hipSuccess) return err;

@@ -115,8 +115,9 @@ class Workspace:
         return int(lib().qmoe_workspace_capacity(self._handle))
 
     def check(self) -> int:
-        """Synchronizes; 1 if a forward on this workspace gave up a bounded
-        cross-block wait since the last check (its routing is not to be trusted)."""
+        """Synchronizes (raising on a device error) and reports whether a forward on
+        this workspace failed a cross-workgroup wait: always 0, since no kernel waits
+        on another workgroup."""
         v = ctypes.c_int32()
         check(lib().qmoe_workspace_check(self._handle, ctypes.byref(v)))
         return int(v.value)

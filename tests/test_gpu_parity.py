@@ -468,9 +468,9 @@ def test_stack_40_layers(gpu, T):
 
 @pytest.mark.parametrize("n_experts,T", [(256, 10), (1024, 16), (16, 3)])
 def test_fused_decode_routing_repeated(gpu, n_experts, T):
-    """The fused decode routing (router blocks signal block 0 with per-forward
-    generation flags) over several forwards on one workspace: every forward's
-    routing matches the oracle, and no bounded wait gave up."""
+    """The decode routing (the router launch, then the routing-table launch) over
+    several forwards on one workspace: every forward's routing matches the oracle,
+    and Workspace.check() reports no fault."""
     from qwenium_amd import Workspace
 
     spec = LayerSpec(256, n_experts, 8 if n_experts >= 8 else 2, 64, True, TYPE_Q4_0)
@@ -510,50 +510,24 @@ def test_forward_norm_matches_unfused(gpu, which, T):
     assert torch.equal(y_fused, y_ref)
 
 
-def test_decode_wait_give_up_is_loud(gpu, monkeypatch):
-    """The decode routing's bounded wait forced to give up from the host (a layer created
-    with no polling passes): every kernel exits normally, the outputs are NaN, the next
-    forward call on the workspace fails with QMOE_ERR_SYNC (read from host-mapped memory,
-    no synchronisation), Workspace.check() reports and clears it, and forwards after that
-    match the oracle again."""
+def test_decode_forwards_queued_back_to_back(gpu):
+    """Decode forwards queued on one workspace with nothing between them (no
+    synchronisation, no check): the routing launches carry no state from one forward
+    to the next, so every forward's routing and output match the oracle, and
+    Workspace.check() reports no fault."""
     from qwenium_amd import Workspace
-    from qwenium_amd._lib import QMOE_ERR_SYNC, QmoeError
 
     spec = synthetic.QWEN35B
     T, seed = 10, 5
     tensors = synthetic.make_layer_tensors(spec, seed)
-    monkeypatch.setenv("QMOE_MAX_SPINS", "0")
-    bad = synthetic.make_layer(spec, seed, tensors=tensors)
-    monkeypatch.delenv("QMOE_MAX_SPINS")
-    good = synthetic.make_layer(spec, seed, tensors=tensors)
-    ws = Workspace(good, 16)
-    x = synthetic.make_x(spec, T, seed)
-    y_bad = bad.forward(x, workspace=ws)
-    torch.cuda.synchronize()
-    assert torch.isnan(y_bad).all()
-    with pytest.raises(QmoeError) as ei:
-        good.forward(x, workspace=ws)
-    assert ei.value.code == QMOE_ERR_SYNC
-    assert ws.check() == 1
-    assert ws.check() == 0
-    # a forward queued right behind a give-up, before the host could see it, is NaN too
-    y_bad = bad.forward(x, workspace=ws)
-    try:
-        y_next = good.forward(x, workspace=ws)
-        torch.cuda.synchronize()
-        assert torch.isnan(y_next).all()
-    except QmoeError as e:
-        assert e.code == QMOE_ERR_SYNC
-    torch.cuda.synchronize()
-    assert torch.isnan(y_bad).all()
-    assert ws.check() == 1
-    # cleared: the same workspace routes correctly again, forward after forward
+    layer = synthetic.make_layer(spec, seed, tensors=tensors)
     ref = host_layer(spec, tensors)
-    for batch in range(3):
-        xb = synthetic.make_x(spec, T, seed, batch=batch)
-        y, dbg = good.forward(xb, workspace=ws, debug=True)
-        torch.cuda.synchronize()
-        y_ref, d_ref = ref.forward(xb.cpu().numpy(), debug=True)
+    ws = Workspace(layer, 16)
+    xs = [synthetic.make_x(spec, T, seed, batch=b) for b in range(4)]
+    outs = [layer.forward(x, workspace=ws, debug=True) for x in xs]
+    torch.cuda.synchronize()
+    for x, (y, dbg) in zip(xs, outs):
+        y_ref, d_ref = ref.forward(x.cpu().numpy(), debug=True)
         assert_parity(y.cpu().numpy(), {k: v.cpu().numpy() for k, v in dbg.items()}, y_ref, d_ref, spec,
                       min_identical=1.0)
     assert ws.check() == 0
