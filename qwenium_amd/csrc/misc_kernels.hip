@@ -9,59 +9,17 @@ namespace qmoe {
 // RMSNorm, restating ggml_rms_norm + ggml_mul as used by build_rms_norm
 // (src/layers/norm.cpp:15-26): sum of f32 squares accumulated in f64,
 // mean rounded to f32, scale = 1/sqrtf(mean + eps), y = (x*scale)*w.
-// One block per token.
+// One block per token; the sum of squares in the order rms_scale_row fixes
+// (runs of four columns, then a pairwise tree), as the fused decode router
+// computes it.
 // ---------------------------------------------------------------------------
-// Values of the token row held in registers (NV = ceil(H/256) per thread): every
-// load in flight at once and x read once.  Same per-thread summation order as
-// k_rms_norm below (thread i adds x[i], x[i+256], ... in turn), so the same bits.
-template <int NV>
-__global__ __launch_bounds__(256) void k_rms_norm_reg(const float* x, const float* w, int H, float eps, float* y) {
-#pragma clang fp contract(off)
-    __shared__ double s_part[4];
-    const int t = blockIdx.x;
-    const float* xr = x + (uint64_t)t * H;
-    float v[NV];
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int i = threadIdx.x + 256 * k;
-        v[k] = i < H ? xr[i] : 0.0f;
-    }
-    double acc = 0.0;
-#pragma unroll
-    for (int k = 0; k < NV; ++k)
-        if ((int)threadIdx.x + 256 * k < H) acc += (double)(v[k] * v[k]);
-    acc = group_sum_f64<64>(acc);
-    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    const double sum = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
-    const float mean = (float)(sum / (double)H);
-    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int i = threadIdx.x + 256 * k;
-        if (i < H) {
-            const float u = v[k] * scale;
-            y[(uint64_t)t * H + i] = w ? u * w[i] : u;
-        }
-    }
-}
-
 __global__ __launch_bounds__(256) void k_rms_norm(const float* x, const float* w, int H, float eps, float* y) {
 #pragma clang fp contract(off)
-    __shared__ double s_part[4];
+    __shared__ double s_chunk[kRmsMaxChunks];
+    __shared__ float s_scale;
     const int t = blockIdx.x;
     const float* xr = x + (uint64_t)t * H;
-    double acc = 0.0;
-    for (int i = threadIdx.x; i < H; i += 256) {
-        const float v = xr[i];
-        acc += (double)(v * v);
-    }
-    acc = group_sum_f64<64>(acc);
-    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    const double sum = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
-    const float mean = (float)(sum / (double)H);
-    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
+    const float scale = rms_scale_row(xr, H, eps, s_chunk, &s_scale);
     for (int i = threadIdx.x; i < H; i += 256) {
         const float v = xr[i] * scale;
         y[(uint64_t)t * H + i] = w ? v * w[i] : v;
@@ -69,11 +27,8 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* x, const float* w
 }
 
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream) {
-    const int nv = (H + 255) / 256;
-    if (nv <= 4) hipLaunchKernelGGL(k_rms_norm_reg<4>, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
-    else if (nv <= 8) hipLaunchKernelGGL(k_rms_norm_reg<8>, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
-    else if (nv <= 16) hipLaunchKernelGGL(k_rms_norm_reg<16>, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
-    else hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
+    if (H > 256 * kRmsMaxChunks) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
     return hipGetLastError();
 }
 
@@ -81,56 +36,28 @@ hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float e
 // Gemma 4 MoE inputs (src/models/gemma4.cpp:555-563): from the residual row x,
 //   expert_in = rms_norm(x) * pre_ffw_norm_2            (build_rms_norm)
 //   router_in = (rms_norm(x) * s) * ffn_gate_inp.scale  (ggml_rms_norm, ggml_scale, ggml_mul)
-// with s = 1/sqrtf(n_embd): the row read once, the scale computed once, in
-// k_rms_norm's summation order (so rms_norm(x) has the same bits).
+// with s = 1/sqrtf(n_embd): the scale computed once, in k_rms_norm's
+// summation order (so rms_norm(x) has the same bits).
 // ---------------------------------------------------------------------------
-template <int NV>
 __global__ __launch_bounds__(256) void k_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int H,
                                                        float eps, float s, float* ei, float* ri) {
 #pragma clang fp contract(off)
-    __shared__ double s_part[4];
+    __shared__ double s_chunk[kRmsMaxChunks];
+    __shared__ float s_scale;
     const int t = blockIdx.x;
     const float* xr = x + (uint64_t)t * H;
-    float v[NV];
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int i = threadIdx.x + 256 * k;
-        v[k] = i < H ? xr[i] : 0.0f;
-    }
-    double acc = 0.0;
-#pragma unroll
-    for (int k = 0; k < NV; ++k)
-        if ((int)threadIdx.x + 256 * k < H) acc += (double)(v[k] * v[k]);
-    acc = group_sum_f64<64>(acc);
-    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    const double sum = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
-    const float mean = (float)(sum / (double)H);
-    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int i = threadIdx.x + 256 * k;
-        if (i < H) {
-            const float u = v[k] * scale;
-            ei[(uint64_t)t * H + i] = u * w_pre[i];
-            const float r = u * s;
-            ri[(uint64_t)t * H + i] = r * w_rs[i];
-        }
+    const float scale = rms_scale_row(xr, H, eps, s_chunk, &s_scale);
+    for (int i = threadIdx.x; i < H; i += 256) {
+        const float u = xr[i] * scale;
+        ei[(uint64_t)t * H + i] = u * w_pre[i];
+        const float r = u * s;
+        ri[(uint64_t)t * H + i] = r * w_rs[i];
     }
 }
 
 hipError_t launch_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps, float s,
                                 float* expert_in, float* router_in, hipStream_t stream) {
-    const int nv = (H + 255) / 256;
-    if (nv > 16) return hipErrorInvalidValue;
-    if (nv <= 4)
-        hipLaunchKernelGGL(k_gemma4_inputs<4>, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
-    else if (nv <= 8)
-        hipLaunchKernelGGL(k_gemma4_inputs<8>, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
-    else if (nv <= 12)
-        hipLaunchKernelGGL(k_gemma4_inputs<12>, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
-    else
-        hipLaunchKernelGGL(k_gemma4_inputs<16>, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
+    hipLaunchKernelGGL(k_gemma4_inputs, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
     return hipGetLastError();
 }
 

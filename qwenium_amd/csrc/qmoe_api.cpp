@@ -157,9 +157,9 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.tiles = (int4*)take((size_t)max_tiles * sizeof(int4));
     ws.gubuf = (float2*)take(R * F * sizeof(float2));
     ws.h_q = (_Float16*)ws.gubuf;  // R*F*2 bytes of the R*F*8 (the rest is its padding)
-    // the prefill GEMMs stage whole 128-wide k chunks: a 64-wide last chunk
-    // reads up to 128 bytes of quants and 4 bytes of scales past a row, so the
-    // four A buffers end in 256 bytes of padding
+    // built with 128-wide k chunks, the prefill GEMMs stage whole chunks: a
+    // 64-wide last chunk reads up to 128 bytes of quants and 4 bytes of scales
+    // past a row, so the four A buffers end in 256 bytes of padding
     ws.h_d = (uint16_t*)take(R * (F / 32) * sizeof(uint16_t) + 256);
     ws.x_q = (_Float16*)take((size_t)T * H * sizeof(_Float16) + 256);
     ws.x_d = (uint16_t*)take((size_t)T * (H / 32) * sizeof(uint16_t) + 256);
@@ -175,6 +175,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.ysh = (float*)take((size_t)T * H * sizeof(float));
     ws.xn = (float*)take((size_t)T * H * sizeof(float));
     ws.xr = (float*)take((size_t)T * H * sizeof(float));
+    ws.x_scale = (float*)take((size_t)T * sizeof(float));
     ws.max_tiles = max_tiles;
     ws.cap_T = T; ws.H = H; ws.E = E; ws.K = K; ws.F = F;
     ws.base = base;
@@ -510,11 +511,23 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
     }
     const float* xin = x;                    // the experts' input
     const float* xr = in.xr ? in.xr : x;     // the router's input
+    // the prefill GEMMs address their A operands (x and h quants as f16) with
+    // 32-bit byte offsets
+    const uint64_t R = (uint64_t)n_tokens * (d.K + d.S);
+    const bool mfma = n_tokens >= d.mfma_min_tokens && !qmoe::gateup_q_fused(d, n_tokens) &&
+                      R * d.F * 2 + 256 < (1ull << 32) && (uint64_t)n_tokens * d.H * 2 + 256 < (1ull << 32);
+    // decode: the routing normalizes x on the fly (no RMSNorm launch, no normalized copy)
+    const float* route_norm_w = nullptr;
     if (in.norm_w) {
-        // the normalized rows go to the workspace; the residual add is the combine epilogue
+        // the residual add is the combine epilogue
         residual = x;
-        if (err == hipSuccess) err = qmoe::launch_rms_norm(x, in.norm_w, n_tokens, d.H, in.eps, v.xn, stream);
-        xin = xr = v.xn;
+        if (!mfma && qmoe::route_norm_fused(d, n_tokens)) {
+            route_norm_w = in.norm_w;
+        } else {
+            // the normalized rows go to the workspace
+            if (err == hipSuccess) err = qmoe::launch_rms_norm(x, in.norm_w, n_tokens, d.H, in.eps, v.xn, stream);
+            xin = xr = v.xn;
+        }
     } else if (in.g4_pre_w) {
         const float s = 1.0f / std::sqrt((float)d.H);  // gemma4.cpp:561-562
         if (err == hipSuccess)
@@ -522,12 +535,7 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         xin = v.xn;
         xr = v.xr;
     }
-    // the prefill GEMMs address their A operands (x and h quants as f16) with
-    // 32-bit byte offsets
-    const uint64_t R = (uint64_t)n_tokens * (d.K + d.S);
-    const bool mfma = n_tokens >= d.mfma_min_tokens && !qmoe::gateup_q_fused(d, n_tokens) &&
-                      R * d.F * 2 + 256 < (1ull << 32) && (uint64_t)n_tokens * d.H * 2 + 256 < (1ull << 32);
-    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, xr, n_tokens, rdbg, mfma, stream);
+    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, xr, n_tokens, rdbg, mfma, stream, route_norm_w, in.eps);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
     // events [1] and [2] are taken by the gate/up launch itself (its own start and end)
     hipEvent_t e1 = layer->record_phases ? layer->phase_events[1] : nullptr;
@@ -711,7 +719,9 @@ int qmoe_rms_norm(const float* x, const float* w, int32_t n_tokens, int32_t n_em
     if (n_tokens < 0) return fail(QMOE_ERR_VALUE, "qmoe: n_tokens expected >= 0, got " + std::to_string(n_tokens));
     if (n_tokens == 0) return QMOE_OK;
     if (!x || !y) return fail(QMOE_ERR_NULL, "qmoe: x/y expected device pointers, got null");
-    if (n_embd < 1) return fail(QMOE_ERR_VALUE, "qmoe: n_embd expected >= 1, got " + std::to_string(n_embd));
+    if (n_embd < 1 || n_embd > 256 * qmoe::kRmsMaxChunks)
+        return fail(QMOE_ERR_VALUE, "qmoe: n_embd expected 1.." + std::to_string(256 * qmoe::kRmsMaxChunks) + ", got " +
+                                        std::to_string(n_embd));
     hipError_t err = qmoe::launch_rms_norm(x, w, n_tokens, n_embd, eps, y, (hipStream_t)hip_stream);
     return err == hipSuccess ? QMOE_OK : hip_fail(err, "rms_norm kernel");
 }

@@ -239,6 +239,71 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// RMSNorm's sum of squares in the one order every RMSNorm here uses (the
+// standalone kernels and the decode router that normalizes on the fly): the
+// columns in runs of four (run r: columns 4r .. 4r+3 below H), each run's
+// f64(f32(v * v)) added in column order; then an adjacent-pairs tree over the
+// run sums zero-padded to a power of two (a longer zero padding changes no
+// bits: its subtrees are exact zeros).  A wave reads 64 consecutive runs with
+// one coalesced load per lane, and dpp_sum_f64<64> is exactly the adjacent-pairs
+// tree over its lanes (xor 1, xor 2, then half-row, row, 16- and 32-lane steps
+// over uniform groups; a + b == b + a).  ggml adds all columns one after another
+// in f64 (src/layers/norm.cpp:15-26 -> ggml_rms_norm); the orders round
+// differently only where the f64 sum lands within a few f64 ulps of an f32
+// rounding boundary of the mean.
+__device__ __forceinline__ double ssq_run4(const float* xr, int H, int r) {
+#pragma clang fp contract(off)
+    const int c0 = 4 * r;
+    float v[4];
+    if (c0 + 4 <= H && ((uintptr_t)(xr + c0) & 15u) == 0) {
+        const f32x4 q = *(const f32x4*)(xr + c0);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = c0 + c < H ? xr[c0 + c] : 0.0f;
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        if (c0 + c < H) s += (double)(v[c] * v[c]);
+    return s;
+}
+// The tree over runs 64 c .. 64 c + 63 (lane i: run 64 c + i), in lane 63.
+__device__ __forceinline__ double ssq_chunk64(const float* xr, int H, int c, int lane) {
+    return dpp_sum_f64<64>(ssq_run4(xr, H, 64 * c + lane));
+}
+// f32 RMSNorm scale from the f64 sum of squares (ggml_rms_norm: mean in f32).
+__device__ __forceinline__ float rms_scale_from_ssq(double ssq, int H, float eps) {
+    const float mean = (float)(ssq / (double)H);
+    return 1.0f / __builtin_sqrtf(mean + eps);
+}
+// scale = 1/sqrtf(fp32(ssq / H) + eps) of one row (H <= 256 kRmsMaxChunks), by
+// the whole workgroup (every thread calls it): the waves take the chunks in
+// turn, their trees go to s_chunk (LDS, kRmsMaxChunks doubles), then the tree
+// over the chunk sums level by level.
+__device__ inline float rms_scale_row(const float* xr, int H, float eps, double* s_chunk, float* s_scale) {
+#pragma clang fp contract(off)
+    const int nc = (H + 255) >> 8;
+    const int nw = (int)blockDim.x >> 6, wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    int L = 1;
+    while (L < nc) L <<= 1;
+    for (int c = wave; c < L; c += nw) {
+        const double v = c < nc ? ssq_chunk64(xr, H, c, lane) : 0.0;
+        if (lane == 63) s_chunk[c] = v;
+    }
+    __syncthreads();
+    for (int w = L >> 1; w >= 1; w >>= 1) {
+        const int i = threadIdx.x;
+        const double v = i < w ? s_chunk[2 * i] + s_chunk[2 * i + 1] : 0.0;
+        __syncthreads();
+        if (i < w) s_chunk[i] = v;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *s_scale = rms_scale_from_ssq(s_chunk[0], H, eps);
+    __syncthreads();
+    return *s_scale;
+}
+
 // The whole wave's f64 sum in every lane (dpp_sum_f64<64> leaves it in lane 63).
 __device__ __forceinline__ double wave_sum_f64(double v) {
     v = dpp_sum_f64<64>(v);

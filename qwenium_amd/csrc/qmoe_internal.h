@@ -16,6 +16,9 @@ constexpr int kTopkTokensPerBlock = 16;
 // finished-workgroup counter (back to 0 after each scan).
 constexpr int kSyncWords = 64;
 constexpr int kSyncScan = 0;
+// RMSNorm: 256-column chunks of a row whose sums fit a workgroup's LDS (rows of
+// at most 65536 columns).
+constexpr int kRmsMaxChunks = 256;
 // Row tile of the prefill grouped GEMM (rows of one expert per tile).
 constexpr int kMfmaTileM = 128;
 // k values per LDS chunk of the prefill GEMMs.
@@ -95,6 +98,7 @@ struct Workspace {
     int fix_max = 0;
     float* xn = nullptr;          // [T][H] RMSNorm(x)*w for fused-norm forwards (the experts' input)
     float* xr = nullptr;          // [T][H] the router's own input when it differs (Gemma 4 slice)
+    float* x_scale = nullptr;     // [T] RMSNorm scales of a decode forward that normalizes in its routing
     float* ybuf = nullptr;        // [R][H] down outputs (unweighted)
     float* ysh = nullptr;         // [T][H] the shared expert's down rows (fused decode)
     int max_tiles = 0;
@@ -134,8 +138,13 @@ bool route_decode_fused(const LayerDesc& L, int T);
 // x_f16: also write x's Q8_0 quants as f16 and its fp16 block scales (ws.x_q,
 // ws.x_d), the prefill GEMMs' A operand (inside the batched router's launch,
 // else a launch of its own).
+// norm_w (decode routing only, T <= 16 without x_f16): x is the residual row and
+// the routing normalizes it on the fly, x_in = (x * rms scale) * norm_w, for the
+// router and for x's Q8_0 (route_norm_fused says when).
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
-                        const RouteDebug& dbg, bool x_f16, hipStream_t stream);
+                        const RouteDebug& dbg, bool x_f16, hipStream_t stream, const float* norm_w = nullptr,
+                        float eps = 0.0f);
+bool route_norm_fused(const LayerDesc& L, int T);
 // ev_start / ev_stop (optional): events recorded at the kernel's own start and
 // end (profiling of the dominant kernel without marker overhead).
 hipError_t launch_experts_gateup(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,

@@ -88,8 +88,10 @@ __device__ __forceinline__ void router_row(const RouterArgs& a, int e, float* s_
 
 // Q8_0 quantization of one token row (one wave; lane b handles 32-value
 // blocks b, b+64, ...): d = fp16(amax/127), q = rint(x * 127/amax), and the
-// block's quant sum for the Q4_0 offset term.
-__device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, int8_t* qs, float2* ds) {
+// block's quant sum for the Q4_0 offset term.  With nw, the row is first
+// normalized as RMSNorm writes it: x = (x * nscale) * nw (f32, two roundings).
+__device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, int8_t* qs, float2* ds,
+                                            const float* nw = nullptr, float nscale = 1.0f) {
     const int nb = H >> 5;
     for (int b = lane; b < nb; b += 64) {
         const f32x4* src = (const f32x4*)(xr + 32 * b);
@@ -98,6 +100,18 @@ __device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, in
         for (int i = 0; i < 8; ++i) {
             const f32x4 q = src[i];
             v[4 * i + 0] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+        }
+        if (nw) {
+            const f32x4* wsrc = (const f32x4*)(nw + 32 * b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const f32x4 w4 = wsrc[i];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float u = v[4 * i + k] * nscale;
+                    v[4 * i + k] = u * w4[k];
+                }
+            }
         }
         float amax = 0.0f;
 #pragma unroll
@@ -126,8 +140,8 @@ __device__ __forceinline__ void quant_x_row(const float* xr, int H, int lane, in
 }
 
 __device__ __forceinline__ void quant_token_row(const float* x, int H, int t, int lane, int8_t* xq_qs,
-                                                float2* xq_ds) {
-    quant_x_row(x + (uint64_t)t * H, H, lane, xq_qs + (uint64_t)t * H, xq_ds + (uint64_t)t * (H >> 5));
+                                                float2* xq_ds, const float* nw = nullptr, float nscale = 1.0f) {
+    quant_x_row(x + (uint64_t)t * H, H, lane, xq_qs + (uint64_t)t * H, xq_ds + (uint64_t)t * (H >> 5), nw, nscale);
 }
 
 // The same Q8_0 quantization of one token row (one wave; lane b handles blocks
@@ -479,6 +493,9 @@ struct TopkArgs {
     uint64_t router_ld;
     const float* w_sh_norm;    // [H] or null
     int T, E, K, S, H;
+    const float* norm_w;  // decode routing: x is normalized on the fly, (x * x_scale[t]) * norm_w (null: not)
+    float norm_eps;
+    float* x_scale;       // [T] the rows' RMSNorm scales (router block 0 writes them for the table launch)
     int32_t* topk_idx;    // [T][K]
     float* topk_w;        // [T][K]
     float* sh_gate;       // [T]
@@ -1023,8 +1040,9 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
     int8_t* lq = (int8_t*)s_dyn;                              // [tpg][H] quants
     float2* ld = (float2*)(lq + (size_t)sg.tpg * a.H);        // [tpg][H/32] {d, sum}
     float2* lgu = ld + (size_t)sg.tpg * (a.H >> 5);           // [tpg][32] (g, u)
-    if (wave < nt) quant_x_row(a.xe + (uint64_t)(t0 + wave) * a.H, a.H, lane, lq + (size_t)wave * a.H,
-                               ld + (size_t)wave * (a.H >> 5));
+    if (wave < nt)
+        quant_x_row(a.xe + (uint64_t)(t0 + wave) * a.H, a.H, lane, lq + (size_t)wave * a.H,
+                    ld + (size_t)wave * (a.H >> 5), a.norm_w, a.norm_w ? a.x_scale[t0 + wave] : 1.0f);
     __syncthreads();
     if (fb == 0) {
         // the workspace copy of these tokens' Q8_0 rows (the routed experts read it),
@@ -1066,10 +1084,21 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
     }
 }
 
-template <int NSW>  // NSW: router slabs per wave (ceil(H/256/4))
+// NORM (H <= 2048: a wave's slabs are one load pair): x is the residual row.
+// The rows' RMSNorm scales come from the x values loaded for the dots: a 256-
+// column slab is one 64-run chunk of the order every RMSNorm here uses (lane i
+// holds run 64 slab + i), so each wave takes its slabs' chunk trees for its
+// tokens (dpp_sum_f64<64>), the chunk sums meet in LDS, and each wave forms its
+// tokens' scales (the tree over the chunks; the same bits in every block and in
+// the standalone RMSNorm).  Block 0 stores them for the table launch's Q8_0 of
+// x; the router input is (x * scale) * norm_w.
+template <int NSW, bool NORM>  // NSW: router slabs per wave (ceil(H/256/4))
 __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits) {
+#pragma clang fp contract(off)
     __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
+    __shared__ double s_chunk[NORM ? kTopkTokensPerBlock : 1][8];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    static_assert(!NORM || NSW <= 2, "the fused norm takes rows of at most 8 slabs");
     const int E1 = a.E + a.S;
     const int nslab = a.H / kRdSlab;
     const int part = wave % kRdParts;
@@ -1081,30 +1110,42 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     double acc[kRdVals];  // [row q][i]: token kRdGroups * i + grp
 #pragma unroll
     for (int k = 0; k < kRdVals; ++k) acc[k] = 0.0;
-    // two slabs at a time: every load of the pair issued before its FMAs
-#pragma unroll
-    for (int s0 = 0; s0 < NSW; s0 += 2) {
-        constexpr int kPair = NSW > 1 ? 2 : 1;
-        if (s0 > 0 && part + kRdParts * s0 >= nslab) break;  // uniform: no slab left for this wave
-        f32x4 w[kPair][kRdRows], xv[kPair][kRdTokSlots];
+    // two slabs at a time: every load of the pair issued before its FMAs (the
+    // first pair's before the RMSNorm scales, whose row loads then overlap them)
+    constexpr int kPair = NSW > 1 ? 2 : 1;
+    f32x4 w[kPair][kRdRows], xv[kPair][kRdTokSlots], wn[kPair];
+    float xs[kRdTokSlots];  // NORM: the RMSNorm scales of this wave's tokens
+    auto load_pair = [&](int s0) {
 #pragma unroll
         for (int u = 0; u < kPair; ++u) {
             const int c = min(part + kRdParts * (s0 + u), nslab - 1);  // this wave's slab (clamped)
 #pragma unroll
             for (int q = 0; q < kRdRows; ++q)
                 w[u][q] = *(const f32x4*)(router_row(e0 + q) + c * kRdSlab + 4 * lane);
+            if constexpr (NORM) wn[u] = *(const f32x4*)(a.norm_w + c * kRdSlab + 4 * lane);
 #pragma unroll
             for (int i = 0; i < kRdTokSlots; ++i)
                 if (kRdGroups * i + grp < a.T)
                     xv[u][i] = *(const f32x4*)(a.x + (uint64_t)(kRdGroups * i + grp) * a.H + c * kRdSlab + 4 * lane);
         }
+    };
+    auto compute_pair = [&](int s0) {
 #pragma unroll
         for (int u = 0; u < kPair; ++u) {
             if (s0 + u >= NSW || e0 >= E1 || part + kRdParts * (s0 + u) >= nslab) continue;  // uniform
 #pragma unroll
             for (int i = 0; i < kRdTokSlots; ++i) {
                 if (kRdGroups * i + grp < a.T) {
-                    const double x0 = xv[u][i].x, x1 = xv[u][i].y, x2 = xv[u][i].z, x3 = xv[u][i].w;
+                    f32x4 xx = xv[u][i];
+                    if constexpr (NORM) {
+                        const float sc = xs[i];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const float v = xx[k] * sc;
+                            xx[k] = v * wn[u][k];
+                        }
+                    }
+                    const double x0 = xx.x, x1 = xx.y, x2 = xx.z, x3 = xx.w;
 #pragma unroll
                     for (int q = 0; q < kRdRows; ++q) {
                         double& d = acc[q * kRdTokSlots + i];
@@ -1116,6 +1157,47 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
                 }
             }
         }
+    };
+    load_pair(0);
+    if constexpr (NORM) {
+#pragma unroll
+        for (int u = 0; u < kPair; ++u) {
+            const int c = part + kRdParts * u;  // slab = chunk
+            if (c >= nslab) continue;           // uniform
+#pragma unroll
+            for (int i = 0; i < kRdTokSlots; ++i) {
+                const int t = kRdGroups * i + grp;
+                if (t >= a.T) continue;  // uniform
+                double run = 0.0;        // run 64 c + lane: its four columns in order
+#pragma unroll
+                for (int k = 0; k < 4; ++k) run += (double)(xv[u][i][k] * xv[u][i][k]);
+                const double cs = dpp_sum_f64<64>(run);
+                if (lane == 63) s_chunk[t][c] = cs;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kRdTokSlots; ++i) {
+            const int t = kRdGroups * i + grp;
+            xs[i] = 1.0f;
+            if (t >= a.T) continue;
+            double cv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cv[k] = k < nslab ? s_chunk[t][k] : 0.0;
+#pragma unroll
+            for (int w2 = 4; w2 >= 1; w2 >>= 1)
+#pragma unroll
+                for (int k = 0; k < w2; ++k) cv[k] = cv[2 * k] + cv[2 * k + 1];
+            xs[i] = rms_scale_from_ssq(cv[0], a.H, a.norm_eps);
+            if (blockIdx.x == 0 && part == 0 && lane == 0) a.x_scale[t] = xs[i];
+        }
+    }
+    compute_pair(0);
+#pragma unroll
+    for (int s0 = 2; s0 < NSW; s0 += 2) {
+        if (part + kRdParts * s0 >= nslab) break;  // uniform: no slab left for this wave
+        load_pair(s0);
+        compute_pair(s0);
     }
     // wave sums of the (row, token) values: one reduce-scatter, a fixed cost
     // below the trees of 6 steps per live value
@@ -1166,7 +1248,8 @@ __global__ __launch_bounds__(1024) void k_route_decode_tables(TopkArgs a, int8_t
         shared_gateup_block<SWT, SLPR>(a, sg, blockIdx.x - 1, s_dyn, xq_qs, xq_ds);
     } else {
         const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-        if (wave < a.T) quant_token_row(a.xe, a.H, wave, lane, xq_qs, xq_ds);
+        if (wave < a.T)
+            quant_token_row(a.xe, a.H, wave, lane, xq_qs, xq_ds, a.norm_w, a.norm_w ? a.x_scale[wave] : 1.0f);
     }
 }
 
@@ -1263,13 +1346,14 @@ bool route_decode_fused(const LayerDesc& L, int T) {
 // The decode router instance for nsw slabs per wave; the routing-table launch
 // for shared-expert type swt (0 none, 1 Q4_0, 2 Q8_0) and the shared blocks'
 // lanes per row (16 for H <= 1024, 32 for H <= 2048, else 64).
-static const void* route_decode_kernel(int nsw) {
+static const void* route_decode_kernel(int nsw, bool norm) {
     static_assert(kRdParts == 4, "slabs per wave: 1 at H <= 1024, 2 at H <= 2048, 3-4 at H <= 4096");
+    if (norm) return nsw == 1 ? (const void*)k_route_decode<1, true> : nsw == 2 ? (const void*)k_route_decode<2, true> : nullptr;
     switch (nsw) {
-        case 1: return (const void*)k_route_decode<1>;
-        case 2: return (const void*)k_route_decode<2>;
-        case 3: return (const void*)k_route_decode<3>;
-        case 4: return (const void*)k_route_decode<4>;
+        case 1: return (const void*)k_route_decode<1, false>;
+        case 2: return (const void*)k_route_decode<2, false>;
+        case 3: return (const void*)k_route_decode<3, false>;
+        case 4: return (const void*)k_route_decode<4, false>;
         default: return nullptr;
     }
 }
@@ -1307,8 +1391,12 @@ static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, c
 }
 
 static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
-                                      const RouteDebug& dbg, bool& x_f16, hipStream_t stream) {
+                                      const RouteDebug& dbg, bool& x_f16, hipStream_t stream, const float* norm_w,
+                                      float eps) {
     TopkArgs ta;
+    ta.norm_w = nullptr;
+    ta.norm_eps = eps;
+    ta.x_scale = ws.x_scale;
     ta.logits = ws.logits;
     ta.logit_bound = ws.logit_bound;
     ta.x = xr;
@@ -1380,6 +1468,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         // the shared expert's h on other CUs meanwhile)
         ta.dslots = ws.dslots;
         ta.defer_softmax = 1;
+        ta.norm_w = norm_w;
         const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
         const int nslab = L.H / kRdSlab;
         SharedGuArgs sg{};
@@ -1399,7 +1488,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         const int lpr = L.H <= 1024 ? 16 : (L.H <= 2048 ? 32 : 64);
         const int nsw = (nslab + kRdParts - 1) / kRdParts;  // slabs per wave
         const int swt = !sg.n_blocks ? 0 : (L.gu_type == kTypeQ4_0 ? 1 : 2);
-        const void* kern = route_decode_kernel(nsw);
+        const void* kern = route_decode_kernel(nsw, ta.norm_w != nullptr);
         if (!kern) return hipErrorInvalidValue;
         float* logits = ws.logits;
         void* args[] = {&ta, &logits};
@@ -1426,9 +1515,12 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
     return hipGetLastError();
 }
 
+bool route_norm_fused(const LayerDesc& L, int T) { return route_decode_fused(L, T) && L.H <= 8 * kRdSlab; }
+
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
-                        const RouteDebug& dbg, bool x_f16, hipStream_t stream) {
-    hipError_t err = launch_route_tables(L, ws, x, xr, T, dbg, x_f16, stream);
+                        const RouteDebug& dbg, bool x_f16, hipStream_t stream, const float* norm_w, float eps) {
+    if (norm_w && (x_f16 || !route_norm_fused(L, T))) return hipErrorInvalidValue;
+    hipError_t err = launch_route_tables(L, ws, x, xr, T, dbg, x_f16, stream, norm_w, eps);
     if (err != hipSuccess || !x_f16) return err;
     // the routing launch did not write x's f16 quants (only the batched router's does)
     hipLaunchKernelGGL(k_x_f16, dim3((T + 3) / 4), dim3(256), 0, stream, x, T, L.H, ws.x_q, ws.x_d, ws.xq_qs, ws.xq_ds);
