@@ -207,10 +207,11 @@ void qmoe_residency_reset(qmoe_residency* tracker);
 
 /* The caller slice of the reference's block (qwen36.cpp:297-304 and 427-432)
  * in one call: y = x + MoE(RMSNorm(x) * norm_w), RMSNorm as qmoe_rms_norm.
- * The normalized rows live in the workspace and the residual add is the
- * combine epilogue.  Bits equal qmoe_rms_norm followed by
- * qmoe_layer_forward(residual = x).  No counterpart as one call in the
- * reference; for callers that own the whole block. */
+ * At decode sizes (n_tokens <= 16, n_embd <= 2048) the routing normalizes x as
+ * it loads it (no RMSNorm launch); otherwise the normalized rows go to the
+ * workspace.  The residual add is the combine epilogue.  Bits equal
+ * qmoe_rms_norm followed by qmoe_layer_forward(residual = x).  No counterpart
+ * as one call in the reference; for callers that own the whole block. */
 int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* norm_w,
                             float eps, int32_t n_tokens, float* y, const qmoe_debug* dbg, void* hip_stream);
 
@@ -255,7 +256,11 @@ int qmoe_gemma4_moe_inputs(const float* x, const float* pre_norm_w, const float*
 int qmoe_gelu_f16_table(uint16_t* out);
 
 /* Replaces build_rms_norm (norm.cpp:15-26): y = x / sqrt(mean(x^2) + eps) * w,
- * per token (ggml_rms_norm followed by ggml_mul).  w may be NULL (no scale). */
+ * per token (ggml_rms_norm followed by ggml_mul).  w may be NULL (no scale).
+ * The sum of squares is f64 of the f32 squares, in one fixed order (runs of four
+ * columns, then a pairwise tree: ggml adds the columns in turn, which rounds
+ * differently only where the sum lies within a few f64 ulps of an f32
+ * rounding boundary of the mean).  n_embd up to 65536 (QMOE_ERR_VALUE above). */
 int qmoe_rms_norm(const float* x, const float* w, int32_t n_tokens, int32_t n_embd,
                   float eps, float* y, void* hip_stream);
 
