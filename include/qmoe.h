@@ -112,6 +112,14 @@ int qmoe_layer_create(const qmoe_tensor* w_router,
 int qmoe_layer_destroy(qmoe_layer* layer);
 /* n_embd of a created layer (ne[0] of w_router). */
 int qmoe_layer_n_embd(const qmoe_layer* layer);
+/* Reads the layer's expert tensors now (their data must be in place) and keeps
+ * chunk-major copies of them for the prefill GEMMs (block pairs of one k chunk
+ * of consecutive rows side by side), which then load a few cache lines per wave
+ * instead of one per lane.  Costs one more copy of the expert weights in device
+ * memory, freed by qmoe_layer_destroy; a layer without it works the same, its
+ * prefill GEMMs reading the GGUF rows.  Idempotent.  No counterpart in the
+ * reference (ggml's mul_mat_id reads the rows as stored). */
+int qmoe_layer_build_prefill_copies(qmoe_layer* layer);
 
 /* Scratch for routing tables, quantized activations and per-row outputs,
  * sized for up to max_tokens tokens of layers no larger than `like`.  One

@@ -48,6 +48,9 @@ public:
     MoELayer& operator=(const MoELayer&) = delete;
 
     int n_embd() const { return qmoe_layer_n_embd(layer_); }
+    // Chunk-major copies of the expert matrices for the prefill GEMMs, read from
+    // the tensors now (their data in place); one more copy of the expert weights.
+    void build_prefill_copies() { check(qmoe_layer_build_prefill_copies(layer_)); }
     // Device histogram u64[n_experts] that every later forward adds its
     // per-expert dispatch counts to (nullptr stops it).
     void set_expert_counts(uint64_t* device_counts) { check(qmoe_layer_set_expert_counts(layer_, device_counts)); }

@@ -30,6 +30,7 @@ EXPORTED = (
     "qmoe_layer_create",
     "qmoe_layer_destroy",
     "qmoe_layer_n_embd",
+    "qmoe_layer_build_prefill_copies",
     "qmoe_workspace_create",
     "qmoe_workspace_destroy",
     "qmoe_workspace_capacity",
@@ -145,6 +146,8 @@ def lib() -> ctypes.CDLL:
     L.qmoe_layer_destroy.argtypes = [vp]
     L.qmoe_layer_n_embd.restype = ctypes.c_int
     L.qmoe_layer_n_embd.argtypes = [vp]
+    L.qmoe_layer_build_prefill_copies.restype = ctypes.c_int
+    L.qmoe_layer_build_prefill_copies.argtypes = [vp]
     L.qmoe_workspace_create.restype = ctypes.c_int
     L.qmoe_workspace_create.argtypes = [vp, ctypes.c_int32, P(vp)]
     L.qmoe_workspace_destroy.restype = ctypes.c_int

@@ -89,10 +89,13 @@ constexpr float kActRel = 4.5e-7f;
 
 struct F16Args {
     int H, F, E;
-    const uint8_t* w0; uint64_t w0_nb1, w0_nb2;  // gate (gate/up) or down
-    const uint8_t* w1; uint64_t w1_nb1, w1_nb2;  // up (gate/up)
-    const uint8_t* sh0; uint64_t sh0_nb1;        // shared gate or shared down
-    const uint8_t* sh1; uint64_t sh1_nb1;        // shared up
+    const uint8_t* w0; uint64_t w0_nb2;  // gate (gate/up) or down; expert stride
+    const uint8_t* w1; uint64_t w1_nb2;  // up (gate/up)
+    const uint8_t* sh0;                  // shared gate or shared down
+    const uint8_t* sh1;                  // shared up
+    // byte strides of a weight row (a GEMM column) and of a block pair: the GGUF
+    // rows (nb1, pair bytes) or the chunk-major copies (pair bytes, rows * pair bytes)
+    uint32_t w0_cs, w0_ps, w1_cs, w1_ps, sh0_cs, sh0_ps, sh1_cs, sh1_ps;
     const int32_t* counters;                     // [1] n_tiles
     const int4* tiles;
     const int32_t* row_token;                    // gate/up: the token of each output row
@@ -386,18 +389,20 @@ __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
     // this lane's weight row (wave-uniform slab base + 32-bit row offset: an
     // expert's slab is far below 4 GiB)
     const uint8_t* wbase;
-    uint32_t woff;
+    uint32_t woff, wps;
     int out_col;
     if (GATEUP) {
         const bool up = wave >= 2;
         const int f = y * 64 + 32 * (wave & 1) + col;
         wbase = up ? (sh ? a.sh1 : a.w1 + (uint64_t)e * a.w1_nb2) : (sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2);
-        woff = (uint32_t)(f * (up ? (sh ? a.sh1_nb1 : a.w1_nb1) : (sh ? a.sh0_nb1 : a.w0_nb1)));
+        woff = (uint32_t)f * (up ? (sh ? a.sh1_cs : a.w1_cs) : (sh ? a.sh0_cs : a.w0_cs));
+        wps = up ? (sh ? a.sh1_ps : a.w1_ps) : (sh ? a.sh0_ps : a.w0_ps);
         out_col = f;
     } else {
         out_col = y * 128 + 32 * wave + col;
         wbase = sh ? a.sh0 : a.w0 + (uint64_t)e * a.w0_nb2;
-        woff = (uint32_t)(out_col * (sh ? a.sh0_nb1 : a.w0_nb1));
+        woff = (uint32_t)out_col * (sh ? a.sh0_cs : a.w0_cs);
+        wps = sh ? a.sh0_ps : a.w0_ps;
     }
     constexpr uint32_t kPairBytes = 2 * BlockTraits<WT>::kBytes;
     const int npairs = nblk >> 1;
@@ -461,7 +466,7 @@ __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
 #pragma unroll
         for (int pp = 0; pp < kPPC; ++pp) {
             const int pair = min(kPPC * c + pp, npairs - 1);
-            dst[pp].load(wbase, woff + (uint32_t)pair * kPairBytes, kh);
+            dst[pp].load(wbase, woff + (uint32_t)pair * wps, kh);
         }
     };
     // this lane's A fragment: row col of each 32-row tile, k offset 8 kh (+ 16 for half 1)
@@ -696,6 +701,85 @@ __global__ __launch_bounds__(256) void k_fix_h(FixArgs a) {
     }
 }
 
+// Chunk-major copy of one expert matrix: pair p of row r of expert e (GGUF rows
+// of nb1 bytes, experts nb2 apart) to dst + ((e * npairs + p) * rows + r) * pb.
+// One thread per dword of the copy (pairs and rows are 4-byte aligned).
+__global__ __launch_bounds__(256) void k_repack_pairs(const uint8_t* src, uint64_t nb1, uint64_t nb2, int rows,
+                                                      int npairs, int pb, uint64_t n_dwords, uint8_t* dst) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_dwords) return;
+    const int pd = pb >> 2;
+    const uint64_t q = i / (uint64_t)pd;  // pair index in the copy: (e * npairs + p) * rows + r
+    const int w = (int)(i - q * pd);
+    const uint64_t r = q % (uint64_t)rows, ep = q / (uint64_t)rows;
+    const uint64_t p = ep % (uint64_t)npairs, e = ep / (uint64_t)npairs;
+    ((uint32_t*)dst)[i] = *(const uint32_t*)(src + e * nb2 + r * nb1 + p * (uint64_t)pb + 4u * (uint32_t)w);
+}
+
+static size_t pk_bytes(int type, int rows, int k, int nexp) {
+    const int pb = 2 * (type == kTypeQ4_0 ? BlockTraits<kTypeQ4_0>::kBytes : BlockTraits<kTypeQ8_0>::kBytes);
+    return (size_t)nexp * (size_t)(k / 64) * (size_t)rows * (size_t)pb;
+}
+
+static hipError_t repack(const uint8_t* src, uint64_t nb1, uint64_t nb2, int type, int rows, int k, int nexp,
+                         uint8_t* dst) {
+    const int pb = 2 * (type == kTypeQ4_0 ? BlockTraits<kTypeQ4_0>::kBytes : BlockTraits<kTypeQ8_0>::kBytes);
+    const uint64_t n = (uint64_t)pk_bytes(type, rows, k, nexp) / 4;
+    hipLaunchKernelGGL(k_repack_pairs, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nullptr, src, nb1, nb2, rows,
+                       k / 64, pb, n, dst);
+    return hipGetLastError();
+}
+
+hipError_t build_prefill_copies(LayerDesc& d) {
+    const size_t g = pk_bytes(d.gu_type, d.F, d.H, d.E), dn = pk_bytes(d.dn_type, d.H, d.F, d.E);
+    const size_t sg = d.S ? pk_bytes(d.gu_type, d.F, d.H, 1) : 0, sd = d.S ? pk_bytes(d.dn_type, d.H, d.F, 1) : 0;
+    void* base = nullptr;
+    hipError_t err = hipMalloc(&base, 2 * g + dn + 2 * sg + sd);
+    if (err != hipSuccess) return err;
+    uint8_t* p = (uint8_t*)base;
+    uint8_t* pg = p; p += g;
+    uint8_t* pu = p; p += g;
+    uint8_t* pd = p; p += dn;
+    uint8_t* psg = d.S ? p : nullptr; p += sg;
+    uint8_t* psu = d.S ? p : nullptr; p += sg;
+    uint8_t* psd = d.S ? p : nullptr;
+    if (err == hipSuccess) err = repack(d.w_gate, d.gate_nb1, d.gate_nb2, d.gu_type, d.F, d.H, d.E, pg);
+    if (err == hipSuccess) err = repack(d.w_up, d.up_nb1, d.up_nb2, d.gu_type, d.F, d.H, d.E, pu);
+    if (err == hipSuccess) err = repack(d.w_down, d.down_nb1, d.down_nb2, d.dn_type, d.H, d.F, d.E, pd);
+    if (d.S) {
+        if (err == hipSuccess) err = repack(d.w_sh_gate, d.sh_gate_nb1, 0, d.gu_type, d.F, d.H, 1, psg);
+        if (err == hipSuccess) err = repack(d.w_sh_up, d.sh_up_nb1, 0, d.gu_type, d.F, d.H, 1, psu);
+        if (err == hipSuccess) err = repack(d.w_sh_down, d.sh_down_nb1, 0, d.dn_type, d.H, d.F, 1, psd);
+    }
+    if (err == hipSuccess) err = hipDeviceSynchronize();
+    if (err != hipSuccess) {
+        (void)hipFree(base);
+        return err;
+    }
+    d.pk_base = base;
+    d.pk_gate = pg; d.pk_up = pu; d.pk_down = pd;
+    d.pk_sh_gate = psg; d.pk_sh_up = psu; d.pk_sh_down = psd;
+    return hipSuccess;
+}
+
+// A weight operand of the prefill GEMMs: its chunk-major copy when the layer has
+// one (rows of the matrix, k its reduction length), else the GGUF rows.
+static void set_weights(const uint8_t*& w, uint64_t& nb2, uint32_t& cs, uint32_t& ps, const uint8_t* pk,
+                        const uint8_t* gguf, uint64_t gguf_nb1, uint64_t gguf_nb2, int type, int rows, int k) {
+    const uint32_t pb = 2 * (type == kTypeQ4_0 ? BlockTraits<kTypeQ4_0>::kBytes : BlockTraits<kTypeQ8_0>::kBytes);
+    if (pk) {
+        w = pk;
+        nb2 = (uint64_t)(k / 64) * (uint64_t)rows * pb;
+        cs = pb;
+        ps = (uint32_t)rows * pb;
+    } else {
+        w = gguf;
+        nb2 = gguf_nb2;
+        cs = (uint32_t)gguf_nb1;
+        ps = pb;
+    }
+}
+
 static F16Args base_f16_args(const LayerDesc& L, const Workspace& ws) {
     F16Args a{};
     a.H = L.H; a.F = L.F; a.E = L.E;
@@ -728,10 +812,11 @@ static hipError_t launch_f16(Kern kern, dim3 grid, hipStream_t stream, hipEvent_
 hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
                               hipEvent_t ev_start, hipEvent_t ev_stop) {
     F16Args a = base_f16_args(L, ws);
-    a.w0 = L.w_gate; a.w0_nb1 = L.gate_nb1; a.w0_nb2 = L.gate_nb2;
-    a.w1 = L.w_up; a.w1_nb1 = L.up_nb1; a.w1_nb2 = L.up_nb2;
-    a.sh0 = L.w_sh_gate; a.sh0_nb1 = L.sh_gate_nb1;
-    a.sh1 = L.w_sh_up; a.sh1_nb1 = L.sh_up_nb1;
+    set_weights(a.w0, a.w0_nb2, a.w0_cs, a.w0_ps, L.pk_gate, L.w_gate, L.gate_nb1, L.gate_nb2, L.gu_type, L.F, L.H);
+    set_weights(a.w1, a.w1_nb2, a.w1_cs, a.w1_ps, L.pk_up, L.w_up, L.up_nb1, L.up_nb2, L.gu_type, L.F, L.H);
+    uint64_t nb2_unused = 0;
+    set_weights(a.sh0, nb2_unused, a.sh0_cs, a.sh0_ps, L.pk_sh_gate, L.w_sh_gate, L.sh_gate_nb1, 0, L.gu_type, L.F, L.H);
+    set_weights(a.sh1, nb2_unused, a.sh1_cs, a.sh1_ps, L.pk_sh_up, L.w_sh_up, L.sh_up_nb1, 0, L.gu_type, L.F, L.H);
     a.a_q = ws.x_q; a.a_d = ws.x_d;
     a.K = L.H;
     a.n_y = L.F / 64;
@@ -767,8 +852,9 @@ hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hi
 
 hipError_t launch_down_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream) {
     F16Args a = base_f16_args(L, ws);
-    a.w0 = L.w_down; a.w0_nb1 = L.down_nb1; a.w0_nb2 = L.down_nb2;
-    a.sh0 = L.w_sh_down; a.sh0_nb1 = L.sh_down_nb1;
+    set_weights(a.w0, a.w0_nb2, a.w0_cs, a.w0_ps, L.pk_down, L.w_down, L.down_nb1, L.down_nb2, L.dn_type, L.H, L.F);
+    uint64_t nb2_unused = 0;
+    set_weights(a.sh0, nb2_unused, a.sh0_cs, a.sh0_ps, L.pk_sh_down, L.w_sh_down, L.sh_down_nb1, 0, L.dn_type, L.H, L.F);
     a.a_q = ws.h_q; a.a_d = ws.h_d;
     a.K = L.F;
     a.n_y = L.H / 128;

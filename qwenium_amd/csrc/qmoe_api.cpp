@@ -302,6 +302,14 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
     return QMOE_OK;
 }
 
+int qmoe_layer_build_prefill_copies(qmoe_layer* layer) {
+    g_last_error.clear();
+    if (!layer) return fail(QMOE_ERR_NULL, "qmoe: layer expected non-null, got null");
+    if (layer->d.pk_base) return QMOE_OK;
+    const hipError_t err = qmoe::build_prefill_copies(layer->d);
+    return err == hipSuccess ? QMOE_OK : hip_fail(err, "prefill weight copies");
+}
+
 int qmoe_geglu_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_gate_up_exps,
                             const qmoe_tensor* w_down_exps, const qmoe_hparams* hp, qmoe_layer** out) {
     g_last_error.clear();
@@ -342,6 +350,7 @@ int qmoe_geglu_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_ga
 int qmoe_layer_destroy(qmoe_layer* layer) {
     if (!layer) return QMOE_OK;
     if (layer->own_ws) qmoe_workspace_destroy(layer->own_ws);
+    if (layer->d.pk_base) (void)hipFree(layer->d.pk_base);
     delete layer;
     return QMOE_OK;
 }

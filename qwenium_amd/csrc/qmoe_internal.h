@@ -52,7 +52,20 @@ struct LayerDesc {
     unsigned long long* expert_counts = nullptr;  // optional device [E]: += each forward's per-expert dispatches
     int act = 0;                            // 0 SwiGLU (silu(g)*u), 1 GeGLU-tanh (gelu(g)*u, ggml's fp16 table)
     const uint16_t* gelu_tab = nullptr;     // device [65536] fp16 gelu table of the layer's device (GeGLU)
+    // Chunk-major copies of the expert matrices for the prefill GEMMs (null: they
+    // read the GGUF rows): [expert][block pair p][row r] raw block pairs, so the
+    // lanes of a wave read consecutive pairs of one k chunk (a few cache lines
+    // per load instead of one per lane).  Built once at creation; pk_base owns them.
+    const uint8_t* pk_gate = nullptr;
+    const uint8_t* pk_up = nullptr;
+    const uint8_t* pk_down = nullptr;
+    const uint8_t* pk_sh_gate = nullptr;
+    const uint8_t* pk_sh_up = nullptr;
+    const uint8_t* pk_sh_down = nullptr;
+    void* pk_base = nullptr;
 };
+// The chunk-major copies (LayerDesc::pk_*) of a layer's expert matrices.
+hipError_t build_prefill_copies(LayerDesc& d);
 
 // Device scratch.  R = T*K + S*T rows: routed assignments sorted by expert,
 // then the shared expert's rows in token order.

@@ -15,6 +15,7 @@ from __future__ import annotations
 import contextlib
 import ctypes
 import dataclasses
+import os
 from typing import Optional
 
 import torch
@@ -139,7 +140,8 @@ class MoELayer:
 
     def __init__(self, w_router: GGMLTensor, w_exp_gate: GGMLTensor, w_exp_up: GGMLTensor,
                  w_exp_down: GGMLTensor, w_sh_gate: Optional[GGMLTensor], w_sh_up: Optional[GGMLTensor],
-                 w_sh_down: Optional[GGMLTensor], w_sh_norm: Optional[GGMLTensor], hp: Hparams):
+                 w_sh_down: Optional[GGMLTensor], w_sh_norm: Optional[GGMLTensor], hp: Hparams, *,
+                 prefill_copies: bool = True):
         self.hp = hp
         # keep the borrowed weights alive for the layer's lifetime
         self._weights = (w_router, w_exp_gate, w_exp_up, w_exp_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_norm)
@@ -150,6 +152,18 @@ class MoELayer:
         check(lib().qmoe_layer_create(*ptrs, ctypes.byref(c_hp), ctypes.byref(h)))
         self._handle = h
         self.n_embd = int(lib().qmoe_layer_n_embd(h))
+        self._maybe_prefill_copies(prefill_copies, w_exp_gate)
+
+    def _maybe_prefill_copies(self, wanted: bool, probe: GGMLTensor) -> None:
+        # the copies read the weights now: only for device-resident tensors, and not
+        # when QMOE_PREFILL_REPACK=0 (the prefill GEMMs then read the GGUF rows)
+        if wanted and probe.data.is_cuda and os.environ.get("QMOE_PREFILL_REPACK", "1") != "0":
+            self.build_prefill_copies()
+
+    def build_prefill_copies(self) -> None:
+        """Chunk-major copies of the expert matrices for the prefill GEMMs (one more copy
+        of the expert weights in device memory); reads the tensors now."""
+        check(lib().qmoe_layer_build_prefill_copies(self._handle))
 
     def close(self) -> None:
         if getattr(self, "_handle", None):
@@ -259,7 +273,8 @@ class GeGLUMoELayer(MoELayer):
     the fused gate_up tensor [n_embd, 2*ffn_dim, n_experts], GeGLU-tanh
     (ggml's CPU gelu), no shared expert, the router on its own input."""
 
-    def __init__(self, w_router: GGMLTensor, w_gate_up_exps: GGMLTensor, w_down_exps: GGMLTensor, hp: Hparams):
+    def __init__(self, w_router: GGMLTensor, w_gate_up_exps: GGMLTensor, w_down_exps: GGMLTensor, hp: Hparams, *,
+                 prefill_copies: bool = True):
         if hp.has_shared_expert:
             raise ValueError("has_shared_expert expected False for the GeGLU MoE, got True")
         self.hp = hp
@@ -270,6 +285,7 @@ class GeGLUMoELayer(MoELayer):
         check(lib().qmoe_geglu_layer_create(*(ctypes.byref(d) for d in descs), ctypes.byref(c_hp), ctypes.byref(h)))
         self._handle = h
         self.n_embd = int(lib().qmoe_layer_n_embd(h))
+        self._maybe_prefill_copies(prefill_copies, w_gate_up_exps)
 
     def forward_gemma4(self, x: torch.Tensor, pre_norm_weight: torch.Tensor, router_scale: torch.Tensor, eps: float,
                        *, out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None,
