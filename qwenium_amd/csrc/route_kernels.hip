@@ -576,6 +576,31 @@ __device__ __forceinline__ void exact_dot2(const float* w0, const float* w1, con
     r1 = (float)wave_sum_f64(a1);
 }
 
+// The same dots for four rows at once (x read once per four rows), each row in
+// the same order as exact_dot2 (so the same bits), two 256-column chunks per step.
+__device__ __forceinline__ void exact_dot4(const float* const (&w)[4], const float* xr, int H, int lane,
+                                           float (&r)[4]) {
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    const int nch = H >> 8;
+    for (int c = 0; c < nch; c += 2) {
+        f32x4 xv[2], v[4][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int o = min(c + i, nch - 1) * 256 + 4 * lane;
+            xv[i] = *(const f32x4*)(xr + o);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k][i] = *(const f32x4*)(w[k] + o);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            if (c + i < nch)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[k] = dot4_f64(v[k][i], xv[i], acc[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = (float)wave_sum_f64(acc[k]);
+}
+
 // Selection keys: the float's bits mapped to an unsigned order (negative values
 // flipped, positive values with the sign bit set) in the high word, ~id in the
 // low word, so the larger key is the larger logit and, among equal logits,
@@ -766,33 +791,63 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
         }
         if (removed >= a.K) { thr = mx; break; }
     }
-    // exact logits of the candidates, two rows per pass
+    // exact logits of the candidates and of the shared gate: one queue over
+    // every group, four rows per pass, a remainder of one or two in a last pass
     const float* xr = a.x + (uint64_t)t * a.H;
     float v[EPL];
     int id[EPL];
+    uint64_t mk[EPL];
+    int n = a.S ? 1 : 0;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
         const int e = i * 64 + lane;
-        const bool cand = e < a.E && up[i] >= thr;
         v[i] = -__builtin_huge_valf();
         id[i] = e < a.E ? e : 0x7fffffff;
-        uint64_t m = __ballot(cand);
-        while (m) {
-            const int b0 = __builtin_ctzll(m);
-            m &= m - 1;
-            int b1 = b0;
-            if (m) { b1 = __builtin_ctzll(m); m &= m - 1; }
-            float r0, r1;
-            exact_dot2(a.w_router + (uint64_t)(i * 64 + b0) * a.router_ld,
-                       a.w_router + (uint64_t)(i * 64 + b1) * a.router_ld, xr, a.H, lane, r0, r1);
-            if (lane == b0) v[i] = r0;
-            if (lane == b1) v[i] = r1;
-        }
+        mk[i] = __ballot(e < a.E && up[i] >= thr);
+        n += __builtin_popcountll(mk[i]);
     }
+    bool sh = a.S != 0;
     float sg = 0.0f;
-    if (a.S) {
-        float sg2;
-        exact_dot2(a.w_sh_norm, a.w_sh_norm, xr, a.H, lane, sg, sg2);
+    // next queue entry: group g (EPL = the shared gate) and lane b
+    auto pop = [&](int& g, int& b) {
+        g = -1;
+        b = 0;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+            if (g < 0 && mk[i]) { g = i; b = __builtin_ctzll(mk[i]); mk[i] &= mk[i] - 1; }
+        if (g < 0 && sh) { g = EPL; sh = false; }
+    };
+    auto row = [&](int g, int b) {
+        return g == EPL ? a.w_sh_norm : a.w_router + (uint64_t)(g * 64 + b) * a.router_ld;
+    };
+    auto put = [&](int g, int b, float r) {
+        if (g == EPL) sg = r;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+            if (g == i && lane == b) v[i] = r;
+    };
+    for (; n >= 3; n -= 4) {
+        int g[4], b[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pop(g[k], b[k]);
+        const float* w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = row(g[k] < 0 ? g[0] : g[k], g[k] < 0 ? b[0] : b[k]);
+        float r[4];
+        exact_dot4(w, xr, a.H, lane, r);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (g[k] >= 0) put(g[k], b[k], r[k]);
+    }
+    if (n > 0) {
+        int g0, b0, g1, b1;
+        pop(g0, b0);
+        pop(g1, b1);
+        if (g1 < 0) { g1 = g0; b1 = b0; }
+        float r0, r1;
+        exact_dot2(row(g0, b0), row(g1, b1), xr, a.H, lane, r0, r1);
+        put(g0, b0, r0);
+        put(g1, b1, r1);
     }
     select_softmax<EPL>(a, t, lane, v, id, sg, s_idx_row, s_val_row, s_ex_row, nullptr);
 }
