@@ -185,7 +185,7 @@ def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
     import numpy as np
     import torch
 
-    from qwenium_amd import TYPE_Q4_0, Workspace, gemma4_moe_inputs, lib, rms_norm, synthetic
+    from qwenium_amd import TYPE_Q4_0, Workspace, gemma4_moe_inputs, lib, rms_norm, ssq_parts, synthetic
     from qwenium_amd._lib import check, row_bytes
 
     T0, spec_name, L0, B0, S0, W0 = WORKLOADS[workload]
@@ -211,18 +211,24 @@ def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
     y = torch.empty((T, H), dtype=torch.float32, device=dev)
     hbuf = torch.empty((T, H), dtype=torch.float32, device=dev)
     xbuf = [torch.empty((T, H), dtype=torch.float32, device=dev) for _ in range(2)]
+    # at decode sizes each block's RMSNorm partial sums go to the next block (its
+    # routing then finishes the sum instead of reading x for it)
+    carry = stack and T <= 16
+    sbuf = [torch.empty((T, ssq_parts(H)), dtype=torch.float64, device=dev) for _ in range(2)] if carry else None
     torch.cuda.synchronize()
 
     def stack_pass(b, keep=None):
         """x <- x + MoE_l(RMSNorm(x) * w_l) for l = 0..L-1 (qwen36.cpp:297-304); keep[l] gets layer l's input."""
-        cur = xs[b]
+        cur, cur_ssq = xs[b], None
         for l in range(L):
             if keep is not None and l in keep:
                 keep[l] = cur.clone()
             nxt = xbuf[l & 1]
+            nxt_ssq = sbuf[l & 1] if carry else None
             # the block's slice in one call: nxt = cur + MoE(RMSNorm(cur) * w_l)
-            layers[l].forward_norm(cur, norms[l], synthetic.NORM_EPS, out=nxt, workspace=ws)
-            cur = nxt
+            layers[l].forward_norm(cur, norms[l], synthetic.NORM_EPS, out=nxt, workspace=ws, x_ssq=cur_ssq,
+                                   y_ssq=nxt_ssq)
+            cur, cur_ssq = nxt, nxt_ssq
         return cur
 
     if stack:

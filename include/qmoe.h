@@ -223,6 +223,26 @@ void qmoe_residency_reset(qmoe_residency* tracker);
 int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const float* norm_w,
                             float eps, int32_t n_tokens, float* y, const qmoe_debug* dbg, void* hip_stream);
 
+/* qmoe_layer_forward_norm for a chain of blocks (qwen36.cpp:297-304 and
+ * 427-432 over the layers, x <- x + MoE_l(RMSNorm(x) * w_l)), carrying each
+ * block's RMSNorm sum of squares to the next:
+ *   x_ssq: NULL, or [n_tokens][ceil(n_embd/32)] doubles, the partial sums of x
+ *          as qmoe_rms_partials defines them (a previous call's y_ssq);
+ *   y_ssq: NULL, or receives y's partial sums in that layout.
+ * Entry c of a row is the sum of squares of columns 32c .. 32c+31 in
+ * qmoe_rms_norm's order (runs of four, then the pairwise tree), so the tree
+ * over a row's entries is the row's sum: with or without x_ssq the bits equal
+ * qmoe_layer_forward_norm's.  Where the decode routing normalizes on the fly
+ * it finishes the tree from x_ssq instead of summing x (elsewhere x_ssq is not
+ * read: n_tokens <= 16 and n_embd <= 2048); at decode sizes the down+combine
+ * epilogue writes y_ssq, otherwise one more launch does (a caller at prefill
+ * sizes gains nothing from the pair and passes NULL for both).  x_ssq and
+ * y_ssq may be the same buffer.  16-byte aligned.
+ * No counterpart in the reference; for callers that run the whole stack. */
+int qmoe_layer_forward_norm_chain(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const double* x_ssq,
+                                  const float* norm_w, float eps, int32_t n_tokens, float* y, double* y_ssq,
+                                  const qmoe_debug* dbg, void* hip_stream);
+
 /* ---------------------------------------------------------------------------
  * Gemma 4 GeGLU MoE (replaces Gemma4ForwardPass::build_moe_geglu,
  * src/models/gemma4.cpp:367-445).  The same router, top-k, softmax, count
@@ -271,6 +291,12 @@ int qmoe_gelu_f16_table(uint16_t* out);
  * rounding boundary of the mean).  n_embd up to 65536 (QMOE_ERR_VALUE above). */
 int qmoe_rms_norm(const float* x, const float* w, int32_t n_tokens, int32_t n_embd,
                   float eps, float* y, void* hip_stream);
+/* out[n_tokens][ceil(n_embd/32)]: qmoe_rms_norm's sum of squares of each row in
+ * pieces of 32 columns -- entry c is the subtree over runs 8c .. 8c+7 (run r:
+ * f64(x[4r]^2) + ... + f64(x[4r+3]^2) in column order, columns past n_embd
+ * skipped), i.e. ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)).  No counterpart in the
+ * reference (it sums inside ggml_rms_norm); the input of forward_norm_chain. */
+int qmoe_rms_partials(const float* x, int32_t n_tokens, int32_t n_embd, double* out, void* hip_stream);
 
 /* Seeded synthetic data for tests and benchmarks, generated on the device.
  * Value i of a stream is N(mean, sigma) from a counter-based hash of

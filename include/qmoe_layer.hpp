@@ -64,6 +64,17 @@ public:
                  const qmoe_debug* dbg = nullptr) {
         check(qmoe_layer_forward(layer_, ws, x, n_tokens, y, residual, dbg, stream));
     }
+    // The block's caller slice (qwen36.cpp:297-304): y = x + MoE(RMSNorm(x) * norm_w).
+    // x_ssq / y_ssq (optional, [n_tokens][ceil(n_embd/32)] doubles): x's RMSNorm
+    // partial sums in, y's out, for a chain of blocks; the bits do not change.
+    void forward_norm(const float* x, const float* norm_w, float eps, int n_tokens, float* y, void* stream = nullptr,
+                      qmoe_workspace* ws = nullptr, const double* x_ssq = nullptr, double* y_ssq = nullptr,
+                      const qmoe_debug* dbg = nullptr) {
+        if (x_ssq || y_ssq)
+            check(qmoe_layer_forward_norm_chain(layer_, ws, x, x_ssq, norm_w, eps, n_tokens, y, y_ssq, dbg, stream));
+        else
+            check(qmoe_layer_forward_norm(layer_, ws, x, norm_w, eps, n_tokens, y, dbg, stream));
+    }
 
 private:
     Hparams hp_;

@@ -84,6 +84,7 @@ def lib() -> ctypes.CDLL:
         "qo_silu_mul": (f32, [f32, f32]),
         "qo_sigmoid": (f32, [f32]),
         "qo_rms_norm": (None, [vp, vp, i32, i32, f32, vp]),
+        "qo_rms_partials": (None, [vp, i32, i32, vp]),
         "qo_gelu_f16": (f32, [f32]),
         "qo_geglu_mul": (f32, [f32, f32]),
         "qo_gemma4_moe_inputs": (None, [vp, vp, vp, i32, i32, f32, vp, vp]),
@@ -168,6 +169,15 @@ def rms_norm(x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
     lib().qo_rms_norm(_p(x), _p(None if w is None else np.ascontiguousarray(w, dtype=np.float32)), T, H,
                       eps, _p(y))
     return y
+
+
+def rms_partials(x: np.ndarray) -> np.ndarray:
+    """qo_rms_partials: float64 [T, ceil(H/32)]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, H = x.shape
+    out = np.empty((T, (H + 31) // 32), dtype=np.float64)
+    lib().qo_rms_partials(_p(x), T, H, _p(out))
+    return out
 
 
 ACT_SILU, ACT_GELU_TANH = 0, 1

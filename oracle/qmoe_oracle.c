@@ -426,6 +426,28 @@ void qo_rms_norm(const float* x, const float* w, int T, int H, float eps, float*
     }
 }
 
+void qo_rms_partials(const float* x, int T, int H, double* out) {
+    const int np = (H + 31) / 32;
+    for (int t = 0; t < T; ++t) {
+        const float* xt = x + (size_t)t * H;
+        for (int c = 0; c < np; ++c) {
+            double r[8];
+            for (int j = 0; j < 8; ++j) {
+                double s = 0.0;
+                for (int k = 0; k < 4; ++k) {
+                    const int col = 32 * c + 4 * j + k;
+                    if (col < H) {
+                        const float q = xt[col] * xt[col];
+                        s += (double)q;
+                    }
+                }
+                r[j] = s;
+            }
+            out[(size_t)t * np + c] = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        }
+    }
+}
+
 void qo_gemma4_moe_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps,
                           float* expert_in, float* router_in) {
     const float s = 1.0f / sqrtf((float)H);

@@ -106,6 +106,12 @@ float qo_gelu_f16(float x);                  /* ggml CPU gelu (fp16 table semant
 float qo_geglu_mul(float g, float u);        /* qo_gelu_f16(g)*u in f32 */
 float qo_sigmoid(float g);
 void  qo_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y);
+/* The RMSNorm sum of squares in pieces of 32 columns, in the library's fixed
+ * order (no reference counterpart: ggml_rms_norm, norm.cpp:15-26, sums inside
+ * the op): run r = f64(f32(x[4r]^2)) + ... + f64(f32(x[4r+3]^2)) in column
+ * order (columns >= H skipped), entry c = ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7))
+ * over runs 8c .. 8c+7.  out[T][ceil(H/32)]. */
+void  qo_rms_partials(const float* x, int T, int H, double* out);
 /* Gemma 4 MoE inputs from one residual row (gemma4.cpp:555-563):
  * expert_in = (x*scale)*w_pre, router_in = ((x*scale)*(1/sqrtf(H)))*w_rs. */
 void  qo_gemma4_moe_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps,

@@ -37,9 +37,11 @@ EXPORTED = (
     "qmoe_workspace_check",
     "qmoe_layer_forward",
     "qmoe_layer_forward_norm",
+    "qmoe_layer_forward_norm_chain",
     "qmoe_layer_forward_static",
     "qmoe_layer_set_phase_events",
     "qmoe_rms_norm",
+    "qmoe_rms_partials",
     "qmoe_synth_f32",
     "qmoe_synth_quant",
     "qmoe_gguf_open",
@@ -166,6 +168,11 @@ def lib() -> ctypes.CDLL:
     L.qmoe_layer_set_phase_events.argtypes = [vp, P(vp)]
     L.qmoe_rms_norm.restype = ctypes.c_int
     L.qmoe_rms_norm.argtypes = [vp, vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, vp, vp]
+    L.qmoe_rms_partials.restype = ctypes.c_int
+    L.qmoe_rms_partials.argtypes = [vp, ctypes.c_int32, ctypes.c_int32, vp, vp]
+    L.qmoe_layer_forward_norm_chain.restype = ctypes.c_int
+    L.qmoe_layer_forward_norm_chain.argtypes = [vp, vp, vp, vp, vp, ctypes.c_float, ctypes.c_int32, vp, vp,
+                                                P(QmoeDebug), vp]
     L.qmoe_synth_f32.restype = ctypes.c_int
     L.qmoe_synth_f32.argtypes = [vp, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double,
                                  ctypes.c_double, vp]

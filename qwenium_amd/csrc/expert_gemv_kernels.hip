@@ -606,6 +606,7 @@ struct DownCombineArgs {
     const int8_t* hq_qs; const float2* hq_ds;
     const float* residual; float* y;
     const float* ysh;  // [T][H] the shared expert's down rows, computed by the gate/up launch (or null)
+    double* y_ssq;     // [T][ssq_parts(H)] y's RMSNorm partial sums (token-per-block kernel, LPR <= 8), or null
 };
 
 template <int WT>
@@ -776,6 +777,27 @@ __global__ __launch_bounds__(256) void k_down_combine_tok(DownCombineArgs a) {
         if (a.residual) acc = acc + a.residual[(uint64_t)t * a.H + n];
         a.y[(uint64_t)t * a.H + n] = acc;
     }
+    if constexpr (LPR <= 8) {
+        // y's RMSNorm partial sums: the block's 4 RPI rows are RPI runs of four,
+        // RPI / 8 whole entries (run sums in row order, then the 8-lane trees)
+        if (a.y_ssq) {  // uniform
+            __shared__ float s_y[4 * RPI];
+            if (lp == LPR - 1) s_y[wave * RPI + sub] = acc;
+            __syncthreads();
+            if (wave == 0) {
+                const int r0 = rg * 4 * RPI + 4 * lane;  // first row of run `lane`
+                double s = 0.0;
+                if (lane < RPI)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (r0 + k < a.H) s += (double)(s_y[4 * lane + k] * s_y[4 * lane + k]);
+                s = dpp_sum_f64<8>(s);
+                const int np = ssq_parts(a.H);
+                const int c = rg * (RPI / 8) + (lane >> 3);
+                if (lane < RPI && (lane & 7) == 7 && c < np) a.y_ssq[(uint64_t)t * np + c] = s;
+            }
+        }
+    }
 }
 
 bool shared_down_in_gateup(const LayerDesc& L, int T) {
@@ -827,7 +849,7 @@ static hipError_t launch_down_combine_t(const DownCombineArgs& a, int ahead, hip
 }
 
 hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
-                               hipStream_t stream) {
+                               hipStream_t stream, double* y_ssq, bool* ssq_done) {
     DownCombineArgs a;
     a.H = L.H; a.F = L.F; a.E = L.E; a.K = L.K; a.S = L.S; a.T = T;
     a.w_down = L.w_down; a.down_nb1 = L.down_nb1; a.down_nb2 = L.down_nb2;
@@ -836,6 +858,10 @@ hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, f
     a.hq_qs = ws.hq_qs; a.hq_ds = ws.hq_ds;
     a.residual = residual; a.y = y;
     a.ysh = shared_down_in_gateup(L, T) ? ws.ysh : nullptr;
+    // the token-per-block kernel with whole entries per block (LPR <= 8: F <= 512)
+    const bool ssq = y_ssq && down_combine_tok_fits(L) && L.F <= 512 && L.H % kSsqCols == 0;
+    a.y_ssq = ssq ? y_ssq : nullptr;
+    if (ssq_done) *ssq_done = ssq;
     return (L.dn_type == kTypeQ4_0) ? launch_down_combine_t<kTypeQ4_0>(a, L.dc_ahead, stream)
                                     : launch_down_combine_t<kTypeQ8_0>(a, L.dc_ahead, stream);
 }

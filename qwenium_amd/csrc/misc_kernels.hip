@@ -32,6 +32,27 @@ hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float e
     return hipGetLastError();
 }
 
+// The RMSNorm partial sums of the rows x[T][H] (ssq_parts(H) per row, each the
+// subtree over 8 runs of four columns): one block per row, lane i of a wave
+// takes run 64 m + i of its windows m, the 8-lane trees give the entries.
+__global__ __launch_bounds__(256) void k_rms_partials(const float* x, int H, double* out) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const float* xr = x + (uint64_t)t * H;
+    const int np = ssq_parts(H);
+    for (int base = 64 * wave; base < 8 * np; base += 256) {
+        const double s = dpp_sum_f64<8>(ssq_run4(xr, H, base + lane));
+        const int c = (base + lane) >> 3;
+        if ((lane & 7) == 7 && c < np) out[(uint64_t)t * np + c] = s;
+    }
+}
+
+hipError_t launch_rms_partials(const float* x, int T, int H, double* out, hipStream_t stream) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rms_partials, dim3(T), dim3(256), 0, stream, x, H, out);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Gemma 4 MoE inputs (src/models/gemma4.cpp:555-563): from the residual row x,
 //   expert_in = rms_norm(x) * pre_ffw_norm_2            (build_rms_norm)

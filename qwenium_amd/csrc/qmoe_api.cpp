@@ -456,6 +456,8 @@ struct ForwardIn {
     const float* g4_pre_w = nullptr;  // y = MoE(rms(x)*pre_w) routed on (rms(x)/sqrt(H))*rs_w
     const float* g4_rs_w = nullptr;
     float eps = 0.0f;
+    const double* x_ssq = nullptr;  // x's RMSNorm partial sums (norm_w only; optional)
+    double* y_ssq = nullptr;        // receives y's RMSNorm partial sums (optional)
 };
 
 static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& in, int32_t n_tokens, float* y,
@@ -544,7 +546,8 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         xin = v.xn;
         xr = v.xr;
     }
-    if (err == hipSuccess) err = qmoe::launch_route(d, v, xin, xr, n_tokens, rdbg, mfma, stream, route_norm_w, in.eps);
+    if (err == hipSuccess)
+        err = qmoe::launch_route(d, v, xin, xr, n_tokens, rdbg, mfma, stream, route_norm_w, in.eps, in.x_ssq);
     if (err != hipSuccess) return hip_fail(err, "route kernels");
     // events [1] and [2] are taken by the gate/up launch itself (its own start and end)
     hipEvent_t e1 = layer->record_phases ? layer->phase_events[1] : nullptr;
@@ -562,9 +565,10 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         if (err != hipSuccess) return hip_fail(err, "gate/up expert kernel");
         err = qmoe::launch_quant_h(d, v, n_tokens, stream);
     }
+    bool ssq_done = false;
     if (qmoe::down_combine_fused(d, n_tokens)) {
-        // decode: the combine runs in the down kernel's epilogue
-        if (err == hipSuccess) err = qmoe::launch_down_combine(d, v, n_tokens, y, residual, stream);
+        // decode: the combine runs in the down kernel's epilogue (and y's partial sums with it)
+        if (err == hipSuccess) err = qmoe::launch_down_combine(d, v, n_tokens, y, residual, stream, in.y_ssq, &ssq_done);
         if (err != hipSuccess) return hip_fail(err, "down+combine kernel");
         err = mark(3);
     } else {
@@ -574,6 +578,10 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         err = mark(3);
         if (err == hipSuccess) err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream);
         if (err != hipSuccess) return hip_fail(err, "combine kernel");
+    }
+    if (in.y_ssq && !ssq_done) {
+        err = qmoe::launch_rms_partials(y, n_tokens, d.H, in.y_ssq, stream);
+        if (err != hipSuccess) return hip_fail(err, "RMSNorm partial sums");
     }
     err = mark(4);
     if (err != hipSuccess) return hip_fail(err, "phase event record");
@@ -651,6 +659,35 @@ int qmoe_layer_forward_norm(qmoe_layer* layer, qmoe_workspace* ws, const float* 
     in.norm_w = norm_w;
     in.eps = eps;
     return forward_impl(layer, ws, in, n_tokens, y, dbg, hip_stream);
+}
+
+int qmoe_layer_forward_norm_chain(qmoe_layer* layer, qmoe_workspace* ws, const float* x, const double* x_ssq,
+                                  const float* norm_w, float eps, int32_t n_tokens, float* y, double* y_ssq,
+                                  const qmoe_debug* dbg, void* hip_stream) {
+    g_last_error.clear();
+    if (!norm_w) return fail(QMOE_ERR_NULL, "qmoe: norm_w expected a device pointer, got null");
+    if (!(eps >= 0.0f)) return fail(QMOE_ERR_VALUE, "qmoe: eps expected >= 0, got " + std::to_string(eps));
+    if (((uintptr_t)x_ssq & 15u) || ((uintptr_t)y_ssq & 15u))
+        return fail(QMOE_ERR_VALUE, "qmoe: x_ssq/y_ssq expected 16-byte aligned device pointers, got a misaligned one");
+    ForwardIn in;
+    in.x = x;
+    in.norm_w = norm_w;
+    in.eps = eps;
+    in.x_ssq = x_ssq;
+    in.y_ssq = y_ssq;
+    return forward_impl(layer, ws, in, n_tokens, y, dbg, hip_stream);
+}
+
+int qmoe_rms_partials(const float* x, int32_t n_tokens, int32_t n_embd, double* out, void* hip_stream) {
+    g_last_error.clear();
+    if (n_tokens < 0 || n_embd <= 0)
+        return fail(QMOE_ERR_VALUE, "qmoe: n_tokens >= 0 and n_embd > 0 expected, got " + std::to_string(n_tokens) +
+                                        ", " + std::to_string(n_embd));
+    if (n_tokens == 0) return QMOE_OK;
+    if (!x || !out) return fail(QMOE_ERR_NULL, "qmoe: x/out expected device pointers, got null");
+    if ((uintptr_t)out & 7u) return fail(QMOE_ERR_VALUE, "qmoe: out expected an 8-byte aligned device pointer");
+    const hipError_t err = qmoe::launch_rms_partials(x, n_tokens, n_embd, out, (hipStream_t)hip_stream);
+    return err == hipSuccess ? QMOE_OK : hip_fail(err, "RMSNorm partial sums");
 }
 
 int qmoe_layer_forward_routed(qmoe_layer* layer, qmoe_workspace* ws, const float* expert_in, const float* router_in,

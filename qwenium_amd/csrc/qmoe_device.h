@@ -28,6 +28,7 @@ template <> struct BlockTraits<kTypeQ8_0> { static constexpr int kBytes = 34; st
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // fp16 <-> fp32 (IEEE binary16, round to nearest even)
@@ -272,9 +273,15 @@ __device__ __forceinline__ double ssq_run4(const float* xr, int H, int r) {
 __device__ __forceinline__ double ssq_chunk64(const float* xr, int H, int c, int lane) {
     return dpp_sum_f64<64>(ssq_run4(xr, H, 64 * c + lane));
 }
+// Partial sums carried from a layer's output to the next layer's RMSNorm: entry
+// c of a row is the subtree over runs 8c .. 8c+7 (columns 32c .. 32c+31), so
+// the adjacent-pairs tree over a row's entries, zero-padded, is the row's sum.
+constexpr int kSsqCols = 32;
+__host__ __device__ constexpr int ssq_parts(int H) { return (H + kSsqCols - 1) / kSsqCols; }
 // f32 RMSNorm scale from the f64 sum of squares (ggml_rms_norm: mean in f32).
 __device__ __forceinline__ float rms_scale_from_ssq(double ssq, int H, float eps) {
-    const float mean = (float)(ssq / (double)H);
+    // a power-of-two H divides by exact scaling (one instruction, the same bits)
+    const float mean = (float)((H & (H - 1)) == 0 ? __builtin_ldexp(ssq, -__builtin_ctz(H)) : ssq / (double)H);
     return 1.0f / __builtin_sqrtf(mean + eps);
 }
 // scale = 1/sqrtf(fp32(ssq / H) + eps) of one row (H <= 256 kRmsMaxChunks), by

@@ -156,7 +156,7 @@ bool route_decode_fused(const LayerDesc& L, int T);
 // router and for x's Q8_0 (route_norm_fused says when).
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
                         const RouteDebug& dbg, bool x_f16, hipStream_t stream, const float* norm_w = nullptr,
-                        float eps = 0.0f);
+                        float eps = 0.0f, const double* x_ssq = nullptr);
 bool route_norm_fused(const LayerDesc& L, int T);
 // ev_start / ev_stop (optional): events recorded at the kernel's own start and
 // end (profiling of the dominant kernel without marker overhead).
@@ -185,9 +185,13 @@ bool down_combine_tok_fits(const LayerDesc& L);
 // into ws.ysh; the down+combine kernel adds ysh * sh_gate as its last step
 // instead of computing it.
 bool shared_down_in_gateup(const LayerDesc& L, int T);
+// y_ssq (optional): y's RMSNorm partial sums, written by the epilogue where the
+// kernel's rows allow it (*ssq_done set), otherwise left to the caller.
 hipError_t launch_down_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
-                               hipStream_t stream);
+                               hipStream_t stream, double* y_ssq = nullptr, bool* ssq_done = nullptr);
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream);
+// out[T][ssq_parts(H)]: the RMSNorm partial sums of the rows x[T][H].
+hipError_t launch_rms_partials(const float* x, int T, int H, double* out, hipStream_t stream);
 // dst[0..n) = v on `stream` (a kernel, never a memset node).
 hipError_t launch_fill_i32(int32_t* dst, int n, int32_t v, hipStream_t stream);
 // Gemma 4 MoE inputs from one pass over x (H <= 4096): expert_in = (x*scale)*w_pre,

@@ -496,6 +496,7 @@ struct TopkArgs {
     const float* norm_w;  // decode routing: x is normalized on the fly, (x * x_scale[t]) * norm_w (null: not)
     float norm_eps;
     float* x_scale;       // [T] the rows' RMSNorm scales (router block 0 writes them for the table launch)
+    const double* x_ssq;  // [T][ssq_parts(H)] x's RMSNorm partial sums, or null (the router sums x itself)
     int32_t* topk_idx;    // [T][K]
     float* topk_w;        // [T][K]
     float* sh_gate;       // [T]
@@ -1213,8 +1214,35 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
             }
         }
     };
+    // x's RMSNorm partial sums when the caller has them (one per lane, loaded
+    // ahead of the slabs): each wave finishes its tokens' trees itself
+    // x's partial sums (NORM with x_ssq): lane l takes entries 8j .. 8j+7
+    // (j = l & 7) of slot l >> 3, so that one pass of 8-lane trees covers every
+    // slot (a row has at most 64 entries: n_embd <= 2048, a multiple of 256)
+    f64x2 pq[NORM ? 4 : 1];
+    const int np = ssq_parts(a.H);
+    const int qs = min(lane >> 3, kRdTokSlots - 1), qj = lane & 7;
+    const int qt = kRdGroups * qs + grp;
+    if constexpr (NORM) {
+        if (a.x_ssq) {  // clamped addresses, masked where the sums are taken
+            const f64x2* src = (const f64x2*)(a.x_ssq + (uint64_t)min(qt, a.T - 1) * np + 8 * min(qj, np / 8 - 1));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) pq[k] = src[k];
+        }
+    }
     load_pair(0);
     if constexpr (NORM) {
+      if (a.x_ssq) {
+        // the adjacent-pairs tree of the entries: 8 in registers, then the 8
+        // lanes of a slot; one divide and square-root chain for all the slots
+        double s = ((pq[0].x + pq[0].y) + (pq[1].x + pq[1].y)) + ((pq[2].x + pq[2].y) + (pq[3].x + pq[3].y));
+        s = (lane >> 3) < kRdTokSlots && qt < a.T && 8 * qj < np ? s : 0.0;
+        s = dpp_sum_f64<8>(s);
+        const float sc = rms_scale_from_ssq(s, a.H, a.norm_eps);
+#pragma unroll
+        for (int i = 0; i < kRdTokSlots; ++i)
+            xs[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 8 * i));
+      } else {
 #pragma unroll
         for (int u = 0; u < kPair; ++u) {
             const int c = part + kRdParts * u;  // slab = chunk
@@ -1244,8 +1272,8 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
 #pragma unroll
                 for (int k = 0; k < w2; ++k) cv[k] = cv[2 * k] + cv[2 * k + 1];
             xs[i] = rms_scale_from_ssq(cv[0], a.H, a.norm_eps);
-            if (blockIdx.x == 0 && part == 0 && lane == 0) a.x_scale[t] = xs[i];
         }
+      }
     }
     compute_pair(0);
 #pragma unroll
@@ -1285,6 +1313,13 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
             for (int q = 1; q < kRdParts; ++q) sum = sum + s_part[rr][q][t];
             logits[(uint64_t)t * (a.E + 1) + er] = (float)sum;
         }
+    }
+    // the scales for the table launch's quantization of x (after every load)
+    if constexpr (NORM) {
+        if (blockIdx.x == 0 && part == 0 && lane == 0)
+#pragma unroll
+            for (int i = 0; i < kRdTokSlots; ++i)
+                if (kRdGroups * i + grp < a.T) a.x_scale[kRdGroups * i + grp] = xs[i];
     }
 }
 
@@ -1447,9 +1482,10 @@ static hipError_t launch_router_exact(const LayerDesc& L, const Workspace& ws, c
 
 static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
                                       const RouteDebug& dbg, bool& x_f16, hipStream_t stream, const float* norm_w,
-                                      float eps) {
+                                      float eps, const double* x_ssq) {
     TopkArgs ta;
     ta.norm_w = nullptr;
+    ta.x_ssq = nullptr;
     ta.norm_eps = eps;
     ta.x_scale = ws.x_scale;
     ta.logits = ws.logits;
@@ -1524,6 +1560,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         ta.dslots = ws.dslots;
         ta.defer_softmax = 1;
         ta.norm_w = norm_w;
+        ta.x_ssq = norm_w ? x_ssq : nullptr;
         const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
         const int nslab = L.H / kRdSlab;
         SharedGuArgs sg{};
@@ -1573,9 +1610,10 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
 bool route_norm_fused(const LayerDesc& L, int T) { return route_decode_fused(L, T) && L.H <= 8 * kRdSlab; }
 
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
-                        const RouteDebug& dbg, bool x_f16, hipStream_t stream, const float* norm_w, float eps) {
+                        const RouteDebug& dbg, bool x_f16, hipStream_t stream, const float* norm_w, float eps,
+                        const double* x_ssq) {
     if (norm_w && (x_f16 || !route_norm_fused(L, T))) return hipErrorInvalidValue;
-    hipError_t err = launch_route_tables(L, ws, x, xr, T, dbg, x_f16, stream, norm_w, eps);
+    hipError_t err = launch_route_tables(L, ws, x, xr, T, dbg, x_f16, stream, norm_w, eps, x_ssq);
     if (err != hipSuccess || !x_f16) return err;
     // the routing launch did not write x's f16 quants (only the batched router's does)
     hipLaunchKernelGGL(k_x_f16, dim3((T + 3) / 4), dim3(256), 0, stream, x, T, L.H, ws.x_q, ws.x_d, ws.xq_qs, ws.xq_ds);

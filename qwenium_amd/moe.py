@@ -97,6 +97,27 @@ def _vec_in(name: str, t: torch.Tensor, H: int, device) -> torch.Tensor:
     return t.contiguous()
 
 
+def ssq_parts(n_embd: int) -> int:
+    """Entries per row of the RMSNorm partial sums (32 columns each)."""
+    return (n_embd + 31) // 32
+
+
+def _ssq_in(name: str, t: torch.Tensor, T: int, H: int, device) -> torch.Tensor:
+    if (not isinstance(t, torch.Tensor) or tuple(t.shape) != (T, ssq_parts(H)) or t.dtype != torch.float64
+            or t.device != device):
+        raise ValueError(f"{name} expected a cuda float64 [{T}, {ssq_parts(H)}] tensor on {device}, got "
+                         f"{_describe(t)}")
+    return t.contiguous()
+
+
+def _ssq_out(name: str, t: torch.Tensor, T: int, H: int, device) -> torch.Tensor:
+    if (not isinstance(t, torch.Tensor) or tuple(t.shape) != (T, ssq_parts(H)) or t.dtype != torch.float64
+            or t.device != device or not t.is_contiguous()):
+        raise ValueError(f"{name} expected a contiguous cuda float64 [{T}, {ssq_parts(H)}] tensor on {device}, got "
+                         f"{_describe(t)}")
+    return t
+
+
 def _describe(t) -> str:
     if not isinstance(t, torch.Tensor):
         return type(t).__name__
@@ -210,19 +231,33 @@ class MoELayer:
 
     def forward_norm(self, x: torch.Tensor, norm_weight: torch.Tensor, eps: float, *,
                      out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None,
+                     x_ssq: Optional[torch.Tensor] = None, y_ssq: Optional[torch.Tensor] = None,
                      debug: bool = False, stream=None):
         """The block's caller slice in one call (qwen36.cpp:297-304):
         y = x + MoE(RMSNorm(x) * norm_weight).  Same bits as
-        forward(rms_norm(x, norm_weight, eps), residual=x)."""
+        forward(rms_norm(x, norm_weight, eps), residual=x).  For a chain of
+        blocks, x_ssq may hold x's RMSNorm partial sums (rms_partials(x), or
+        the previous block's y_ssq) and y_ssq receives y's: float64
+        [T, ceil(n_embd/32)] (qmoe_layer_forward_norm_chain); the bits do not
+        change."""
         with _on(stream):
             x = self._check_x(x)
+            T = x.shape[0]
             w = _vec_in("norm_weight", norm_weight, self.n_embd, x.device)
-            y = _rows_out("out", out, x.shape[0], self.n_embd, x.device, x)
-            dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
-            check(lib().qmoe_layer_forward_norm(
-                self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), w.data_ptr(),
-                float(eps), int(x.shape[0]), y.data_ptr(), ctypes.byref(dbg) if dbg is not None else None,
-                _stream_ptr(stream)))
+            y = _rows_out("out", out, T, self.n_embd, x.device, x)
+            dbg, dbg_tensors = self._debug(T, x.device) if debug else (None, None)
+            ws = workspace._handle if workspace is not None else None
+            d = ctypes.byref(dbg) if dbg is not None else None
+            if x_ssq is None and y_ssq is None:
+                check(lib().qmoe_layer_forward_norm(self._handle, ws, x.data_ptr(), w.data_ptr(), float(eps), int(T),
+                                                    y.data_ptr(), d, _stream_ptr(stream)))
+            else:
+                xs = _ssq_in("x_ssq", x_ssq, T, self.n_embd, x.device) if x_ssq is not None else None
+                ys = _ssq_out("y_ssq", y_ssq, T, self.n_embd, x.device) if y_ssq is not None else None
+                check(lib().qmoe_layer_forward_norm_chain(
+                    self._handle, ws, x.data_ptr(), xs.data_ptr() if xs is not None else None, w.data_ptr(),
+                    float(eps), int(T), y.data_ptr(), ys.data_ptr() if ys is not None else None, d,
+                    _stream_ptr(stream)))
         return (y, dbg_tensors) if debug else y
 
     def forward_routed(self, expert_in: torch.Tensor, router_in: torch.Tensor, *, out: Optional[torch.Tensor] = None,
@@ -341,6 +376,20 @@ def rms_norm(x: torch.Tensor, w: Optional[torch.Tensor], eps: float, out: Option
         y = _rows_out("out", out, T, H, x.device, x) if out is not None else torch.empty_like(x)
         check(lib().qmoe_rms_norm(x.data_ptr(), wc.data_ptr() if wc is not None else None, int(T), int(H),
                                   float(eps), y.data_ptr(), _stream_ptr(stream)))
+    return y
+
+
+def rms_partials(x: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """rms_norm's sum of squares of each row of x in pieces of 32 columns
+    (float64 [T, ceil(n_embd/32)]; qmoe_rms_partials)."""
+    with _on(stream):
+        if not isinstance(x, torch.Tensor) or x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda:
+            raise ValueError(f"x expected a cuda float32 [T, n_embd] tensor, got {_describe(x)}")
+        x = x.contiguous()
+        T, H = x.shape
+        y = (_ssq_out("out", out, T, H, x.device) if out is not None else
+             torch.empty((T, ssq_parts(H)), dtype=torch.float64, device=x.device))
+        check(lib().qmoe_rms_partials(x.data_ptr(), int(T), int(H), y.data_ptr(), _stream_ptr(stream)))
     return y
 
 

@@ -167,6 +167,17 @@ def test_workspace_and_misc_checks_without_gpu():
     assert L.qmoe_workspace_check(None, None) == 1  # QMOE_ERR_NULL
     assert L.qmoe_rms_norm(FAKE, None, 0, 2048, 1e-6, FAKE, None) == QMOE_OK
     assert L.qmoe_rms_norm(None, None, 3, 2048, 1e-6, FAKE, None) == QMOE_ERR_NULL
+    assert L.qmoe_rms_partials(FAKE, 0, 2048, FAKE, None) == QMOE_OK
+    assert L.qmoe_rms_partials(None, 3, 2048, FAKE, None) == QMOE_ERR_NULL
+    assert L.qmoe_rms_partials(FAKE, 3, 0, FAKE, None) == QMOE_ERR_VALUE
+    assert L.qmoe_rms_partials(FAKE, 3, 2048, FAKE + 4, None) == QMOE_ERR_VALUE
+    assert L.qmoe_layer_forward_norm_chain(None, None, FAKE, None, FAKE, 1e-6, 4, FAKE + 0x1000, None, None,
+                                           None) == QMOE_ERR_NULL  # no layer
+    assert L.qmoe_layer_forward_norm_chain(None, None, FAKE, None, None, 1e-6, 4, FAKE + 0x1000, None, None,
+                                           None) == QMOE_ERR_NULL  # no norm_w
+    assert L.qmoe_layer_forward_norm_chain(None, None, FAKE, FAKE + 8, FAKE, 1e-6, 4, FAKE + 0x1000, None, None,
+                                           None) == QMOE_ERR_VALUE
+    assert "aligned" in _lib.last_error()
     assert L.qmoe_synth_quant(FAKE, TYPE_F32, 4, 64, 0, 0, 0.02, None) == QMOE_ERR_TYPE
     assert L.qmoe_synth_quant(FAKE, TYPE_Q4_0, 4, 40, 0, 0, 0.02, None) == QMOE_ERR_VALUE
     assert L.qmoe_synth_f32(FAKE, 0, 0, 0, 0.0, 1.0, None) == QMOE_OK

@@ -190,6 +190,15 @@ def test_rms_norm_matches_oracle(gpu):
     np.testing.assert_allclose(y, ref, rtol=2e-7, atol=0)
 
 
+@pytest.mark.parametrize("H", [2048, 1000, 4096])
+def test_rms_partials_matches_oracle(gpu, H):
+    """The RMSNorm partial sums (32 columns per entry) equal the oracle's bits."""
+    from qwenium_amd import rms_partials
+    x = synthetic.synth_f32(7 * H, 4, 91).view(7, H)
+    got = rms_partials(x).cpu().numpy()
+    np.testing.assert_array_equal(got, po.rms_partials(x.cpu().numpy()))
+
+
 def test_config1_matches_committed_golden(gpu):
     """GPU path vs tests/golden/config1_seed0.npz (written by the CPU oracle)."""
     import os
@@ -413,16 +422,20 @@ def test_skewed_q8_0_t2048(gpu):
 def test_stack_40_layers(gpu, T):
     """Config 5: 40 consecutive blocks x <- x + MoE_l(RMSNorm(x) * w_l) (qwen36.cpp:297-304 at
     prefill, :427-432 at decode) through the fused-norm call, at decode batches 1, 10 and 64
-    and at 8192-token prefill.  Layers 0 and 39 are checked against the oracle on their actual
-    inputs (and against the unfused rms_norm + forward): routing bit-exact on every token,
+    and at 8192-token prefill, each block's RMSNorm partial sums carried to the next.  Layers 0
+    and 39 are checked against the oracle on their actual inputs (and against the unfused
+    rms_norm + forward and the call without partial sums): routing bit-exact on every token,
     outputs within tolerance (all tokens up to 64, a sample of 48 at 8192)."""
-    from qwenium_amd import Workspace, rms_norm
+    from qwenium_amd import Workspace, rms_norm, ssq_parts
 
     spec = synthetic.QWEN35B
     L, seed = 40, 11
     ws = None
     x = synthetic.make_x(spec, T, seed)
     h = torch.empty_like(x)
+    ssq = [None, torch.empty((T, ssq_parts(spec.n_embd)), dtype=torch.float64, device=x.device),
+           torch.empty((T, ssq_parts(spec.n_embd)), dtype=torch.float64, device=x.device)]
+    x_ssq = None
     keep = {}
     for l in range(L):
         t = synthetic.make_layer_tensors(spec, seed, layer=l)
@@ -430,17 +443,20 @@ def test_stack_40_layers(gpu, T):
         if ws is None:
             ws = Workspace(layer, T)
         wn = synthetic.make_norm_weight(spec, seed, l)
+        y_ssq = ssq[1 + (l & 1)]
         if l in (0, L - 1):
             rms_norm(x, wn, synthetic.NORM_EPS, out=h)
             y, dbg = layer.forward(h, workspace=ws, residual=x, debug=True)
             y_fused = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws)
+            y_chain = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws, x_ssq=x_ssq, y_ssq=y_ssq)
             torch.cuda.synchronize()
             assert torch.equal(y, y_fused), f"layer {l}: fused RMSNorm path"
+            assert torch.equal(y, y_chain), f"layer {l}: with carried partial sums"
             keep[l] = (x.cpu().numpy(), wn.cpu().numpy(), t, y.cpu().numpy(),
                        {k: dbg[k].cpu().numpy() for k in ("topk_idx", "offsets", "rows")})
         else:
-            y = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws)
-        x = y
+            y = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws, x_ssq=x_ssq, y_ssq=y_ssq)
+        x, x_ssq = y, y_ssq
         del t, layer
     torch.cuda.synchronize()
     assert np.isfinite(x.cpu().numpy()).all()
@@ -485,6 +501,37 @@ def test_fused_decode_routing_repeated(gpu, n_experts, T):
         y_ref, d_ref = ref.forward(x.cpu().numpy(), debug=True)
         got = {k: v.cpu().numpy() for k, v in dbg.items()}
         assert_parity(y.cpu().numpy(), got, y_ref, d_ref, spec, min_identical=1.0)
+    assert ws.check() == 0
+
+
+@pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 300),
+                                     ("config1", 5), ("h4096", 10)])
+def test_forward_norm_chain(gpu, which, T):
+    """Three blocks with the RMSNorm partial sums carried from each to the next
+    (x_ssq in, y_ssq out; the first block without x_ssq): every block's y has the
+    bits of forward_norm without them, and y_ssq equals the oracle's partial sums
+    of y (written by the down+combine epilogue at decode sizes, by one more
+    launch otherwise)."""
+    from qwenium_amd import Workspace, ssq_parts
+
+    spec = {"35b": synthetic.QWEN35B, "config1": synthetic.CONFIG1,
+            "h4096": synthetic.LayerSpec(4096, 16, 2, 64, True, synthetic.TYPE_Q4_0)}[which]
+    seed = 23
+    x = synthetic.make_x(spec, T, seed, batch=T)
+    x_ssq = None
+    ws = None
+    for l in range(3):
+        layer = synthetic.make_layer(spec, seed, layer=l)
+        if ws is None:
+            ws = Workspace(layer, T)
+        wn = synthetic.make_norm_weight(spec, seed, l)
+        y_ssq = torch.empty((T, ssq_parts(spec.n_embd)), dtype=torch.float64, device=x.device)
+        y = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws, x_ssq=x_ssq, y_ssq=y_ssq)
+        y_ref = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), f"block {l}"
+        np.testing.assert_array_equal(y_ssq.cpu().numpy(), po.rms_partials(y.cpu().numpy()), err_msg=f"block {l}")
+        x, x_ssq = y, y_ssq
     assert ws.check() == 0
 
 

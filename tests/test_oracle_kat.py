@@ -222,3 +222,47 @@ def test_rms_norm_reference_kat():
         np.testing.assert_allclose(y[0], [1.697056, 0.565685], atol=1e-4)
     y = po.rms_norm(np.array([[3.0, 4.0]], np.float32), None, 0.0)
     np.testing.assert_allclose(y[0], [0.848528, 1.131371], atol=1e-5)
+
+
+def test_rms_partials_exact_on_integers():
+    """Small integers: every square and sum is exact, so entry c is the integer
+    sum of squares of columns 32c .. 32c+31 (a dropped, doubled or misplaced
+    column fails), including the short last piece (1000 = 31 * 32 + 8)."""
+    x = np.random.default_rng(3).integers(-60, 61, size=(3, 1000)).astype(np.float32)
+    got = po.rms_partials(x)
+    sq = (x.astype(np.int64) ** 2)
+    want = np.stack([sq[:, 32 * c:32 * c + 32].sum(axis=1) for c in range(32)], axis=1).astype(np.float64)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_rms_partials_square_rounded_to_f32():
+    """Each square is rounded to f32 before the f64 sum (ggml_rms_norm's
+    f64(x*x) on f32 x): the entries are the correctly rounded sums of those f32
+    squares to within a few f64 ulps; summing the exact f64 squares instead
+    would differ by ~1e-8 relative."""
+    x = np.random.default_rng(4).standard_normal((4, 2048)).astype(np.float32)
+    got = po.rms_partials(x)
+    sq32 = (x * x).astype(np.float64)
+    want = np.array([[math.fsum(sq32[t, 32 * c:32 * c + 32]) for c in range(64)] for t in range(4)])
+    np.testing.assert_allclose(got, want, rtol=1e-15, atol=0)
+    exact = np.array([[math.fsum(x[t, 32 * c:32 * c + 32].astype(np.float64) ** 2) for c in range(64)]
+                      for t in range(4)])
+    assert np.max(np.abs(exact - want) / want) > 1e-10  # the case separates the two
+
+
+def test_rms_partials_order():
+    """The order, fixed by hand-derived values where other orders round
+    differently (a = 2^-54 is a quarter of an ulp of 1, 2a half of one):
+    - within a run, columns in turn: a + a + a + 1 = 1 + 2^-52 (1 first gives 1;
+      pairs (a+a) + (a+1) give 1 + 2^-53, a tie rounded to 1);
+    - runs in adjacent pairs: runs [1, a, a, a, a, a, a, a] give
+      ((1+a) + (a+a)) + ((a+a) + (a+a)) = (1 + 2^-53) + 2^-52 = 1 + 2^-52,
+      while adding the runs in turn gives 1."""
+    s = np.float32(2.0 ** -27)  # s * s = 2^-54 exactly in f32
+    x = np.zeros((2, 32), np.float32)
+    x[0, :4] = [s, s, s, 1.0]
+    x[1, 0] = 1.0
+    x[1, 4:32:4] = s
+    got = po.rms_partials(x)
+    assert got[0, 0] == 1.0 + 2.0 ** -52
+    assert got[1, 0] == 1.0 + 2.0 ** -52
