@@ -820,9 +820,8 @@ hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hi
     a.a_q = ws.x_q; a.a_d = ws.x_d;
     a.K = L.H;
     a.n_y = L.F / 64;
-    // the fixup list starts empty (a kernel node, not a memset, under capture)
-    hipError_t err = launch_fill_i32(ws.counters + kCounterFix, 1, 0, stream);
-    if (err != hipSuccess) return err;
+    // the fixup list starts empty: the routing's expert scan clears its counter
+    hipError_t err = hipSuccess;
     const dim3 grid(8 * ((f16_max_tiles(L, ws, T) + 7) / 8) * a.n_y);
     const bool gelu = L.act == kActGeluTanh;
     if (L.gu_type == kTypeQ4_0)

@@ -961,6 +961,7 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
             }
             a.counters[0] = n_act;
             a.counters[1] = n_tiles;
+            a.counters[kCounterFix] = 0;  // the prefill gate/up's list of uncertain h blocks starts empty
         }
     }
 }
