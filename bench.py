@@ -486,9 +486,9 @@ def run_leg(args, pool: LayerPool, workload: str, headline: bool) -> dict:
                       "forwards": lg["forwards"]} for th, lg in sorted(legs.items())],
         }
 
-    fault = ws.check()
-    if fault:
-        raise RuntimeError(f"workload {workload}: a decode routing wait gave up during the run (outputs are NaN)")
+    # synchronizes and raises on any device error of the run (no kernel waits on another workgroup)
+    if ws.check():
+        raise RuntimeError(f"workload {workload}: the workspace check reported a fault")
     return {
         "metric": metric,
         "value": tok_per_s,
