@@ -497,6 +497,9 @@ struct TopkArgs {
     float norm_eps;
     float* x_scale;       // [T] the rows' RMSNorm scales (router block 0 writes them for the table launch)
     const double* x_ssq;  // [T][ssq_parts(H)] x's RMSNorm partial sums, or null (the router sums x itself)
+    int quant_rows;       // router launch over token groups: its last ceil(T/16) workgroups write x's Q8_0 ...
+    int8_t* xq_qs;        // ... quants [T][H]
+    float2* xq_ds;        // ... and {d, sum} [T][H/32]
     int32_t* topk_idx;    // [T][K]
     float* topk_w;        // [T][K]
     float* sh_gate;       // [T]
@@ -1150,12 +1153,30 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
 // the standalone RMSNorm).  Block 0 stores them for the table launch's Q8_0 of
 // x; the router input is (x * scale) * norm_w.
 template <int NSW, bool NORM>  // NSW: router slabs per wave (ceil(H/256/4))
-__global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits) {
+__global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a0, float* logits0) {
 #pragma clang fp contract(off)
     __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
     __shared__ double s_chunk[NORM ? kTopkTokensPerBlock : 1][8];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     static_assert(!NORM || NSW <= 2, "the fused norm takes rows of at most 8 slabs");
+    // more than 16 tokens run in groups of 16: workgroup b takes router rows of
+    // block b % nbr for the tokens of group b / nbr; with quant_rows, the last
+    // ceil(T/16) workgroups write x's Q8_0 rows (one wave per token)
+    const int nbr = (a0.E + a0.S + kRdRows - 1) / kRdRows;
+    const int ngr = (a0.T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
+    if (a0.quant_rows && (int)blockIdx.x >= nbr * ngr) {
+        const int t = ((int)blockIdx.x - nbr * ngr) * kTopkTokensPerBlock + wave;
+        if (wave < kTopkTokensPerBlock && t < a0.T) quant_token_row(a0.xe, a0.H, t, lane, a0.xq_qs, a0.xq_ds);
+        return;
+    }
+    const int gi = (int)blockIdx.x / nbr, rb = (int)blockIdx.x - gi * nbr;
+    const int tb = gi * kTopkTokensPerBlock;
+    TopkArgs a = a0;  // this group's tokens
+    a.T = min(kTopkTokensPerBlock, a0.T - tb);
+    a.x = a0.x + (uint64_t)tb * a0.H;
+    a.x_scale = a0.x_scale + tb;
+    if (a0.x_ssq) a.x_ssq = a0.x_ssq + (uint64_t)tb * ssq_parts(a0.H);
+    float* logits = logits0 + (uint64_t)tb * (a0.E + 1);
     const int E1 = a.E + a.S;
     const int nslab = a.H / kRdSlab;
     const int part = wave % kRdParts;
@@ -1163,7 +1184,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
         return e < a.E ? a.w_router + (uint64_t)min(e, a.E - 1) * a.router_ld : (a.S ? a.w_sh_norm : a.w_router);
     };
     const int grp = wave / kRdParts;
-    const int e0 = blockIdx.x * kRdRows;
+    const int e0 = rb * kRdRows;
     double acc[kRdVals];  // [row q][i]: token kRdGroups * i + grp
 #pragma unroll
     for (int k = 0; k < kRdVals; ++k) acc[k] = 0.0;
@@ -1307,7 +1328,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     __syncthreads();
     if (tid < kRdRows * a.T) {
         const int rr = tid / a.T, t = tid % a.T;
-        const int er = blockIdx.x * kRdRows + rr;
+        const int er = e0 + rr;
         if (er < E1) {
             double sum = s_part[rr][0][t];
 #pragma unroll
@@ -1317,7 +1338,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a, float* logits
     }
     // the scales for the table launch's quantization of x (after every load)
     if constexpr (NORM) {
-        if (blockIdx.x == 0 && part == 0 && lane == 0)
+        if (rb == 0 && part == 0 && lane == 0)
 #pragma unroll
             for (int i = 0; i < kRdTokSlots; ++i)
                 if (kRdGroups * i + grp < a.T) a.x_scale[kRdGroups * i + grp] = xs[i];
@@ -1487,6 +1508,9 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
     TopkArgs ta;
     ta.norm_w = nullptr;
     ta.x_ssq = nullptr;
+    ta.quant_rows = 0;
+    ta.xq_qs = ws.xq_qs;
+    ta.xq_ds = ws.xq_ds;
     ta.norm_eps = eps;
     ta.x_scale = ws.x_scale;
     ta.logits = ws.logits;
@@ -1598,7 +1622,20 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
             return err;
         return hipGetLastError();
     } else {
-        if ((err = launch_router_exact(L, ws, xr, x, T, true, stream)) != hipSuccess) return err;
+        // the decode router over groups of 16 tokens, x's Q8_0 on the same launch's
+        // last workgroups; then the top-k
+        ta.quant_rows = 1;
+        const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
+        const int ngr = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
+        const int nsw = (L.H / kRdSlab + kRdParts - 1) / kRdParts;
+        const void* kern = route_decode_kernel(nsw, false);
+        if (!kern) return hipErrorInvalidValue;
+        float* logits = ws.logits;
+        void* args[] = {&ta, &logits};
+        if ((err = hipLaunchKernel(kern, dim3(nb * ngr + ngr), dim3(64 * kTopkTokensPerBlock), args, 0, stream)) !=
+            hipSuccess)
+            return err;
+        ta.quant_rows = 0;
         hipLaunchKernelGGL(k_topk<false>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
         if ((err = hipGetLastError()) != hipSuccess) return err;
     }
