@@ -61,8 +61,23 @@ struct GuItem {
     static constexpr int NI = RPW / RPI;
     WPair<WT> wg[NI], wu[NI];
     XPair x;
-    int e, p0, nrows, f0;
+    int e, p0, nrows, f0, t0;  // t0: the shared expert's first token (its rows are tokens t0, t0 + 1, ...)
 };
+
+// The shared expert's rows (one per token) go to items of kShChunk rows each, so
+// that no item walks all T rows one after another.
+constexpr int kShChunk = 8;
+__device__ __forceinline__ int sh_chunks(const ExpertArgs& a) { return a.S ? (a.T + kShChunk - 1) / kShChunk : 0; }
+// Slot entry of item `item` (ips items per slot or shared chunk): the shared
+// expert's chunks first (the heaviest items), then the routed experts' slots.
+__device__ __forceinline__ int4 item_slot_info(const ExpertArgs& a, const int4* slots, int item, int ips, int n_act) {
+    const int k = item / ips, nsh = sh_chunks(a);
+    if (k < nsh) {
+        const int c0 = k * kShChunk;
+        return make_int4(a.E, a.T * a.K + c0, min(kShChunk, a.T - c0), c0);
+    }
+    return slots[k - nsh];
+}
 
 // Activation source of the gate/up kernel: the quantized token rows and the
 // row -> token map, in LDS (decode: staged once per block) or in global memory.
@@ -72,20 +87,13 @@ struct XSrc {
     const int32_t* rtok;  // [R]
 };
 
-// Item order over slots: the shared expert's slot (last in the table, with a
-// row per token: the heaviest items) first, then the routed experts.
-__device__ __forceinline__ int item_slot(int item, int ips, int n_act, int S) {
-    const int k = item / ips;
-    return S ? (k == 0 ? n_act - 1 : k - 1) : k;
-}
-
 // Weights of one item (RPW rows of gate and of up of the slot's expert).
 template <int WT, int LPR, int RPW>
 __device__ __forceinline__ void gu_load_w(const ExpertArgs& a, const int4 si, int item, int ips, int sub, int lp,
                                           GuItem<WT, LPR, RPW>& it) {
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
-    it.e = si.x; it.p0 = si.y; it.nrows = si.z;
+    it.e = si.x; it.p0 = si.y; it.nrows = si.z; it.t0 = si.w;
     it.f0 = (item % ips) * RPW;
     const bool sh = it.e >= a.E;
     const uint8_t* gb = sh ? a.w_sh_gate : a.w_gate + (uint64_t)it.e * a.gate_nb2;
@@ -111,7 +119,7 @@ __device__ __forceinline__ void gu_load_x(const ExpertArgs& a, const XSrc& xs, i
 template <int WT, int LPR, int RPW>
 __device__ __forceinline__ void gu_load(const ExpertArgs& a, const XSrc& xs, const int4* s_slots, int n_act, int item,
                                         int ips, int sub, int lp, GuItem<WT, LPR, RPW>& it) {
-    const int4 si = s_slots[item_slot(item, ips, n_act, a.S)];
+    const int4 si = item_slot_info(a, s_slots, item, ips, n_act);
     gu_load_w(a, si, item, ips, sub, lp, it);
     gu_load_x(a, xs, si.w, lp, it);
 }
@@ -122,11 +130,11 @@ __device__ __forceinline__ void gu_compute(const ExpertArgs& a, const XSrc& xs, 
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
     const bool live = lp < (a.H >> 6);
-    XPair x = it.x;
+    XPair x = it.x, xn;
     for (int c = 0; c < it.nrows; ++c) {
-        if (c > 0) {
-            const int tok = it.e >= a.E ? c : xs.rtok[it.p0 + c];
-            x.load(xs.qs + (uint64_t)tok * a.H, xs.ds + (uint64_t)tok * (a.H >> 5), min(lp, (a.H >> 6) - 1));
+        if (c + 1 < it.nrows) {  // the next row's activations, requested before this row's dots
+            const int tok = it.e >= a.E ? it.t0 + c + 1 : xs.rtok[it.p0 + c + 1];
+            xn.load(xs.qs + (uint64_t)tok * a.H, xs.ds + (uint64_t)tok * (a.H >> 5), min(lp, (a.H >> 6) - 1));
         }
 #pragma unroll
         for (int m = 0; m < NI; ++m) {
@@ -140,6 +148,7 @@ __device__ __forceinline__ void gu_compute(const ExpertArgs& a, const XSrc& xs, 
                 if (lp == LPR - 1) o = make_float2((float)g, (float)u);
             }
         }
+        x = xn;
     }
 }
 
@@ -173,9 +182,10 @@ template <int WT, int LPR, int RPW, bool XLDS>
 __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
     int4* s_slots = (int4*)s_dyn;
-    const int n_act = __builtin_amdgcn_readfirstlane(a.counters[0]);
+    // routed slots (the table's last slot is the shared expert's, which goes to chunks)
+    const int n_act = __builtin_amdgcn_readfirstlane(a.counters[0]) - a.S;
     const int ips = a.F / RPW;
-    const int n_items = n_act * ips;
+    const int n_items = (n_act + sh_chunks(a)) * ips;
     const int lane = threadIdx.x & 63;
     const int sub = lane / LPR, lp = lane % LPR;
     const int tw = gridDim.x * (blockDim.x >> 6);
@@ -186,10 +196,10 @@ __global__ __launch_bounds__(256) void k_gateup_stream(ExpertArgs a) {
     GuItem<WT, LPR, RPW> b0, b1;
     int4 si0 = make_int4(0, 0, 0, 0), si1 = si0;
     if (item < n_items) {
-        si0 = a.slot_info[item_slot(item, ips, n_act, a.S)];
+        si0 = item_slot_info(a, a.slot_info, item, ips, n_act);
         gu_load_w(a, si0, item, ips, sub, lp, b0);
         if (item + tw < n_items) {
-            si1 = a.slot_info[item_slot(item + tw, ips, n_act, a.S)];
+            si1 = item_slot_info(a, a.slot_info, item + tw, ips, n_act);
             gu_load_w(a, si1, item + tw, ips, sub, lp, b1);
         }
     }
@@ -491,16 +501,16 @@ struct DnItem {
     static constexpr int NI = RPW / RPI;
     WPair<WT> w[NI];
     XPair x;
-    int e, p0, nrows, n0;
+    int e, p0, nrows, n0, t0;  // t0: the shared expert's first token
 };
 
 template <int WT, int LPR, int RPW>
 __device__ __forceinline__ void dn_load(const ExpertArgs& a, const XSrc& hs, const int4* s_slots, int item, int ips,
-                                        int sub, int lp, DnItem<WT, LPR, RPW>& it) {
+                                        int sub, int lp, int n_act, DnItem<WT, LPR, RPW>& it) {
     constexpr int RPI = 64 / LPR;
     constexpr int NI = RPW / RPI;
-    const int4 si = s_slots[item / ips];
-    it.e = si.x; it.p0 = si.y; it.nrows = si.z;
+    const int4 si = item_slot_info(a, s_slots, item, ips, n_act);
+    it.e = si.x; it.p0 = si.y; it.nrows = si.z; it.t0 = si.w;
     it.n0 = (item % ips) * RPW;
     const bool sh = it.e >= a.E;
     const uint8_t* db = sh ? a.w_sh_down : a.w_down + (uint64_t)it.e * a.down_nb2;
@@ -508,7 +518,7 @@ __device__ __forceinline__ void dn_load(const ExpertArgs& a, const XSrc& hs, con
     const int pair = min(lp, (a.F >> 6) - 1);
 #pragma unroll
     for (int m = 0; m < NI; ++m) it.w[m].load(db + (uint64_t)(it.n0 + m * RPI + sub) * dnb1, pair);
-    if (sh && hs.qs) it.x.load(hs.qs, hs.ds, pair);  // uniform branches keep the address spaces known
+    if (sh && hs.qs) it.x.load(hs.qs + (uint64_t)it.t0 * a.F, hs.ds + (uint64_t)it.t0 * (a.F >> 5), pair);  // uniform branches keep the address spaces known
     else it.x.load(a.hq_qs + (uint64_t)it.p0 * a.F, a.hq_ds + (uint64_t)it.p0 * (a.F >> 5), pair);
 }
 
@@ -519,20 +529,23 @@ __device__ __forceinline__ void dn_compute(const ExpertArgs& a, const XSrc& hs, 
     constexpr int NI = RPW / RPI;
     const bool live = lp < (a.F >> 6);
     const bool sh = it.e >= a.E;
-    XPair x = it.x;
+    XPair x = it.x, xn;
     for (int c = 0; c < it.nrows; ++c) {
         const int p = it.p0 + c;
-        if (c > 0) {
-            // shared-expert rows come from the block's LDS copy (hs), routed rows from global memory
+        if (c + 1 < it.nrows) {
+            // the next row, requested before this row's dots: shared-expert rows from
+            // the block's LDS copy (hs), routed rows from global memory
             const int pair = min(lp, (a.F >> 6) - 1);
-            if (sh && hs.qs) x.load(hs.qs + (uint64_t)c * a.F, hs.ds + (uint64_t)c * (a.F >> 5), pair);
-            else x.load(a.hq_qs + (uint64_t)p * a.F, a.hq_ds + (uint64_t)p * (a.F >> 5), pair);
+            const int tn = it.t0 + c + 1;
+            if (sh && hs.qs) xn.load(hs.qs + (uint64_t)tn * a.F, hs.ds + (uint64_t)tn * (a.F >> 5), pair);
+            else xn.load(a.hq_qs + (uint64_t)(p + 1) * a.F, a.hq_ds + (uint64_t)(p + 1) * (a.F >> 5), pair);
         }
 #pragma unroll
         for (int m = 0; m < NI; ++m) {
             const double y = dpp_sum_f64<LPR>(live ? pair_dot<WT>(it.w[m], x) : 0.0);
             if (lp == LPR - 1) a.ybuf[(uint64_t)p * a.H + it.n0 + m * RPI + sub] = (float)y;
         }
+        x = xn;
     }
 }
 
@@ -559,24 +572,24 @@ __global__ __launch_bounds__(256) void k_down_stream(ExpertArgs a) {
         for (int i = threadIdx.x; i < nd; i += blockDim.x) ((u32x4*)ld)[i] = gd[i];
         hs = XSrc{lq, ld, nullptr};
     }
-    const int n_act = stage_slots(a, s_slots, &s_nact);
+    const int n_act = stage_slots(a, s_slots, &s_nact) - a.S;  // routed slots; the shared expert goes to chunks
     const int ips = a.H / RPW;
-    const int n_items = n_act * ips;
+    const int n_items = (n_act + sh_chunks(a)) * ips;
     const int lane = threadIdx.x & 63;
     const int sub = lane / LPR, lp = lane % LPR;
     const int tw = gridDim.x * (blockDim.x >> 6);
     int item = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (item >= n_items) return;
     DnItem<WT, LPR, RPW> b0, b1;
-    dn_load(a, hs, s_slots, item, ips, sub, lp, b0);
+    dn_load(a, hs, s_slots, item, ips, sub, lp, n_act, b0);
     for (;;) {
         int nitem = item + tw;
-        if (nitem < n_items) dn_load(a, hs, s_slots, nitem, ips, sub, lp, b1);
+        if (nitem < n_items) dn_load(a, hs, s_slots, nitem, ips, sub, lp, n_act, b1);
         dn_compute(a, hs, b0, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
         nitem = item + tw;
-        if (nitem < n_items) dn_load(a, hs, s_slots, nitem, ips, sub, lp, b0);
+        if (nitem < n_items) dn_load(a, hs, s_slots, nitem, ips, sub, lp, n_act, b0);
         dn_compute(a, hs, b1, sub, lp);
         if (nitem >= n_items) break;
         item = nitem;
