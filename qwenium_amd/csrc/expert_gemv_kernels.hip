@@ -915,7 +915,7 @@ static hipError_t launch_gateup(const ExpertArgs& a, int max_slots, int n_cu, hi
                                 hipEvent_t e1) {
     const int npairs = a.H / 64;
     if (npairs <= 16) return launch_gateup_v<WT, 16, 4>(a, max_slots, n_cu, stream, e0, e1);
-    if (npairs <= 32) return launch_gateup_v<WT, 32, 2>(a, max_slots, n_cu, stream, e0, e1);
+    if (npairs <= 32) return launch_gateup_v<WT, 32, 4>(a, max_slots, n_cu, stream, e0, e1);  // 4 rows: twice the bytes per request (2 rows: +14%, 8 rows: +19% at 64 tokens)
     return launch_gateup_v<WT, 64, 2>(a, max_slots, n_cu, stream, e0, e1);
 }
 
