@@ -921,7 +921,7 @@ static hipError_t launch_gateup(const ExpertArgs& a, int max_slots, int n_cu, hi
 
 template <int WT, int LPR>
 static hipError_t launch_down_v(const ExpertArgs& a, int max_slots, int n_cu, hipStream_t stream) {
-    constexpr int RPW = 2 * (64 / LPR);  // two load instructions per item
+    constexpr int RPW = 4 * (64 / LPR);  // four load instructions per item (at 64 tokens: two +8%, one +40%, eight +25%)
     const bool shlds = a.S && dn_lds_bytes(a.E, a.T, a.F, true) - dn_lds_bytes(a.E, a.T, a.F, false) <= kGuXLdsMax;
     const size_t lds = dn_lds_bytes(a.E, a.T, a.F, shlds);
     if (shlds) {
