@@ -822,8 +822,13 @@ bool down_combine_tok_fits(const LayerDesc& L) {
     return nj <= 9 && dc_lds_bytes(L.F, nj) <= 64 * 1024 && dc_stage_chunks(L.F, nj) <= 1024 && L.dc_ahead <= 2;
 }
 
+// Up to 16 tokens either down+combine kernel; beyond, below the MFMA path, the
+// token-per-workgroup one (its step tables are per token; measured faster than
+// the streaming down + k_combine from 24 to 127 tokens: 99 -> 86 us at 24 tokens,
+// 156 -> 146 at 64, 221 -> 215 at 127).
 bool down_combine_fused(const LayerDesc& L, int T) {
-    return T <= kTopkTokensPerBlock && L.K + L.S <= kDcMaxSteps && T < L.mfma_min_tokens;
+    return T < L.mfma_min_tokens && L.K + L.S <= kDcMaxSteps &&
+           (T <= kTopkTokensPerBlock || down_combine_tok_fits(L));
 }
 
 // Up to 9 steps (8 routed + shared) whose activation rows fit in 64 KiB of
