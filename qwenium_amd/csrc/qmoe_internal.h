@@ -16,6 +16,8 @@ constexpr int kTopkTokensPerBlock = 16;
 // finished-workgroup counter (back to 0 after each scan).
 constexpr int kSyncWords = 64;
 constexpr int kSyncScan = 0;
+constexpr int kSyncTopk = 1;  // the merged top-k's finished-workgroup counter
+constexpr int kTopkMergeMax = 4096;  // top-k blocks x experts the merged top-k keeps in LDS
 // RMSNorm: 256-column chunks of a row whose sums fit a workgroup's LDS (rows of
 // at most 65536 columns).
 constexpr int kRmsMaxChunks = 256;

@@ -872,11 +872,17 @@ __device__ __forceinline__ void topk_dispatch(const TopkArgs& a, int t, int lane
 #undef QMOE_TOPK_CASE
 }
 
+__device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint32_t* first_token, int32_t* s_off,
+                             int32_t* s_misc);
+
 // blockDim = 64 * kTopkTokensPerBlock: one wave per token.  Writes the
 // selection, the per-block expert histogram and each assignment's rank among
-// the block's assignments to the same expert (token order).
-template <bool REFINE>
-__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a) {
+// the block's assignments to the same expert (token order).  MERGE (blocks x
+// experts <= kTopkMergeMax): those are written through, and the last block to
+// finish (a counter in sync) runs the expert scan and the stable scatter that
+// k_scan and k_scatter run otherwise, with the same results.
+template <bool REFINE, bool MERGE = false>
+__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, int32_t* sync = nullptr) {
     __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
     __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
     __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
@@ -896,10 +902,69 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a) {
         const int ti = asg / a.K;
         const int j = asg % a.K;
         const int ex = s_idx[ti][j];
-        a.local_rank[(uint64_t)(t0 + ti) * a.K + j] = __builtin_popcount(s_mask[ex] & ((1u << ti) - 1u));
+        const int rank = __builtin_popcount(s_mask[ex] & ((1u << ti) - 1u));
+        const uint64_t i = (uint64_t)(t0 + ti) * a.K + j;
+        if constexpr (MERGE) {  // written through: the last block reads them
+            __hip_atomic_store(a.local_rank + i, rank, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.topk_idx + i, ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            a.local_rank[i] = rank;
+        }
     }
-    for (int e = threadIdx.x; e < a.E; e += blockDim.x)
-        a.hist[(uint64_t)blockIdx.x * a.E + e] = __builtin_popcount(s_mask[e]);
+    for (int e = threadIdx.x; e < a.E; e += blockDim.x) {
+        const int cnt = __builtin_popcount(s_mask[e]);
+        if constexpr (MERGE)
+            __hip_atomic_store(a.hist + (uint64_t)blockIdx.x * a.E + e, cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            a.hist[(uint64_t)blockIdx.x * a.E + e] = cnt;
+    }
+    if constexpr (MERGE) {
+        __shared__ int32_t s_base[kTopkMergeMax];  // [block][expert]: the block's first rank in the expert's rows
+        __shared__ int32_t s_cnt[1024], s_off[1024], s_misc[64];
+        __shared__ int s_last;
+        const int tid = threadIdx.x;
+        __builtin_amdgcn_s_waitcnt(0);  // this block's write-through stores have completed
+        __syncthreads();
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(sync + kSyncTopk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (int)gridDim.x - 1;
+        __syncthreads();
+        if (!s_last) return;
+        if (tid == 0) __hip_atomic_store(sync + kSyncTopk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // per expert: the blocks' bases (exclusive prefix of their counts) and the total
+        for (int e = tid; e < a.E; e += blockDim.x) {
+            int run = 0;
+            for (int b = 0; b < (int)gridDim.x; ++b) {
+                const int c = __hip_atomic_load(a.hist + (uint64_t)b * a.E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_base[b * a.E + e] = run;
+                run += c;
+            }
+            s_cnt[e] = run;
+        }
+        __syncthreads();
+        scan_experts(a, s_cnt, nullptr, s_off, s_misc);
+        __syncthreads();
+        // the stable scatter: assignment i of expert e to row offsets[e] + its block's
+        // base + its rank in the block; the first row's token into the slot table;
+        // the shared expert's rows in token order
+        const int A = a.T * a.K;
+        for (int i = tid; i < A + a.S * a.T; i += blockDim.x) {
+            if (i < A) {
+                const int t = i / a.K;
+                const int ex = __hip_atomic_load(a.topk_idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int off = s_off[ex];
+                const int p = off + s_base[(t / kTopkTokensPerBlock) * a.E + ex] +
+                              __hip_atomic_load(a.local_rank + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                a.rows[p] = i;
+                a.row_token[p] = t;
+                a.pos[i] = p;
+                if (p == off) ((int*)(a.slot_info + a.expert_slot[ex]))[3] = t;
+            } else {
+                a.rows[i] = -1;
+                a.row_token[i] = i - A;
+            }
+        }
+    }
 }
 
 // Exclusive scans over experts of the per-expert counts in s_cnt: offsets,
@@ -1636,7 +1701,13 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
             hipSuccess)
             return err;
         ta.quant_rows = 0;
-        hipLaunchKernelGGL(k_topk<false>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
+        if (ta.nblk * L.E <= kTopkMergeMax) {
+            // the last top-k block runs the expert scan and the scatter: no more launches
+            hipLaunchKernelGGL((k_topk<false, true>), dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta,
+                               ws.sync);
+            return hipGetLastError();
+        }
+        hipLaunchKernelGGL((k_topk<false>), dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta, nullptr);
         if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     hipLaunchKernelGGL(k_scan, dim3((L.E + 63) / 64), dim3(1024), 0, stream, ta, ws.sync);
