@@ -497,7 +497,7 @@ struct TopkArgs {
     float norm_eps;
     float* x_scale;       // [T] the rows' RMSNorm scales (router block 0 writes them for the table launch)
     const double* x_ssq;  // [T][ssq_parts(H)] x's RMSNorm partial sums, or null (the router sums x itself)
-    int quant_rows;       // router launch over token groups: its last ceil(T/16) workgroups write x's Q8_0 ...
+    int quant_rows;       // router launch over token groups: its blocks also write x's Q8_0 ...
     int8_t* xq_qs;        // ... quants [T][H]
     float2* xq_ds;        // ... and {d, sum} [T][H/32]
     int32_t* topk_idx;    // [T][K]
@@ -1097,7 +1097,6 @@ constexpr int kRdRows = 2;                                     // router rows pe
 constexpr int kRdGroups = 4;                                   // token groups (t = g mod kRdGroups)
 constexpr int kRdParts = 16 / kRdGroups;                       // waves per token group
 constexpr int kRdTokSlots = kTopkTokensPerBlock / kRdGroups;   // token slots per wave
-constexpr int kRdVals = kRdRows * kRdTokSlots;                 // (row, token) sums per wave
 constexpr int kRdSlab = 256;        // columns per lane-float4 sweep
 constexpr int kMaxRdSlabs = 16;     // decode routing for H <= 4096
 // dynamic LDS: block 0's routing tables, the shared-expert blocks' token rows
@@ -1217,23 +1216,18 @@ __device__ __forceinline__ void shared_gateup_block(const TopkArgs& a, const Sha
 // tokens' scales (the tree over the chunks; the same bits in every block and in
 // the standalone RMSNorm).  Block 0 stores them for the table launch's Q8_0 of
 // x; the router input is (x * scale) * norm_w.
-template <int NSW, bool NORM>  // NSW: router slabs per wave (ceil(H/256/4))
+template <int NSW, bool NORM, int RR = kRdRows>  // NSW: router slabs per wave (ceil(H/256/4)); RR: rows per block
 __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a0, float* logits0) {
 #pragma clang fp contract(off)
-    __shared__ double s_part[kRdRows][kRdParts][kTopkTokensPerBlock];
+    constexpr int RVALS = RR * kRdTokSlots;  // (row, token) sums per wave
+    __shared__ double s_part[RR][kRdParts][kTopkTokensPerBlock];
     __shared__ double s_chunk[NORM ? kTopkTokensPerBlock : 1][8];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     static_assert(!NORM || NSW <= 2, "the fused norm takes rows of at most 8 slabs");
     // more than 16 tokens run in groups of 16: workgroup b takes router rows of
-    // block b % nbr for the tokens of group b / nbr; with quant_rows, the last
-    // ceil(T/16) workgroups write x's Q8_0 rows (one wave per token)
-    const int nbr = (a0.E + a0.S + kRdRows - 1) / kRdRows;
-    const int ngr = (a0.T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
-    if (a0.quant_rows && (int)blockIdx.x >= nbr * ngr) {
-        const int t = ((int)blockIdx.x - nbr * ngr) * kTopkTokensPerBlock + wave;
-        if (wave < kTopkTokensPerBlock && t < a0.T) quant_token_row(a0.xe, a0.H, t, lane, a0.xq_qs, a0.xq_ds);
-        return;
-    }
+    // block b % nbr for the tokens of group b / nbr; with quant_rows, router block
+    // rb of a group also writes the Q8_0 rows of its tokens rb + nbr * w (at the end)
+    const int nbr = (a0.E + a0.S + RR - 1) / RR;
     const int gi = (int)blockIdx.x / nbr, rb = (int)blockIdx.x - gi * nbr;
     const int tb = gi * kTopkTokensPerBlock;
     TopkArgs a = a0;  // this group's tokens
@@ -1249,21 +1243,21 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a0, float* logit
         return e < a.E ? a.w_router + (uint64_t)min(e, a.E - 1) * a.router_ld : (a.S ? a.w_sh_norm : a.w_router);
     };
     const int grp = wave / kRdParts;
-    const int e0 = rb * kRdRows;
-    double acc[kRdVals];  // [row q][i]: token kRdGroups * i + grp
+    const int e0 = rb * RR;
+    double acc[RVALS];  // [row q][i]: token kRdGroups * i + grp
 #pragma unroll
-    for (int k = 0; k < kRdVals; ++k) acc[k] = 0.0;
+    for (int k = 0; k < RVALS; ++k) acc[k] = 0.0;
     // two slabs at a time: every load of the pair issued before its FMAs (the
     // first pair's before the RMSNorm scales, whose row loads then overlap them)
     constexpr int kPair = NSW > 1 ? 2 : 1;
-    f32x4 w[kPair][kRdRows], xv[kPair][kRdTokSlots], wn[kPair];
+    f32x4 w[kPair][RR], xv[kPair][kRdTokSlots], wn[kPair];
     float xs[kRdTokSlots];  // NORM: the RMSNorm scales of this wave's tokens
     auto load_pair = [&](int s0) {
 #pragma unroll
         for (int u = 0; u < kPair; ++u) {
             const int c = min(part + kRdParts * (s0 + u), nslab - 1);  // this wave's slab (clamped)
 #pragma unroll
-            for (int q = 0; q < kRdRows; ++q)
+            for (int q = 0; q < RR; ++q)
                 w[u][q] = *(const f32x4*)(router_row(e0 + q) + c * kRdSlab + 4 * lane);
             if constexpr (NORM) wn[u] = *(const f32x4*)(a.norm_w + c * kRdSlab + 4 * lane);
 #pragma unroll
@@ -1290,7 +1284,7 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a0, float* logit
                     }
                     const double x0 = xx.x, x1 = xx.y, x2 = xx.z, x3 = xx.w;
 #pragma unroll
-                    for (int q = 0; q < kRdRows; ++q) {
+                    for (int q = 0; q < RR; ++q) {
                         double& d = acc[q * kRdTokSlots + i];
                         d = __builtin_fma((double)w[u][q].x, x0, d);
                         d = __builtin_fma((double)w[u][q].y, x1, d);
@@ -1370,28 +1364,20 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a0, float* logit
         compute_pair(s0);
     }
     // wave sums of the (row, token) values: one reduce-scatter, a fixed cost
-    // below the trees of 6 steps per live value
-    if (kRdVals <= 8 || a.T > 4) {
-        double sums[kRdVals / 4];
-        wave_sum_rs_f64<kRdVals>(acc, sums);
-        const int j = lane & 15, k = j + (kRdVals / 4) * (lane >> 4);
+    // below the trees of 6 steps per live value (each slot's sum in the same
+    // order for any row count)
+    {
+        double sums[RVALS / 4];
+        wave_sum_rs_f64<RVALS>(acc, sums);
+        const int j = lane & 15, k = j + (RVALS / 4) * (lane >> 4);
         const int t = kRdGroups * (k % kRdTokSlots) + grp;
         double v = sums[0];
 #pragma unroll
-        for (int m = 1; m < kRdVals / 4; ++m) v = j == m ? sums[m] : v;
-        if (j < kRdVals / 4 && t < a.T) s_part[k / kRdTokSlots][part][t] = v;
-    } else {
-#pragma unroll
-        for (int k = 0; k < kRdVals; ++k) {
-            const int t = kRdGroups * (k % kRdTokSlots) + grp;
-            if (t < a.T) {
-                const double sum = dpp_sum_f64<64>(acc[k]);
-                if (lane == 63) s_part[k / kRdTokSlots][part][t] = sum;
-            }
-        }
+        for (int m = 1; m < RVALS / 4; ++m) v = j == m ? sums[m] : v;
+        if (j < RVALS / 4 && t < a.T) s_part[k / kRdTokSlots][part][t] = v;
     }
     __syncthreads();
-    if (tid < kRdRows * a.T) {
+    if (tid < RR * a.T) {
         const int rr = tid / a.T, t = tid % a.T;
         const int er = e0 + rr;
         if (er < E1) {
@@ -1407,6 +1393,10 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a0, float* logit
 #pragma unroll
             for (int i = 0; i < kRdTokSlots; ++i)
                 if (kRdGroups * i + grp < a.T) a.x_scale[kRdGroups * i + grp] = xs[i];
+    }
+    if (a0.quant_rows) {  // wave w: the group's token rb + nbr * w (at most one per block when nbr >= 16)
+        const int t = rb + nbr * wave;
+        if (t < a.T) quant_token_row(a0.xe, a0.H, tb + t, lane, a0.xq_qs, a0.xq_ds);
     }
 }
 
@@ -1529,6 +1519,19 @@ static const void* route_decode_kernel(int nsw, bool norm) {
     switch (nsw) {
         case 1: return (const void*)k_route_decode<1, false>;
         case 2: return (const void*)k_route_decode<2, false>;
+        case 3: return (const void*)k_route_decode<3, false>;
+        case 4: return (const void*)k_route_decode<4, false>;
+        default: return nullptr;
+    }
+}
+// The router over groups of 16 tokens: five rows per block for rows of at most
+// 2048 columns (a 256-expert layer's 52 blocks per group fill the CUs in one
+// round up to 64 tokens), two for wider rows (five would spill registers).
+static const void* route_group_kernel(int nsw, int* rows) {
+    *rows = nsw <= 2 ? 5 : kRdRows;
+    switch (nsw) {
+        case 1: return (const void*)k_route_decode<1, false, 5>;
+        case 2: return (const void*)k_route_decode<2, false, 5>;
         case 3: return (const void*)k_route_decode<3, false>;
         case 4: return (const void*)k_route_decode<4, false>;
         default: return nullptr;
@@ -1687,17 +1690,18 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
             return err;
         return hipGetLastError();
     } else {
-        // the decode router over groups of 16 tokens, x's Q8_0 on the same launch's
-        // last workgroups; then the top-k
+        // the decode router over groups of 16 tokens, x's Q8_0 on the same launch
+        // (after each block's logits); then the top-k
         ta.quant_rows = 1;
-        const int nb = (L.E + L.S + kRdRows - 1) / kRdRows;
         const int ngr = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
         const int nsw = (L.H / kRdSlab + kRdParts - 1) / kRdParts;
-        const void* kern = route_decode_kernel(nsw, false);
+        int rows = 0;
+        const void* kern = route_group_kernel(nsw, &rows);
         if (!kern) return hipErrorInvalidValue;
+        const int nb = (L.E + L.S + rows - 1) / rows;
         float* logits = ws.logits;
         void* args[] = {&ta, &logits};
-        if ((err = hipLaunchKernel(kern, dim3(nb * ngr + ngr), dim3(64 * kTopkTokensPerBlock), args, 0, stream)) !=
+        if ((err = hipLaunchKernel(kern, dim3(nb * ngr), dim3(64 * kTopkTokensPerBlock), args, 0, stream)) !=
             hipSuccess)
             return err;
         ta.quant_rows = 0;

@@ -119,6 +119,17 @@ def test_decode_hidden_sizes(gpu, spec, T):
     assert_parity(y, got, y_ref, d_ref, spec)
 
 
+@pytest.mark.parametrize("spec,T", [(LayerSpec(4096, 64, 4, 256, True, TYPE_Q8_0), 20),
+                                    (LayerSpec(3072, 96, 6, 512, True, TYPE_Q4_0), 40),
+                                    (LayerSpec(1280, 40, 4, 512, False, TYPE_Q4_0), 50)])
+def test_grouped_router_hidden_sizes(gpu, spec, T):
+    """17-255 tokens (the router over groups of 16 tokens, x's Q8_0 rows written by its
+    blocks) at hidden 4096 / 3072 (two router rows per block) and 1280 (five rows per
+    block, the last wave with one slab fewer, 9 blocks per group for 16 tokens)."""
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=310 + T)
+    assert_parity(y, got, y_ref, d_ref, spec)
+
+
 @pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 33, 64])
 def test_token_counts_small_layer(gpu, T):
     """Edge token counts: single token, block boundaries of the top-k sort (16 per block)."""
