@@ -98,7 +98,13 @@ const char* qmoe_last_error(void);
  * Q4_0 or Q8_0; w_sh_gate/up [n_embd, ffn_dim], w_sh_down [ffn_dim, n_embd]
  * (same types as the routed gate/up and down); w_sh_norm [n_embd] F32.
  * w_sh_* must be non-NULL iff hp->has_shared_expert.  Weights are borrowed:
- * they must outlive the layer.  The layer is bound to the current device. */
+ * they must outlive the layer.  The layer is bound to the current device.
+ * n_embd and ffn_dim: multiples of 32 (whole Q4_0/Q8_0 blocks) up to 4096.
+ * When n_embd is not a multiple of 256 or ffn_dim not of 64, the layer keeps
+ * zero-padded copies of the weights at those widths (made here, one more copy
+ * of the weights, any byte strides accepted) and every forward pads its rows
+ * into the workspace and writes back the caller's width; results are those of
+ * the unpadded layer (zero columns add exact zeros). */
 int qmoe_layer_create(const qmoe_tensor* w_router,
                       const qmoe_tensor* w_exp_gate,
                       const qmoe_tensor* w_exp_up,

@@ -3,6 +3,8 @@
 #include "qmoe_device.h"
 #include "qmoe_internal.h"
 
+#include <algorithm>
+
 namespace qmoe {
 
 // ---------------------------------------------------------------------------
@@ -96,6 +98,43 @@ __global__ __launch_bounds__(256) void k_fill_i32(int32_t* dst, int n, int32_t v
 hipError_t launch_fill_i32(int32_t* dst, int n, int32_t v, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_fill_i32, dim3((n + 255) / 256), dim3(256), 0, stream, dst, n, v);
+    return hipGetLastError();
+}
+
+// Zero padding of rows for layers built with padded widths (the padded
+// columns meet zero weights, so every dot and every Q8_0 block of the real
+// columns keeps its value).
+__global__ __launch_bounds__(256) void k_pad_rows(const float* src, int T, int hs, int hd, float* dst) {
+    const uint64_t n = (uint64_t)T * hd;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const uint64_t t = i / (uint64_t)hd, c = i - t * (uint64_t)hd;
+        dst[i] = c < (uint64_t)hs ? src[t * hs + c] : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_unpad_rows(const float* src, int T, int hs, int hd, const float* residual,
+                                                    float* dst) {
+#pragma clang fp contract(off)
+    const uint64_t n = (uint64_t)T * hd;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const uint64_t t = i / (uint64_t)hd, c = i - t * (uint64_t)hd;
+        const float v = src[t * hs + c];
+        dst[i] = residual ? v + residual[i] : v;
+    }
+}
+
+static int pad_grid(int T, int hd) { return (int)std::min<uint64_t>(((uint64_t)T * hd + 255) / 256, 1u << 16); }
+
+hipError_t launch_pad_rows(const float* src, int T, int hs, int hd, float* dst, hipStream_t stream) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_pad_rows, dim3(pad_grid(T, hd)), dim3(256), 0, stream, src, T, hs, hd, dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpad_rows(const float* src, int T, int hs, int hd, const float* residual, float* dst,
+                             hipStream_t stream) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_unpad_rows, dim3(pad_grid(T, hd)), dim3(256), 0, stream, src, T, hs, hd, residual, dst);
     return hipGetLastError();
 }
 

@@ -66,9 +66,11 @@ uint64_t block_bytes(int type) {
 }
 
 // Checks type, rank, ne (ne_expect[i] < 0 means "any"), contiguous rows and
-// 4-byte aligned data/strides.  Returns 0 or an error code (message set).
+// (aligned) 4-byte aligned data/strides: the kernels read the rows in place;
+// tensors that are copied first (padded widths) may have any byte strides.
+// Returns 0 or an error code (message set).
 int check_tensor(const char* slot, const qmoe_tensor* t, int n_dims, const int64_t* ne_expect,
-                 bool quantized) {
+                 bool quantized, bool aligned = true) {
     if (!t) return fail(QMOE_ERR_NULL, slot_error(slot, "a tensor", "null"));
     if (!t->data) return fail(QMOE_ERR_NULL, slot_error(slot, "device data", "null data pointer"));
     if (quantized) {
@@ -96,6 +98,7 @@ int check_tensor(const char* slot, const qmoe_tensor* t, int n_dims, const int64
     if (n_dims >= 3 && t->nb[2] < t->nb[1] * (uint64_t)t->ne[1])
         return fail(QMOE_ERR_SHAPE, slot_error(slot, "nb[2]>=" + std::to_string(t->nb[1] * (uint64_t)t->ne[1]),
                                                "nb[2]=" + std::to_string(t->nb[2])));
+    if (!aligned) return QMOE_OK;
     if (((uintptr_t)t->data & 3u) != 0)
         return fail(QMOE_ERR_SHAPE, slot_error(slot, "4-byte aligned data", "misaligned pointer"));
     for (int i = 1; i < n_dims; ++i)
@@ -121,7 +124,7 @@ int hip_error(hipError_t err, const char* what) { return hip_fail(err, what); }
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Carves the workspace buffers out of `base` (when non-null) and returns the byte size.
-size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* base) {
+size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* base, bool pad) {
     const size_t A = (size_t)T * K;
     const size_t R = A + (size_t)T;  // room for a shared expert
     const int nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
@@ -176,6 +179,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.xn = (float*)take((size_t)T * H * sizeof(float));
     ws.xr = (float*)take((size_t)T * H * sizeof(float));
     ws.x_scale = (float*)take((size_t)T * sizeof(float));
+    ws.yp = pad ? (float*)take((size_t)T * H * sizeof(float)) : nullptr;
     ws.max_tiles = max_tiles;
     ws.cap_T = T; ws.H = H; ws.E = E; ws.K = K; ws.F = F;
     ws.base = base;
@@ -187,6 +191,8 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
 
 struct qmoe_layer {
     LayerDesc d;
+    int Hu = 0, Fu = 0;         // the caller's widths; d.H, d.F are larger when the weights were padded
+    void* pad_base = nullptr;   // the padded weight copies (owned), or null
     int device = 0;
     qmoe_workspace* own_ws = nullptr;
     hipEvent_t phase_events[QMOE_N_PHASE_EVENTS] = {};
@@ -197,6 +203,73 @@ struct qmoe_workspace {
     Workspace w;
     int device = 0;
 };
+
+namespace {
+
+// Zero-padded copies of the layer's weights at widths Hp >= H, Fp >= F (one
+// allocation, owned by the layer); the descriptor then points at them.
+hipError_t build_padded(qmoe_layer& L, int Hp, int Fp) {
+    LayerDesc& d = L.d;
+    const int H = d.H, F = d.F, E = d.E;
+    const uint64_t bg = block_bytes(d.gu_type), bd = block_bytes(d.dn_type);
+    const uint64_t row_g = (uint64_t)(Hp / 32) * bg, row_d = (uint64_t)(Fp / 32) * bd;  // padded row bytes
+    const uint64_t n_router = qmoe::align_up((uint64_t)E * Hp * 4, 256), n_gu = qmoe::align_up((uint64_t)E * Fp * row_g, 256);
+    const uint64_t n_dn = qmoe::align_up((uint64_t)E * Hp * row_d, 256);
+    const uint64_t n_sgu = d.S ? qmoe::align_up((uint64_t)Fp * row_g, 256) : 0, n_sdn = d.S ? qmoe::align_up((uint64_t)Hp * row_d, 256) : 0;
+    const uint64_t n_snorm = d.S ? qmoe::align_up((uint64_t)Hp * 4, 256) : 0;
+    const uint64_t total = n_router + 2 * n_gu + n_dn + 2 * n_sgu + n_sdn + n_snorm;
+    void* base = nullptr;
+    hipError_t err = hipMalloc(&base, total);
+    if (err != hipSuccess) return err;
+    uint8_t* p = (uint8_t*)base;
+    float* router = (float*)p; p += n_router;
+    uint8_t* gate = p; p += n_gu;
+    uint8_t* up = p; p += n_gu;
+    uint8_t* down = p; p += n_dn;
+    uint8_t* sgate = p; p += n_sgu;
+    uint8_t* sup = p; p += n_sgu;
+    uint8_t* sdown = p; p += n_sdn;
+    float* snorm = (float*)p;
+    err = hipMemset(base, 0, total);
+    const hipMemcpyKind k = hipMemcpyDeviceToDevice;
+    if (err == hipSuccess)
+        err = hipMemcpy2D(router, (size_t)Hp * 4, d.w_router, (size_t)d.router_ld * 4, (size_t)H * 4, E, k);
+    const uint64_t wg = (uint64_t)(H / 32) * bg, wd = (uint64_t)(F / 32) * bd;  // real row bytes
+    for (int e = 0; e < E && err == hipSuccess; ++e) {
+        err = hipMemcpy2D(gate + e * Fp * row_g, row_g, d.w_gate + e * d.gate_nb2, d.gate_nb1, wg, F, k);
+        if (err == hipSuccess) err = hipMemcpy2D(up + e * Fp * row_g, row_g, d.w_up + e * d.up_nb2, d.up_nb1, wg, F, k);
+        if (err == hipSuccess)
+            err = hipMemcpy2D(down + e * Hp * row_d, row_d, d.w_down + e * d.down_nb2, d.down_nb1, wd, H, k);
+    }
+    if (d.S && err == hipSuccess) {
+        err = hipMemcpy2D(sgate, row_g, d.w_sh_gate, d.sh_gate_nb1, wg, F, k);
+        if (err == hipSuccess) err = hipMemcpy2D(sup, row_g, d.w_sh_up, d.sh_up_nb1, wg, F, k);
+        if (err == hipSuccess) err = hipMemcpy2D(sdown, row_d, d.w_sh_down, d.sh_down_nb1, wd, H, k);
+        if (err == hipSuccess) err = hipMemcpy(snorm, d.w_sh_norm, (size_t)H * 4, k);
+    }
+    if (err == hipSuccess) err = hipDeviceSynchronize();
+    if (err != hipSuccess) {
+        (void)hipFree(base);
+        return err;
+    }
+    d.H = Hp;
+    d.F = Fp;
+    d.w_router = router;
+    d.router_ld = Hp;
+    d.w_gate = gate; d.gate_nb1 = row_g; d.gate_nb2 = Fp * row_g;
+    d.w_up = up; d.up_nb1 = row_g; d.up_nb2 = Fp * row_g;
+    d.w_down = down; d.down_nb1 = row_d; d.down_nb2 = Hp * row_d;
+    if (d.S) {
+        d.w_sh_gate = sgate; d.sh_gate_nb1 = row_g;
+        d.w_sh_up = sup; d.sh_up_nb1 = row_g;
+        d.w_sh_down = sdown; d.sh_down_nb1 = row_d;
+        d.w_sh_norm = snorm;
+    }
+    L.pad_base = base;
+    return hipSuccess;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -218,15 +291,16 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
     if (hp->top_k < 1 || hp->top_k > hp->n_experts || hp->top_k > 64)
         return fail(QMOE_ERR_VALUE, "qmoe: hparam \"top_k\" expected 1..min(n_experts, 64) (n_experts=" +
                                         std::to_string(hp->n_experts) + "), got " + std::to_string(hp->top_k));
-    if (hp->ffn_dim < 64 || hp->ffn_dim > 4096 || hp->ffn_dim % 64 != 0)
-        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"ffn_dim\" expected a multiple of 64 in [64, 4096], got " +
+    if (hp->ffn_dim < 32 || hp->ffn_dim > 4096 || hp->ffn_dim % 32 != 0)
+        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"ffn_dim\" expected a multiple of 32 in [32, 4096], got " +
                                         std::to_string(hp->ffn_dim));
     if (!w_router) return fail(QMOE_ERR_NULL, slot_error("w_router", "a tensor", "null"));
     const int64_t H = w_router->ne[0];
-    if (H < 256 || H > 4096 || H % 256 != 0)
-        return fail(QMOE_ERR_SHAPE, slot_error("w_router", "ne[0]=n_embd a multiple of 256 in [256, 4096]",
+    if (H < 32 || H > 4096 || H % 32 != 0)
+        return fail(QMOE_ERR_SHAPE, slot_error("w_router", "ne[0]=n_embd a multiple of 32 in [32, 4096]",
                                                "ne[0]=" + std::to_string(H)));
     const int64_t E = hp->n_experts, F = hp->ffn_dim;
+    const bool al = H % 256 == 0 && F % 64 == 0;  // else padded copies are read, not these rows
     int rc;
     {
         const int64_t ne[2] = {H, E};
@@ -234,23 +308,23 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
     }
     {
         const int64_t ne[3] = {H, F, E};
-        if ((rc = check_tensor("w_exp_gate", w_exp_gate, 3, ne, true))) return rc;
-        if ((rc = check_tensor("w_exp_up", w_exp_up, 3, ne, true))) return rc;
+        if ((rc = check_tensor("w_exp_gate", w_exp_gate, 3, ne, true, al))) return rc;
+        if ((rc = check_tensor("w_exp_up", w_exp_up, 3, ne, true, al))) return rc;
         if (w_exp_up->type != w_exp_gate->type)
             return fail(QMOE_ERR_TYPE, slot_error("w_exp_up", "type " + type_str(w_exp_gate->type) + " (as w_exp_gate)",
                                                   type_str(w_exp_up->type)));
     }
     {
         const int64_t ne[3] = {F, H, E};
-        if ((rc = check_tensor("w_exp_down", w_exp_down, 3, ne, true))) return rc;
+        if ((rc = check_tensor("w_exp_down", w_exp_down, 3, ne, true, al))) return rc;
     }
     if (hp->has_shared_expert) {
         const int64_t ne_gu[2] = {H, F};
         const int64_t ne_d[2] = {F, H};
         const int64_t ne_n[1] = {H};
-        if ((rc = check_tensor("w_sh_gate", w_sh_gate, 2, ne_gu, true))) return rc;
-        if ((rc = check_tensor("w_sh_up", w_sh_up, 2, ne_gu, true))) return rc;
-        if ((rc = check_tensor("w_sh_down", w_sh_down, 2, ne_d, true))) return rc;
+        if ((rc = check_tensor("w_sh_gate", w_sh_gate, 2, ne_gu, true, al))) return rc;
+        if ((rc = check_tensor("w_sh_up", w_sh_up, 2, ne_gu, true, al))) return rc;
+        if ((rc = check_tensor("w_sh_down", w_sh_down, 2, ne_d, true, al))) return rc;
         if ((rc = check_tensor("w_sh_norm", w_sh_norm, 1, ne_n, false))) return rc;
         if (w_sh_gate->type != w_exp_gate->type)
             return fail(QMOE_ERR_TYPE, slot_error("w_sh_gate", "type " + type_str(w_exp_gate->type) + " (as w_exp_gate)",
@@ -298,6 +372,18 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 1) d.big_router_min_tokens = (int)std::min<long>(v, 1 << 30);
     }
+    L->Hu = d.H;
+    L->Fu = d.F;
+    if (d.H % 256 != 0 || d.F % 64 != 0) {
+        // widths off the kernels' grid: zero-padded copies (n_embd to a multiple of
+        // 256, ffn_dim of 64); the padded columns and rows meet zero weights and
+        // zero activations, so every real dot, sum and Q8_0 block keeps its value
+        const hipError_t err = build_padded(*L, (d.H + 255) / 256 * 256, (d.F + 63) / 64 * 64);
+        if (err != hipSuccess) {
+            delete L;
+            return hip_fail(err, "padded weight copies");
+        }
+    }
     *out = L;
     return QMOE_OK;
 }
@@ -320,14 +406,14 @@ int qmoe_geglu_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_ga
         return fail(QMOE_ERR_VALUE, "qmoe: hparam \"has_shared_expert\" expected 0 for the GeGLU MoE (Gemma 4 has none), got " +
                                         std::to_string(hp->has_shared_expert));
     if (!w_router) return fail(QMOE_ERR_NULL, slot_error("w_router", "a tensor", "null"));
-    if (hp->ffn_dim < 64 || hp->ffn_dim > 4096 || hp->ffn_dim % 64 != 0)
-        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"ffn_dim\" expected a multiple of 64 in [64, 4096], got " +
+    if (hp->ffn_dim < 32 || hp->ffn_dim > 4096 || hp->ffn_dim % 32 != 0)
+        return fail(QMOE_ERR_VALUE, "qmoe: hparam \"ffn_dim\" expected a multiple of 32 in [32, 4096], got " +
                                         std::to_string(hp->ffn_dim));
     const int64_t H = w_router->ne[0], E = hp->n_experts, F = hp->ffn_dim;
     {
         // [n_embd, 2*ffn_dim, n_experts]: gate rows 0..F-1, up rows F..2F-1 of each expert (gemma4.cpp:397-409)
         const int64_t ne[3] = {H, 2 * F, E};
-        int rc = check_tensor("w_gate_up_exps", w_gate_up_exps, 3, ne, true);
+        int rc = check_tensor("w_gate_up_exps", w_gate_up_exps, 3, ne, true, H % 256 == 0 && F % 64 == 0);
         if (rc) return rc;
     }
     qmoe_tensor gate = *w_gate_up_exps, up = *w_gate_up_exps;
@@ -351,11 +437,12 @@ int qmoe_layer_destroy(qmoe_layer* layer) {
     if (!layer) return QMOE_OK;
     if (layer->own_ws) qmoe_workspace_destroy(layer->own_ws);
     if (layer->d.pk_base) (void)hipFree(layer->d.pk_base);
+    if (layer->pad_base) (void)hipFree(layer->pad_base);
     delete layer;
     return QMOE_OK;
 }
 
-int qmoe_layer_n_embd(const qmoe_layer* layer) { return layer ? layer->d.H : 0; }
+int qmoe_layer_n_embd(const qmoe_layer* layer) { return layer ? layer->Hu : 0; }
 
 int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_workspace** out) {
     g_last_error.clear();
@@ -367,14 +454,15 @@ int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_works
     const LayerDesc& d = like->d;
     qmoe_workspace* ws = new (std::nothrow) qmoe_workspace();
     if (!ws) return fail(QMOE_ERR_VALUE, "qmoe: host allocation failed");
-    const size_t bytes = qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, nullptr, nullptr);
+    const bool pad = like->pad_base != nullptr;
+    const size_t bytes = qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, nullptr, nullptr, pad);
     void* base = nullptr;
     hipError_t err = hipMalloc(&base, bytes);
     if (err != hipSuccess) {
         delete ws;
         return hip_fail(err, "hipMalloc(workspace)");
     }
-    qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, &ws->w, base);
+    qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, &ws->w, base, pad);
     // the signalling area (the expert scan's finished-workgroup counter) starts at zero
     err = hipMemset(ws->w.sync, 0, qmoe::kSyncWords * sizeof(int32_t));
     if (err == hipSuccess) err = hipDeviceSynchronize();
@@ -458,7 +546,58 @@ struct ForwardIn {
     float eps = 0.0f;
     const double* x_ssq = nullptr;  // x's RMSNorm partial sums (norm_w only; optional)
     double* y_ssq = nullptr;        // receives y's RMSNorm partial sums (optional)
+    bool padded_rows = false;       // x (and xr) already at the layer's padded width, y too
 };
+
+static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& in, int32_t n_tokens, float* y,
+                        const qmoe_debug* dbg, void* hip_stream);
+
+// A layer with padded widths: the caller's rows (n_embd = Hu) are prepared at
+// that width (RMSNorm, the Gemma 4 inputs), zero-padded to the layer's width
+// into the workspace, run there, and the first Hu columns of each output row
+// written back with the residual added (the same single f32 add the combine
+// ends with).
+static int forward_padded(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& in, int32_t T, float* y,
+                          const qmoe_debug* dbg, void* hip_stream) {
+    const LayerDesc& d = layer->d;
+    const Workspace& w = ws->w;
+    if (!w.yp)
+        return fail(QMOE_ERR_SHAPE, "qmoe: workspace expected one created for this layer (padded widths), got one "
+                                    "without padded output rows");
+    const int Hu = layer->Hu, Hp = d.H;
+    hipStream_t stream = (hipStream_t)hip_stream;
+    // scratch rows in ybuf (at least 2 T rows; the down stage writes it later)
+    float* t0 = w.ybuf;
+    float* t1 = w.ybuf + (size_t)T * Hp;
+    ForwardIn pin;
+    pin.padded_rows = true;
+    pin.x = w.xn;
+    const float* res = in.residual;
+    hipError_t err;
+    if (in.norm_w) {
+        err = qmoe::launch_rms_norm(in.x, in.norm_w, T, Hu, in.eps, t0, stream);
+        if (err == hipSuccess) err = qmoe::launch_pad_rows(t0, T, Hu, Hp, w.xn, stream);
+        res = in.x;
+    } else if (in.g4_pre_w) {
+        const float s = 1.0f / std::sqrt((float)Hu);  // gemma4.cpp:561-562, the caller's n_embd
+        err = qmoe::launch_gemma4_inputs(in.x, in.g4_pre_w, in.g4_rs_w, T, Hu, in.eps, s, t0, t1, stream);
+        if (err == hipSuccess) err = qmoe::launch_pad_rows(t0, T, Hu, Hp, w.xn, stream);
+        if (err == hipSuccess) err = qmoe::launch_pad_rows(t1, T, Hu, Hp, w.xr, stream);
+        pin.xr = w.xr;
+    } else {
+        err = qmoe::launch_pad_rows(in.x, T, Hu, Hp, w.xn, stream);
+        if (in.xr && err == hipSuccess) {
+            err = qmoe::launch_pad_rows(in.xr, T, Hu, Hp, w.xr, stream);
+            pin.xr = w.xr;
+        }
+    }
+    if (err != hipSuccess) return hip_fail(err, "padded input rows");
+    const int rc = forward_impl(layer, ws, pin, T, w.yp, dbg, hip_stream);
+    if (rc) return rc;
+    err = qmoe::launch_unpad_rows(w.yp, T, Hp, Hu, res, y, stream);
+    if (err == hipSuccess && in.y_ssq) err = qmoe::launch_rms_partials(y, T, Hu, in.y_ssq, stream);
+    return err == hipSuccess ? QMOE_OK : hip_fail(err, "padded output rows");
+}
 
 static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& in, int32_t n_tokens, float* y,
                         const qmoe_debug* dbg, void* hip_stream) {
@@ -507,6 +646,7 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
                                         std::to_string(d.E) + "," + std::to_string(d.K) + "," + std::to_string(d.F) +
                                         "), got (" + std::to_string(w.H) + "," + std::to_string(w.E) + "," +
                                         std::to_string(w.K) + "," + std::to_string(w.F) + ")");
+    if (layer->pad_base && !in.padded_rows) return forward_padded(layer, ws, in, n_tokens, y, dbg, hip_stream);
     // buffers are sized for the workspace's (larger or equal) dims; kernels index with the layer's
     const Workspace& v = w;
     hipStream_t stream = (hipStream_t)hip_stream;
@@ -623,7 +763,9 @@ int qmoe_layer_forward_static(qmoe_layer* layer, const float* x, int32_t n_token
     if (n_tokens < 0) return fail(QMOE_ERR_VALUE, "qmoe: n_tokens expected >= 0, got " + std::to_string(n_tokens));
     if (n_tokens == 0) return QMOE_OK;
     const LayerDesc& d = layer->d;
-    const size_t need = kStaticSyncBytes + qmoe::workspace_bytes(n_tokens, d.H, d.E, d.K, d.F, nullptr, nullptr);
+    const bool pad = layer->pad_base != nullptr;
+    const size_t need =
+        kStaticSyncBytes + qmoe::workspace_bytes(n_tokens, d.H, d.E, d.K, d.F, nullptr, nullptr, pad);
     if (need > QMOE_STATIC_SCRATCH_BYTES)
         return fail(QMOE_ERR_CAPACITY, "qmoe: n_tokens expected a scratch of at most " +
                                            std::to_string(QMOE_STATIC_SCRATCH_BYTES) + " bytes (the static scratch), got " +
@@ -641,7 +783,7 @@ int qmoe_layer_forward_static(qmoe_layer* layer, const float* x, int32_t n_token
     // call; the rest is carved for this call's token count
     qmoe_workspace ws;
     ws.device = dev;
-    qmoe::workspace_bytes(n_tokens, d.H, d.E, d.K, d.F, &ws.w, (char*)base + kStaticSyncBytes);
+    qmoe::workspace_bytes(n_tokens, d.H, d.E, d.K, d.F, &ws.w, (char*)base + kStaticSyncBytes, pad);
     ws.w.sync = (int32_t*)base;
     ForwardIn in;
     in.x = x;

@@ -116,10 +116,11 @@ struct Workspace {
     float* x_scale = nullptr;     // [T] RMSNorm scales of a decode forward that normalizes in its routing
     float* ybuf = nullptr;        // [R][H] down outputs (unweighted)
     float* ysh = nullptr;         // [T][H] the shared expert's down rows (fused decode)
+    float* yp = nullptr;          // [T][H] output rows of a layer with padded widths (null otherwise)
     int max_tiles = 0;
 };
 
-size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* carve, void* base);
+size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* carve, void* base, bool pad = false);
 
 // Launch with optional start/stop events recorded by the launch itself.
 template <typename K, typename... Args>
@@ -196,6 +197,12 @@ hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float e
 hipError_t launch_rms_partials(const float* x, int T, int H, double* out, hipStream_t stream);
 // dst[0..n) = v on `stream` (a kernel, never a memset node).
 hipError_t launch_fill_i32(int32_t* dst, int n, int32_t v, hipStream_t stream);
+// Rows of hs floats -> rows of hd >= hs floats, zeros after column hs (the
+// input of a layer whose widths were padded); and back: the first hd of each
+// hs-wide row, plus residual (when non-null) as one f32 add per value.
+hipError_t launch_pad_rows(const float* src, int T, int hs, int hd, float* dst, hipStream_t stream);
+hipError_t launch_unpad_rows(const float* src, int T, int hs, int hd, const float* residual, float* dst,
+                             hipStream_t stream);
 // Gemma 4 MoE inputs from one pass over x (H <= 4096): expert_in = (x*scale)*w_pre,
 // router_in = ((x*scale)*s)*w_rs with scale = 1/sqrtf(mean(x^2) + eps).
 hipError_t launch_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps, float s,

@@ -105,14 +105,16 @@ def test_shape_mismatch_names_slot():
 
 
 def test_router_width_rules():
-    rc, msg = create(layer_descs(H=320), QmoeHparams(256, 8, 512, 1))
+    rc, msg = create(layer_descs(H=300), QmoeHparams(256, 8, 512, 1))
     assert rc == QMOE_ERR_SHAPE and '"w_router"' in msg
 
 
-@pytest.mark.parametrize("H,F,slot", [(1056, 512, '"w_router"'), (2048, 96, '"ffn_dim"')])
+@pytest.mark.parametrize("H,F,slot", [(4128, 512, '"w_router"'), (2048, 100, '"ffn_dim"'),
+                                      (2048, 4160, '"ffn_dim"'), (16, 512, '"w_router"')])
 def test_widths_outside_the_limits_rejected(H, F, slot):
-    """Widths the reference's Q4_0/Q8_0 rows allow (multiples of 32) but this
-    build does not: rejected before any launch, naming the slot and the limit."""
+    """Widths that are not whole Q4_0/Q8_0 blocks (multiples of 32) or exceed 4096:
+    rejected before any allocation or launch, naming the slot and the limit.  (Other
+    multiples of 32 run on zero-padded weight copies: GPU tests.)"""
     rc, msg = create(layer_descs(H=H, F=F), QmoeHparams(256, 8, F, 1))
     assert rc in (QMOE_ERR_SHAPE, QMOE_ERR_VALUE)
     assert slot in msg and "multiple of" in msg and "got" in msg

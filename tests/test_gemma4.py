@@ -232,6 +232,33 @@ def test_gemma4_layer_matches_oracle(gpu, wname, T):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T", [10, 40, 150])
+def test_geglu_padded_widths(gpu, T):
+    """A GeGLU layer at widths off the kernels' grid (n_embd 160, ffn_dim 96): the Gemma 4
+    slice (inputs at the caller's width, then zero-padded) against the oracle."""
+    import torch
+
+    from qwenium_amd import Workspace, gemma4_moe_inputs, synthetic
+
+    spec = synthetic.LayerSpec(160, 16, 4, 96, False, TYPE_Q4_0, geglu=True)
+    seed = 61 + T
+    tensors = synthetic.make_layer_tensors(spec, seed)
+    layer = synthetic.make_layer(spec, seed, tensors=tensors)
+    x = synthetic.make_x(spec, T, seed)
+    w_pre, w_rs = synthetic.make_gemma4_norms(spec, seed, 0)
+    ei, ri = gemma4_moe_inputs(x, w_pre, w_rs, synthetic.NORM_EPS)
+    ws = Workspace(layer, T)
+    y, dbg = layer.forward_routed(ei, ri, workspace=ws, debug=True)
+    y_one = layer.forward_gemma4(x, w_pre, w_rs, synthetic.NORM_EPS, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_one)
+    ref = host_layer(spec, tensors)
+    y_ref, d_ref = ref.forward(ei.cpu().numpy(), debug=True, router_in=ri.cpu().numpy())
+    got = {k: v.cpu().numpy() for k, v in dbg.items()}
+    assert_parity(y.cpu().numpy(), got, y_ref, d_ref, mfma=T >= 128)
+
+
+@pytest.mark.gpu
 def test_gemma4_inputs_match_oracle(gpu):
     from qwenium_amd import gemma4_moe_inputs, synthetic
 

@@ -130,6 +130,20 @@ def test_grouped_router_hidden_sizes(gpu, spec, T):
     assert_parity(y, got, y_ref, d_ref, spec)
 
 
+@pytest.mark.parametrize("spec,T", [(LayerSpec(96, 8, 2, 32, True, TYPE_Q4_0), 1),
+                                    (LayerSpec(96, 8, 2, 32, True, TYPE_Q4_0), 10),
+                                    (LayerSpec(320, 16, 4, 96, True, TYPE_Q8_0), 17),
+                                    (LayerSpec(160, 12, 3, 224, False, TYPE_Q4_0), 300)])
+def test_padded_widths(gpu, spec, T):
+    """n_embd and ffn_dim that Q4_0/Q8_0 rows allow (multiples of 32) but the kernels'
+    grid does not (multiples of 256 and 64): the layer runs on zero-padded weight copies
+    and zero-padded rows, and routing and outputs match the oracle at the caller's widths
+    as on every other path (decode, streaming, and MFMA with the batched router)."""
+    y, got, y_ref, d_ref, layer, *_ = run_pair(spec, T, seed=400 + T)
+    assert layer.n_embd == spec.n_embd and y.shape == (T, spec.n_embd)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= 128)
+
+
 @pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 33, 64])
 def test_token_counts_small_layer(gpu, T):
     """Edge token counts: single token, block boundaries of the top-k sort (16 per block)."""
@@ -516,7 +530,7 @@ def test_fused_decode_routing_repeated(gpu, n_experts, T):
 
 
 @pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 300),
-                                     ("config1", 5), ("h4096", 10)])
+                                     ("config1", 5), ("h4096", 10), ("pad", 10)])
 def test_forward_norm_chain(gpu, which, T):
     """Three blocks with the RMSNorm partial sums carried from each to the next
     (x_ssq in, y_ssq out; the first block without x_ssq): every block's y has the
@@ -526,7 +540,8 @@ def test_forward_norm_chain(gpu, which, T):
     from qwenium_amd import Workspace, ssq_parts
 
     spec = {"35b": synthetic.QWEN35B, "config1": synthetic.CONFIG1,
-            "h4096": synthetic.LayerSpec(4096, 16, 2, 64, True, synthetic.TYPE_Q4_0)}[which]
+            "h4096": synthetic.LayerSpec(4096, 16, 2, 64, True, synthetic.TYPE_Q4_0),
+            "pad": synthetic.LayerSpec(96, 8, 2, 32, True, synthetic.TYPE_Q4_0)}[which]
     seed = 23
     x = synthetic.make_x(spec, T, seed, batch=T)
     x_ssq = None
@@ -547,7 +562,7 @@ def test_forward_norm_chain(gpu, which, T):
 
 
 @pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 300),
-                                     ("config1", 5), ("config1", 32), ("h4096", 10)])
+                                     ("config1", 5), ("config1", 32), ("h4096", 10), ("pad", 10), ("pad", 130)])
 def test_forward_norm_matches_unfused(gpu, which, T):
     """y = x + MoE(RMSNorm(x) * w) in one call (the decode routing normalizes while it
     stages x; other sizes normalize into the workspace) gives the bits of rms_norm
@@ -555,7 +570,8 @@ def test_forward_norm_matches_unfused(gpu, which, T):
     from qwenium_amd import Workspace, rms_norm
 
     spec = {"35b": synthetic.QWEN35B, "config1": synthetic.CONFIG1,
-            "h4096": synthetic.LayerSpec(4096, 16, 2, 64, True, synthetic.TYPE_Q4_0)}[which]
+            "h4096": synthetic.LayerSpec(4096, 16, 2, 64, True, synthetic.TYPE_Q4_0),
+            "pad": synthetic.LayerSpec(96, 8, 2, 32, True, synthetic.TYPE_Q4_0)}[which]
     seed = 21
     layer = synthetic.make_layer(spec, seed)
     ws = Workspace(layer, T)

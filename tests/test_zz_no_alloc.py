@@ -32,14 +32,16 @@ def test_static_forward_rejects_sizes_above_the_scratch():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("spec_name,sizes", [("QWEN35B", (40, 3)), ("QWEN35B", (10, 1)), ("CONFIG1", (32, 17)),
-                                             ("GEMMA4", (16, 5))])
+                                             ("GEMMA4", (16, 5)), ("PADDED", (20, 3))])
 def test_static_forward_matches_workspace_forward(gpu, spec_name, sizes):
     import torch
 
     from qwenium_amd import Workspace, synthetic
     from qwenium_amd._lib import check, lib
 
-    spec = getattr(synthetic, spec_name)
+    # PADDED: widths off the kernels' grid (the static scratch also holds the padded rows)
+    spec = (synthetic.LayerSpec(96, 8, 2, 32, True, synthetic.TYPE_Q4_0) if spec_name == "PADDED"
+            else getattr(synthetic, spec_name))
     layer = synthetic.make_layer(spec, 29)
     ws = Workspace(layer, max(sizes))
     stream = torch.cuda.current_stream().cuda_stream
