@@ -133,7 +133,9 @@ def test_grouped_router_hidden_sizes(gpu, spec, T):
 @pytest.mark.parametrize("spec,T", [(LayerSpec(96, 8, 2, 32, True, TYPE_Q4_0), 1),
                                     (LayerSpec(96, 8, 2, 32, True, TYPE_Q4_0), 10),
                                     (LayerSpec(320, 16, 4, 96, True, TYPE_Q8_0), 17),
-                                    (LayerSpec(160, 12, 3, 224, False, TYPE_Q4_0), 300)])
+                                    (LayerSpec(160, 12, 3, 224, False, TYPE_Q4_0), 300),
+                                    (LayerSpec(1056, 32, 4, 96, True, TYPE_Q4_0), 10),
+                                    (LayerSpec(1056, 32, 4, 96, True, TYPE_Q4_0), 150)])
 def test_padded_widths(gpu, spec, T):
     """n_embd and ffn_dim that Q4_0/Q8_0 rows allow (multiples of 32) but the kernels'
     grid does not (multiples of 256 and 64): the layer runs on zero-padded weight copies
