@@ -2,9 +2,9 @@
 // re-run through the C++ drop-in (include/qmoe_layer.hpp) on the HIP path.
 //
 // Same cases and constant fills as the reference (router 0.1, experts 0.05,
-// shared 0.02, shared gate 0.5, input 0.5), at the smallest shapes the
-// quantized kernels take (n_embd 256, ffn 64, 8 experts, top-2, 2 tokens),
-// with Q8_0 expert weights.  TopKGatingCorrectness feeds the reference's KAT
+// shared 0.02, shared gate 0.5, input 0.5), at the smallest widths Q8_0 rows
+// allow (n_embd 32, ffn 32: one block each; the layer runs them on its
+// zero-padded copies), 8 experts, top-2, 2 tokens, with Q8_0 expert weights.  TopKGatingCorrectness feeds the reference's KAT
 // logits {1,3,0.5,2,-1,0,4,1.5} through the real router (one-hot input, so
 // logits equal the router column exactly) and checks ids [6,1] and weights
 // 0.7310586 / 0.2689414.
@@ -42,7 +42,7 @@ static int g_failures = 0;
         }                                                                                    \
     } while (0)
 
-constexpr int N_EMBD = 256, N_EXPERTS = 8, TOP_K = 2, FFN_DIM = 64, N_TOKENS = 2;
+constexpr int N_EMBD = 32, N_EXPERTS = 8, TOP_K = 2, FFN_DIM = 32, N_TOKENS = 2;
 
 // Q8_0 bytes of n values all equal to v (quantize_row_q8_0_ref of a constant block).
 static std::vector<uint8_t> q8_const(float v, size_t n) {
@@ -169,22 +169,26 @@ static void OutputShapeMatchesInput() {
     HIP_OK(hipDeviceSynchronize());
 }
 
-// Host-only: the constructor's fail-loud contract (moe.cpp:47-52), fake pointers.
+// Host-only: the constructor's fail-loud contract (moe.cpp:47-52), fake pointers,
+// at widths on the kernels' grid (256, 64): such a layer reads its weights in
+// place, so constructing it touches no device memory (a padded one copies them).
 static void ConstructorThrowsWithoutSharedWeights() {
     const void* fake = (const void*)0x10000000;
-    qmoe_tensor r = qmoe::make_tensor(fake, QMOE_TYPE_F32, 2, N_EMBD, N_EXPERTS);
-    qmoe_tensor g = qmoe::make_tensor(fake, QMOE_TYPE_Q8_0, 3, N_EMBD, FFN_DIM, N_EXPERTS);
-    qmoe_tensor d = qmoe::make_tensor(fake, QMOE_TYPE_Q8_0, 3, FFN_DIM, N_EMBD, N_EXPERTS);
+    constexpr int kEmbd = 256, kFfn = 64;
+    qmoe_tensor r = qmoe::make_tensor(fake, QMOE_TYPE_F32, 2, kEmbd, N_EXPERTS);
+    qmoe_tensor g = qmoe::make_tensor(fake, QMOE_TYPE_Q8_0, 3, kEmbd, kFfn, N_EXPERTS);
+    qmoe_tensor d = qmoe::make_tensor(fake, QMOE_TYPE_Q8_0, 3, kFfn, kEmbd, N_EXPERTS);
+    const qmoe::MoELayer::Hparams hp_shared{N_EXPERTS, TOP_K, kFfn, true}, hp_plain{N_EXPERTS, TOP_K, kFfn, false};
     std::string msg;
     try {
-        qmoe::MoELayer layer(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hparams(true));
+        qmoe::MoELayer layer(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hp_shared);
     } catch (const std::runtime_error& e) {
         msg = e.what();
     }
     EXPECT(msg == "moe_layer: has_shared_expert=true but shared expert weights are null", "reference message");
     bool threw = false;
     try {
-        qmoe::MoELayer ok(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hparams(false));
+        qmoe::MoELayer ok(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hp_plain);
     } catch (const std::runtime_error&) {
         threw = true;
     }
