@@ -563,8 +563,9 @@ def test_forward_norm_chain(gpu, which, T):
     assert ws.check() == 0
 
 
-@pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 300),
-                                     ("config1", 5), ("config1", 32), ("h4096", 10), ("pad", 10), ("pad", 130)])
+@pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 64), ("35b", 100),
+                                     ("35b", 300), ("config1", 5), ("config1", 32), ("h4096", 10), ("pad", 10),
+                                     ("pad", 130)])
 def test_forward_norm_matches_unfused(gpu, which, T):
     """y = x + MoE(RMSNorm(x) * w) in one call (the decode routing normalizes while it
     stages x; other sizes normalize into the workspace) gives the bits of rms_norm
