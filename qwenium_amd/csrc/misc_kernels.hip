@@ -15,14 +15,16 @@ namespace qmoe {
 // (runs of four columns, then a pairwise tree), as the fused decode router
 // computes it.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_rms_norm(const float* x, const float* w, int H, float eps, float* y) {
+// one 1024-thread block per row: each 256-column chunk's tree in its own wave (one
+// round of row loads), the same order as with fewer waves
+__global__ __launch_bounds__(1024) void k_rms_norm(const float* x, const float* w, int H, float eps, float* y) {
 #pragma clang fp contract(off)
     __shared__ double s_chunk[kRmsMaxChunks];
     __shared__ float s_scale;
     const int t = blockIdx.x;
     const float* xr = x + (uint64_t)t * H;
     const float scale = rms_scale_row(xr, H, eps, s_chunk, &s_scale);
-    for (int i = threadIdx.x; i < H; i += 256) {
+    for (int i = threadIdx.x; i < H; i += 1024) {
         const float v = xr[i] * scale;
         y[(uint64_t)t * H + i] = w ? v * w[i] : v;
     }
@@ -30,7 +32,7 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* x, const float* w
 
 hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float eps, float* y, hipStream_t stream) {
     if (H > 256 * kRmsMaxChunks) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(256), 0, stream, x, w, H, eps, y);
+    hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(1024), 0, stream, x, w, H, eps, y);
     return hipGetLastError();
 }
 
@@ -62,7 +64,7 @@ hipError_t launch_rms_partials(const float* x, int T, int H, double* out, hipStr
 // with s = 1/sqrtf(n_embd): the scale computed once, in k_rms_norm's
 // summation order (so rms_norm(x) has the same bits).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int H,
+__global__ __launch_bounds__(1024) void k_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int H,
                                                        float eps, float s, float* ei, float* ri) {
 #pragma clang fp contract(off)
     __shared__ double s_chunk[kRmsMaxChunks];
@@ -70,7 +72,7 @@ __global__ __launch_bounds__(256) void k_gemma4_inputs(const float* x, const flo
     const int t = blockIdx.x;
     const float* xr = x + (uint64_t)t * H;
     const float scale = rms_scale_row(xr, H, eps, s_chunk, &s_scale);
-    for (int i = threadIdx.x; i < H; i += 256) {
+    for (int i = threadIdx.x; i < H; i += 1024) {
         const float u = xr[i] * scale;
         ei[(uint64_t)t * H + i] = u * w_pre[i];
         const float r = u * s;
@@ -80,7 +82,7 @@ __global__ __launch_bounds__(256) void k_gemma4_inputs(const float* x, const flo
 
 hipError_t launch_gemma4_inputs(const float* x, const float* w_pre, const float* w_rs, int T, int H, float eps, float s,
                                 float* expert_in, float* router_in, hipStream_t stream) {
-    hipLaunchKernelGGL(k_gemma4_inputs, dim3(T), dim3(256), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
+    hipLaunchKernelGGL(k_gemma4_inputs, dim3(T), dim3(1024), 0, stream, x, w_pre, w_rs, H, eps, s, expert_in, router_in);
     return hipGetLastError();
 }
 
