@@ -84,6 +84,25 @@ typedef struct qmoe_debug {
      * counterpart in the reference. */
     float*   router_approx; /* [T][n_experts] */
     float*   router_bound;  /* [T][n_experts] */
+    /* The Q8_0 of h = silu(gate) * up (GeGLU: gelu(gate) * up) as the down
+     * projection reads it: the reference's moe_exp_act (moe.cpp:117-118),
+     * which ggml's mul_mat_id quantizes for the down GEMM (:127), and the
+     * shared expert's sh_act (:163-164).  Rows: assignment t*top_k + j, then
+     * with a shared expert one row per token (row T*top_k + t).  Written on
+     * every path. */
+    int8_t*  h_qs;      /* [T*top_k + S*T][ffn_dim] quants */
+    float*   h_d;       /* [T*top_k + S*T][ffn_dim/32] block scales (fp16 values) */
+    /* [1] h blocks whose f32 rounding the large-token-count (f16-MFMA) path
+     * could not settle and recomputed exactly; 0 on the other paths.  No
+     * counterpart in the reference. */
+    int32_t* h_fixed;
+    /* [T*top_k + S*T][n_embd] the unweighted expert rows, the reference's
+     * moe_exp_down (moe.cpp:127-128) and moe_shared_out (:165), same row
+     * order as h.  Written only where the forward materializes them (the
+     * f16-MFMA path and the streaming path without the fused combine); at
+     * decode sizes the combine consumes them in registers and this buffer is
+     * left as it was. */
+    float*   exp_down;
 } qmoe_debug;
 
 typedef struct qmoe_layer qmoe_layer;

@@ -45,7 +45,7 @@ class QoLayer(ctypes.Structure):
 
 class QoDebug(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in
-                ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows", "h", "y", "sh_out")]
+                ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows", "h", "y", "sh_out", "sh_h")]
 
 
 _lib = None
@@ -230,10 +230,10 @@ class Layer:
                 "topk_w": np.empty((T, self.K), np.float32), "sh_gate": np.empty(T, np.float32),
                 "offsets": np.empty(self.E + 1, np.int32), "rows": np.empty(A, np.int32),
                 "h": np.empty((A, self.F), np.float32), "y": np.empty((A, self.H), np.float32),
-                "sh_out": np.empty((T, self.H), np.float32),
+                "sh_out": np.empty((T, self.H), np.float32), "sh_h": np.empty((T, self.F), np.float32),
             }
             dbg = QoDebug(*(_p(d[n]) for n in
-                            ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows", "h", "y", "sh_out")))
+                            ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows", "h", "y", "sh_out", "sh_h")))
         rc = lib().qo_moe_forward_routed(ctypes.byref(self._c), _p(x), _p(xr), T, _p(y),
                                          ctypes.byref(dbg) if dbg is not None else None, nthreads)
         if rc != 0:

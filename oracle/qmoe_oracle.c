@@ -567,6 +567,7 @@ int qo_moe_forward_routed(const qo_layer* L, const float* x, const float* xr, in
                 const float u = qo_vec_dot(wt, (const uint8_t*)L->w_sh_up + (size_t)f * wrow_h, xq + xq_row * t, H);
                 hs[f] = qo_act_mul(act, g, u);
             }
+            if (dbg && dbg->sh_h) memcpy(dbg->sh_h + (size_t)t * F, hs, sizeof(float) * (size_t)F);
             qo_quantize_q8_0_act(hs, hsq, F);
             for (int n = 0; n < H; ++n)
                 sh_out[(size_t)t * H + n] = qo_vec_dot(wt, (const uint8_t*)L->w_sh_down + (size_t)n * wrow_f, hsq, F);

@@ -145,6 +145,7 @@ typedef struct qo_debug {            /* every pointer optional (NULL) */
     float*   h;                      /* [T*k][F] SwiGLU activations, (t,j) order */
     float*   y;                      /* [T*k][H] down outputs before weighting, (t,j) order */
     float*   sh_out;                 /* [T][H] shared down output before gating */
+    float*   sh_h;                   /* [T][F] shared expert's h = act(g)*u (before its Q8_0) */
 } qo_debug;
 
 /* y[T][H] = MoE(x[T][H]).  nthreads <= 0 selects the OpenMP default.

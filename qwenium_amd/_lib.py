@@ -102,6 +102,10 @@ class QmoeDebug(ctypes.Structure):
         ("rows", ctypes.c_void_p),
         ("router_approx", ctypes.c_void_p),
         ("router_bound", ctypes.c_void_p),
+        ("h_qs", ctypes.c_void_p),
+        ("h_d", ctypes.c_void_p),
+        ("h_fixed", ctypes.c_void_p),
+        ("exp_down", ctypes.c_void_p),
     ]
 
 

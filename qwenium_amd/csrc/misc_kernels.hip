@@ -103,6 +103,57 @@ hipError_t launch_fill_i32(int32_t* dst, int n, int32_t v, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Debug copies of per-row intermediates in assignment order.  Workspace row p
+// holds routed assignment rows[p] for p < A (rows grouped by expert) and the
+// shared expert's row of token p - A after them; output row = rows[p] or p.
+// h: from the int8 quants + {d, sum} records of the decode and streaming paths
+// (qs8, ds8) or the f16 quants + fp16 scale bits of the MFMA path (q16, d16);
+// the first fo of each f-wide row (fo: the caller's ffn width).
+__global__ __launch_bounds__(256) void k_debug_h(const int32_t* rows, int A, int R, int f, int fo, const int8_t* qs8,
+                                                 const float2* ds8, const _Float16* q16, const uint16_t* d16,
+                                                 int8_t* out_q, float* out_d) {
+    const uint64_t n = (uint64_t)R * fo;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const int p = (int)(i / (uint64_t)fo), c = (int)(i - (uint64_t)p * fo);
+        const uint64_t dst = p < A ? (uint64_t)rows[p] : (uint64_t)p;
+        const uint64_t s = (uint64_t)p * f + c;
+        out_q[dst * fo + c] = qs8 ? qs8[s] : (int8_t)(float)q16[s];
+        if ((c & 31) == 0) {
+            const uint64_t b = (uint64_t)p * (f >> 5) + (c >> 5);
+            out_d[dst * (fo >> 5) + (c >> 5)] = ds8 ? ds8[b].x : fp16_to_f32(d16[b]);
+        }
+    }
+}
+
+// The unweighted down rows (ybuf, h-wide) in assignment order, first ho columns.
+__global__ __launch_bounds__(256) void k_debug_rows(const int32_t* rows, int A, int R, int h, int ho, const float* src,
+                                                    float* out) {
+    const uint64_t n = (uint64_t)R * ho;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const int p = (int)(i / (uint64_t)ho), c = (int)(i - (uint64_t)p * ho);
+        const uint64_t dst = p < A ? (uint64_t)rows[p] : (uint64_t)p;
+        out[dst * ho + c] = src[(uint64_t)p * h + c];
+    }
+}
+
+hipError_t launch_debug_h(const int32_t* rows, int A, int R, int f, int fo, const int8_t* qs8, const float2* ds8,
+                          const _Float16* q16, const uint16_t* d16, int8_t* out_q, float* out_d, hipStream_t stream) {
+    const uint64_t n = (uint64_t)R * fo;
+    if (n == 0) return hipSuccess;
+    const unsigned g = (unsigned)std::min<uint64_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_debug_h, dim3(g), dim3(256), 0, stream, rows, A, R, f, fo, qs8, ds8, q16, d16, out_q, out_d);
+    return hipGetLastError();
+}
+
+hipError_t launch_debug_rows(const int32_t* rows, int A, int R, int h, int ho, const float* src, float* out,
+                             hipStream_t stream) {
+    const uint64_t n = (uint64_t)R * ho;
+    if (n == 0) return hipSuccess;
+    const unsigned g = (unsigned)std::min<uint64_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_debug_rows, dim3(g), dim3(256), 0, stream, rows, A, R, h, ho, src, out);
+    return hipGetLastError();
+}
+
 // Zero padding of rows for layers built with padded widths (the padded
 // columns meet zero weights, so every dot and every Q8_0 block of the real
 // columns keeps its value).

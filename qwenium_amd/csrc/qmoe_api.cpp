@@ -155,7 +155,7 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.expert_slot = (int32_t*)take((size_t)E * sizeof(int32_t));
     ws.slot_info = (int4*)take((size_t)(E + 1) * sizeof(int4));
     ws.dslots = (int4*)take((size_t)(E + 2) * sizeof(int4));
-    ws.counters = (int32_t*)take(16 * sizeof(int32_t));
+    ws.counters = (int32_t*)take(qmoe::kCounters * sizeof(int32_t));
     ws.sync = (int32_t*)take(kSyncWords * sizeof(int32_t));
     ws.tiles = (int4*)take((size_t)max_tiles * sizeof(int4));
     ws.gubuf = (float2*)take(R * F * sizeof(float2));
@@ -743,6 +743,25 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
             if (!c.dst) continue;
             err = hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice, stream);
             if (err != hipSuccess) return hip_fail(err, c.what);
+        }
+        // per-row intermediates in assignment order, at the caller's widths
+        const int A = n_tokens * d.K, R = A + d.S * n_tokens;
+        const int Fo = layer->Fu ? layer->Fu : d.F, Ho = layer->Hu ? layer->Hu : d.H;
+        if (dbg->h_qs && dbg->h_d) {
+            err = mfma ? qmoe::launch_debug_h(v.rows, A, R, d.F, Fo, nullptr, nullptr, v.h_q, v.h_d, dbg->h_qs, dbg->h_d,
+                                              stream)
+                       : qmoe::launch_debug_h(v.rows, A, R, d.F, Fo, v.hq_qs, v.hq_ds, nullptr, nullptr, dbg->h_qs,
+                                              dbg->h_d, stream);
+            if (err != hipSuccess) return hip_fail(err, "debug copy (h)");
+        }
+        if (dbg->h_fixed) {
+            err = mfma ? hipMemcpyAsync(dbg->h_fixed, v.counters + qmoe::kCounterFix, 4, hipMemcpyDeviceToDevice, stream)
+                       : qmoe::launch_fill_i32(dbg->h_fixed, 1, 0, stream);
+            if (err != hipSuccess) return hip_fail(err, "debug copy (h_fixed)");
+        }
+        if (dbg->exp_down && !qmoe::down_combine_fused(d, n_tokens)) {
+            err = qmoe::launch_debug_rows(v.rows, A, R, d.H, Ho, v.ybuf, dbg->exp_down, stream);
+            if (err != hipSuccess) return hip_fail(err, "debug copy (exp_down)");
         }
     }
     return QMOE_OK;

@@ -25,8 +25,12 @@ constexpr int kRmsMaxChunks = 256;
 constexpr int kMfmaTileM = 128;
 // k values per LDS chunk of the prefill GEMMs.
 constexpr int kF16ChunkK = 64;
-// Workspace counters: [0] active slots, [1] tiles, [kCounterFix] listed h blocks.
+// Workspace counters (kCounters ints): [0] active slots, [1] tiles,
+// [kCounterFix] listed h blocks, [kCounterXcd + x] (x = 1..7) the first tile of
+// XCD x in the prefill GEMMs (the routing's scan balances the tiles by work).
+constexpr int kCounters = 32;
 constexpr int kCounterFix = 4;
+constexpr int kCounterXcd = 16;
 constexpr int kFixStride = 36;  // floats per listed h block: 32 values, amax's error estimate, padding
 // Expert activations: SwiGLU (moe.cpp:117) or GeGLU-tanh (gemma4.cpp:423).
 constexpr int kActSilu = 0;
@@ -93,7 +97,7 @@ struct Workspace {
     int4* slot_info = nullptr;    // [E+1] per active slot {expert, first row, rows, 0}
     int4* dslots = nullptr;       // [E+2] decode slot list {expert, first row, rows, token mask}:
                                   // active routed experts, then expert -1 up to min(E, T*K)
-    int32_t* counters = nullptr;  // [16] n_active, n_tiles, ...
+    int32_t* counters = nullptr;  // [kCounters] n_active, n_tiles, ...
     int32_t* sync = nullptr;      // [kSyncWords] zeroed at creation: the scan's finished-workgroup counter
     int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
     float2* gubuf = nullptr;      // [R][F] (gate, up) projections
@@ -197,6 +201,14 @@ hipError_t launch_rms_norm(const float* x, const float* w, int T, int H, float e
 hipError_t launch_rms_partials(const float* x, int T, int H, double* out, hipStream_t stream);
 // dst[0..n) = v on `stream` (a kernel, never a memset node).
 hipError_t launch_fill_i32(int32_t* dst, int n, int32_t v, hipStream_t stream);
+// Debug copies in assignment order (workspace row p -> row rows[p] for p < A,
+// p for the shared rows after them): h's Q8_0 from either representation
+// (qs8/ds8: int8 quants and {d, sum}; q16/d16: f16 quants and fp16 scale bits),
+// the first fo columns of f; and f32 rows, the first ho columns of h.
+hipError_t launch_debug_h(const int32_t* rows, int A, int R, int f, int fo, const int8_t* qs8, const float2* ds8,
+                          const _Float16* q16, const uint16_t* d16, int8_t* out_q, float* out_d, hipStream_t stream);
+hipError_t launch_debug_rows(const int32_t* rows, int A, int R, int h, int ho, const float* src, float* out,
+                             hipStream_t stream);
 // Rows of hs floats -> rows of hd >= hs floats, zeros after column hs (the
 // input of a layer whose widths were padded); and back: the first hd of each
 // hs-wide row, plus residual (when non-null) as one f32 add per value.

@@ -222,7 +222,7 @@ class MoELayer:
             T = x.shape[0]
             res = _rows_in("residual", residual, T, self.n_embd, x.device) if residual is not None else None
             y = _rows_out("out", out, T, self.n_embd, x.device, x)
-            dbg, dbg_tensors = self._debug(T, x.device) if debug else (None, None)
+            dbg, dbg_tensors = self._debug(T, x.device, debug) if debug else (None, None)
             check(lib().qmoe_layer_forward(
                 self._handle, workspace._handle if workspace is not None else None,
                 x.data_ptr(), int(T), y.data_ptr(), res.data_ptr() if res is not None else None,
@@ -245,7 +245,7 @@ class MoELayer:
             T = x.shape[0]
             w = _vec_in("norm_weight", norm_weight, self.n_embd, x.device)
             y = _rows_out("out", out, T, self.n_embd, x.device, x)
-            dbg, dbg_tensors = self._debug(T, x.device) if debug else (None, None)
+            dbg, dbg_tensors = self._debug(T, x.device, debug) if debug else (None, None)
             ws = workspace._handle if workspace is not None else None
             d = ctypes.byref(dbg) if dbg is not None else None
             if x_ssq is None and y_ssq is None:
@@ -270,7 +270,7 @@ class MoELayer:
             y = _rows_out("out", out, x.shape[0], self.n_embd, x.device, x)
             if y.data_ptr() == xr.data_ptr():
                 raise ValueError("out expected a buffer distinct from router_in, got the same storage")
-            dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
+            dbg, dbg_tensors = self._debug(x.shape[0], x.device, debug) if debug else (None, None)
             check(lib().qmoe_layer_forward_routed(
                 self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), xr.data_ptr(),
                 int(x.shape[0]), y.data_ptr(), ctypes.byref(dbg) if dbg is not None else None,
@@ -283,8 +283,16 @@ class MoELayer:
             raise ValueError(f"x expected a cuda float32 [T, {self.n_embd}] tensor, got {_describe(x)}")
         return x.contiguous()
 
-    def _debug(self, T: int, dev):
-        E, k = self.hp.n_experts, self.hp.top_k
+    def _debug(self, T: int, dev, what=True):
+        """Device buffers for the forward's intermediates: the routing (logits,
+        topk_idx, topk_w, sh_gate, offsets, rows, router_approx/router_bound),
+        h's Q8_0 as the down projection reads it (h_qs [R, ffn_dim] int8, h_d
+        [R, ffn_dim/32] scales; R = T*top_k assignment rows, then one shared row
+        per token) and h_fixed (h blocks recomputed exactly on the MFMA path);
+        with what == "rows" also exp_down [R, n_embd], the unweighted expert rows
+        (left NaN where the combine consumes them in registers)."""
+        E, k, F = self.hp.n_experts, self.hp.top_k, self.hp.ffn_dim
+        R = T * k + (T if self.hp.has_shared_expert else 0)
         t = {
             "logits": torch.empty((T, E), dtype=torch.float32, device=dev),
             "topk_idx": torch.empty((T, k), dtype=torch.int32, device=dev),
@@ -294,10 +302,15 @@ class MoELayer:
             "rows": torch.empty((T * k,), dtype=torch.int32, device=dev),
             "router_approx": torch.full((T, E), float("nan"), dtype=torch.float32, device=dev),
             "router_bound": torch.full((T, E), float("nan"), dtype=torch.float32, device=dev),
+            "h_qs": torch.empty((R, F), dtype=torch.int8, device=dev),
+            "h_d": torch.empty((R, F // 32), dtype=torch.float32, device=dev),
+            "h_fixed": torch.full((1,), -1, dtype=torch.int32, device=dev),
         }
-        dbg = QmoeDebug(*(t[n].data_ptr() for n in
-                          ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows", "router_approx",
-                           "router_bound")))
+        if what == "rows":
+            t["exp_down"] = torch.full((R, self.n_embd), float("nan"), dtype=torch.float32, device=dev)
+        names = ("logits", "topk_idx", "topk_w", "sh_gate", "offsets", "rows", "router_approx", "router_bound",
+                 "h_qs", "h_d", "h_fixed", "exp_down")
+        dbg = QmoeDebug(*(t[n].data_ptr() if n in t else None for n in names))
         return dbg, t
 
     __call__ = forward
@@ -332,7 +345,7 @@ class GeGLUMoELayer(MoELayer):
             w = _vec_in("pre_norm_weight", pre_norm_weight, self.n_embd, x.device)
             rs = _vec_in("router_scale", router_scale, self.n_embd, x.device)
             y = _rows_out("out", out, x.shape[0], self.n_embd, x.device, x)
-            dbg, dbg_tensors = self._debug(x.shape[0], x.device) if debug else (None, None)
+            dbg, dbg_tensors = self._debug(x.shape[0], x.device, debug) if debug else (None, None)
             check(lib().qmoe_layer_forward_gemma4(
                 self._handle, workspace._handle if workspace is not None else None, x.data_ptr(), w.data_ptr(),
                 rs.data_ptr(), float(eps), int(x.shape[0]), y.data_ptr(),

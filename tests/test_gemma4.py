@@ -191,6 +191,15 @@ def assert_parity(y, got, y_ref, d_ref, min_identical=0.999, mfma=False):
     ulp = np.abs(got["logits"].view(np.int32).astype(np.int64) - d_ref["logits"].view(np.int32).astype(np.int64))
     assert ulp.max() <= 1, f"router logits differ by {ulp.max()} ulp"
     np.testing.assert_allclose(got["topk_w"], d_ref["topk_w"], rtol=1e-6, atol=0)
+    if "h_qs" in got:
+        # h's Q8_0 as the down projection reads it equals the oracle's, bit for bit
+        h = d_ref["h"]
+        if got["h_qs"].shape[0] > h.shape[0]:
+            h = np.concatenate([h, d_ref["sh_h"]], axis=0)
+        R, F = h.shape
+        blocks = po.quantize_act(h).reshape(R, F // 32, 34)
+        np.testing.assert_array_equal(got["h_qs"], blocks[:, :, 2:].copy().view(np.int8).reshape(R, F))
+        np.testing.assert_array_equal(got["h_d"], blocks[:, :, :2].copy().view(np.float16)[..., 0].astype(np.float32))
     rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
     err = float(np.max(np.abs(y - y_ref)))
     assert err <= TOL * rms, f"max |y - y_ref| = {err:.3e} > {TOL} * rms ({rms:.3e})"

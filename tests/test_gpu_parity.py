@@ -52,6 +52,28 @@ def run_pair(spec: LayerSpec, T: int, seed: int, batch: int = 0, x=None):
     return y.cpu().numpy(), got, y_ref, d_ref, layer, tensors, ref
 
 
+def ref_h_q8(d_ref, spec: LayerSpec):
+    """The oracle's Q8_0 of h, as the down projection reads it: quants [R, F] and
+    block scales [R, F/32] (R = assignment rows, then the shared expert's rows)."""
+    h = d_ref["h"]
+    if spec.shared:
+        h = np.concatenate([h, d_ref["sh_h"]], axis=0)
+    R, F = h.shape
+    blocks = po.quantize_act(h).reshape(R, F // 32, 34)
+    d = blocks[:, :, :2].copy().view(np.float16)[..., 0].astype(np.float32)
+    q = blocks[:, :, 2:].copy().view(np.int8).reshape(R, F)
+    return q, d
+
+
+def assert_h_exact(got, d_ref, spec: LayerSpec):
+    """h's Q8_0 (every quant and block scale) equals the oracle's, bit for bit."""
+    q, d = ref_h_q8(d_ref, spec)
+    bad = np.argwhere(got["h_qs"] != q)
+    assert bad.size == 0, f"{len(bad)} h quants differ, first at (row, col) {tuple(bad[0])}: " \
+                          f"{int(got['h_qs'][tuple(bad[0])])} vs {int(q[tuple(bad[0])])}"
+    np.testing.assert_array_equal(got["h_d"].view(np.int32), d.view(np.int32), err_msg="h block scales")
+
+
 def assert_parity(y, got, y_ref, d_ref, spec: LayerSpec, min_identical=0.999, mfma=False):
     np.testing.assert_array_equal(got["topk_idx"], d_ref["topk_idx"])
     np.testing.assert_array_equal(got["offsets"], d_ref["offsets"])
@@ -62,6 +84,9 @@ def assert_parity(y, got, y_ref, d_ref, spec: LayerSpec, min_identical=0.999, mf
     np.testing.assert_allclose(got["topk_w"], d_ref["topk_w"], rtol=1e-6, atol=0)
     if spec.shared:
         np.testing.assert_allclose(got["sh_gate"], d_ref["sh_gate"], rtol=1e-6, atol=0)
+    if "h_qs" in got and "h" in d_ref:
+        assert_h_exact(got, d_ref, spec)
+        assert got["h_fixed"][0] >= 0 and (mfma or got["h_fixed"][0] == 0)
     rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
     err = float(np.max(np.abs(y - y_ref)))
     assert err <= TOL * rms, f"max |y - y_ref| = {err:.3e} > {TOL} * rms ({rms:.3e})"
@@ -386,63 +411,108 @@ def test_batched_router_ties(gpu, monkeypatch, dup):
         assert (got["topk_idx"] == np.arange(spec.top_k)[None, :]).all()
 
 
+def assert_rows_close(got, d_ref, spec: LayerSpec, T: int):
+    """The unweighted expert rows (moe_exp_down, moe_shared_out) against the
+    oracle's: within MFMA_TOL x their rms plus a few f32 ulps of the value
+    itself (2^-20 |ref|: the f32 accumulation of large rows, e.g. under outlier
+    activations, rounds at the scale of the row's own values)."""
+    rows = got["exp_down"]
+    ref = d_ref["y"] if not spec.shared else np.concatenate([d_ref["y"], d_ref["sh_out"]], axis=0)
+    assert rows.shape == ref.shape and np.isfinite(rows).all()
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    err = np.abs(rows.astype(np.float64) - ref)
+    lim = MFMA_TOL * rms + 2.0 ** -20 * np.abs(ref.astype(np.float64))
+    worst = np.unravel_index(np.argmax(err - lim), err.shape)
+    assert (err <= lim).all(), f"expert rows: |err| {err[worst]:.3e} at {worst} (ref {ref[worst]:.4g}, rms {rms:.3g})"
+
+
+def run_prefill(spec: LayerSpec, T: int, seed: int):
+    """Forward on the GPU and the oracle over every token, with the per-row
+    intermediates of both."""
+    tensors = synthetic.make_layer_tensors(spec, seed)
+    layer = synthetic.make_layer(spec, seed, tensors=tensors)
+    x = synthetic.make_x(spec, T, seed)
+    y, dbg = layer.forward(x, debug="rows")
+    torch.cuda.synchronize()
+    got = {k: v.cpu().numpy() for k, v in dbg.items()}
+    ref = host_layer(spec, tensors)
+    y_ref, d_ref = ref.forward(x.cpu().numpy(), debug=True)
+    return y.cpu().numpy(), got, y_ref, d_ref
+
+
 def test_prefill_35b_q4_0_t4096(gpu):
-    """The 4096-token prefill workload: routing checked for every token, outputs on
-    a sample of tokens (a token's output depends on that token only)."""
+    """The 4096-token prefill workload against the oracle on every token: routing,
+    h's Q8_0 (every quant and scale, through the exact fixup of the blocks the f32
+    sums leave open, which must have run), the unweighted expert rows and the
+    layer output."""
     spec = synthetic.QWEN35B
     T = 4096
-    tensors = synthetic.make_layer_tensors(spec, 3)
-    layer = synthetic.make_layer(spec, 3, tensors=tensors)
-    x = synthetic.make_x(spec, T, 3)
-    y, dbg = layer.forward(x, debug=True)
-    torch.cuda.synchronize()
-    ref = host_layer(spec, tensors)
-    xh = x.cpu().numpy()
-    logits = po.router_logits(ref.t["router"], xh)
-    idx, w = po.topk_softmax(logits, spec.top_k)
-    off, rows, _ = po.sort_assignments(idx, spec.n_experts)
-    np.testing.assert_array_equal(dbg["topk_idx"].cpu().numpy(), idx)
-    np.testing.assert_array_equal(dbg["offsets"].cpu().numpy(), off)
-    np.testing.assert_array_equal(dbg["rows"].cpu().numpy(), rows)
-    check_router_bound({k: dbg[k].cpu().numpy() for k in ("router_approx", "router_bound")}, logits)
-    counts = np.diff(off)
+    y, got, y_ref, d_ref = run_prefill(spec, T, 3)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=True)
+    assert check_router_bound(got, d_ref["logits"]) < 0.5
+    assert got["h_fixed"][0] > 0, "the exact fixup listed no h block"
+    assert_rows_close(got, d_ref, spec, T)
+    counts = np.diff(d_ref["offsets"])
     assert counts.sum() == T * spec.top_k and counts.max() < 4 * T * spec.top_k / spec.n_experts
-    sample = np.random.default_rng(0).choice(T, 48, replace=False)
-    y_ref = ref.forward(xh[sample])
-    yg = y.cpu().numpy()[sample]
-    rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
-    assert np.max(np.abs(yg - y_ref)) <= MFMA_TOL * rms
 
 
 def test_skewed_q8_0_t2048(gpu):
     """Zipf-skewed routing (2048 tokens, Q8_0): hot experts with hundreds of rows, ~46
-    empty experts; routing for every token, outputs on a sample of tokens."""
+    empty experts; every token against the oracle (routing, h's Q8_0, expert rows,
+    outputs)."""
     spec = synthetic.QWEN35B_SKEW
     T = 2048
-    tensors = synthetic.make_layer_tensors(spec, 5)
-    layer = synthetic.make_layer(spec, 5, tensors=tensors)
-    x = synthetic.make_x(spec, T, 5)
-    y, dbg = layer.forward(x, debug=True)
-    torch.cuda.synchronize()
-    ref = host_layer(spec, tensors)
-    xh = x.cpu().numpy()
-    logits = po.router_logits(ref.t["router"], xh)
-    idx, w = po.topk_softmax(logits, spec.top_k)
-    off, rows, _ = po.sort_assignments(idx, spec.n_experts)
-    np.testing.assert_array_equal(dbg["topk_idx"].cpu().numpy(), idx)
-    np.testing.assert_array_equal(dbg["offsets"].cpu().numpy(), off)
-    np.testing.assert_array_equal(dbg["rows"].cpu().numpy(), rows)
-    np.testing.assert_allclose(dbg["topk_w"].cpu().numpy(), w, rtol=1e-6, atol=0)
-    counts = np.diff(off)
+    y, got, y_ref, d_ref = run_prefill(spec, T, 5)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=True)
+    assert_rows_close(got, d_ref, spec, T)
+    counts = np.diff(d_ref["offsets"])
     hot = spec.skew.hot_experts(spec.n_experts)
     share = counts[hot].sum() / counts.sum()
     assert 0.4 <= share <= 0.6, f"hot-8 share {share:.3f}"
     assert (counts == 0).sum() >= 40 and counts.max() > 16 * 64
-    sample = np.concatenate([np.arange(8), np.random.default_rng(1).choice(T, 40, replace=False)])
-    y_ref = ref.forward(xh[sample])
-    yg = y.cpu().numpy()[sample]
-    rms = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
-    assert np.max(np.abs(yg - y_ref)) <= MFMA_TOL * rms
+
+
+def heavy_tail_x(spec: LayerSpec, T: int, seed: int, cols: int = 6, scale: float = 50.0):
+    """x ~ N(0,1) with a few columns about `scale` times larger on every token: the
+    outlier columns of real residual streams."""
+    x = synthetic.make_x(spec, T, seed)
+    c = np.random.default_rng(seed).choice(spec.n_embd, cols, replace=False)
+    x[:, torch.as_tensor(c, device=x.device)] *= scale
+    return x
+
+
+@pytest.mark.parametrize("wtype", [TYPE_Q4_0, TYPE_Q8_0])
+def test_mfma_heavy_tails(gpu, wtype):
+    """The f16-MFMA path where its f32 error estimate is stressed: 6 activation columns
+    50x the others (partial sums far larger than the results they cancel to) and
+    outlier weight rows (a few gate/up rows of each expert scaled 30x before
+    quantization).  h's Q8_0 must still equal the oracle's exactly (the fixup
+    catches every value the estimate leaves open) and outputs stay within MFMA_TOL."""
+    spec = LayerSpec(2048, 32, 8, 512, True, wtype)
+    T, seed = 512, 61
+    tensors = synthetic.make_layer_tensors(spec, seed)
+    rng = np.random.default_rng(seed)
+    for name, n_rows in (("gate", spec.n_experts * spec.ffn_dim), ("up", spec.n_experts * spec.ffn_dim),
+                         ("sh_gate", spec.ffn_dim)):
+        rows = rng.choice(n_rows, max(4, n_rows // 64), replace=False)
+        t = tensors[name]
+        rb = po.row_bytes(wtype, spec.n_embd)
+        raw = t.data.view(torch.uint8).view(n_rows, rb)
+        # the f32 values of the chosen rows, scaled 30x and requantized
+        vals = po.dequantize(wtype, raw[torch.as_tensor(rows, device=raw.device)].cpu().numpy().reshape(-1),
+                             len(rows) * spec.n_embd)
+        raw[torch.as_tensor(rows, device=raw.device)] = torch.as_tensor(
+            po.quantize(wtype, vals * 30.0).reshape(len(rows), rb), device=raw.device)
+    layer = synthetic.make_layer(spec, seed, tensors=tensors)
+    x = heavy_tail_x(spec, T, seed)
+    y, dbg = layer.forward(x, debug="rows")
+    torch.cuda.synchronize()
+    got = {k: v.cpu().numpy() for k, v in dbg.items()}
+    ref = host_layer(spec, tensors)
+    y_ref, d_ref = ref.forward(x.cpu().numpy(), debug=True)
+    assert_parity(y.cpu().numpy(), got, y_ref, d_ref, spec, mfma=True)
+    assert_rows_close(got, d_ref, spec, T)
+    assert got["h_fixed"][0] > 0
 
 
 @pytest.mark.parametrize("T", [1, 10, 64, 8192])
@@ -451,8 +521,8 @@ def test_stack_40_layers(gpu, T):
     prefill, :427-432 at decode) through the fused-norm call, at decode batches 1, 10 and 64
     and at 8192-token prefill, each block's RMSNorm partial sums carried to the next.  Layers 0
     and 39 are checked against the oracle on their actual inputs (and against the unfused
-    rms_norm + forward and the call without partial sums): routing bit-exact on every token,
-    outputs within tolerance (all tokens up to 64, a sample of 48 at 8192)."""
+    rms_norm + forward and the call without partial sums), on every token: routing and h's
+    Q8_0 bit-exact, outputs within tolerance."""
     from qwenium_amd import Workspace, rms_norm, ssq_parts
 
     spec = synthetic.QWEN35B
@@ -480,7 +550,7 @@ def test_stack_40_layers(gpu, T):
             assert torch.equal(y, y_fused), f"layer {l}: fused RMSNorm path"
             assert torch.equal(y, y_chain), f"layer {l}: with carried partial sums"
             keep[l] = (x.cpu().numpy(), wn.cpu().numpy(), t, y.cpu().numpy(),
-                       {k: dbg[k].cpu().numpy() for k in ("topk_idx", "offsets", "rows")})
+                       {k: dbg[k].cpu().numpy() for k in ("topk_idx", "offsets", "rows", "h_qs", "h_d", "h_fixed")})
         else:
             y = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws, x_ssq=x_ssq, y_ssq=y_ssq)
         x, x_ssq = y, y_ssq
@@ -497,10 +567,11 @@ def test_stack_40_layers(gpu, T):
         np.testing.assert_array_equal(got["topk_idx"], idx, err_msg=f"layer {l}")
         np.testing.assert_array_equal(got["offsets"], off, err_msg=f"layer {l}")
         np.testing.assert_array_equal(got["rows"], rows, err_msg=f"layer {l}")
-        sample = np.arange(T) if T <= 64 else np.concatenate(
-            [np.arange(8), np.random.default_rng(l).choice(T, 40, replace=False)])
-        yr = ref.forward(hh[sample]) + xin[sample]
-        ys = yg[sample]
+        yr, d_ref = ref.forward(hh, debug=True)
+        yr = yr + xin
+        ys = yg
+        assert_h_exact(got, d_ref, spec)
+        assert (got["h_fixed"][0] > 0) == (T >= 128), f"layer {l}: h blocks fixed {got['h_fixed'][0]}"
         rms = float(np.sqrt(np.mean(yr.astype(np.float64) ** 2)))
         assert np.max(np.abs(ys - yr)) <= TOL * rms, f"layer {l}"
         if T >= 128:  # the f16-MFMA prefill path
