@@ -180,7 +180,10 @@ int qmoe_layer_forward(qmoe_layer* layer, qmoe_workspace* ws,
  * workspace of its own, but the scratch is a file-scope device array of
  * QMOE_STATIC_SCRATCH_BYTES per GPU (held until the process ends), so no call
  * allocates or frees.  Its first call on a GPU (with that GPU current) looks
- * the array up and clears its signalling area on `hip_stream`.  Sizes whose
+ * the array up; its signalling area (counters the routing returns to zero
+ * after each use) is zero when the library loads, and a first call on a
+ * stream that is not being captured also clears it and waits for that clear
+ * (the one synchronisation this entry point performs).  Sizes whose
  * scratch exceeds the maximum (at the 35B-A3B shape: above about 100 tokens)
  * fail with QMOE_ERR_CAPACITY.  Every call on one GPU shares that GPU's
  * array: calls that overlap in time on one GPU (other streams, other threads)

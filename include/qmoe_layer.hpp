@@ -34,14 +34,29 @@ public:
     };
 
     // All tensors are borrowed device views in GGUF block layout; the w_sh_*
-    // slots may be nullptr when !hp.has_shared_expert.
+    // slots may be nullptr when !hp.has_shared_expert.  prefill_copies (no
+    // counterpart in the reference; the reference's nine arguments keep the
+    // default): also keep chunk-major copies of the expert matrices for the
+    // prefill GEMMs (qmoe_layer_build_prefill_copies), read from the tensors
+    // here, so their data must be in place; one more copy of the expert weights
+    // in device memory (455 MB for a Qwen3.6-35B-A3B layer in Q4_0).  false: the
+    // prefill GEMMs read the GGUF rows (same results, slower prefill).
     MoELayer(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate, const qmoe_tensor* w_exp_up,
              const qmoe_tensor* w_exp_down, const qmoe_tensor* w_sh_gate, const qmoe_tensor* w_sh_up,
-             const qmoe_tensor* w_sh_down, const qmoe_tensor* w_sh_norm, const Hparams& hp)
+             const qmoe_tensor* w_sh_down, const qmoe_tensor* w_sh_norm, const Hparams& hp,
+             bool prefill_copies = true)
         : hp_(hp) {
         const qmoe_hparams c{hp.n_experts, hp.top_k, hp.ffn_dim, hp.has_shared_expert ? 1 : 0};
         check(qmoe_layer_create(w_router, w_exp_gate, w_exp_up, w_exp_down, w_sh_gate, w_sh_up, w_sh_down,
                                 w_sh_norm, &c, &layer_));
+        if (prefill_copies) {
+            const int rc = qmoe_layer_build_prefill_copies(layer_);
+            if (rc != QMOE_OK) {
+                const std::string msg = qmoe_last_error();
+                qmoe_layer_destroy(layer_);
+                throw std::runtime_error(msg);
+            }
+        }
     }
     ~MoELayer() { qmoe_layer_destroy(layer_); }
     MoELayer(const MoELayer&) = delete;
@@ -88,11 +103,20 @@ class GeGLUMoELayer {
 public:
     using Hparams = MoELayer::Hparams;
 
+    // prefill_copies: as MoELayer's.
     GeGLUMoELayer(const qmoe_tensor* w_router, const qmoe_tensor* w_gate_up_exps, const qmoe_tensor* w_down_exps,
-                  const Hparams& hp)
+                  const Hparams& hp, bool prefill_copies = true)
         : hp_(hp) {
         const qmoe_hparams c{hp.n_experts, hp.top_k, hp.ffn_dim, hp.has_shared_expert ? 1 : 0};
         check(qmoe_geglu_layer_create(w_router, w_gate_up_exps, w_down_exps, &c, &layer_));
+        if (prefill_copies) {
+            const int rc = qmoe_layer_build_prefill_copies(layer_);
+            if (rc != QMOE_OK) {
+                const std::string msg = qmoe_last_error();
+                qmoe_layer_destroy(layer_);
+                throw std::runtime_error(msg);
+            }
+        }
     }
     ~GeGLUMoELayer() { qmoe_layer_destroy(layer_); }
     GeGLUMoELayer(const GeGLUMoELayer&) = delete;

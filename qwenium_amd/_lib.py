@@ -9,7 +9,9 @@ import ctypes
 import os
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG_DIR, "libqmoe.so")
+# QMOE_LIB: another build of the same library (the host-sanitizer build,
+# qwenium_amd.sanitize); default: the in-tree libqmoe.so
+LIB_PATH = os.environ.get("QMOE_LIB") or os.path.join(PKG_DIR, "libqmoe.so")
 
 TYPE_F32 = 0
 TYPE_Q4_0 = 2

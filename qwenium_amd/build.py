@@ -53,9 +53,20 @@ def common_flags() -> list[str]:
     ]
 
 
-def _compile(src: str, verbose: bool) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [_hipcc()] + common_flags() + ["-c", os.path.join(CSRC, src), "-o", obj]
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer (each -fsanitize= after
+# -Xarch_host: the host code of every source is instrumented, the gfx950 device
+# code is built as usual).
+SAN_DIR = os.path.join(BUILD_DIR, "san")
+SAN_LIB = os.path.join(SAN_DIR, "libqmoe.so")
+SAN_TEST_BIN = os.path.join(SAN_DIR, "test_moe_layer")
+SAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
+             "-Xarch_host", "-g"]
+
+
+def _compile(src: str, verbose: bool, extra: list[str] | None = None, out_dir: str | None = None) -> str:
+    obj = os.path.join(out_dir or BUILD_DIR, os.path.splitext(src)[0] + ".o")
+    cmd = [_hipcc()] + common_flags() + (extra or []) + ["-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     if verbose:
@@ -84,6 +95,25 @@ def build(verbose: bool = False, jobs: int = 5) -> str:
     os.replace(tmp, LIB_PATH)
     build_cpp_tests(verbose)
     return LIB_PATH
+
+
+def build_sanitized(verbose: bool = False, jobs: int = 5) -> str:
+    """The library and the C++ drop-in test with host-side ASan + UBSan, under
+    qwenium_amd/_build/san (run them with qwenium_amd.sanitize)."""
+    os.makedirs(SAN_DIR, exist_ok=True)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose, SAN_FLAGS, SAN_DIR), SOURCES))
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libsan"] + SAN_FLAGS + ["-o", SAN_LIB] + objs
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{res.stdout}{res.stderr}")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-O1", "-std=c++17", "-shared-libsan"] + SAN_FLAGS + [
+        "-I", os.path.join(REPO_DIR, "include"), CPP_TEST_SRC, "-o", SAN_TEST_BIN, "-L", SAN_DIR, "-lqmoe",
+        "-Wl,-rpath," + SAN_DIR]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"sanitized C++ test build failed:\n{res.stdout}{res.stderr}")
+    return SAN_LIB
 
 
 CPP_TEST_SRC = os.path.join(REPO_DIR, "tests", "cpp", "test_moe_layer.cpp")

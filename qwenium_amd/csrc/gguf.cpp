@@ -185,14 +185,20 @@ struct qmoe_gguf {
 
 static int gguf_fail(const std::string& msg) { return qmoe::set_error(QMOE_ERR_VALUE, msg); }
 
-static bool tensor_bytes(const TensorRec& t, uint64_t* out) {
+// The tensor's byte size: 0 on success; 1 for a type of unknown size or rows
+// that are not whole blocks; 2 when a dimension is negative or the element
+// count or byte size does not fit 64 bits (a crafted inventory must not wrap
+// around to a small size that passes the end-of-file check).
+static int tensor_bytes(const TensorRec& t, uint64_t* out) {
     uint64_t blk = 0, bytes = 0;
-    if (!type_geometry(t.type, &blk, &bytes)) return false;
+    if (!type_geometry(t.type, &blk, &bytes)) return 1;
     uint64_t n = 1;
-    for (int d = 0; d < 4; ++d) n *= (uint64_t)t.ne[d];
-    if (n % blk) return false;
-    *out = n / blk * bytes;
-    return true;
+    for (int d = 0; d < 4; ++d) {
+        if (t.ne[d] < 0 || __builtin_mul_overflow(n, (uint64_t)t.ne[d], &n)) return 2;
+    }
+    if (n % blk) return 1;
+    if (__builtin_mul_overflow(n / blk, bytes, out)) return 2;
+    return 0;
 }
 
 extern "C" {
@@ -337,11 +343,15 @@ int qmoe_gguf_find(const qmoe_gguf* g, const char* name, qmoe_gguf_tensor* out) 
     if (it == g->tensors.end()) return qmoe::set_error(QMOE_ERR_VALUE, std::string("gguf: tensor \"") + name + "\" expected present, got absent");
     const TensorRec& t = it->second;
     uint64_t bytes = 0;
-    if (!tensor_bytes(t, &bytes))
+    const int tb = tensor_bytes(t, &bytes);
+    if (tb == 1)
         return qmoe::set_error(QMOE_ERR_TYPE, std::string("gguf: tensor \"") + name + "\" has ggml type " + std::to_string(t.type) +
                                              " whose size is unknown here (or a row not a whole number of blocks)");
-    const uint64_t start = g->data_offset + t.offset;
-    if (start > g->size || bytes > g->size - start)
+    if (tb == 2)
+        return qmoe::set_error(QMOE_ERR_VALUE, std::string("gguf: tensor \"") + name +
+                                                  "\" expected a shape whose byte size fits 64 bits, got one that overflows");
+    uint64_t start = 0;
+    if (__builtin_add_overflow(g->data_offset, t.offset, &start) || start > g->size || bytes > g->size - start)
         return qmoe::set_error(QMOE_ERR_VALUE, std::string("gguf: tensor data for \"") + name + "\" would read past end of file");
     out->type = t.type;
     out->n_dims = t.n_dims;

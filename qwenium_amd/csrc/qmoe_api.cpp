@@ -511,9 +511,12 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch[kMaxDevices] = {};
 
-// The device address of this GPU's scratch (dev current), set up on first use:
-// the symbol lookup, then a fill kernel on `stream` that zeroes the signalling
-// area (a kernel node, never a memset, in case the caller is capturing).
+// The device address of this GPU's scratch (dev current), set up on first use.
+// The signalling area (the routing scans' last-workgroup counters) must start
+// at zero: device globals are zero when the code object loads, every scan
+// returns its counter to zero, and a first use on a stream that is not being
+// captured also clears the area with a fill kernel and waits for it, so the
+// array is published only after the clear has run.
 int static_scratch(int dev, hipStream_t stream, void** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (dev < 0 || dev >= kMaxDevices)
@@ -523,8 +526,14 @@ int static_scratch(int dev, hipStream_t stream, void** out) {
         void* p = nullptr;
         hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
-        err = qmoe::launch_fill_i32((int32_t*)p, (int)(kStaticSyncBytes / sizeof(int32_t)), 0, stream);
-        if (err != hipSuccess) return hip_fail(err, "scratch signalling area clear");
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        err = hipStreamIsCapturing(stream, &cs);
+        if (err != hipSuccess) return hip_fail(err, "hipStreamIsCapturing");
+        if (cs == hipStreamCaptureStatusNone) {
+            err = qmoe::launch_fill_i32((int32_t*)p, (int)(kStaticSyncBytes / sizeof(int32_t)), 0, stream);
+            if (err == hipSuccess) err = hipStreamSynchronize(stream);
+            if (err != hipSuccess) return hip_fail(err, "scratch signalling area clear");
+        }
         g_scratch[dev] = p;
     }
     *out = g_scratch[dev];

@@ -925,8 +925,10 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, i
         const int tid = threadIdx.x;
         __builtin_amdgcn_s_waitcnt(0);  // this block's write-through stores have completed
         __syncthreads();
+        // the counter's add releases this block's stores (barrier, then an
+        // agent-scope release by thread 0) and acquires the other blocks'
         if (tid == 0)
-            s_last = __hip_atomic_fetch_add(sync + kSyncTopk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            s_last = __hip_atomic_fetch_add(sync + kSyncTopk, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
                      (int)gridDim.x - 1;
         __syncthreads();
         if (!s_last) return;
@@ -1492,8 +1494,10 @@ __global__ __launch_bounds__(1024) void k_scan(TopkArgs a, int32_t* sync) {
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    // release this block's totals, acquire the others' (agent scope, thread 0
+    // after the barrier)
     if (tid == 0)
-        s_last = __hip_atomic_fetch_add(sync + kSyncScan, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        s_last = __hip_atomic_fetch_add(sync + kSyncScan, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
                  (int)gridDim.x - 1;
     __syncthreads();
     if (!s_last) return;

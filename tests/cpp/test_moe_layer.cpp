@@ -150,6 +150,36 @@ static void TopKGatingCorrectness() {
     EXPECT(std::fabs(wh[0] - 0.7310586f) < 1e-6f && std::fabs(wh[1] - 0.2689414f) < 1e-6f, "KAT weights");
 }
 
+// The prefill path (300 tokens: the f16-MFMA expert GEMMs and the batched
+// router) of the drop-in constructor, which builds the chunk-major weight copies
+// by default, gives the same bits as a layer constructed without them.
+static void PrefillCopiesGiveTheSameOutput() {
+    std::vector<float> router((size_t)N_EMBD * N_EXPERTS);
+    for (size_t i = 0; i < router.size(); ++i) router[i] = 0.01f * (float)((i * 37) % 23) - 0.1f;
+    Fixture f(router, 0.05f);
+    const int n_tok = 300;
+    std::vector<float> xh((size_t)n_tok * N_EMBD);
+    for (size_t i = 0; i < xh.size(); ++i) xh[i] = 0.25f * (float)((i * 13) % 11) - 1.0f;
+    DevBuf x(xh);
+    DevBuf y0((size_t)n_tok * N_EMBD * sizeof(float)), y1((size_t)n_tok * N_EMBD * sizeof(float));
+    {
+        qmoe::MoELayer with(&f.t_router, &f.t_gate, &f.t_up, &f.t_down, &f.t_sh_gate, &f.t_sh_up, &f.t_sh_down,
+                            &f.t_sh_norm, hparams(true));
+        qmoe::MoELayer without(&f.t_router, &f.t_gate, &f.t_up, &f.t_down, &f.t_sh_gate, &f.t_sh_up, &f.t_sh_down,
+                               &f.t_sh_norm, hparams(true), false);
+        with.forward((const float*)x.p, n_tok, (float*)y0.p);
+        without.forward((const float*)x.p, n_tok, (float*)y1.p);
+        HIP_OK(hipDeviceSynchronize());
+    }
+    std::vector<float> a(xh.size()), b(xh.size());
+    HIP_OK(hipMemcpy(a.data(), y0.p, a.size() * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(b.data(), y1.p, b.size() * 4, hipMemcpyDeviceToHost));
+    EXPECT(std::memcmp(a.data(), b.data(), a.size() * 4) == 0, "same bits with and without the prefill copies");
+    bool finite = true;
+    for (float v : a) finite = finite && std::isfinite(v);
+    EXPECT(finite, "finite");
+}
+
 static void SharedExpertChangesOutput() {
     const std::vector<float> a = run_forward(false), b = run_forward(true);
     bool any = false;
@@ -171,7 +201,8 @@ static void OutputShapeMatchesInput() {
 
 // Host-only: the constructor's fail-loud contract (moe.cpp:47-52), fake pointers,
 // at widths on the kernels' grid (256, 64): such a layer reads its weights in
-// place, so constructing it touches no device memory (a padded one copies them).
+// place, so constructing it without the prefill copies touches no device memory
+// (a padded one, or the copies, read them).
 static void ConstructorThrowsWithoutSharedWeights() {
     const void* fake = (const void*)0x10000000;
     constexpr int kEmbd = 256, kFfn = 64;
@@ -181,14 +212,14 @@ static void ConstructorThrowsWithoutSharedWeights() {
     const qmoe::MoELayer::Hparams hp_shared{N_EXPERTS, TOP_K, kFfn, true}, hp_plain{N_EXPERTS, TOP_K, kFfn, false};
     std::string msg;
     try {
-        qmoe::MoELayer layer(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hp_shared);
+        qmoe::MoELayer layer(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hp_shared, false);
     } catch (const std::runtime_error& e) {
         msg = e.what();
     }
     EXPECT(msg == "moe_layer: has_shared_expert=true but shared expert weights are null", "reference message");
     bool threw = false;
     try {
-        qmoe::MoELayer ok(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hp_plain);
+        qmoe::MoELayer ok(&r, &g, &g, &d, nullptr, nullptr, nullptr, nullptr, hp_plain, false);
     } catch (const std::runtime_error&) {
         threw = true;
     }
@@ -441,6 +472,7 @@ int main(int argc, char** argv) {
         {"TopKGatingCorrectness", TopKGatingCorrectness, true},
         {"SharedExpertChangesOutput", SharedExpertChangesOutput, true},
         {"OutputShapeMatchesInput", OutputShapeMatchesInput, true},
+        {"PrefillCopiesGiveTheSameOutput", PrefillCopiesGiveTheSameOutput, true},
     };
     int run = 0;
     for (const auto& c : cases) {

@@ -163,6 +163,41 @@ def test_tensor_data_past_end_and_unknown_type(tmp_path):
         assert e.value.code == QMOE_ERR_TYPE
 
 
+def _crafted_inventory(entries):
+    """A v3 file with no metadata and the given inventory (name, ne tuple, ggml
+    type, offset), data start aligned to 32 bytes, 64 bytes of data."""
+    b = struct.pack("<IIQQ", 0x46554747, 3, len(entries), 0)
+    for name, ne, typ, off in entries:
+        b += struct.pack("<Q", len(name)) + name + struct.pack("<I", len(ne))
+        b += b"".join(struct.pack("<Q", v % 2**64) for v in ne) + struct.pack("<IQ", typ, off % 2**64)
+    b += b"\0" * (-len(b) % 32)
+    return b, len(b), b + bytes(range(64))
+
+
+def test_crafted_sizes_and_offsets_do_not_wrap(tmp_path):
+    """An element count or byte size past 64 bits, or a data offset whose sum with the
+    data start wraps, is rejected instead of aliasing other bytes of the file
+    (the reference bounds-checks the tensor data, gguf_loader.cpp:621-639)."""
+    entries = [
+        (b"a", (2**62, 4), TYPE_F32, 0),      # 2^64 elements: wraps to 0 bytes
+        (b"b", (2**61 + 1, 8), TYPE_F32, 0),  # 2^64 + 8 elements: wraps to 32 bytes
+        (b"c", (2**62 + 2,), TYPE_F32, 0),    # 2^62 + 2 elements fit, their bytes wrap to 8
+        (b"d", (2,), TYPE_F32, 0),
+    ]
+    start = _crafted_inventory(entries)[1]  # the data start (offsets do not change the layout)
+    entries[3] = (b"d", (2,), TYPE_F32, 2**64 - start + 8)  # data start + offset wraps to byte 8
+    b = _crafted_inventory(entries)[2]
+    assert 8 + 8 <= len(b)  # a wrapped read would land inside the file
+    p = tmp_path / "crafted.gguf"
+    p.write_bytes(b)
+    with G.GGUFFile(str(p)) as f:
+        for name in ("a", "b", "c"):
+            with pytest.raises(QmoeError, match=f'tensor "{name}" expected a shape whose byte size fits 64 bits'):
+                f.find(name)
+        with pytest.raises(QmoeError, match='tensor data for "d" would read past end of file'):
+            f.find("d")
+
+
 def test_read_buffer_too_small(tmp_path):
     import ctypes
 
