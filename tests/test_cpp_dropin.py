@@ -25,4 +25,4 @@ def test_cpp_dropin_gpu(gpu):
     res = subprocess.run([binary()], capture_output=True, text=True, timeout=120)
     print(res.stdout)
     assert res.returncode == 0, res.stdout + res.stderr
-    assert "27 tests, 0 failures" in res.stdout
+    assert "28 tests, 0 failures" in res.stdout
