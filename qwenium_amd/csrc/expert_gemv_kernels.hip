@@ -1035,47 +1035,63 @@ struct CombineArgs {
     int H, K, S, T;
     const float* ybuf; const int32_t* pos; const float* topk_w; const float* sh_gate;
     const float* residual; float* y;
+    double* y_ssq;  // [T][ssq_parts(H)] y's RMSNorm partial sums (H a multiple of 32), or null
 };
 
 __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
 #pragma clang fp contract(off)
     const int t = blockIdx.y;
     const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
-    if (n >= a.H) return;
+    if (!a.y_ssq && n >= a.H) return;
+    const bool live = n < a.H;  // (with y_ssq every lane takes part in the 8-lane trees)
     const int A = a.T * a.K;
-    const int32_t* pt = a.pos + (uint64_t)t * a.K;
-    const float* wt = a.topk_w + (uint64_t)t * a.K;
-    f32x4 acc;
-    {
-        const float w = wt[0];
-        const f32x4 v = *(const f32x4*)(a.ybuf + (uint64_t)pt[0] * a.H + n);
-        acc = f32x4{w * v.x, w * v.y, w * v.z, w * v.w};
+    f32x4 acc = {};
+    if (live) {
+        const int32_t* pt = a.pos + (uint64_t)t * a.K;
+        const float* wt = a.topk_w + (uint64_t)t * a.K;
+        {
+            const float w = wt[0];
+            const f32x4 v = *(const f32x4*)(a.ybuf + (uint64_t)pt[0] * a.H + n);
+            acc = f32x4{w * v.x, w * v.y, w * v.z, w * v.w};
+        }
+        for (int j = 1; j < a.K; ++j) {
+            const float w = wt[j];
+            const f32x4 v = *(const f32x4*)(a.ybuf + (uint64_t)pt[j] * a.H + n);
+            const f32x4 term = f32x4{w * v.x, w * v.y, w * v.z, w * v.w};
+            acc = acc + term;
+        }
+        if (a.S) {
+            const float s = a.sh_gate[t];
+            const f32x4 v = *(const f32x4*)(a.ybuf + (uint64_t)(A + t) * a.H + n);
+            const f32x4 term = f32x4{v.x * s, v.y * s, v.z * s, v.w * s};
+            acc = acc + term;
+        }
+        if (a.residual) {
+            const f32x4 r = *(const f32x4*)(a.residual + (uint64_t)t * a.H + n);
+            acc = acc + r;
+        }
+        *(f32x4*)(a.y + (uint64_t)t * a.H + n) = acc;
     }
-    for (int j = 1; j < a.K; ++j) {
-        const float w = wt[j];
-        const f32x4 v = *(const f32x4*)(a.ybuf + (uint64_t)pt[j] * a.H + n);
-        const f32x4 term = f32x4{w * v.x, w * v.y, w * v.z, w * v.w};
-        acc = acc + term;
+    if (a.y_ssq) {
+        // this thread's 4 columns are run n / 4 of the row (f64 of each f32
+        // square, in column order); 8 consecutive lanes hold the 8 runs of entry
+        // n / 32, whose adjacent-pairs tree is dpp_sum_f64<8>
+        double s = 0.0;
+        if (live)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s += (double)(acc[c] * acc[c]);
+        s = dpp_sum_f64<8>(s);
+        if (live && (threadIdx.x & 7) == 7) a.y_ssq[(uint64_t)t * ssq_parts(a.H) + (n >> 5)] = s;
     }
-    if (a.S) {
-        const float s = a.sh_gate[t];
-        const f32x4 v = *(const f32x4*)(a.ybuf + (uint64_t)(A + t) * a.H + n);
-        const f32x4 term = f32x4{v.x * s, v.y * s, v.z * s, v.w * s};
-        acc = acc + term;
-    }
-    if (a.residual) {
-        const f32x4 r = *(const f32x4*)(a.residual + (uint64_t)t * a.H + n);
-        acc = acc + r;
-    }
-    *(f32x4*)(a.y + (uint64_t)t * a.H + n) = acc;
 }
 
 hipError_t launch_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
-                          hipStream_t stream) {
+                          hipStream_t stream, double* y_ssq) {
     CombineArgs a;
     a.H = L.H; a.K = L.K; a.S = L.S; a.T = T;
     a.ybuf = ws.ybuf; a.pos = ws.pos; a.topk_w = ws.topk_w; a.sh_gate = ws.sh_gate;
     a.residual = residual; a.y = y;
+    a.y_ssq = (L.H % 32 == 0) ? y_ssq : nullptr;
     const dim3 grid((L.H / 4 + 255) / 256, T);
     hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, stream, a);
     return hipGetLastError();

@@ -683,6 +683,11 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
         residual = x;
         if (!mfma && qmoe::route_norm_fused(d, n_tokens)) {
             route_norm_w = in.norm_w;
+        } else if (mfma && qmoe::route_uses_mfma(d, n_tokens) && !dbg && d.H <= 4096) {
+            // prefill: the batched router's preparation normalizes the rows (the
+            // scale from x_ssq when carried) into every operand it writes, the
+            // exact refinement normalizes on the fly: no normalized copy of x
+            route_norm_w = in.norm_w;
         } else {
             // the normalized rows go to the workspace
             if (err == hipSuccess) err = qmoe::launch_rms_norm(x, in.norm_w, n_tokens, d.H, in.eps, v.xn, stream);
@@ -725,8 +730,9 @@ static int forward_impl(qmoe_layer* layer, qmoe_workspace* ws, const ForwardIn& 
             err = mfma ? qmoe::launch_down_mfma(d, v, n_tokens, stream) : qmoe::launch_experts_down(d, v, n_tokens, stream);
         if (err != hipSuccess) return hip_fail(err, "down expert kernel");
         err = mark(3);
-        if (err == hipSuccess) err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream);
+        if (err == hipSuccess) err = qmoe::launch_combine(d, v, n_tokens, y, residual, stream, in.y_ssq);
         if (err != hipSuccess) return hip_fail(err, "combine kernel");
+        ssq_done = in.y_ssq != nullptr && d.H % 32 == 0;
     }
     if (in.y_ssq && !ssq_done) {
         err = qmoe::launch_rms_partials(y, n_tokens, d.H, in.y_ssq, stream);

@@ -320,6 +320,34 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
+// A row's sum of squares by one wave (every lane gets it), in the order every
+// RMSNorm here uses: the trees of 64-run chunks, then the adjacent-pairs tree
+// over the chunks, zero-padded to 16 leaves (H <= 4096; a longer zero padding
+// changes no bits).
+__device__ inline double ssq_row(const float* xr, int H, int lane) {
+    const int nc = (H + 255) >> 8;
+    double c[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c[i] = i < nc ? wave_sum_f64(ssq_run4(xr, H, 64 * i + lane)) : 0.0;
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) c[i] = c[2 * i] + c[2 * i + 1];
+    return c[0];
+}
+// The same sum from a row's carried partial sums (np <= 128 entries, each the
+// subtree of 8 runs): the adjacent-pairs tree over the entries zero-padded,
+// 64-entry chunks by DPP trees, then the chunks' pair.
+__device__ inline double ssq_from_parts(const double* parts, int np, int lane) {
+    double c[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int e = 64 * i + lane;
+        c[i] = 64 * i < np ? wave_sum_f64(e < np ? parts[e] : 0.0) : 0.0;
+    }
+    return c[0] + c[1];
+}
+
 // One reduce-scatter step over an f64 pair (x, y): the 32-lane swap (W = 32)
 // leaves lanes 0..31 with x[l] + x[l + 32] and lanes 32..63 with y[l - 32] + y[l];
 // the 16-lane swap (W = 16) does the same between the even and odd rows of 16.

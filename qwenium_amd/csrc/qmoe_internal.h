@@ -117,7 +117,7 @@ struct Workspace {
     int fix_max = 0;
     float* xn = nullptr;          // [T][H] RMSNorm(x)*w for fused-norm forwards (the experts' input)
     float* xr = nullptr;          // [T][H] the router's own input when it differs (Gemma 4 slice)
-    float* x_scale = nullptr;     // [T] RMSNorm scales of a decode forward that normalizes in its routing
+    float* x_scale = nullptr;     // [T] RMSNorm scales of a forward that normalizes in its routing
     float* ybuf = nullptr;        // [R][H] down outputs (unweighted)
     float* ysh = nullptr;         // [T][H] the shared expert's down rows (fused decode)
     float* yp = nullptr;          // [T][H] output rows of a layer with padded widths (null otherwise)
@@ -158,9 +158,10 @@ bool route_decode_fused(const LayerDesc& L, int T);
 // x_f16: also write x's Q8_0 quants as f16 and its fp16 block scales (ws.x_q,
 // ws.x_d), the prefill GEMMs' A operand (inside the batched router's launch,
 // else a launch of its own).
-// norm_w (decode routing only, T <= 16 without x_f16): x is the residual row and
-// the routing normalizes it on the fly, x_in = (x * rms scale) * norm_w, for the
-// router and for x's Q8_0 (route_norm_fused says when).
+// norm_w: x (== xr) is the residual row and the routing normalizes it on the
+// fly, x_in = (x * rms scale) * norm_w, for the router and for x's Q8_0: at
+// decode (T <= 16 without x_f16, route_norm_fused says when) and in the batched
+// router (route_uses_mfma, with x_f16); x_ssq (optional): x's partial sums.
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
                         const RouteDebug& dbg, bool x_f16, hipStream_t stream, const float* norm_w = nullptr,
                         float eps = 0.0f, const double* x_ssq = nullptr);
@@ -180,8 +181,10 @@ hipError_t launch_gateup_q(const LayerDesc& L, const Workspace& ws, int T, hipSt
 hipError_t launch_gateup_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream,
                               hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 hipError_t launch_down_mfma(const LayerDesc& L, const Workspace& ws, int T, hipStream_t stream);
+// y_ssq (optional): y's RMSNorm partial sums, written with the rows (n_embd a
+// multiple of 32; otherwise ignored and left to the caller).
 hipError_t launch_combine(const LayerDesc& L, const Workspace& ws, int T, float* y, const float* residual,
-                          hipStream_t stream);
+                          hipStream_t stream, double* y_ssq = nullptr);
 // Decode sizes: token-major down projection with the combine in its epilogue
 // (replaces launch_experts_down + launch_combine when down_combine_fused()).
 bool down_combine_fused(const LayerDesc& L, int T);

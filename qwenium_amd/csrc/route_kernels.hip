@@ -250,6 +250,14 @@ struct RouterMfmaArgs {
     uint16_t* rx;           // [2][T][H] bf16 hi, lo of the router input
     uint16_t* rw;           // [2][E][H] bf16 hi, lo of the router weights
     float* rnorm;           // [T + E]
+    // pre-MoE RMSNorm on the fly (norm_w non-null; then x == xe is the residual
+    // row): every operand is of (x * scale) * norm_w, scale = 1/sqrtf(mean(x^2)
+    // + eps) from the row's sum of squares (x_ssq: its carried partial sums);
+    // the scales go to x_scale for the exact refinement
+    const float* norm_w;
+    float eps;
+    const double* x_ssq;    // [T][ssq_parts(H)] or null
+    float* x_scale;         // [T]
 };
 
 // bf16 split of 8 floats (round to nearest both times): hi = bf16(v), lo = bf16(v - hi);
@@ -296,14 +304,19 @@ typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 // Writes the f16 quants when q is non-null; with hi non-null also the row's
 // bf16 hi/lo split and returns this lane's sum of squares.
 __device__ float quant_split_row(const float* xr, int H, int lane, _Float16* q, uint16_t* d, int8_t* qs, float2* ds,
-                                 uint16_t* hi, uint16_t* lo) {
+                                 uint16_t* hi, uint16_t* lo, const float* nw = nullptr, float scale = 1.0f) {
+#pragma clang fp contract(off)
     const int nb = H >> 5;
     const int sub = lane & 7;
     float sq = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += 8) {
         const int b = b0 + (lane >> 3);
         const int o = 32 * b + 4 * sub;
-        const f32x4 v = *(const f32x4*)(xr + o);
+        f32x4 v = *(const f32x4*)(xr + o);
+        if (nw) {  // the RMSNorm output (x * scale) * w, as k_rms_norm writes it
+            const f32x4 w4 = *(const f32x4*)(nw + o);
+            v = f32x4{(v.x * scale) * w4.x, (v.y * scale) * w4.y, (v.z * scale) * w4.z, (v.w * scale) * w4.w};
+        }
         float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)), fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
         amax = dpp8_max<kDppQuadXor1>(amax);
         amax = dpp8_max<kDppQuadXor2>(amax);
@@ -360,9 +373,17 @@ __global__ __launch_bounds__(256) void k_router_prep(RouterMfmaArgs a) {
         uint16_t* hi = a.rx + (uint64_t)t * a.H;
         uint16_t* lo = a.rx + ((uint64_t)a.T + t) * a.H;
         const bool same = a.x == a.xe;  // one pass over the row: quants and the router operand
+        float scale = 1.0f;
+        if (a.norm_w) {
+            const double ssq = a.x_ssq ? ssq_from_parts(a.x_ssq + (uint64_t)t * ssq_parts(a.H), ssq_parts(a.H), lane)
+                                       : ssq_row(a.xe + (uint64_t)t * a.H, a.H, lane);
+            scale = rms_scale_from_ssq(ssq, a.H, a.eps);
+            if (lane == 0) a.x_scale[t] = scale;
+        }
         float sq = quant_split_row(a.xe + (uint64_t)t * a.H, a.H, lane, a.x_q ? a.x_q + (uint64_t)t * a.H : nullptr,
                                    a.x_d + (uint64_t)t * (a.H >> 5), a.xq_qs + (uint64_t)t * a.H,
-                                   a.xq_ds + (uint64_t)t * (a.H >> 5), same ? hi : nullptr, same ? lo : nullptr);
+                                   a.xq_ds + (uint64_t)t * (a.H >> 5), same ? hi : nullptr, same ? lo : nullptr,
+                                   a.norm_w, scale);
         if (same) {
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
@@ -493,7 +514,7 @@ struct TopkArgs {
     uint64_t router_ld;
     const float* w_sh_norm;    // [H] or null
     int T, E, K, S, H;
-    const float* norm_w;  // decode routing: x is normalized on the fly, (x * x_scale[t]) * norm_w (null: not)
+    const float* norm_w;  // x is normalized on the fly, (x * x_scale[t]) * norm_w (null: not)
     float norm_eps;
     float* x_scale;       // [T] the rows' RMSNorm scales (router block 0 writes them for the table launch)
     const double* x_ssq;  // [T][ssq_parts(H)] x's RMSNorm partial sums, or null (the router sums x itself)
@@ -553,8 +574,18 @@ __device__ __forceinline__ double dot4_f64(const f32x4 w, const f32x4 v, double 
 
 // Exact router logits of one token against two router rows (one wave; f32
 // products are exact in f64, the sum is f64), rounded once to f32.
+// The router input's 4 values at column o: x itself, or with nw the RMSNorm
+// output (x * scale) * nw as k_rms_norm writes it.
+__device__ __forceinline__ f32x4 router_in4(const float* xr, const float* nw, float scale, int o) {
+#pragma clang fp contract(off)
+    const f32x4 v = *(const f32x4*)(xr + o);
+    if (!nw) return v;
+    const f32x4 w = *(const f32x4*)(nw + o);
+    return f32x4{(v.x * scale) * w.x, (v.y * scale) * w.y, (v.z * scale) * w.z, (v.w * scale) * w.w};
+}
+
 __device__ __forceinline__ void exact_dot2(const float* w0, const float* w1, const float* xr, int H, int lane,
-                                           float& r0, float& r1) {
+                                           float& r0, float& r1, const float* nw = nullptr, float scale = 1.0f) {
     double a0 = 0.0, a1 = 0.0;
     const int nch = H >> 8;
     int c = 0;
@@ -563,7 +594,7 @@ __device__ __forceinline__ void exact_dot2(const float* w0, const float* w1, con
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int o = (c + i) * 256 + 4 * lane;
-            xv[i] = *(const f32x4*)(xr + o);
+            xv[i] = router_in4(xr, nw, scale, o);
             v0[i] = *(const f32x4*)(w0 + o);
             v1[i] = *(const f32x4*)(w1 + o);
         }
@@ -572,7 +603,7 @@ __device__ __forceinline__ void exact_dot2(const float* w0, const float* w1, con
     }
     for (; c < nch; ++c) {
         const int o = c * 256 + 4 * lane;
-        const f32x4 xv = *(const f32x4*)(xr + o);
+        const f32x4 xv = router_in4(xr, nw, scale, o);
         a0 = dot4_f64(*(const f32x4*)(w0 + o), xv, a0);
         a1 = dot4_f64(*(const f32x4*)(w1 + o), xv, a1);
     }
@@ -583,7 +614,7 @@ __device__ __forceinline__ void exact_dot2(const float* w0, const float* w1, con
 // The same dots for four rows at once (x read once per four rows), each row in
 // the same order as exact_dot2 (so the same bits), two 256-column chunks per step.
 __device__ __forceinline__ void exact_dot4(const float* const (&w)[4], const float* xr, int H, int lane,
-                                           float (&r)[4]) {
+                                           float (&r)[4], const float* nw = nullptr, float scale = 1.0f) {
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
     const int nch = H >> 8;
     for (int c = 0; c < nch; c += 2) {
@@ -591,7 +622,7 @@ __device__ __forceinline__ void exact_dot4(const float* const (&w)[4], const flo
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int o = min(c + i, nch - 1) * 256 + 4 * lane;
-            xv[i] = *(const f32x4*)(xr + o);
+            xv[i] = router_in4(xr, nw, scale, o);
 #pragma unroll
             for (int k = 0; k < 4; ++k) v[k][i] = *(const f32x4*)(w[k] + o);
         }
@@ -798,6 +829,9 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
     // exact logits of the candidates and of the shared gate: one queue over
     // every group, four rows per pass, a remainder of one or two in a last pass
     const float* xr = a.x + (uint64_t)t * a.H;
+    // prefill with the pre-MoE RMSNorm on the fly: x is the residual row
+    const float* nw = a.norm_w;
+    const float xscale = nw ? a.x_scale[t] : 1.0f;
     float v[EPL];
     int id[EPL];
     uint64_t mk[EPL];
@@ -838,7 +872,7 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
 #pragma unroll
         for (int k = 0; k < 4; ++k) w[k] = row(g[k] < 0 ? g[0] : g[k], g[k] < 0 ? b[0] : b[k]);
         float r[4];
-        exact_dot4(w, xr, a.H, lane, r);
+        exact_dot4(w, xr, a.H, lane, r, nw, xscale);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             if (g[k] >= 0) put(g[k], b[k], r[k]);
@@ -849,7 +883,7 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
         pop(g1, b1);
         if (g1 < 0) { g1 = g0; b1 = b0; }
         float r0, r1;
-        exact_dot2(row(g0, b0), row(g1, b1), xr, a.H, lane, r0, r1);
+        exact_dot2(row(g0, b0), row(g1, b1), xr, a.H, lane, r0, r1, nw, xscale);
         put(g0, b0, r0);
         put(g1, b1, r1);
     }
@@ -1655,6 +1689,13 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         ma.rx = ws.rx_split;
         ma.rw = ws.rw_split;
         ma.rnorm = ws.rnorm;
+        // the pre-MoE RMSNorm on the fly (x == xr is the residual row): the
+        // preparation normalizes (and writes the scales), the refinement too
+        ma.norm_w = norm_w;
+        ma.eps = eps;
+        ma.x_ssq = norm_w ? x_ssq : nullptr;
+        ma.x_scale = ws.x_scale;
+        ta.norm_w = norm_w;
         x_f16 = false;  // written by the preparation
         hipLaunchKernelGGL(k_router_prep, dim3((T + 3) / 4 + (L.E + 3) / 4), dim3(256), 0, stream, ma);
         if ((err = hipGetLastError()) != hipSuccess) return err;
@@ -1753,7 +1794,10 @@ bool route_norm_fused(const LayerDesc& L, int T) { return route_decode_fused(L, 
 hipError_t launch_route(const LayerDesc& L, const Workspace& ws, const float* x, const float* xr, int T,
                         const RouteDebug& dbg, bool x_f16, hipStream_t stream, const float* norm_w, float eps,
                         const double* x_ssq) {
-    if (norm_w && (x_f16 || !route_norm_fused(L, T))) return hipErrorInvalidValue;
+    // norm_w: decode routing (route_norm_fused, no f16 operands) or the batched
+    // router (its preparation writes the f16 operands), with x == xr
+    if (norm_w && (x != xr || (route_uses_mfma(L, T) ? !x_f16 : (x_f16 || !route_norm_fused(L, T)))))
+        return hipErrorInvalidValue;
     hipError_t err = launch_route_tables(L, ws, x, xr, T, dbg, x_f16, stream, norm_w, eps, x_ssq);
     if (err != hipSuccess || !x_f16) return err;
     // the routing launch did not write x's f16 quants (only the batched router's does)

@@ -603,7 +603,8 @@ def test_fused_decode_routing_repeated(gpu, n_experts, T):
 
 
 @pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 300),
-                                     ("config1", 5), ("h4096", 10), ("pad", 10)])
+                                     ("config1", 5), ("config1", 300), ("h4096", 10), ("h4096", 300), ("pad", 10),
+                                     ("pad", 300)])
 def test_forward_norm_chain(gpu, which, T):
     """Three blocks with the RMSNorm partial sums carried from each to the next
     (x_ssq in, y_ssq out; the first block without x_ssq): every block's y has the
@@ -635,11 +636,12 @@ def test_forward_norm_chain(gpu, which, T):
 
 
 @pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 64), ("35b", 100),
-                                     ("35b", 300), ("config1", 5), ("config1", 32), ("h4096", 10), ("pad", 10),
-                                     ("pad", 130)])
+                                     ("35b", 300), ("35b", 1024), ("config1", 5), ("config1", 32), ("config1", 300),
+                                     ("h4096", 10), ("h4096", 300), ("pad", 10), ("pad", 130), ("pad", 300)])
 def test_forward_norm_matches_unfused(gpu, which, T):
     """y = x + MoE(RMSNorm(x) * w) in one call (the decode routing normalizes while it
-    stages x; other sizes normalize into the workspace) gives the bits of rms_norm
+    stages x, the batched router's preparation and refinement normalize from 256
+    tokens on, other sizes normalize into the workspace) gives the bits of rms_norm
     followed by forward(residual=x)."""
     from qwenium_amd import Workspace, rms_norm
 
