@@ -9,6 +9,15 @@
     python -m qwenium_amd.profiling counters <prefix>_counter_collection.csv [--kernel SUBSTR]
         per-kernel mean of every collected counter (one dispatch = one sample)
 
+    python -m qwenium_amd.profiling mfma <prefix>_counter_collection.csv [--kernel SUBSTR]
+        per-kernel MFMA-pipe ratios from a run that collected GRBM_GUI_ACTIVE,
+        SQ_VALU_MFMA_BUSY_CYCLES, SQ_VALU_MFMA_COEXEC_CYCLES, SQ_INSTS_MFMA,
+        SQ_INSTS_VALU and SQ_INSTS_SALU: the kernel's cycles (GRBM_GUI_ACTIVE is
+        summed over the XCDs: it reads 8 x 2.4 GHz x the duration of a timed
+        sleep kernel), the fraction of SIMD-cycles the MFMA pipe is busy, the
+        share of those in which a VALU instruction co-issues, and the VALU and
+        SALU instructions per MFMA instruction
+
     python -m qwenium_amd.profiling traffic --fetch F.csv --write W.csv --kernel SUBSTR \
             --copy-mib N [--workload NAME] [--out profiles/traffic_<workload>.json]
         HBM bytes per launch of one kernel from a FETCH_SIZE run and a
@@ -81,6 +90,23 @@ def counter_means(path: str, kernel: str | None = None) -> dict:
             for n, cs in acc.items()}
 
 
+def mfma_ratios(path: str, kernel: str | None = None, xcds: int = 8, simds: int = 1024) -> str:
+    """Markdown table of the MFMA-pipe ratios of every kernel with MFMA instructions."""
+    means = counter_means(path, kernel)
+    out = ["| kernel | dispatches | cycles per dispatch | MFMA busy (of SIMD-cycles) | VALU co-issue (of MFMA-busy) "
+           "| VALU instr / MFMA instr | SALU instr / MFMA instr |",
+           "|---|---:|---:|---:|---:|---:|---:|"]
+    for n, m in sorted(means.items()):
+        if not m.get("SQ_INSTS_MFMA"):
+            continue
+        cyc = m["GRBM_GUI_ACTIVE"] / xcds
+        busy = m["SQ_VALU_MFMA_BUSY_CYCLES"]
+        out.append("| `%s` | %d | %.4g | %.3f | %.3f | %.2f | %.2f |" % (
+            n[:90], m["dispatches"], cyc, busy / (simds * cyc), m["SQ_VALU_MFMA_COEXEC_CYCLES"] / busy,
+            m["SQ_INSTS_VALU"] / m["SQ_INSTS_MFMA"], m["SQ_INSTS_SALU"] / m["SQ_INSTS_MFMA"]))
+    return "\n".join(out)
+
+
 def copy_counter(path: str, counter: str) -> float:
     """Mean counter value of the calibration copies: the runtime's copy kernel
     also serves small copies, so only dispatches within 2x of the largest count."""
@@ -135,6 +161,11 @@ def main(argv=None) -> int:
     c = sub.add_parser("counters")
     c.add_argument("csv")
     c.add_argument("--kernel", default=None)
+    f = sub.add_parser("mfma")
+    f.add_argument("csv")
+    f.add_argument("--kernel", default=None)
+    f.add_argument("--xcds", type=int, default=8)
+    f.add_argument("--simds", type=int, default=1024, help="SIMDs on the device (256 CUs x 4 on MI355X)")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
@@ -147,6 +178,8 @@ def main(argv=None) -> int:
         print(kernel_stats(a.csv))
     elif a.cmd == "medians":
         print(dispatch_medians(a.csv, a.prefix))
+    elif a.cmd == "mfma":
+        print(mfma_ratios(a.csv, a.kernel, a.xcds, a.simds))
     elif a.cmd == "counters":
         means = counter_means(a.csv, a.kernel)
         names = sorted({c for m in means.values() for c in m})
