@@ -539,6 +539,7 @@ struct TopkArgs {
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
+    int xcd_ranges;       // 1: the prefill GEMMs follow, the scan writes their XCD tile ranges
     int nblk;
 };
 
@@ -1031,8 +1032,9 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
         // expert-major, the shared expert's tiles last) is cut at x / 8 of the
         // total, x = 1..7, and XCD x starts at the tile boundary nearest its cut
         // inside the expert whose work holds it (160 per full tile).
+        const bool xcd = a.xcd_ranges != 0;
         int routed_tiles = 0;
-        for (int w = 0; w < nchunk; ++w) routed_tiles += s_misc[3 * w + 2];
+        for (int w = 0; xcd && w < nchunk; ++w) routed_tiles += s_misc[3 * w + 2];
         const int64_t A64 = (int64_t)a.T * a.K;
         const int ntt_sh = a.S ? (a.T + kMfmaTileM - 1) / kMfmaTileM : 0;
         const int64_t w_routed = A64 + 32 * (int64_t)routed_tiles;
@@ -1052,7 +1054,7 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
             const int tb = base_t + inc_t - nt;
             for (int i = 0; i < nt && tb + i < a.max_tiles; ++i)
                 a.tiles[tb + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, cnt - i * kMfmaTileM), 0);
-            if (cnt > 0) {
+            if (xcd && cnt > 0) {
                 const int64_t ws = off + 32 * (int64_t)tb, we = ws + cnt + 32 * (int64_t)nt;
                 for (int x = 1; x < 8; ++x) {
                     const int64_t bx = x * w_total / 8;
@@ -1082,7 +1084,7 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
                 for (int i = 0; i < ntt && n_tiles < a.max_tiles; ++i)
                     a.tiles[n_tiles++] = make_int4(a.E, A + i * kMfmaTileM, min(kMfmaTileM, a.T - i * kMfmaTileM), 0);
             }
-            for (int x = 1; x < 8; ++x) {
+            for (int x = 1; xcd && x < 8; ++x) {
                 const int64_t bx = x * w_total / 8;
                 if (bx >= w_routed)
                     a.counters[kCounterXcd + x] = routed_tiles + (int)min((int64_t)ntt_sh, (bx - w_routed + 80) / 160);
@@ -1669,6 +1671,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
     ta.counters = ws.counters;
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
+    ta.xcd_ranges = x_f16 ? 1 : 0;  // x_f16: the f16-MFMA GEMMs run next
     ta.nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
     hipError_t err;
     if (route_uses_mfma(L, T)) {
