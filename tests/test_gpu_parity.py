@@ -331,6 +331,34 @@ def test_graph_replay_matches_eager(gpu):
         torch.cuda.synchronize()
 
 
+def test_graph_replay_prefill_matches_eager(gpu):
+    """Prefill forwards (batched router, f16-MFMA GEMMs, fixups) captured in a
+    HIP graph: every replay equals the eager result bit for bit."""
+    from qwenium_amd import Workspace
+    spec = synthetic.QWEN35B
+    T = 512
+    layers = [synthetic.make_layer(spec, 70 + i) for i in range(2)]
+    xs = [synthetic.make_x(spec, T, 70, batch=b) for b in range(2)]
+    ws = Workspace(layers[0], T)
+    eager = [layers[i].forward(xs[i], workspace=ws).clone() for i in range(2)]
+    outs = [torch.empty_like(xs[0]) for _ in range(2)]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(2):
+            layers[i].forward(xs[i], out=outs[i], workspace=ws)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            np.testing.assert_array_equal(outs[i].cpu().numpy().view(np.int32), eager[i].cpu().numpy().view(np.int32))
+        layers[1].forward(xs[0], workspace=ws)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 # ---- f16-MFMA grouped GEMM path (prefill) -------------------------------------------------
 @pytest.mark.parametrize("wtype", [TYPE_Q4_0, TYPE_Q8_0])
 @pytest.mark.parametrize("T", [1, 17, 64, 65, 130])
