@@ -35,16 +35,17 @@ public:
 
     // All tensors are borrowed device views in GGUF block layout; the w_sh_*
     // slots may be nullptr when !hp.has_shared_expert.  prefill_copies (no
-    // counterpart in the reference; the reference's nine arguments keep the
-    // default): also keep chunk-major copies of the expert matrices for the
-    // prefill GEMMs (qmoe_layer_build_prefill_copies), read from the tensors
-    // here, so their data must be in place; one more copy of the expert weights
-    // in device memory (455 MB for a Qwen3.6-35B-A3B layer in Q4_0).  false: the
-    // prefill GEMMs read the GGUF rows (same results, slower prefill).
+    // counterpart in the reference; opt-in, so the reference's nine arguments
+    // keep one copy of the weights): also keep chunk-major copies of the expert
+    // matrices for the prefill GEMMs (qmoe_layer_build_prefill_copies), read from
+    // the tensors here, so their data must be in place; one more copy of the
+    // expert weights in device memory (455 MB for a Qwen3.6-35B-A3B layer in
+    // Q4_0, 18.2 GB for its 40 layers).  Without them the prefill GEMMs read the
+    // GGUF rows (same results, slower prefill).
     MoELayer(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate, const qmoe_tensor* w_exp_up,
              const qmoe_tensor* w_exp_down, const qmoe_tensor* w_sh_gate, const qmoe_tensor* w_sh_up,
              const qmoe_tensor* w_sh_down, const qmoe_tensor* w_sh_norm, const Hparams& hp,
-             bool prefill_copies = true)
+             bool prefill_copies = false)
         : hp_(hp) {
         const qmoe_hparams c{hp.n_experts, hp.top_k, hp.ffn_dim, hp.has_shared_expert ? 1 : 0};
         check(qmoe_layer_create(w_router, w_exp_gate, w_exp_up, w_exp_down, w_sh_gate, w_sh_up, w_sh_down,
@@ -105,7 +106,7 @@ public:
 
     // prefill_copies: as MoELayer's.
     GeGLUMoELayer(const qmoe_tensor* w_router, const qmoe_tensor* w_gate_up_exps, const qmoe_tensor* w_down_exps,
-                  const Hparams& hp, bool prefill_copies = true)
+                  const Hparams& hp, bool prefill_copies = false)
         : hp_(hp) {
         const qmoe_hparams c{hp.n_experts, hp.top_k, hp.ffn_dim, hp.has_shared_expert ? 1 : 0};
         check(qmoe_geglu_layer_create(w_router, w_gate_up_exps, w_down_exps, &c, &layer_));

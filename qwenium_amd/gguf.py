@@ -159,20 +159,22 @@ class GGUFFile:
             out[slot] = self.upload(name, device)
         return out
 
-    def moe_layer(self, block: int, device="cuda") -> MoELayer:
-        """MoELayer of block `block` (weights uploaded; the layer keeps them alive)."""
+    def moe_layer(self, block: int, device="cuda", prefill_copies: bool = False) -> MoELayer:
+        """MoELayer of block `block` (weights uploaded; the layer keeps them alive);
+        prefill_copies as MoELayer's (opt-in)."""
         hp = self.moe_hparams(block=block)
         t = self.moe_tensors(block, device, shared=hp.has_shared_expert)
         layer = MoELayer(t["router"], t["gate"], t["up"], t["down"], t.get("sh_gate"), t.get("sh_up"),
-                         t.get("sh_down"), t.get("sh_norm"), hp)
+                         t.get("sh_down"), t.get("sh_norm"), hp, prefill_copies=prefill_copies)
         return layer
 
     def ffn_norm(self, block: int, device="cuda") -> torch.Tensor:
         """The block's pre-MoE RMSNorm weight [n_embd] f32."""
         return self.upload(f"blk.{block}.{FFN_NORM}", device).data
 
-    def gemma4_moe_layer(self, block: int, device="cuda") -> GeGLUMoELayer:
-        """GeGLUMoELayer of Gemma 4 block `block` (gemma4.* hparams, fused gate_up)."""
+    def gemma4_moe_layer(self, block: int, device="cuda", prefill_copies: bool = False) -> GeGLUMoELayer:
+        """GeGLUMoELayer of Gemma 4 block `block` (gemma4.* hparams, fused gate_up);
+        prefill_copies as GeGLUMoELayer's (opt-in)."""
         hp = self.moe_hparams(arch="gemma4", block=block)
         names = set(self.tensor_names())
         t = {}
@@ -181,7 +183,7 @@ class GGUFFile:
             if name not in names:
                 raise ValueError(f"gemma4: missing tensor '{name}': expected in block weights, got absent")
             t[slot] = self.upload(name, device)
-        return GeGLUMoELayer(t["router"], t["gate_up"], t["down"], hp)
+        return GeGLUMoELayer(t["router"], t["gate_up"], t["down"], hp, prefill_copies=prefill_copies)
 
     def gemma4_moe_norms(self, block: int, device="cuda"):
         """(pre_ffw_norm_2, ffn_gate_inp.scale) of Gemma 4 block `block`, [n_embd] f32 each."""

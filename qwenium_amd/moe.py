@@ -162,7 +162,7 @@ class MoELayer:
     def __init__(self, w_router: GGMLTensor, w_exp_gate: GGMLTensor, w_exp_up: GGMLTensor,
                  w_exp_down: GGMLTensor, w_sh_gate: Optional[GGMLTensor], w_sh_up: Optional[GGMLTensor],
                  w_sh_down: Optional[GGMLTensor], w_sh_norm: Optional[GGMLTensor], hp: Hparams, *,
-                 prefill_copies: bool = True):
+                 prefill_copies: bool = False):
         self.hp = hp
         # keep the borrowed weights alive for the layer's lifetime
         self._weights = (w_router, w_exp_gate, w_exp_up, w_exp_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_norm)
@@ -182,8 +182,10 @@ class MoELayer:
             self.build_prefill_copies()
 
     def build_prefill_copies(self) -> None:
-        """Chunk-major copies of the expert matrices for the prefill GEMMs (one more copy
-        of the expert weights in device memory); reads the tensors now."""
+        """Chunk-major copies of the expert matrices for the prefill GEMMs, opt-in: one more
+        copy of the expert weights in device memory (455 MB for a 35B-A3B layer in Q4_0,
+        18.2 GB for its 40 layers); reads the tensors now.  Without them the prefill GEMMs
+        read the GGUF rows: the same results, slower prefill."""
         check(lib().qmoe_layer_build_prefill_copies(self._handle))
 
     def close(self) -> None:
@@ -322,7 +324,7 @@ class GeGLUMoELayer(MoELayer):
     (ggml's CPU gelu), no shared expert, the router on its own input."""
 
     def __init__(self, w_router: GGMLTensor, w_gate_up_exps: GGMLTensor, w_down_exps: GGMLTensor, hp: Hparams, *,
-                 prefill_copies: bool = True):
+                 prefill_copies: bool = False):
         if hp.has_shared_expert:
             raise ValueError("has_shared_expert expected False for the GeGLU MoE, got True")
         self.hp = hp

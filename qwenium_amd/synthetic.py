@@ -135,12 +135,14 @@ def make_layer_tensors(spec: LayerSpec, seed: int, layer: int = 0, device="cuda"
 
 
 def make_layer(spec: LayerSpec, seed: int, layer: int = 0, device="cuda",
-               tensors: Optional[dict] = None) -> MoELayer:
+               tensors: Optional[dict] = None, prefill_copies: bool = True) -> MoELayer:
+    """The layer over seeded synthetic weights; prefill_copies: opt in to the
+    chunk-major copies of the expert matrices (the faster prefill GEMMs)."""
     t = tensors if tensors is not None else make_layer_tensors(spec, seed, layer, device)
     if spec.geglu:
-        return GeGLUMoELayer(t["router"], t["gate_up"], t["down"], spec.hparams)
+        return GeGLUMoELayer(t["router"], t["gate_up"], t["down"], spec.hparams, prefill_copies=prefill_copies)
     return MoELayer(t["router"], t["gate"], t["up"], t["down"], t.get("sh_gate"), t.get("sh_up"),
-                    t.get("sh_down"), t.get("sh_norm"), spec.hparams)
+                    t.get("sh_down"), t.get("sh_norm"), spec.hparams, prefill_copies=prefill_copies)
 
 
 def make_x(spec: LayerSpec, n_tokens: int, seed: int, batch: int = 0, device="cuda") -> torch.Tensor:

@@ -164,7 +164,7 @@ static void PrefillCopiesGiveTheSameOutput() {
     DevBuf y0((size_t)n_tok * N_EMBD * sizeof(float)), y1((size_t)n_tok * N_EMBD * sizeof(float));
     {
         qmoe::MoELayer with(&f.t_router, &f.t_gate, &f.t_up, &f.t_down, &f.t_sh_gate, &f.t_sh_up, &f.t_sh_down,
-                            &f.t_sh_norm, hparams(true));
+                            &f.t_sh_norm, hparams(true), true);
         qmoe::MoELayer without(&f.t_router, &f.t_gate, &f.t_up, &f.t_down, &f.t_sh_gate, &f.t_sh_up, &f.t_sh_down,
                                &f.t_sh_norm, hparams(true), false);
         with.forward((const float*)x.p, n_tok, (float*)y0.p);
