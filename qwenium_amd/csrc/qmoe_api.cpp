@@ -357,7 +357,14 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, L->device) == hipSuccess && n_cu > 0)
         d.n_cu = n_cu;
-    // token count from which the grouped int8-MFMA GEMMs replace the streaming GEMVs
+    // token count from which the grouped f16-MFMA GEMMs replace the streaming GEMVs:
+    // where an expert averages about 5.5 rows (T * top_k / n_experts), and from 128
+    // tokens at least (measured: the 35B-A3B shape crosses over near 176 tokens,
+    // Gemma 4's below 128)
+    {
+        const int64_t t = (11 * (int64_t)d.E + 2 * d.K - 1) / (2 * d.K);  // ceil(5.5 E / K)
+        d.mfma_min_tokens = (int)std::max<int64_t>(128, std::min<int64_t>(4096, (t + 15) / 16 * 16));
+    }
     if (const char* env = std::getenv("QMOE_MFMA_MIN_TOKENS")) {
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 1) d.mfma_min_tokens = (int)std::min<long>(v, 1 << 30);

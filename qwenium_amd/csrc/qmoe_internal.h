@@ -52,7 +52,7 @@ struct LayerDesc {
     uint64_t sh_gate_nb1 = 0, sh_up_nb1 = 0, sh_down_nb1 = 0;
     const float* w_sh_norm = nullptr;
     int n_cu = 256;                         // compute units of the layer's device
-    int mfma_min_tokens = 128;              // token count from which the int8-MFMA path runs
+    int mfma_min_tokens = 128;              // token count from which the f16-MFMA GEMMs run (set per shape)
     int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs
     int dc_ahead = 2;                       // decode down+combine: steps with loads in flight (2 or 4)
     unsigned long long* expert_counts = nullptr;  // optional device [E]: += each forward's per-expert dispatches

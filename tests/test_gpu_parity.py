@@ -2,11 +2,12 @@
 same seeded inputs.
 
 Bar: top-k expert ids, per-expert offsets and row lists bit-exact (ties to the
-lowest expert id); layer outputs within max-abs 2e-3 x output RMS.  Below 128
-tokens the kernels accumulate quantized block dots exactly (f64) and use the
+lowest expert id); layer outputs within max-abs 2e-3 x output RMS.  Below the
+MFMA threshold the kernels accumulate quantized block dots exactly (f64) and use the
 same deterministic exp, so outputs are in practice bit-identical; that is
 asserted separately as a fraction so a rare router rounding flip does not hide
-behind it.  From 128 tokens (or when forced) the grouped GEMMs run f16 MFMAs:
+behind it.  From max(128, 5.5 n_experts / top_k) tokens (176 at the 35B-A3B shape) or when
+forced, the grouped GEMMs run f16 MFMAs:
 the block dots are exact, their scaled sum is accumulated in f32, and every h
 value whose Q8_0 rounding that error could change is recomputed exactly, so the
 h quants match the oracle's; outputs differ by f32 rounding of the sums (about
@@ -132,6 +133,16 @@ def test_decode_35b_token_counts(gpu, spec, T):
     kernel as its last step; routing and outputs match the oracle as on every other path."""
     y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=200 + T)
     assert_parity(y, got, y_ref, d_ref, spec)
+
+
+@pytest.mark.parametrize("T", [160, 175, 176])
+def test_35b_around_mfma_threshold(gpu, T):
+    """The 35B shape switches to the f16-MFMA GEMMs where an expert averages 5.5 rows
+    (176 tokens): 160 and 175 tokens stream (outputs bit-identical to the oracle), 176 runs
+    the MFMA GEMMs (h quants exact, outputs within MFMA_TOL); routing bit-exact on all."""
+    spec = synthetic.QWEN35B
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=500 + T)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= 176, min_identical=1.0)
 
 
 @pytest.mark.parametrize("spec,T", [(LayerSpec(4096, 64, 4, 256, True, TYPE_Q8_0), 7),
