@@ -53,7 +53,7 @@ struct LayerDesc {
     const float* w_sh_norm = nullptr;
     int n_cu = 256;                         // compute units of the layer's device
     int mfma_min_tokens = 128;              // token count from which the f16-MFMA GEMMs run (set per shape)
-    int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs
+    int big_router_min_tokens = 256;        // token count from which the bf16-MFMA router runs (set per shape)
     int dc_ahead = 2;                       // decode down+combine: steps with loads in flight (2 or 4)
     unsigned long long* expert_counts = nullptr;  // optional device [E]: += each forward's per-expert dispatches
     int act = 0;                            // 0 SwiGLU (silu(g)*u), 1 GeGLU-tanh (gelu(g)*u, ggml's fp16 table)

@@ -159,7 +159,7 @@ def test_decode_hidden_sizes(gpu, spec, T):
                                     (LayerSpec(3072, 96, 6, 512, True, TYPE_Q4_0), 40),
                                     (LayerSpec(1280, 40, 4, 512, False, TYPE_Q4_0), 50)])
 def test_grouped_router_hidden_sizes(gpu, spec, T):
-    """17-255 tokens (the router over groups of 16 tokens, x's Q8_0 rows written by its
+    """17 tokens to the batched router's threshold (the router over groups of 16 tokens, x's Q8_0 rows written by its
     blocks) at hidden 4096 / 3072 (two router rows per block) and 1280 (five rows per
     block, the last wave with one slab fewer, 9 blocks per group for 16 tokens)."""
     y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=310 + T)
@@ -170,13 +170,15 @@ def test_grouped_router_hidden_sizes(gpu, spec, T):
                                     (LayerSpec(96, 8, 2, 32, True, TYPE_Q4_0), 10),
                                     (LayerSpec(320, 16, 4, 96, True, TYPE_Q8_0), 17),
                                     (LayerSpec(160, 12, 3, 224, False, TYPE_Q4_0), 300),
+                                    (LayerSpec(160, 12, 3, 224, False, TYPE_Q4_0), 1100),
                                     (LayerSpec(1056, 32, 4, 96, True, TYPE_Q4_0), 10),
                                     (LayerSpec(1056, 32, 4, 96, True, TYPE_Q4_0), 150)])
 def test_padded_widths(gpu, spec, T):
     """n_embd and ffn_dim that Q4_0/Q8_0 rows allow (multiples of 32) but the kernels'
     grid does not (multiples of 256 and 64): the layer runs on zero-padded weight copies
     and zero-padded rows, and routing and outputs match the oracle at the caller's widths
-    as on every other path (decode, streaming, and MFMA with the batched router)."""
+    as on every other path (decode, streaming, MFMA with the grouped router (300 tokens)
+    and with the batched router (1100 tokens: from 1024 at these widths))."""
     y, got, y_ref, d_ref, layer, *_ = run_pair(spec, T, seed=400 + T)
     assert layer.n_embd == spec.n_embd and y.shape == (T, spec.n_embd)
     assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= 128)
@@ -416,12 +418,17 @@ def test_batched_router_forced_small_layer(gpu, monkeypatch, T):
     check_router_bound(got, d_ref["logits"])
 
 
-def test_batched_router_35b_t300(gpu):
-    """The default threshold (256 tokens) selects the batched router."""
+@pytest.mark.parametrize("T", [300, 600])
+def test_router_threshold_35b(gpu, T):
+    """At the 35B-A3B shape the exact grouped router runs up to 543 tokens (cheaper there)
+    and the batched router from 544: both give the oracle's routing."""
     spec = synthetic.QWEN35B
-    y, got, y_ref, d_ref, *_ = run_pair(spec, 300, seed=31)
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=31)
     assert_parity(y, got, y_ref, d_ref, spec, mfma=True)
-    assert check_router_bound(got, d_ref["logits"]) < 0.5
+    if T >= 544:
+        assert check_router_bound(got, d_ref["logits"]) < 0.5
+    else:
+        assert not np.isfinite(got["router_approx"]).any(), "the batched router ran below its threshold"
 
 
 @pytest.mark.parametrize("dup", ["pairs", "all"])
@@ -642,8 +649,8 @@ def test_fused_decode_routing_repeated(gpu, n_experts, T):
 
 
 @pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 300),
-                                     ("config1", 5), ("config1", 300), ("h4096", 10), ("h4096", 300), ("pad", 10),
-                                     ("pad", 300)])
+                                     ("35b", 1024), ("config1", 5), ("config1", 300), ("h4096", 10), ("h4096", 300),
+                                     ("h4096", 1100), ("pad", 10), ("pad", 300)])
 def test_forward_norm_chain(gpu, which, T):
     """Three blocks with the RMSNorm partial sums carried from each to the next
     (x_ssq in, y_ssq out; the first block without x_ssq): every block's y has the
@@ -679,8 +686,9 @@ def test_forward_norm_chain(gpu, which, T):
                                      ("h4096", 10), ("h4096", 300), ("pad", 10), ("pad", 130), ("pad", 300)])
 def test_forward_norm_matches_unfused(gpu, which, T):
     """y = x + MoE(RMSNorm(x) * w) in one call (the decode routing normalizes while it
-    stages x, the batched router's preparation and refinement normalize from 256
-    tokens on, other sizes normalize into the workspace) gives the bits of rms_norm
+    stages x, the batched router's preparation and refinement normalize from its
+    threshold on (544 tokens at the 35B-A3B shape), other sizes normalize into the
+    workspace) gives the bits of rms_norm
     followed by forward(residual=x)."""
     from qwenium_amd import Workspace, rms_norm
 
