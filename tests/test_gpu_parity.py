@@ -648,6 +648,21 @@ def test_fused_decode_routing_repeated(gpu, n_experts, T):
     assert ws.check() == 0
 
 
+@pytest.mark.parametrize("T", [300, 720, 800])
+def test_1024_experts_prefill(gpu, T):
+    """1024 experts (the most a layer takes): the grouped router with the streaming GEMVs
+    (300 tokens), the f16-MFMA GEMMs (from 5.5 * 1024 / 8 = 704 tokens) with the grouped
+    router (720) and with the batched router (from 784 at n_embd 256: 800 tokens), sixteen
+    64-expert router tiles and a 16-wave expert scan."""
+    spec = LayerSpec(256, 1024, 8, 64, True, TYPE_Q4_0)
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=600 + T)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= 704, min_identical=1.0)
+    if T >= 784:
+        check_router_bound(got, d_ref["logits"])
+    else:
+        assert not np.isfinite(got["router_approx"]).any()
+
+
 @pytest.mark.parametrize("which,T", [("35b", 1), ("35b", 10), ("35b", 16), ("35b", 17), ("35b", 300),
                                      ("35b", 1024), ("config1", 5), ("config1", 300), ("h4096", 10), ("h4096", 300),
                                      ("h4096", 1100), ("pad", 10), ("pad", 300)])
