@@ -648,6 +648,39 @@ def test_fused_decode_routing_repeated(gpu, n_experts, T):
     assert ws.check() == 0
 
 
+def _random_cases(n=32, seed=2024):
+    """Seeded layer shapes and token counts across every path (decode, grouped
+    router + streaming, MFMA GEMMs, batched router), padded widths and both
+    weight types; fixed at import, so the parametrization is stable."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        H = int(rng.choice([256, 512, 1024, 1056, 2048]))
+        E = int(rng.choice([8, 16, 64, 128, 256]))
+        K = int(min(E, rng.choice([1, 2, 4, 6, 8])))
+        F = int(rng.choice([64, 96, 128, 256, 512]))
+        shared = bool(rng.integers(2))
+        wtype = TYPE_Q4_0 if rng.integers(2) else TYPE_Q8_0
+        T = int(rng.choice([1, 5, 16, 17, 40, 130, 200, 300, 600]))
+        cases.append(pytest.param(LayerSpec(H, E, K, F, shared, wtype), T, id=f"H{H}-E{E}-k{K}-F{F}-s{int(shared)}-"
+                                  f"{'q4' if wtype == TYPE_Q4_0 else 'q8'}-T{T}"))
+    return cases
+
+
+def _mfma_min_tokens(spec: LayerSpec) -> int:
+    t = (11 * spec.n_experts + 2 * spec.top_k - 1) // (2 * spec.top_k)
+    return max(128, min(4096, (t + 15) // 16 * 16))
+
+
+@pytest.mark.parametrize("spec,T", _random_cases())
+def test_random_shapes(gpu, spec, T):
+    """Seeded random shapes against the oracle: routing bit-exact; outputs bit-identical
+    below the MFMA threshold (max(128, 5.5 n_experts / top_k) tokens), within MFMA_TOL
+    with exact h quants above it."""
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=700 + T)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= _mfma_min_tokens(spec), min_identical=1.0)
+
+
 @pytest.mark.parametrize("T", [300, 720, 800])
 def test_1024_experts_prefill(gpu, T):
     """1024 experts (the most a layer takes): the grouped router with the streaming GEMVs
