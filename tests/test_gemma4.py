@@ -337,3 +337,47 @@ def test_geglu_layer_rejects_bad_inputs(gpu):
     with pytest.raises(ValueError):
         layer.forward_routed(x, x[:3])
     torch.cuda.synchronize()
+
+
+def _geglu_cases(n=16, seed=4042):
+    """Seeded GeGLU layer shapes and token counts over every path (fixed at import)."""
+    from qwenium_amd import synthetic
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        H = int(rng.choice([256, 512, 1056, 2816]))
+        E = int(rng.choice([8, 16, 64, 128]))
+        K = int(min(E, rng.choice([1, 2, 4, 8])))
+        F = int(rng.choice([64, 96, 128, 704]))
+        wtype = TYPE_Q4_0 if rng.integers(2) else TYPE_Q8_0
+        T = int(rng.choice([1, 10, 17, 40, 130, 300]))
+        cases.append(pytest.param(synthetic.LayerSpec(H, E, K, F, False, wtype, geglu=True), T,
+                                  id=f"H{H}-E{E}-k{K}-F{F}-{'q4' if wtype == TYPE_Q4_0 else 'q8'}-T{T}"))
+    return cases
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("spec,T", _geglu_cases())
+def test_geglu_random_shapes(gpu, spec, T):
+    """Seeded random GeGLU shapes, the Gemma 4 slice against the oracle: routing bit-exact,
+    outputs bit-identical below the MFMA threshold (max(128, 5.5 n_experts / top_k)
+    tokens), within MFMA_TOL with exact h quants above it."""
+    import torch
+
+    from qwenium_amd import Workspace, gemma4_moe_inputs, synthetic
+
+    seed = 90 + T
+    tensors = synthetic.make_layer_tensors(spec, seed)
+    layer = synthetic.make_layer(spec, seed, tensors=tensors)
+    x = synthetic.make_x(spec, T, seed)
+    w_pre, w_rs = synthetic.make_gemma4_norms(spec, seed, 0)
+    ei, ri = gemma4_moe_inputs(x, w_pre, w_rs, synthetic.NORM_EPS)
+    ws = Workspace(layer, T)
+    y, dbg = layer.forward_routed(ei, ri, workspace=ws, debug=True)
+    torch.cuda.synchronize()
+    ref = host_layer(spec, tensors)
+    y_ref, d_ref = ref.forward(ei.cpu().numpy(), debug=True, router_in=ri.cpu().numpy())
+    got = {k: v.cpu().numpy() for k, v in dbg.items()}
+    t = (11 * spec.n_experts + 2 * spec.top_k - 1) // (2 * spec.top_k)
+    mfma_min = max(128, min(4096, (t + 15) // 16 * 16))
+    assert_parity(y.cpu().numpy(), got, y_ref, d_ref, min_identical=1.0, mfma=T >= mfma_min)
