@@ -681,6 +681,46 @@ def test_random_shapes(gpu, spec, T):
     assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= _mfma_min_tokens(spec), min_identical=1.0)
 
 
+def _chain_cases(n=12, seed=77):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        H = int(rng.choice([256, 512, 1056, 2048, 4096]))
+        E = int(rng.choice([8, 16, 64, 256]))
+        K = int(min(E, rng.choice([2, 4, 8])))
+        F = int(rng.choice([64, 96, 256, 512]))
+        T = int(rng.choice([1, 7, 16, 17, 64, 200, 600, 1100]))
+        cases.append(pytest.param(LayerSpec(H, E, K, F, bool(rng.integers(2)), TYPE_Q4_0), T,
+                                  id=f"H{H}-E{E}-k{K}-F{F}-T{T}"))
+    return cases
+
+
+@pytest.mark.parametrize("spec,T", _chain_cases())
+def test_forward_norm_chain_random(gpu, spec, T):
+    """Seeded random shapes, two chained blocks: with the RMSNorm partial sums carried
+    (normalized on the fly at decode and in the batched router, into the workspace
+    otherwise) every block equals rms_norm + forward bit for bit, and y's partial
+    sums equal the oracle's."""
+    from qwenium_amd import Workspace, rms_norm, ssq_parts
+
+    x = synthetic.make_x(spec, T, 80 + T, batch=1)
+    x_ssq = None
+    ws = None
+    for l in range(2):
+        layer = synthetic.make_layer(spec, 80 + T, layer=l)
+        if ws is None:
+            ws = Workspace(layer, T)
+        wn = synthetic.make_norm_weight(spec, 80 + T, l)
+        y_ssq = torch.empty((T, ssq_parts(spec.n_embd)), dtype=torch.float64, device=x.device)
+        y = layer.forward_norm(x, wn, synthetic.NORM_EPS, workspace=ws, x_ssq=x_ssq, y_ssq=y_ssq)
+        y_ref = layer.forward(rms_norm(x, wn, synthetic.NORM_EPS), residual=x, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), f"block {l}"
+        np.testing.assert_array_equal(y_ssq.cpu().numpy(), po.rms_partials(y.cpu().numpy()), err_msg=f"block {l}")
+        x, x_ssq = y, y_ssq
+    assert ws.check() == 0
+
+
 @pytest.mark.parametrize("T", [300, 720, 800])
 def test_1024_experts_prefill(gpu, T):
     """1024 experts (the most a layer takes): the grouped router with the streaming GEMVs
