@@ -361,35 +361,15 @@ __global__ __launch_bounds__(256, 3) void k_expert_f16(F16Args a) {
     uint32_t* s_rowoff = (uint32_t*)(s_dyn + 2 * kStageBytes + kSinkBytes);
     uint32_t* s_doff = s_rowoff + kTM;
     // XCD-aware mapping (workgroups are dealt to the 8 XCDs round-robin): XCD x
-    // takes the tiles [f[x], f[x+1]) in order, each with all its column chunks,
-    // so the tiles of one expert run back to back on one XCD and its weights and
-    // activation rows are read into one L2.  The routing's scan balanced the
-    // boundaries by work; here they are clamped so that every XCD's range fits
-    // the launch (gx tiles per XCD, 8 gx >= the tile count).
+    // takes tiles x, x + 8, ... and all column chunks of each, so a tile's
+    // activation rows are read into one L2 and the XCDs get statistically
+    // equal shares of the (unequal) tiles.  (Contiguous work-balanced expert
+    // ranges per XCD fetch less past the L2s but run slower, most of all under
+    // skewed routing.)
     const int jb = (int)(blockIdx.x >> 3);
     const int tile_local = jb / a.n_y, y = jb - tile_local * a.n_y;
-    int tile_id, tile_end;
-    {
-        const int xcd = (int)(blockIdx.x & 7);
-        const int gx = (int)gridDim.x / (8 * a.n_y);
-        const int n_tiles = a.counters[1];
-        int f[9];
-        f[0] = 0;
-        f[8] = n_tiles;
-#pragma unroll
-        for (int x = 1; x < 8; ++x) f[x] = min(n_tiles, min(max(a.counters[kCounterXcd + x], f[x - 1]), f[x - 1] + gx));
-#pragma unroll
-        for (int x = 7; x > 0; --x) f[x] = max(f[x], f[x + 1] - gx);
-        int lo = 0, hi = n_tiles;
-#pragma unroll
-        for (int x = 1; x < 8; ++x) {
-            if (x == xcd) lo = f[x];
-            if (x == xcd + 1) hi = f[x];
-        }
-        tile_id = lo + tile_local;
-        tile_end = hi;
-    }
-    if (tile_id >= tile_end) return;
+    const int tile_id = (int)(blockIdx.x & 7) + 8 * tile_local;
+    if (tile_id >= a.counters[1]) return;
     const int4 tile = a.tiles[tile_id];
     const int e = tile.x, p0 = tile.y, nr = tile.z;
     const int tid = threadIdx.x;

@@ -26,11 +26,9 @@ constexpr int kMfmaTileM = 128;
 // k values per LDS chunk of the prefill GEMMs.
 constexpr int kF16ChunkK = 64;
 // Workspace counters (kCounters ints): [0] active slots, [1] tiles,
-// [kCounterFix] listed h blocks, [kCounterXcd + x] (x = 1..7) the first tile of
-// XCD x in the prefill GEMMs (the routing's scan balances the tiles by work).
+// [kCounterFix] listed h blocks.
 constexpr int kCounters = 32;
 constexpr int kCounterFix = 4;
-constexpr int kCounterXcd = 16;
 constexpr int kFixStride = 36;  // floats per listed h block: 32 values, amax's error estimate, padding
 // Expert activations: SwiGLU (moe.cpp:117) or GeGLU-tanh (gemma4.cpp:423).
 constexpr int kActSilu = 0;

@@ -539,7 +539,6 @@ struct TopkArgs {
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
-    int xcd_ranges;       // 1: the prefill GEMMs follow, the scan writes their XCD tile ranges
     int nblk;
 };
 
@@ -1027,18 +1026,6 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
     if (wave < nchunk) {
         int base = 0, base_act = 0, base_t = 0;
         for (int w = 0; w < wave; ++w) { base += s_misc[3 * w]; base_act += s_misc[3 * w + 1]; base_t += s_misc[3 * w + 2]; }
-        // Work-balanced tile ranges of the 8 XCDs for the prefill GEMMs (which deal
-        // workgroups to the XCDs round-robin): the tiles' work (rows + 32 per tile,
-        // expert-major, the shared expert's tiles last) is cut at x / 8 of the
-        // total, x = 1..7, and XCD x starts at the tile boundary nearest its cut
-        // inside the expert whose work holds it (160 per full tile).
-        const bool xcd = a.xcd_ranges != 0;
-        int routed_tiles = 0;
-        for (int w = 0; xcd && w < nchunk; ++w) routed_tiles += s_misc[3 * w + 2];
-        const int64_t A64 = (int64_t)a.T * a.K;
-        const int ntt_sh = a.S ? (a.T + kMfmaTileM - 1) / kMfmaTileM : 0;
-        const int64_t w_routed = A64 + 32 * (int64_t)routed_tiles;
-        const int64_t w_total = w_routed + (int64_t)a.S * (a.T + 32 * (int64_t)ntt_sh);
         if (e < a.E) {
             const int off = base + inc - cnt;
             a.offsets[e] = off;
@@ -1054,14 +1041,6 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
             const int tb = base_t + inc_t - nt;
             for (int i = 0; i < nt && tb + i < a.max_tiles; ++i)
                 a.tiles[tb + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, cnt - i * kMfmaTileM), 0);
-            if (xcd && cnt > 0) {
-                const int64_t ws = off + 32 * (int64_t)tb, we = ws + cnt + 32 * (int64_t)nt;
-                for (int x = 1; x < 8; ++x) {
-                    const int64_t bx = x * w_total / 8;
-                    if (bx >= ws && bx < we)
-                        a.counters[kCounterXcd + x] = tb + (int)min((int64_t)nt, (bx - ws + 80) / 160);
-                }
-            }
         }
         if (wave == nchunk - 1 && a.dslots && first_token) {
             // decode slot list: the active routed experts, then "none" up to the
@@ -1083,11 +1062,6 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
                 const int ntt = (a.T + kMfmaTileM - 1) / kMfmaTileM;
                 for (int i = 0; i < ntt && n_tiles < a.max_tiles; ++i)
                     a.tiles[n_tiles++] = make_int4(a.E, A + i * kMfmaTileM, min(kMfmaTileM, a.T - i * kMfmaTileM), 0);
-            }
-            for (int x = 1; xcd && x < 8; ++x) {
-                const int64_t bx = x * w_total / 8;
-                if (bx >= w_routed)
-                    a.counters[kCounterXcd + x] = routed_tiles + (int)min((int64_t)ntt_sh, (bx - w_routed + 80) / 160);
             }
             a.counters[0] = n_act;
             a.counters[1] = n_tiles;
@@ -1671,7 +1645,6 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
     ta.counters = ws.counters;
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
-    ta.xcd_ranges = x_f16 ? 1 : 0;  // x_f16: the f16-MFMA GEMMs run next
     ta.nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
     hipError_t err;
     if (route_uses_mfma(L, T)) {
