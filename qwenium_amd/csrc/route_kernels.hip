@@ -572,68 +572,45 @@ __device__ __forceinline__ double dot4_f64(const f32x4 w, const f32x4 v, double 
     return __builtin_fma((double)w.w, (double)v.w, acc);
 }
 
-// Exact router logits of one token against two router rows (one wave; f32
-// products are exact in f64, the sum is f64), rounded once to f32.
-// The router input's 4 values at column o: x itself, or with nw the RMSNorm
-// output (x * scale) * nw as k_rms_norm writes it.
-__device__ __forceinline__ f32x4 router_in4(const float* xr, const float* nw, float scale, int o) {
+// Exact router logits of one token against NR router rows (one wave; f32
+// products are exact in f64, each row's sum is f64 in column order), rounded
+// once to f32.  The router input is x itself or, with NORM, the RMSNorm output
+// (x * scale) * nw as k_rms_norm writes it.  Each step loads two 256-column
+// chunks of x and of every row before any arithmetic (no branch between the
+// loads: a step past the last chunk reloads it and multiplies it by x = 0,
+// which leaves the f64 sums' bits unchanged, as they are never -0).
+template <int NR, bool NORM>
+__device__ __forceinline__ void exact_dots(const float* const (&w)[NR], const float* xr, int H, int lane,
+                                           float (&r)[NR], const float* nw, float scale) {
 #pragma clang fp contract(off)
-    const f32x4 v = *(const f32x4*)(xr + o);
-    if (!nw) return v;
-    const f32x4 w = *(const f32x4*)(nw + o);
-    return f32x4{(v.x * scale) * w.x, (v.y * scale) * w.y, (v.z * scale) * w.z, (v.w * scale) * w.w};
-}
-
-__device__ __forceinline__ void exact_dot2(const float* w0, const float* w1, const float* xr, int H, int lane,
-                                           float& r0, float& r1, const float* nw = nullptr, float scale = 1.0f) {
-    double a0 = 0.0, a1 = 0.0;
-    const int nch = H >> 8;
-    int c = 0;
-    for (; c + 4 <= nch; c += 4) {
-        f32x4 xv[4], v0[4], v1[4];
+    double acc[NR];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int o = (c + i) * 256 + 4 * lane;
-            xv[i] = router_in4(xr, nw, scale, o);
-            v0[i] = *(const f32x4*)(w0 + o);
-            v1[i] = *(const f32x4*)(w1 + o);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { a0 = dot4_f64(v0[i], xv[i], a0); a1 = dot4_f64(v1[i], xv[i], a1); }
-    }
-    for (; c < nch; ++c) {
-        const int o = c * 256 + 4 * lane;
-        const f32x4 xv = router_in4(xr, nw, scale, o);
-        a0 = dot4_f64(*(const f32x4*)(w0 + o), xv, a0);
-        a1 = dot4_f64(*(const f32x4*)(w1 + o), xv, a1);
-    }
-    r0 = (float)wave_sum_f64(a0);
-    r1 = (float)wave_sum_f64(a1);
-}
-
-// The same dots for four rows at once (x read once per four rows), each row in
-// the same order as exact_dot2 (so the same bits), two 256-column chunks per step.
-__device__ __forceinline__ void exact_dot4(const float* const (&w)[4], const float* xr, int H, int lane,
-                                           float (&r)[4], const float* nw = nullptr, float scale = 1.0f) {
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int k = 0; k < NR; ++k) acc[k] = 0.0;
     const int nch = H >> 8;
     for (int c = 0; c < nch; c += 2) {
-        f32x4 xv[2], v[4][2];
+        f32x4 xv[2], nv[2], v[NR][2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int o = min(c + i, nch - 1) * 256 + 4 * lane;
-            xv[i] = router_in4(xr, nw, scale, o);
+            xv[i] = *(const f32x4*)(xr + o);
+            if (NORM) nv[i] = *(const f32x4*)(nw + o);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[k][i] = *(const f32x4*)(w[k] + o);
+            for (int k = 0; k < NR; ++k) v[k][i] = *(const f32x4*)(w[k] + o);
         }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the step in flight before the arithmetic
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            if (c + i < nch)
+            if (NORM)
+                xv[i] = f32x4{(xv[i].x * scale) * nv[i].x, (xv[i].y * scale) * nv[i].y, (xv[i].z * scale) * nv[i].z,
+                              (xv[i].w * scale) * nv[i].w};
+        if (c + 1 >= nch) xv[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int k = 0; k < 4; ++k) acc[k] = dot4_f64(v[k][i], xv[i], acc[k]);
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int k = 0; k < NR; ++k) acc[k] = dot4_f64(v[k][i], xv[i], acc[k]);
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) r[k] = (float)wave_sum_f64(acc[k]);
+    for (int k = 0; k < NR; ++k) r[k] = (float)wave_sum_f64(acc[k]);
 }
 
 // Selection keys: the float's bits mapped to an unsigned order (negative values
@@ -790,7 +767,7 @@ __device__ void topk_one_token(const TopkArgs& a, int t, int lane, int32_t* s_id
 // expert with L~ + d < thr is strictly below the K-th selected value and
 // cannot be selected (whatever the tie rule).  The rest are recomputed
 // exactly and ranked as on the exact path; the selection is identical.
-template <int EPL>
+template <int EPL, bool NORM>
 __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s_idx_row, float* s_val_row,
                                   double* s_ex_row) {
     const float* l = a.logits + (uint64_t)t * (a.E + 1);
@@ -827,11 +804,12 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
         if (removed >= a.K) { thr = mx; break; }
     }
     // exact logits of the candidates and of the shared gate: one queue over
-    // every group, four rows per pass, a remainder of one or two in a last pass
+    // every group, eight rows per pass, then four, then two (as the registers
+    // allow: eight up to 256 experts, four up to 512)
     const float* xr = a.x + (uint64_t)t * a.H;
     // prefill with the pre-MoE RMSNorm on the fly: x is the residual row
     const float* nw = a.norm_w;
-    const float xscale = nw ? a.x_scale[t] : 1.0f;
+    const float xscale = NORM ? a.x_scale[t] : 1.0f;
     float v[EPL];
     int id[EPL];
     uint64_t mk[EPL];
@@ -864,7 +842,21 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
         for (int i = 0; i < EPL; ++i)
             if (g == i && lane == b) v[i] = r;
     };
-    for (; n >= 3; n -= 4) {
+    // eight rows per pass where the registers allow (up to 256 experts)
+    for (; EPL <= 4 && n >= 7; n -= 8) {
+        int g[8], b[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pop(g[k], b[k]);
+        const float* w[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) w[k] = row(g[k] < 0 ? g[0] : g[k], g[k] < 0 ? b[0] : b[k]);
+        float r[8];
+        exact_dots<8, NORM>(w, xr, a.H, lane, r, nw, xscale);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (g[k] >= 0) put(g[k], b[k], r[k]);
+    }
+    for (; EPL <= 8 && n >= 3; n -= 4) {
         int g[4], b[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) pop(g[k], b[k]);
@@ -872,38 +864,50 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
 #pragma unroll
         for (int k = 0; k < 4; ++k) w[k] = row(g[k] < 0 ? g[0] : g[k], g[k] < 0 ? b[0] : b[k]);
         float r[4];
-        exact_dot4(w, xr, a.H, lane, r, nw, xscale);
+        exact_dots<4, NORM>(w, xr, a.H, lane, r, nw, xscale);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             if (g[k] >= 0) put(g[k], b[k], r[k]);
     }
-    if (n > 0) {
+    for (; n > 0; n -= 2) {
         int g0, b0, g1, b1;
         pop(g0, b0);
         pop(g1, b1);
         if (g1 < 0) { g1 = g0; b1 = b0; }
-        float r0, r1;
-        exact_dot2(row(g0, b0), row(g1, b1), xr, a.H, lane, r0, r1, nw, xscale);
-        put(g0, b0, r0);
-        put(g1, b1, r1);
+        const float* w[2] = {row(g0, b0), row(g1, b1)};
+        float r[2];
+        exact_dots<2, NORM>(w, xr, a.H, lane, r, nw, xscale);
+        put(g0, b0, r[0]);
+        put(g1, b1, r[1]);
     }
     select_softmax<EPL>(a, t, lane, v, id, sg, s_idx_row, s_val_row, s_ex_row, nullptr);
 }
 
 // s_sg (deferred softmax only): where the shared-gate logit is kept for token_softmax.
-template <bool REFINE>
+// EPL: experts per lane (1, 2, 4, 8 or 16; 0: chosen here from E).
+template <bool REFINE, int EPL = 0>
 __device__ __forceinline__ void topk_dispatch(const TopkArgs& a, int t, int lane, int32_t* s_idx_row,
                                               float* s_val_row, double* s_ex_row, float* s_sg = nullptr) {
-    const int epl = (a.E + 63) >> 6;
-#define QMOE_TOPK_CASE(N)                                                   \
-    if (REFINE) topk_refine_token<N>(a, t, lane, s_idx_row, s_val_row, s_ex_row); \
-    else topk_one_token<N>(a, t, lane, s_idx_row, s_val_row, s_ex_row, s_sg);
-    if (epl <= 1) { QMOE_TOPK_CASE(1) }
-    else if (epl <= 2) { QMOE_TOPK_CASE(2) }
-    else if (epl <= 4) { QMOE_TOPK_CASE(4) }
-    else if (epl <= 8) { QMOE_TOPK_CASE(8) }
-    else { QMOE_TOPK_CASE(16) }
-#undef QMOE_TOPK_CASE
+    if constexpr (EPL > 0) {
+        if (REFINE) {
+            if (a.norm_w) topk_refine_token<EPL, true>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+            else topk_refine_token<EPL, false>(a, t, lane, s_idx_row, s_val_row, s_ex_row);
+        }
+        else topk_one_token<EPL>(a, t, lane, s_idx_row, s_val_row, s_ex_row, s_sg);
+    } else {
+        const int epl = (a.E + 63) >> 6;
+        if (epl <= 1) topk_dispatch<REFINE, 1>(a, t, lane, s_idx_row, s_val_row, s_ex_row, s_sg);
+        else if (epl <= 2) topk_dispatch<REFINE, 2>(a, t, lane, s_idx_row, s_val_row, s_ex_row, s_sg);
+        else if (epl <= 4) topk_dispatch<REFINE, 4>(a, t, lane, s_idx_row, s_val_row, s_ex_row, s_sg);
+        else if (epl <= 8) topk_dispatch<REFINE, 8>(a, t, lane, s_idx_row, s_val_row, s_ex_row, s_sg);
+        else topk_dispatch<REFINE, 16>(a, t, lane, s_idx_row, s_val_row, s_ex_row, s_sg);
+    }
+}
+
+// Experts per lane of a top-k over E experts: 1, 2, 4, 8 or 16.
+static inline int topk_epl(int E) {
+    const int epl = (E + 63) >> 6;
+    return epl <= 1 ? 1 : epl <= 2 ? 2 : epl <= 4 ? 4 : epl <= 8 ? 8 : 16;
 }
 
 __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint32_t* first_token, int32_t* s_off,
@@ -914,9 +918,10 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
 // the block's assignments to the same expert (token order).  MERGE (blocks x
 // experts <= kTopkMergeMax): those are written through, and the last block to
 // finish (a counter in sync) runs the expert scan and the stable scatter that
-// k_scan and k_scatter run otherwise, with the same results.
-template <bool REFINE, bool MERGE = false>
-__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, int32_t* sync = nullptr) {
+// k_scan and k_scatter run otherwise, with the same results.  EPL: experts per
+// lane (an instance per expert count class, so each gets its own registers).
+template <bool REFINE, bool MERGE, int EPL>
+__global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, int32_t* sync) {
     __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
     __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
     __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
@@ -928,7 +933,7 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, i
     for (int e = threadIdx.x; e < a.E; e += blockDim.x) s_mask[e] = 0;
     __syncthreads();
     if (wave < ntok) {
-        topk_dispatch<REFINE>(a, t0 + wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
+        topk_dispatch<REFINE, EPL>(a, t0 + wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
         if (lane < a.K) atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
     }
     __syncthreads();
@@ -1551,6 +1556,23 @@ bool route_decode_fused(const LayerDesc& L, int T) {
 // The decode router instance for nsw slabs per wave; the routing-table launch
 // for shared-expert type swt (0 none, 1 Q4_0, 2 Q8_0) and the shared blocks'
 // lanes per row (16 for H <= 1024, 32 for H <= 2048, else 64).
+template <bool REFINE, bool MERGE>
+static const void* topk_kernel(int E) {
+    switch (topk_epl(E)) {
+        case 1: return (const void*)k_topk<REFINE, MERGE, 1>;
+        case 2: return (const void*)k_topk<REFINE, MERGE, 2>;
+        case 4: return (const void*)k_topk<REFINE, MERGE, 4>;
+        case 8: return (const void*)k_topk<REFINE, MERGE, 8>;
+        default: return (const void*)k_topk<REFINE, MERGE, 16>;
+    }
+}
+
+static hipError_t launch_topk(const void* kern, TopkArgs& ta, int32_t* sync, hipStream_t stream) {
+    void* args[] = {&ta, &sync};
+    hipError_t err = hipLaunchKernel(kern, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), args, 0, stream);
+    return err != hipSuccess ? err : hipGetLastError();
+}
+
 static const void* route_decode_kernel(int nsw, bool norm) {
     static_assert(kRdParts == 4, "slabs per wave: 1 at H <= 1024, 2 at H <= 2048, 3-4 at H <= 4096");
     if (norm) return nsw == 1 ? (const void*)k_route_decode<1, true> : nsw == 2 ? (const void*)k_route_decode<2, true> : nullptr;
@@ -1681,8 +1703,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
             return err;
         hipLaunchKernelGGL(k_router_mfma, dim3(ma.n_tiles), dim3(256), lds, stream, ma);
         if ((err = hipGetLastError()) != hipSuccess) return err;
-        hipLaunchKernelGGL(k_topk<true>, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
+        if ((err = launch_topk(topk_kernel<true, false>(L.E), ta, nullptr, stream)) != hipSuccess) return err;
         if (dbg.approx &&
             (err = hipMemcpy2DAsync(dbg.approx, L.E * sizeof(float), ws.logits, (L.E + 1) * sizeof(float),
                                     L.E * sizeof(float), T, hipMemcpyDeviceToDevice, stream)) != hipSuccess)
@@ -1752,12 +1773,9 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         ta.quant_rows = 0;
         if (ta.nblk * L.E <= kTopkMergeMax) {
             // the last top-k block runs the expert scan and the scatter: no more launches
-            hipLaunchKernelGGL((k_topk<false, true>), dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta,
-                               ws.sync);
-            return hipGetLastError();
+            return launch_topk(topk_kernel<false, true>(L.E), ta, ws.sync, stream);
         }
-        hipLaunchKernelGGL((k_topk<false>), dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), 0, stream, ta, nullptr);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
+        if ((err = launch_topk(topk_kernel<false, false>(L.E), ta, nullptr, stream)) != hipSuccess) return err;
     }
     hipLaunchKernelGGL(k_scan, dim3((L.E + 63) / 64), dim3(1024), 0, stream, ta, ws.sync);
     if ((err = hipGetLastError()) != hipSuccess) return err;
