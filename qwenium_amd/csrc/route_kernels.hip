@@ -1077,19 +1077,82 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
 
 // Whole routing for T <= kTopkTokensPerBlock in ONE block of 1024 threads,
 // everything in LDS: top-k per token (one wave each), per-expert token masks,
-// counts, offsets, active slots (with the token of each slot's first row =
-// lowest mask bit), stable scatter (rank = earlier tokens in the expert's
-// mask) and tiles.  Reads the exact logits from a.logits.
+// then wave 0 alone (no further barrier): counts, offsets, active slots (with
+// the token of each slot's first row = lowest mask bit), tiles, and the stable
+// scatter (rank = earlier tokens in the expert's mask), while the other waves
+// run the deferred softmax.  Reads the exact logits from a.logits.
 struct SmallRouteLds {
     int32_t idx[kTopkTokensPerBlock][kMaxTopK];
     float val[kTopkTokensPerBlock][kMaxTopK];
     double ex[kTopkTokensPerBlock][kMaxTopK + 1];
     float sg[kTopkTokensPerBlock];  // shared-gate logits (deferred softmax)
     uint32_t mask[1024];
-    int32_t cnt[1024];
     int32_t off[1024];
-    int32_t misc[64];
 };
+
+// The expert scans of scan_experts (same tables) for the masks of at most 32
+// tokens, by one wave: lane l takes experts l * epl .. l * epl + epl - 1 in
+// order, three wave scans give each lane its bases.  Writes the offsets to
+// s_off as well.
+static_assert(kTopkTokensPerBlock <= 32, "token masks are 32-bit");
+__device__ void scan_experts_wave(const TopkArgs& a, const uint32_t* mask, int32_t* s_off) {
+    const int lane = threadIdx.x & 63;
+    const int epl = (a.E + 63) >> 6;
+    const int e0 = lane * epl, e1 = min(a.E, e0 + epl);
+    int c = 0, ac = 0, tc = 0;
+    for (int e = e0; e < e1; ++e) {
+        const int n = __builtin_popcount(mask[e]);
+        c += n;
+        ac += n > 0 ? 1 : 0;
+        tc += (n + kMfmaTileM - 1) / kMfmaTileM;
+    }
+    const int ic = wave_incl_scan_i32(c), ia = wave_incl_scan_i32(ac), it = wave_incl_scan_i32(tc);
+    int off = ic - c, slot = ia - ac, tile = it - tc;
+    for (int e = e0; e < e1; ++e) {
+        const uint32_t m = mask[e];
+        const int n = __builtin_popcount(m);
+        a.offsets[e] = off;
+        s_off[e] = off;
+        if (n > 0) {
+            if (a.expert_counts) atomicAdd(a.expert_counts + e, (unsigned long long)n);
+            a.active[slot] = e;
+            a.expert_slot[e] = slot;
+            a.slot_info[slot] = make_int4(e, off, n, (int)__builtin_ctz(m));
+            if (a.dslots) a.dslots[slot] = make_int4(e, off, n, (int)m);
+            const int nt = (n + kMfmaTileM - 1) / kMfmaTileM;
+            for (int i = 0; i < nt && tile + i < a.max_tiles; ++i)
+                a.tiles[tile + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, n - i * kMfmaTileM), 0);
+            tile += nt;
+            ++slot;
+        }
+        off += n;
+    }
+    const int A = a.T * a.K;
+    const int n_routed = __builtin_amdgcn_readlane(ia, 63);
+    if (a.dslots) {
+        // decode slot list: the active routed experts, then "none" up to the
+        // most a forward can have (the shared expert is not in it)
+        const int max_v = min(a.E, A);
+        for (int i = n_routed + lane; i < max_v; i += 64) a.dslots[i] = make_int4(-1, 0, 0, 0);
+    }
+    if (lane == 0) {
+        int n_act = n_routed;
+        int n_tiles = __builtin_amdgcn_readlane(it, 63);
+        a.offsets[a.E] = A;
+        a.offsets[a.E + 1] = A + a.S * a.T;
+        if (a.S) {
+            a.active[n_act] = a.E;
+            a.slot_info[n_act] = make_int4(a.E, A, a.T, 0);
+            n_act++;
+            const int ntt = (a.T + kMfmaTileM - 1) / kMfmaTileM;
+            for (int i = 0; i < ntt && n_tiles < a.max_tiles; ++i)
+                a.tiles[n_tiles++] = make_int4(a.E, A + i * kMfmaTileM, min(kMfmaTileM, a.T - i * kMfmaTileM), 0);
+        }
+        a.counters[0] = n_act;
+        a.counters[1] = n_tiles;
+        a.counters[kCounterFix] = 0;
+    }
+}
 
 __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1101,28 +1164,25 @@ __device__ void route_small_body(const TopkArgs& a, SmallRouteLds& L) {
         if (lane < a.K) atomicOr(&L.mask[L.idx[wave][lane]], 1u << wave);
     }
     __syncthreads();
-    for (int e = tid; e < a.E; e += blockDim.x) L.cnt[e] = __builtin_popcount(L.mask[e]);
-    __syncthreads();
-    scan_experts(a, L.cnt, L.mask, L.off, L.misc);
-    __syncthreads();
-    for (int asg = tid; asg < A; asg += blockDim.x) {
-        const int t = asg / a.K, j = asg % a.K;
-        const int ex = L.idx[t][j];
-        const int p = L.off[ex] + __builtin_popcount(L.mask[ex] & ((1u << t) - 1u));
-        a.rows[p] = asg;
-        a.row_token[p] = t;
-        a.pos[asg] = p;
-    }
-    if (a.S && tid < a.T) {
-        a.rows[A + tid] = -1;
-        a.row_token[A + tid] = tid;
-    }
-    if (a.defer_softmax) {
-        // the softmax of every token, on the waves the scatter above leaves idle:
-        // off the path from the top-k to the end of the routing
-        const int w0 = (A + 63) >> 6 < 16 ? (A + 63) >> 6 : 0;
-        for (int t = wave - w0; t >= 0 && t < a.T; t += 16 - w0)
-            token_softmax(a, t, lane, L.val[t], L.ex[t], L.sg[t]);
+    if (wave == 0) {
+        scan_experts_wave(a, L.mask, L.off);
+        wave_lds_sync();  // the offsets written by the other lanes
+        for (int asg = lane; asg < A; asg += 64) {
+            const int t = asg / a.K, j = asg % a.K;
+            const int ex = L.idx[t][j];
+            const int p = L.off[ex] + __builtin_popcount(L.mask[ex] & ((1u << t) - 1u));
+            a.rows[p] = asg;
+            a.row_token[p] = t;
+            a.pos[asg] = p;
+        }
+        if (a.S && lane < a.T) {
+            a.rows[A + lane] = -1;
+            a.row_token[A + lane] = lane;
+        }
+    } else if (a.defer_softmax) {
+        // the softmax of every token on the other waves: off the path from the
+        // top-k to the end of the routing
+        for (int t = wave - 1; t < a.T; t += 15) token_softmax(a, t, lane, L.val[t], L.ex[t], L.sg[t]);
     }
 }
 
