@@ -13,9 +13,11 @@
 //   scale: one v_mfma_f32_32x32x16_f16 outer product dx (rows) x dw (columns),
 //         exact in f32 (two 11-bit significands);
 // then one FMA per output, acc += scale * isum, in f32 (as ggml's CPU dot
-// accumulates its block terms in f32).  VALU and MFMA instructions do not
-// overlap on this pipe (measured), so the work per tile is 3 MFMAs + ~24 VALU
-// instructions, the weight unpack shared by four row tiles.
+// accumulates its block terms in f32).  The work per tile is 3 MFMAs (96
+// cycles) + ~21 VALU instructions (the 16 FMAs and the weight unpack shared by
+// four row tiles); the two pipes overlap only partly (about four independent
+// VALU instructions hide under each MFMA), so the loop runs at ~160 SIMD-cycles
+// per tile and block with three waves per SIMD.
 //
 // Tiles come from the routing: tiles[i] = {expert, first row, rows <= 128}.
 // A workgroup (4 waves) computes 128 rows x 128 weight columns of one tile;
@@ -23,8 +25,10 @@
 //   gate/up: wave w takes gate (w < 2) or up (w >= 2) rows f = 64 y + 32 (w & 1) + lane % 32;
 //   down:    output columns n = 128 y + 32 w + lane % 32.
 // Activation rows (f16 quants and f16 block scales) are staged in LDS by
-// direct global->LDS loads, 128 k values per chunk, double buffered; weights
-// are read per lane straight from the GGUF blocks, one chunk ahead.
+// direct global->LDS loads, kF16ChunkK (64) k values per chunk, double
+// buffered; weights are read per lane one chunk ahead, from the chunk-major
+// copies of the expert matrices when the layer has them (each lane's block pair
+// of a chunk next to its neighbours'), else straight from the GGUF rows.
 //
 // Gate/up epilogue: h = act(g) * u in f32 and the Q8_0 of h per 32-wide block
 // (ggml's activation quantizer: d = fp16(amax / 127), q = rint(h * 127 / amax)),
