@@ -14,7 +14,10 @@
 namespace qmoe {
 
 // ---------------------------------------------------------------------------
-// R1: router logits (one wave per router row, all tokens) + activation quant
+// R1: exact router logits of every token, for the debug copy when the batched
+// router runs (its own logits are approximate); the forward paths compute
+// theirs in k_route_decode (up to the batched router's threshold) or refine
+// the batched router's candidates in k_topk
 // ---------------------------------------------------------------------------
 struct RouterArgs {
     const float* x;         // [T][H] router input
@@ -29,11 +32,11 @@ struct RouterArgs {
     float2* xq_ds;          // [T][H/32]
 };
 
-// Router GEMV for small token counts: one 256-thread block per router row
-// (row E is the shared-expert gate vector).  Wave w owns float4 chunks
-// c = w + 4i of the row (chunk = 64 float4 = 256 values); every load is
-// unconditional (clamped index, zeroed weight) so a token chunk's loads issue
-// back to back.  Products are exact in f64; the sum is exact-order-free f64.
+// One 256-thread block per router row (row E is the shared-expert gate
+// vector).  Wave w owns float4 chunks c = w + 4i of the row (chunk = 64 float4
+// = 256 values); every load is unconditional (clamped index, zeroed weight) so
+// a token chunk's loads issue back to back.  Products are exact in f64, summed
+// in f64 and rounded once to f32.
 constexpr int kRouterTokChunk = 8;
 
 template <int NCH>
