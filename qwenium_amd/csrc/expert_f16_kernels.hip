@@ -230,6 +230,11 @@ __device__ __forceinline__ uint32_t block_quants<kTypeQ8_0>(const RawPair<kTypeQ
     return (kh ? r.w[5] : r.w[6]) >> 16;
 }
 
+// fp16 bit patterns: -0 as +0, and the next value up of a finite one (toward
+// zero for negatives; -min subnormal's next is 0).
+__device__ __forceinline__ uint32_t fp16_canon(uint32_t h) { return h == 0x8000u ? 0u : h; }
+__device__ __forceinline__ uint32_t fp16_next_up(uint32_t h) { return fp16_canon((h & 0x8000u) ? h - 1u : h + 1u); }
+
 __device__ __forceinline__ v16f mfma16(v8h a, v8h b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -276,23 +281,40 @@ __device__ __forceinline__ void h_block(const F16Args& a, f32x4* pg, f32x4* pu, 
         for (int k = 0; k < 4; ++k) {
             const float gv = g4[k], uv = u4[k];
             const float ag = __builtin_fabsf(gv), au = __builtin_fabsf(uv);
-            const float av = act_f32<ACT>(a.gelu_tab, gv);
+            // GeGLU: the table entries at fp16(g) and at the ends of g's error
+            // range, loaded unconditionally (16-bit indices) so that no load waits
+            // behind a branch
+            float av, tl = 0.0f, th = 0.0f, lo = 0.0f, hi = 0.0f, eg = 0.0f;
+            uint32_t l16 = 0, h16 = 0;
+            if (ACT == kActGeluTanh) {
+                eg = a.acc_err * fmaxf(ag, rg);
+                lo = gv - eg;
+                hi = gv + eg;
+                l16 = f32_to_fp16(lo) & 0xffffu;
+                h16 = f32_to_fp16(hi) & 0xffffu;
+                const float tv = fp16_to_f32(a.gelu_tab[f32_to_fp16(gv) & 0xffffu]);
+                tl = fp16_to_f32(a.gelu_tab[l16]);
+                th = fp16_to_f32(a.gelu_tab[h16]);
+                av = gv <= -10.0f ? 0.0f : (gv >= 10.0f ? gv : tv);
+            } else {
+                av = act_f32<ACT>(a.gelu_tab, gv);
+            }
             const float h = av * uv;
             const float ah = __builtin_fabsf(h);
             // g and u are within eg = acc_err max(|g|, rg) and eu = acc_err
             // max(|u|, ru); the activation's error: SiLU's from g's error through
-            // its slope; GeGLU's table entry is exact for a settled fp16(g) (and
-            // |g| >= 10 threshold), else it may be any entry of the range, within
-            // the slope bound of it
+            // its slope.  GeGLU's: at g >= 10 the activation is g itself (error
+            // eg), at g <= -10 it is 0; between, it is the table entry at fp16(g),
+            // and the exact g's fp16 lies in [fp16(g - eg), fp16(g + eg)]: one
+            // value leaves the entry exact, two adjacent values leave it one of
+            // two entries (within their difference), a wider range or one
+            // crossing +-10 is bounded through the slope
             float eh;
             if (ACT == kActGeluTanh) {
-                const float eg = a.acc_err * fmaxf(ag, rg);
-                const float lo = gv - eg, hi = gv + eg;
-                const uint32_t l16 = f32_to_fp16(lo), h16 = f32_to_fp16(hi);
-                const float eav =
-                    (l16 == h16 && (lo <= -10.0f) == (hi <= -10.0f) && (lo >= 10.0f) == (hi >= 10.0f))
-                        ? 0.0f
-                        : kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
+                const uint32_t cl = fp16_canon(l16), ch = fp16_canon(h16);
+                const bool near = lo > -10.0f && hi < 10.0f && (cl == ch || fp16_next_up(cl) == ch);
+                const float wide = kActSlope * (fp16_to_f32(h16) - fp16_to_f32(l16) + 2.0f * eg) + 2e-3f * __builtin_fabsf(av);
+                const float eav = lo >= 10.0f ? eg : (hi <= -10.0f ? 0.0f : (near ? __builtin_fabsf(th - tl) : wide));
                 eh = au * eav + __builtin_fabsf(av) * (a.acc_err * fmaxf(au, ru));
             } else {
                 // |u| kActSlope eg + |av| eu
