@@ -146,7 +146,8 @@ size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* ba
     ws.topk_w = (float*)take(A * sizeof(float));
     ws.sh_gate = (float*)take((size_t)T * sizeof(float));
     ws.local_rank = (int32_t*)take(A * sizeof(int32_t));
-    ws.hist = (int32_t*)take((size_t)(nblk + 1) * E * sizeof(int32_t));  // + a row of per-expert totals
+    ws.hist = (int32_t*)take((size_t)(nblk + kTotalCopies) * E * sizeof(int32_t));  // + the per-expert totals
+    ws.jslot = (uint64_t*)take((size_t)nblk * E * sizeof(uint64_t));
     ws.offsets = (int32_t*)take((size_t)(E + 2) * sizeof(int32_t));
     ws.rows = (int32_t*)take(R * sizeof(int32_t));
     ws.row_token = (int32_t*)take(R * sizeof(int32_t));
@@ -478,7 +479,7 @@ int qmoe_workspace_create(const qmoe_layer* like, int32_t max_tokens, qmoe_works
         return hip_fail(err, "hipMalloc(workspace)");
     }
     qmoe::workspace_bytes(max_tokens, d.H, d.E, d.K, d.F, &ws->w, base, pad);
-    // the signalling area (the expert scan's finished-workgroup counter) starts at zero
+    // the signalling area (the merged top-k's finished-workgroup counter) starts at zero
     err = hipMemset(ws->w.sync, 0, qmoe::kSyncWords * sizeof(int32_t));
     if (err == hipSuccess) err = hipDeviceSynchronize();
     if (err != hipSuccess) {
@@ -527,11 +528,11 @@ std::mutex g_scratch_mu;
 void* g_scratch[kMaxDevices] = {};
 
 // The device address of this GPU's scratch (dev current), set up on first use.
-// The signalling area (the routing scans' last-workgroup counters) must start
-// at zero: device globals are zero when the code object loads, every scan
-// returns its counter to zero, and a first use on a stream that is not being
-// captured also clears the area with a fill kernel and waits for it, so the
-// array is published only after the clear has run.
+// The signalling area (the merged top-k's last-workgroup counter) must start
+// at zero: device globals are zero when the code object loads, the top-k
+// returns its counter to zero after each use, and a first use on a stream
+// that is not being captured also clears the area with a fill kernel and
+// waits for it, so the array is published only after the clear has run.
 int static_scratch(int dev, hipStream_t stream, void** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (dev < 0 || dev >= kMaxDevices)

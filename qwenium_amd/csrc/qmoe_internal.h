@@ -12,12 +12,14 @@ namespace qmoe {
 // Tokens handled by one top-k block; the per-block histogram granularity of
 // the stable counting sort.
 constexpr int kTopkTokensPerBlock = 16;
-// Cross-block signalling area of a workspace: the expert-count scan's
-// finished-workgroup counter (back to 0 after each scan).
+// Cross-block signalling area of a workspace: the merged top-k's
+// finished-workgroup counter (back to 0 after each use).
 constexpr int kSyncWords = 64;
-constexpr int kSyncScan = 0;
-constexpr int kSyncTopk = 1;  // the merged top-k's finished-workgroup counter
+constexpr int kSyncTopk = 1;
 constexpr int kTopkMergeMax = 4096;  // top-k blocks x experts the merged top-k keeps in LDS
+// Copies of the per-expert totals that the top-k blocks add into (block b into
+// copy b % kTotalCopies: fewer atomics on one address).
+constexpr int kTotalCopies = 8;
 // RMSNorm: 256-column chunks of a row whose sums fit a workgroup's LDS (rows of
 // at most 65536 columns).
 constexpr int kRmsMaxChunks = 256;
@@ -85,7 +87,8 @@ struct Workspace {
     float* topk_w = nullptr;      // [T][K]
     float* sh_gate = nullptr;     // [T]
     int32_t* local_rank = nullptr;  // [T*K]
-    int32_t* hist = nullptr;      // [nblk][E] per top-k block counts -> bases
+    int32_t* hist = nullptr;      // [nblk + kTotalCopies][E] per top-k block counts or token masks, then the totals
+    uint64_t* jslot = nullptr;    // [nblk][E] the slot of each masked token, four bits each
     int32_t* offsets = nullptr;   // [E+2]
     int32_t* rows = nullptr;      // [R] assignment id (t*K+j); shared rows: -1
     int32_t* row_token = nullptr; // [R]
@@ -96,7 +99,7 @@ struct Workspace {
     int4* dslots = nullptr;       // [E+2] decode slot list {expert, first row, rows, token mask}:
                                   // active routed experts, then expert -1 up to min(E, T*K)
     int32_t* counters = nullptr;  // [kCounters] n_active, n_tiles, ...
-    int32_t* sync = nullptr;      // [kSyncWords] zeroed at creation: the scan's finished-workgroup counter
+    int32_t* sync = nullptr;      // [kSyncWords] zeroed at creation: the merged top-k's finished-workgroup counter
     int4* tiles = nullptr;        // [max tiles] {expert, row0, nrows, 0}
     float2* gubuf = nullptr;      // [R][F] (gate, up) projections
     int8_t* hq_qs = nullptr;      // [R][F]   Q8_0 quants of h = silu(g)*u

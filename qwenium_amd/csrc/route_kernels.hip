@@ -261,6 +261,7 @@ struct RouterMfmaArgs {
     float eps;
     const double* x_ssq;    // [T][ssq_parts(H)] or null
     float* x_scale;         // [T]
+    int32_t* ecount;        // [kTotalCopies][E] per-expert totals, zeroed here for the top-k blocks to add into
 };
 
 // bf16 split of 8 floats (round to nearest both times): hi = bf16(v), lo = bf16(v - hi);
@@ -366,7 +367,8 @@ __device__ float quant_split_row(const float* xr, int H, int lane, _Float16* q, 
 
 // Batched-router preparation, one wave per row: blocks [0, ceil(T/4)) take
 // tokens (the experts' Q8_0 of x, the router input's split and norm), the
-// rest take router rows (split and norm).
+// rest take router rows (split and norm); the first of those also zeroes the
+// per-expert totals that the top-k blocks add into.
 __global__ __launch_bounds__(256) void k_router_prep(RouterMfmaArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ntb = (a.T + 3) / 4;
@@ -397,6 +399,8 @@ __global__ __launch_bounds__(256) void k_router_prep(RouterMfmaArgs a) {
         }
         return;
     }
+    if ((int)blockIdx.x == ntb)
+        for (int i = threadIdx.x; i < kTotalCopies * a.E; i += 256) a.ecount[i] = 0;
     const int e = ((int)blockIdx.x - ntb) * 4 + wave;
     if (e >= a.E) return;
     const float n = split_row(a.w + (uint64_t)e * a.ld, a.H, lane, a.rw + (uint64_t)e * a.H,
@@ -528,7 +532,8 @@ struct TopkArgs {
     float* topk_w;        // [T][K]
     float* sh_gate;       // [T]
     int32_t* local_rank;  // [T*K]
-    int32_t* hist;        // [nblk][E]
+    int32_t* hist;        // [nblk + kTotalCopies][E] per top-k block counts (merged top-k) or token masks, then the totals
+    uint64_t* jslot;      // [nblk][E] the masked tokens' slots j, four bits each (top_k <= 16)
     int32_t* offsets;     // [E+2]
     int32_t* rows;        // [R]
     int32_t* row_token;   // [R]
@@ -917,48 +922,67 @@ __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint
                              int32_t* s_misc);
 
 // blockDim = 64 * kTopkTokensPerBlock: one wave per token.  Writes the
-// selection, the per-block expert histogram and each assignment's rank among
-// the block's assignments to the same expert (token order).  MERGE (blocks x
-// experts <= kTopkMergeMax): those are written through, and the last block to
-// finish (a counter in sync) runs the expert scan and the stable scatter that
-// k_scan and k_scatter run otherwise, with the same results.  EPL: experts per
-// lane (an instance per expert count class, so each gets its own registers).
+// selection and, per expert, the mask of the block's tokens that chose it.
+// MERGE (blocks x experts <= kTopkMergeMax): the per-block counts and each
+// assignment's rank among the block's assignments to the same expert (token
+// order) are written through, and the last block to finish (a counter in sync)
+// runs the expert scan and the stable scatter.  Otherwise the masks go to hist
+// (with the slot j of each token whose mask bit is set, four bits each, in
+// jslot when top_k <= 16) and the block adds its counts into the per-expert
+// totals (hist's rows from nblk on, zeroed by the router launch) for k_lists.  EPL:
+// experts per lane (an instance per expert count class, so each gets its own
+// registers).
 template <bool REFINE, bool MERGE, int EPL>
 __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, int32_t* sync) {
     __shared__ int32_t s_idx[kTopkTokensPerBlock][kMaxTopK];
     __shared__ float s_val[kTopkTokensPerBlock][kMaxTopK];
     __shared__ double s_ex[kTopkTokensPerBlock][kMaxTopK + 1];
     __shared__ uint32_t s_mask[1024];  // per expert: bit ti set if block token ti chose it
+    __shared__ uint64_t s_jslot[MERGE ? 1 : 1024];  // per expert: nibble ti = the slot j of token ti
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kTopkTokensPerBlock;
     const int ntok = min(kTopkTokensPerBlock, a.T - t0);
-    for (int e = threadIdx.x; e < a.E; e += blockDim.x) s_mask[e] = 0;
+    const bool jslot = !MERGE && a.K <= 16;
+    for (int e = threadIdx.x; e < a.E; e += blockDim.x) {
+        s_mask[e] = 0;
+        if (jslot) s_jslot[e] = 0;
+    }
     __syncthreads();
     if (wave < ntok) {
         topk_dispatch<REFINE, EPL>(a, t0 + wave, lane, s_idx[wave], s_val[wave], s_ex[wave]);
-        if (lane < a.K) atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
+        if (lane < a.K) {
+            atomicOr(&s_mask[s_idx[wave][lane]], 1u << wave);
+            if (jslot) atomicOr((unsigned long long*)&s_jslot[s_idx[wave][lane]], (unsigned long long)lane << (4 * wave));
+        }
     }
     __syncthreads();
-    for (int asg = threadIdx.x; asg < ntok * a.K; asg += blockDim.x) {
-        const int ti = asg / a.K;
-        const int j = asg % a.K;
-        const int ex = s_idx[ti][j];
-        const int rank = __builtin_popcount(s_mask[ex] & ((1u << ti) - 1u));
-        const uint64_t i = (uint64_t)(t0 + ti) * a.K + j;
-        if constexpr (MERGE) {  // written through: the last block reads them
+    if constexpr (MERGE) {
+        for (int asg = threadIdx.x; asg < ntok * a.K; asg += blockDim.x) {
+            const int ti = asg / a.K;
+            const int j = asg % a.K;
+            const int ex = s_idx[ti][j];
+            const int rank = __builtin_popcount(s_mask[ex] & ((1u << ti) - 1u));
+            const uint64_t i = (uint64_t)(t0 + ti) * a.K + j;
+            // written through: the last block reads them
             __hip_atomic_store(a.local_rank + i, rank, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(a.topk_idx + i, ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            a.local_rank[i] = rank;
         }
     }
     for (int e = threadIdx.x; e < a.E; e += blockDim.x) {
-        const int cnt = __builtin_popcount(s_mask[e]);
-        if constexpr (MERGE)
-            __hip_atomic_store(a.hist + (uint64_t)blockIdx.x * a.E + e, cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-            a.hist[(uint64_t)blockIdx.x * a.E + e] = cnt;
+        const uint32_t m = s_mask[e];
+        const uint64_t h = (uint64_t)blockIdx.x * a.E + e;
+        if constexpr (MERGE) {
+            __hip_atomic_store(a.hist + h, (int)__builtin_popcount(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            a.hist[h] = (int32_t)m;
+            if (m) {
+                if (jslot) a.jslot[h] = s_jslot[e];
+                __hip_atomic_fetch_add(a.hist + ((uint64_t)a.nblk + blockIdx.x % kTotalCopies) * a.E + e,
+                                       (int)__builtin_popcount(m),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
     }
     if constexpr (MERGE) {
         __shared__ int32_t s_base[kTopkMergeMax];  // [block][expert]: the block's first rank in the expert's rows
@@ -1334,6 +1358,8 @@ __global__ __launch_bounds__(1024) void k_route_decode(TopkArgs a0, float* logit
     const int nbr = (a0.E + a0.S + RR - 1) / RR;
     const int gi = (int)blockIdx.x / nbr, rb = (int)blockIdx.x - gi * nbr;
     const int tb = gi * kTopkTokensPerBlock;
+    if (a0.quant_rows && blockIdx.x == 0)  // the per-expert totals that the top-k blocks add into
+        for (int i = tid; i < kTotalCopies * a0.E; i += 1024) a0.hist[(uint64_t)a0.nblk * a0.E + i] = 0;
     TopkArgs a = a0;  // this group's tokens
     a.T = min(kTopkTokensPerBlock, a0.T - tb);
     a.x = a0.x + (uint64_t)tb * a0.H;
@@ -1524,87 +1550,152 @@ __global__ __launch_bounds__(1024) void k_route_decode_tables(TopkArgs a, int8_t
     }
 }
 
-// Per-expert exclusive prefix of the per-block histograms (in place: hist
-// becomes each block's base inside its expert), then the expert scans.  One
-// workgroup per 64 experts (lane = expert), its 16 waves each owning a
-// contiguous range of blocks (all of a range's loads in flight at once); the
-// workgroups publish their experts' totals (row nblk of hist, written
-// through), and the last one to finish runs the expert scans.
-constexpr int kScanPer = 16;  // blocks per wave and pass (one pass for nblk <= 256, i.e. T <= 4096)
+// The expert lists from the top-k blocks' token masks, one workgroup per
+// expert and one more (index E) for the shared expert's rows and the totals.
+// The top-k blocks added their counts into the per-expert totals, so each
+// workgroup finds its expert's first row, active slot and first tile by
+// summing the totals below it, and none waits for another.  It then scans its
+// column of masks (threads own consecutive blocks) and writes the expert's rows
+// in token order: the same offsets, slots, tiles, rows and positions as
+// scan_experts followed by the stable scatter.
+constexpr int kListThreads = 256;
+constexpr int kListRegs = 4;  // masks per thread held in registers (nblk <= 1024); beyond, loaded twice
 
-__global__ __launch_bounds__(1024) void k_scan(TopkArgs a, int32_t* sync) {
-    __shared__ int32_t s_part[16][64];
-    __shared__ int32_t s_cnt[1024];
-    __shared__ int32_t s_misc[64];
-    __shared__ int s_last;
+__global__ __launch_bounds__(kListThreads) void k_lists(TopkArgs a) {
+    __shared__ int32_t s_red[3][kListThreads / 64];
+    __shared__ int32_t s_wtot[kListThreads / 64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int e = blockIdx.x * 64 + lane;
-    const bool live = e < a.E;
-    const int per = (a.nblk + 15) / 16;
-    const int b0 = min(a.nblk, wave * per), b1 = min(a.nblk, b0 + per);
-    int32_t* col = a.hist + min(e, a.E - 1);
-    int sum = 0;
-    for (int bb = b0; bb < b1; bb += kScanPer) {
-        int vals[kScanPer];
+    const int e = (int)blockIdx.x;
+    const bool routed = e < a.E;
+    const uint32_t* masks = (const uint32_t*)a.hist;
+    const int32_t* total = a.hist + (uint64_t)a.nblk * a.E;
+    const bool jslot = a.K <= 16;
+    const int per = (a.nblk + kListThreads - 1) / kListThreads;
+    const int b0 = min(a.nblk, tid * per), b1 = min(a.nblk, b0 + per);
+    // this thread's masks (and slots), issued with the totals' loads
+    uint32_t mk[kListRegs];
+    uint64_t js[kListRegs];
 #pragma unroll
-        for (int i = 0; i < kScanPer; ++i) vals[i] = col[(uint32_t)min(bb + i, b1 - 1) * (uint32_t)a.E];
-#pragma unroll
-        for (int i = 0; i < kScanPer; ++i) sum += bb + i < b1 ? vals[i] : 0;
-    }
-    s_part[wave][lane] = sum;
-    __syncthreads();
-    int run = 0;
-    for (int q = 0; q < wave; ++q) run += s_part[q][lane];
-    if (live) {
-        for (int bb = b0; bb < b1; bb += kScanPer) {
-            int vals[kScanPer];
-#pragma unroll
-            for (int i = 0; i < kScanPer; ++i) vals[i] = col[(uint32_t)min(bb + i, b1 - 1) * (uint32_t)a.E];
-#pragma unroll
-            for (int i = 0; i < kScanPer; ++i)
-                if (bb + i < b1) {
-                    col[(uint32_t)(bb + i) * (uint32_t)a.E] = run;
-                    run += vals[i];
-                }
+    for (int i = 0; i < kListRegs; ++i) {
+        mk[i] = 0;
+        js[i] = 0;
+        if (routed && b0 + i < b1) {
+            const uint64_t h = (uint64_t)(b0 + i) * a.E + e;
+            mk[i] = masks[h];
+            if (jslot) js[i] = a.jslot[h];
         }
-        if (wave == 15)  // written through: the last workgroup reads it
-            __hip_atomic_store(a.hist + (uint64_t)a.nblk * a.E + e, run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    // rows, active experts and tiles of the experts below e (all of them for e = E)
+    int below = 0, below_act = 0, below_t = 0;
+    for (int i = tid; i < a.E; i += kListThreads) {
+        int cp[kTotalCopies];
+#pragma unroll
+        for (int r = 0; r < kTotalCopies; ++r) cp[r] = total[r * a.E + i];
+        int c = 0;
+#pragma unroll
+        for (int r = 0; r < kTotalCopies; ++r) c += cp[r];
+        if (i < e) {
+            below += c;
+            below_act += c > 0 ? 1 : 0;
+            below_t += (c + kMfmaTileM - 1) / kMfmaTileM;
+        }
+    }
+    int here = 0;
+#pragma unroll
+    for (int i = 0; i < kListRegs; ++i) here += __builtin_popcount(mk[i]);
+    if (routed)
+        for (int b = b0 + kListRegs; b < b1; ++b) here += __builtin_popcount(masks[(uint64_t)b * a.E + e]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        below += __shfl_xor(below, o, 64);
+        below_act += __shfl_xor(below_act, o, 64);
+        below_t += __shfl_xor(below_t, o, 64);
+    }
+    const int inc = wave_incl_scan_i32(here);
+    if (lane == 63) s_wtot[wave] = inc;
+    if (lane == 0) {
+        s_red[0][wave] = below;
+        s_red[1][wave] = below_act;
+        s_red[2][wave] = below_t;
+    }
     __syncthreads();
-    // release this block's totals, acquire the others' (agent scope, thread 0
-    // after the barrier)
-    if (tid == 0)
-        s_last = __hip_atomic_fetch_add(sync + kSyncScan, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
-                 (int)gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    if (tid == 0) __hip_atomic_store(sync + kSyncScan, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int i = tid; i < a.E; i += 1024)
-        s_cnt[i] = __hip_atomic_load(a.hist + (uint64_t)a.nblk * a.E + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    scan_experts(a, s_cnt, nullptr, nullptr, s_misc);
-}
-
-// Stable scatter: assignment (t, j) of expert e goes to row offsets[e] + its
-// block's base + its rank inside the block.  The first row of each expert
-// also records its token in the slot table.  Shared-expert rows follow in
-// token order.
-__global__ __launch_bounds__(256) void k_scatter(TopkArgs a) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const int A = a.T * a.K;
-    if (i < A) {
-        const int t = i / a.K;
-        const int ex = a.topk_idx[i];
-        const int off = a.offsets[ex];
-        const int p = off + a.hist[(uint64_t)(t / kTopkTokensPerBlock) * a.E + ex] + a.local_rank[i];
-        a.rows[p] = i;
-        a.row_token[p] = t;
-        a.pos[i] = p;
-        if (p == off) ((int*)(a.slot_info + a.expert_slot[ex]))[3] = t;
-    } else if (a.S && i < A + a.T) {
-        a.rows[i] = -1;
-        a.row_token[i] = i - A;
+    int off = 0, slot = 0, tb = 0, wbase = 0, cnt = 0;
+#pragma unroll
+    for (int w = 0; w < kListThreads / 64; ++w) {
+        off += s_red[0][w];
+        slot += s_red[1][w];
+        tb += s_red[2][w];
+        wbase += w < wave ? s_wtot[w] : 0;
+        cnt += s_wtot[w];
+    }
+    if (!routed) {
+        // the shared expert's rows in token order, the slot and tile totals, the counters
+        const int A = a.T * a.K;
+        if (a.S)
+            for (int t = tid; t < a.T; t += kListThreads) {
+                a.rows[A + t] = -1;
+                a.row_token[A + t] = t;
+            }
+        if (tid == 0) {
+            int n_act = slot, n_tiles = tb;
+            a.offsets[a.E] = A;
+            a.offsets[a.E + 1] = A + a.S * a.T;
+            if (a.S) {
+                a.active[n_act] = a.E;
+                a.slot_info[n_act] = make_int4(a.E, A, a.T, 0);
+                n_act++;
+                const int ntt = (a.T + kMfmaTileM - 1) / kMfmaTileM;
+                for (int i = 0; i < ntt && n_tiles < a.max_tiles; ++i)
+                    a.tiles[n_tiles++] = make_int4(a.E, A + i * kMfmaTileM, min(kMfmaTileM, a.T - i * kMfmaTileM), 0);
+            }
+            a.counters[0] = n_act;
+            a.counters[1] = n_tiles;
+            a.counters[kCounterFix] = 0;  // the prefill gate/up's list of uncertain h blocks starts empty
+        }
+        return;
+    }
+    if (tid == 0) a.offsets[e] = off;
+    if (cnt == 0) return;
+    const int nt = (cnt + kMfmaTileM - 1) / kMfmaTileM;
+    for (int i = tid; i < nt && tb + i < a.max_tiles; i += kListThreads)
+        a.tiles[tb + i] = make_int4(e, off + i * kMfmaTileM, min(kMfmaTileM, cnt - i * kMfmaTileM), 0);
+    if (tid == 0) {
+        a.active[slot] = e;
+        a.expert_slot[e] = slot;
+        if (a.expert_counts) atomicAdd(a.expert_counts + e, (unsigned long long)cnt);
+    }
+    // this thread's rows start after the rows of the blocks before its own
+    int p = off + wbase + inc - here;
+    auto put = [&](int b, uint32_t m, uint64_t jw) {
+        while (m) {
+            const int ti = __builtin_ctz(m);
+            m &= m - 1;
+            const int t = b * kTopkTokensPerBlock + ti;
+            int j = (int)((jw >> (4 * ti)) & 15u);
+            if (!jslot) {  // top_k > 16: find e in the token's selection
+                const int32_t* ir = a.topk_idx + (uint64_t)t * a.K;
+                for (int j0 = 0; j0 < a.K; j0 += 8) {
+                    int v[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) v[q] = ir[min(j0 + q, a.K - 1)];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        if (j0 + q < a.K && v[q] == e) j = j0 + q;
+                }
+            }
+            const int i = t * a.K + j;
+            if (p == off) a.slot_info[slot] = make_int4(e, off, cnt, t);
+            a.rows[p] = i;
+            a.row_token[p] = t;
+            a.pos[i] = p;
+            ++p;
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < kListRegs; ++i) put(b0 + i, mk[i], js[i]);
+    for (int b = b0 + kListRegs; b < b1; ++b) {
+        const uint64_t h = (uint64_t)b * a.E + e;
+        put(b, masks[h], jslot ? a.jslot[h] : 0);
     }
 }
 
@@ -1717,6 +1808,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
     ta.sh_gate = ws.sh_gate;
     ta.local_rank = ws.local_rank;
     ta.hist = ws.hist;
+    ta.jslot = ws.jslot;
     ta.offsets = ws.offsets;
     ta.rows = ws.rows;
     ta.row_token = ws.row_token;
@@ -1756,6 +1848,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         ma.eps = eps;
         ma.x_ssq = norm_w ? x_ssq : nullptr;
         ma.x_scale = ws.x_scale;
+        ma.ecount = ws.hist + (uint64_t)ta.nblk * L.E;
         ta.norm_w = norm_w;
         x_f16 = false;  // written by the preparation
         hipLaunchKernelGGL(k_router_prep, dim3((T + 3) / 4 + (L.E + 3) / 4), dim3(256), 0, stream, ma);
@@ -1840,9 +1933,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         }
         if ((err = launch_topk(topk_kernel<false, false>(L.E), ta, nullptr, stream)) != hipSuccess) return err;
     }
-    hipLaunchKernelGGL(k_scan, dim3((L.E + 63) / 64), dim3(1024), 0, stream, ta, ws.sync);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL(k_scatter, dim3((T * L.K + L.S * T + 255) / 256), dim3(256), 0, stream, ta);
+    hipLaunchKernelGGL(k_lists, dim3(L.E + 1), dim3(kListThreads), 0, stream, ta);
     return hipGetLastError();
 }
 
