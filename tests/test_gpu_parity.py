@@ -184,6 +184,18 @@ def test_padded_widths(gpu, spec, T):
     assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= 128)
 
 
+@pytest.mark.parametrize("spec,T", [(LayerSpec(256, 256, 16, 64, True, TYPE_Q4_0), 300),
+                                    (LayerSpec(256, 256, 17, 64, True, TYPE_Q4_0), 300),
+                                    (LayerSpec(256, 64, 24, 128, False, TYPE_Q8_0), 1100)])
+def test_expert_lists_wide_top_k(gpu, spec, T):
+    """The per-expert lists built from the top-k blocks' token masks (top-k blocks x experts
+    above 4096) at top_k 16, 17 and 24: each listed token's slot comes from the four-bit
+    fields that the top-k writes up to top_k 16 and from a search of the token's selection
+    above it; grouped router (300 tokens) and batched router (1100 tokens)."""
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=450 + spec.top_k)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=True)
+
+
 @pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 33, 64])
 def test_token_counts_small_layer(gpu, T):
     """Edge token counts: single token, block boundaries of the top-k sort (16 per block)."""
