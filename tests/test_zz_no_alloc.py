@@ -32,15 +32,18 @@ def test_static_forward_rejects_sizes_above_the_scratch():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("spec_name,sizes", [("QWEN35B", (40, 3)), ("QWEN35B", (10, 1)), ("CONFIG1", (32, 17)),
-                                             ("GEMMA4", (16, 5)), ("PADDED", (20, 3))])
+                                             ("GEMMA4", (16, 5)), ("PADDED", (20, 3)), ("LISTS", (300, 130))])
 def test_static_forward_matches_workspace_forward(gpu, spec_name, sizes):
     import torch
 
     from qwenium_amd import Workspace, synthetic
     from qwenium_amd._lib import check, lib
 
-    # PADDED: widths off the kernels' grid (the static scratch also holds the padded rows)
+    # PADDED: widths off the kernels' grid (the static scratch also holds the padded rows);
+    # LISTS: 300 tokens over 256 experts take the per-expert list launch and the MFMA GEMMs with
+    # their fixup list, then 130 tokens the merged top-k and the streaming GEMVs on the same scratch
     spec = (synthetic.LayerSpec(96, 8, 2, 32, True, synthetic.TYPE_Q4_0) if spec_name == "PADDED"
+            else synthetic.LayerSpec(256, 256, 8, 64, True, synthetic.TYPE_Q4_0) if spec_name == "LISTS"
             else getattr(synthetic, spec_name))
     layer = synthetic.make_layer(spec, 29)
     ws = Workspace(layer, max(sizes))
