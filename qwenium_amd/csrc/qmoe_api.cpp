@@ -127,7 +127,7 @@ static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 size_t workspace_bytes(int T, int H, int E, int K, int F, Workspace* w, void* base, bool pad) {
     const size_t A = (size_t)T * K;
     const size_t R = A + (size_t)T;  // room for a shared expert
-    const int nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
+    const int nblk = (T + kTopkMinTokensPerBlock - 1) / kTopkMinTokensPerBlock;  // top-k blocks, at most
     const int max_tiles = (int)((A + kMfmaTileM - 1) / kMfmaTileM) + std::min<int>(E, (int)A) +
                           (T + kMfmaTileM - 1) / kMfmaTileM + 1;
     size_t off = 0;

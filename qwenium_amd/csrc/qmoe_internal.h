@@ -12,6 +12,7 @@ namespace qmoe {
 // Tokens handled by one top-k block; the per-block histogram granularity of
 // the stable counting sort.
 constexpr int kTopkTokensPerBlock = 16;
+constexpr int kTopkMinTokensPerBlock = 4;  // the unmerged top-k's smallest blocks (more blocks to fill the CUs)
 // Cross-block signalling area of a workspace: the merged top-k's
 // finished-workgroup counter (back to 0 after each use).
 constexpr int kSyncWords = 64;

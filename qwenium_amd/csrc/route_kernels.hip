@@ -547,7 +547,8 @@ struct TopkArgs {
     int32_t* counters;    // [0] n_active, [1] n_tiles
     int4* tiles;
     int max_tiles;
-    int nblk;
+    int nblk;             // top-k blocks
+    int tpb;              // tokens per top-k block (a wave each): 16, or 8 / 4 where fewer tokens fill the CUs
 };
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
@@ -921,8 +922,8 @@ static inline int topk_epl(int E) {
 __device__ void scan_experts(const TopkArgs& a, const int32_t* s_cnt, const uint32_t* first_token, int32_t* s_off,
                              int32_t* s_misc);
 
-// blockDim = 64 * kTopkTokensPerBlock: one wave per token.  Writes the
-// selection and, per expert, the mask of the block's tokens that chose it.
+// blockDim = 64 * a.tpb: one wave per token.  Writes the selection and, per
+// expert, the mask of the block's tokens that chose it.
 // MERGE (blocks x experts <= kTopkMergeMax): the per-block counts and each
 // assignment's rank among the block's assignments to the same expert (token
 // order) are written through, and the last block to finish (a counter in sync)
@@ -941,8 +942,8 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, i
     __shared__ uint64_t s_jslot[MERGE ? 1 : 1024];  // per expert: nibble ti = the slot j of token ti
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int t0 = blockIdx.x * kTopkTokensPerBlock;
-    const int ntok = min(kTopkTokensPerBlock, a.T - t0);
+    const int t0 = blockIdx.x * a.tpb;
+    const int ntok = min(a.tpb, a.T - t0);
     const bool jslot = !MERGE && a.K <= 16;
     for (int e = threadIdx.x; e < a.E; e += blockDim.x) {
         s_mask[e] = 0;
@@ -1021,7 +1022,7 @@ __global__ __launch_bounds__(64 * kTopkTokensPerBlock) void k_topk(TopkArgs a, i
                 const int t = i / a.K;
                 const int ex = __hip_atomic_load(a.topk_idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const int off = s_off[ex];
-                const int p = off + s_base[(t / kTopkTokensPerBlock) * a.E + ex] +
+                const int p = off + s_base[(t / a.tpb) * a.E + ex] +
                               __hip_atomic_load(a.local_rank + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 a.rows[p] = i;
                 a.row_token[p] = t;
@@ -1670,7 +1671,7 @@ __global__ __launch_bounds__(kListThreads) void k_lists(TopkArgs a) {
         while (m) {
             const int ti = __builtin_ctz(m);
             m &= m - 1;
-            const int t = b * kTopkTokensPerBlock + ti;
+            const int t = b * a.tpb + ti;
             int j = (int)((jw >> (4 * ti)) & 15u);
             if (!jslot) {  // top_k > 16: find e in the token's selection
                 const int32_t* ir = a.topk_idx + (uint64_t)t * a.K;
@@ -1723,7 +1724,7 @@ static const void* topk_kernel(int E) {
 
 static hipError_t launch_topk(const void* kern, TopkArgs& ta, int32_t* sync, hipStream_t stream) {
     void* args[] = {&ta, &sync};
-    hipError_t err = hipLaunchKernel(kern, dim3(ta.nblk), dim3(64 * kTopkTokensPerBlock), args, 0, stream);
+    hipError_t err = hipLaunchKernel(kern, dim3(ta.nblk), dim3(64 * ta.tpb), args, 0, stream);
     return err != hipSuccess ? err : hipGetLastError();
 }
 
@@ -1822,7 +1823,16 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
     ta.counters = ws.counters;
     ta.tiles = ws.tiles;
     ta.max_tiles = ws.max_tiles;
-    ta.nblk = (T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock;
+    // the merged top-k keeps 16 tokens per block; otherwise blocks of 8 or 4 tokens
+    // where blocks of 16 would leave CUs idle (a block's tokens run one after another
+    // on its four SIMDs)
+    ta.tpb = kTopkTokensPerBlock;
+    ta.nblk = (T + ta.tpb - 1) / ta.tpb;
+    const bool merge = !route_uses_mfma(L, T) && !route_decode_fused(L, T) && ta.nblk * L.E <= kTopkMergeMax;
+    if (!merge && T > kTopkTokensPerBlock) {
+        while (ta.tpb > kTopkMinTokensPerBlock && (T + ta.tpb - 1) / ta.tpb < L.n_cu) ta.tpb >>= 1;
+        ta.nblk = (T + ta.tpb - 1) / ta.tpb;
+    }
     hipError_t err;
     if (route_uses_mfma(L, T)) {
         RouterMfmaArgs ma;
@@ -1927,7 +1937,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
             hipSuccess)
             return err;
         ta.quant_rows = 0;
-        if (ta.nblk * L.E <= kTopkMergeMax) {
+        if (merge) {
             // the last top-k block runs the expert scan and the scatter: no more launches
             return launch_topk(topk_kernel<false, true>(L.E), ta, ws.sync, stream);
         }
