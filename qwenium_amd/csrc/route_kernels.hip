@@ -262,6 +262,8 @@ struct RouterMfmaArgs {
     const double* x_ssq;    // [T][ssq_parts(H)] or null
     float* x_scale;         // [T]
     int32_t* ecount;        // [kTotalCopies][E] per-expert totals, zeroed here for the top-k blocks to add into
+    int ksplit;             // k ranges per tile (1: logits and bounds; 2, 4: f64 partial sums into part)
+    double* part;           // [ksplit][T][E] when ksplit > 1
 };
 
 // bf16 split of 8 floats (round to nearest both times): hi = bf16(v), lo = bf16(v - hi);
@@ -411,6 +413,9 @@ __global__ __launch_bounds__(256) void k_router_prep(RouterMfmaArgs a) {
 // Router tiles of 64 tokens x 64 experts, one 32x32 MFMA tile per wave.  The
 // four split operands of each 64-wide k step are loaded straight into LDS
 // (three buffers, issued two steps ahead: a fixed 9 loads per wave and step).
+// Where the tiles alone would leave CUs idle, each tile's k steps are split
+// into ksplit ranges on separate workgroups, which write their f64 sums; the
+// top-k adds them (in f64, then rounds to f32) and forms the bound itself.
 constexpr int kRtStages = 3;
 constexpr int kRtRowUnits = kRtLd / 8;                   // 16-byte units per LDS row (8 + 1 padding)
 constexpr int kRtSlots = 4 * kRtTile * kRtRowUnits;      // per stage
@@ -426,7 +431,9 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
     // takes logical tile (b % 8) * (n/8) + b / 8 and the expert tiles of one
     // token tile run on one XCD and share its L2.
     const int b = blockIdx.x;
-    const int g = (a.n_tiles & 7) == 0 ? (b & 7) * (a.n_tiles >> 3) + (b >> 3) : b;
+    const int nwg = a.n_tiles * a.ksplit;
+    const int gk = (nwg & 7) == 0 ? (b & 7) * (nwg >> 3) + (b >> 3) : b;
+    const int g = gk / a.ksplit, kp = gk - g * a.ksplit;
     const int t0 = (g / a.n_etiles) * kRtTile;
     const int e0 = (g % a.n_etiles) * kRtTile;
     // this thread's staging slots: slot s = (array, row, unit); unit 8 (the
@@ -448,9 +455,11 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
                                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base));
         soff[i] = (uint32_t)row * (uint32_t)a.H * 2u + (u < 8 ? 16u * u : 0u);
     }
-    const int nstep = a.H / kRtK;
+    // this workgroup's k steps [s0, s0 + nstep)
+    const int s0 = kp * (a.H / kRtK) / a.ksplit;
+    const int nstep = (kp + 1) * (a.H / kRtK) / a.ksplit - s0;
     auto stage = [&](int st) {
-        const int stc = min(st, nstep - 1);  // past the end: a repeat into a buffer that is not read
+        const int stc = s0 + min(st, nstep - 1);  // past the end: a repeat into a buffer that is not read
         __bf16* dst = s_op + (st % kRtStages) * kRtStageHalfs;
 #pragma unroll
         for (int i = 0; i < kRtDma; ++i) {
@@ -494,6 +503,14 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
     // D[row][col]: row = 8 (r / 4) + 4 (lane / 32) + r % 4, col = lane % 32
     const int col = ns * 32 + (lane & 31);
     const int e = e0 + col;
+    if (a.ksplit > 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + ms * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (t < a.T && e < a.E) a.part[((uint64_t)kp * a.T + t) * a.E + e] = acc64[r];
+        }
+        return;
+    }
     const float nw = a.rnorm[a.T + min(e, a.E - 1)];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -515,6 +532,9 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
 struct TopkArgs {
     const float* logits;       // [T][E+1] (approximate on the refined path)
     const float* logit_bound;  // [T][E]   refined path only
+    const double* rpart;       // [rsplit][T][E] refined path with rsplit > 1: the router's k-range sums
+    const float* rnorm;        // [T + E] ... and the row norms for their bound
+    int rsplit;
     const float* x;            // [T][H]   router input: exact logits (refined path), decode router
     const float* xe;           // [T][H]   expert input: its Q8_0 (decode routing launch)
     const float* w_router;     // [E][router_ld]
@@ -782,13 +802,38 @@ __device__ void topk_refine_token(const TopkArgs& a, int t, int lane, int32_t* s
     const float* l = a.logits + (uint64_t)t * (a.E + 1);
     const float* bd = a.logit_bound + (uint64_t)t * a.E;
     float lo[EPL], up[EPL];
+    if (a.rsplit > 1) {
+        // the router's k-range sums (f64, added in range order), its bound formed here
+        double ps[EPL];
+        float nw[EPL];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const int e = i * 64 + lane;
-        const int ec = min(e, a.E - 1);
-        const float L = l[ec], d = bd[ec];
-        lo[i] = e < a.E ? L - d : -__builtin_huge_valf();
-        up[i] = e < a.E ? L + d : -__builtin_huge_valf();
+        for (int i = 0; i < EPL; ++i) {
+            const int ec = min(i * 64 + lane, a.E - 1);
+            ps[i] = a.rpart[(uint64_t)t * a.E + ec];
+            nw[i] = a.rnorm[a.T + ec];
+        }
+        for (int p = 1; p < a.rsplit; ++p)
+#pragma unroll
+            for (int i = 0; i < EPL; ++i)
+                ps[i] += a.rpart[((uint64_t)p * a.T + t) * a.E + min(i * 64 + lane, a.E - 1)];
+        const float nx = a.rnorm[t];
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const int e = i * 64 + lane;
+            const float L = (float)ps[i];
+            const float d = kRouterBoundRel * nx * nw[i] + 0x1p-21f * __builtin_fabsf(L) + 1e-30f;
+            lo[i] = e < a.E ? L - d : -__builtin_huge_valf();
+            up[i] = e < a.E ? L + d : -__builtin_huge_valf();
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const int e = i * 64 + lane;
+            const int ec = min(e, a.E - 1);
+            const float L = l[ec], d = bd[ec];
+            lo[i] = e < a.E ? L - d : -__builtin_huge_valf();
+            up[i] = e < a.E ? L + d : -__builtin_huge_valf();
+        }
     }
     // K-th largest lower bound (with multiplicity)
     float s[EPL];
@@ -1798,6 +1843,9 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
     ta.x_scale = ws.x_scale;
     ta.logits = ws.logits;
     ta.logit_bound = ws.logit_bound;
+    ta.rpart = nullptr;
+    ta.rnorm = ws.rnorm;
+    ta.rsplit = 1;
     ta.x = xr;
     ta.xe = x;
     ta.w_router = L.w_router;
@@ -1852,6 +1900,18 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         ma.rx = ws.rx_split;
         ma.rw = ws.rw_split;
         ma.rnorm = ws.rnorm;
+        // k ranges per tile where the tiles alone would leave CUs idle (up to 4,
+        // at least 4 steps each); their f64 sums go to the expert-row buffer, free
+        // until the down projection, and the top-k adds them.  The debug copies of
+        // the approximate logits and bounds take the unsplit form.
+        ma.ksplit = 1;
+        ma.part = (double*)ws.ybuf;
+        if (!dbg.approx && !dbg.bound)
+            while (ma.ksplit < 4 && ma.n_tiles * ma.ksplit < L.n_cu && L.H / kRtK >= 8 * ma.ksplit &&
+                   (size_t)2 * ma.ksplit * T * L.E * sizeof(double) <= (size_t)T * (L.K + L.S) * L.H * sizeof(float))
+                ma.ksplit *= 2;
+        ta.rsplit = ma.ksplit;
+        ta.rpart = ma.part;
         // the pre-MoE RMSNorm on the fly (x == xr is the residual row): the
         // preparation normalizes (and writes the scales), the refinement too
         ma.norm_w = norm_w;
@@ -1867,7 +1927,7 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         if ((err = hipFuncSetAttribute((const void*)k_router_mfma, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)lds)) != hipSuccess)
             return err;
-        hipLaunchKernelGGL(k_router_mfma, dim3(ma.n_tiles), dim3(256), lds, stream, ma);
+        hipLaunchKernelGGL(k_router_mfma, dim3(ma.n_tiles * ma.ksplit), dim3(256), lds, stream, ma);
         if ((err = hipGetLastError()) != hipSuccess) return err;
         if ((err = launch_topk(topk_kernel<true, false>(L.E), ta, nullptr, stream)) != hipSuccess) return err;
         if (dbg.approx &&
