@@ -412,17 +412,19 @@ __global__ __launch_bounds__(256) void k_router_prep(RouterMfmaArgs a) {
 
 // Router tiles of 64 tokens x 64 experts, one 32x32 MFMA tile per wave.  The
 // four split operands of each 64-wide k step are loaded straight into LDS
-// (three buffers, issued two steps ahead: a fixed 9 loads per wave and step).
-// Where the tiles alone would leave CUs idle, each tile's k steps are split
-// into ksplit ranges on separate workgroups, which write their f64 sums; the
-// top-k adds them (in f64, then rounds to f32) and forms the bound itself.
-constexpr int kRtStages = 3;
+// (NST buffers, issued NST - 1 steps ahead: a fixed 9 loads per wave and step;
+// three buffers take 110 KB, one workgroup per CU, two take 74 KB, two per CU).
+// Where the tiles alone would not give every CU two workgroups, each tile's k
+// steps are split into ksplit ranges on separate workgroups, which write their
+// f64 sums; the top-k adds them (in f64, then rounds to f32) and forms the
+// bound itself.
 constexpr int kRtRowUnits = kRtLd / 8;                   // 16-byte units per LDS row (8 + 1 padding)
 constexpr int kRtSlots = 4 * kRtTile * kRtRowUnits;      // per stage
 constexpr int kRtDma = kRtSlots / 256;                   // loads per thread and step
 static_assert(kRtSlots % 256 == 0 && (kRtTile * kRtRowUnits) % 64 == 0, "router staging slots");
 constexpr int kRtStageHalfs = 4 * kRtTile * kRtLd;
 
+template <int NST>
 __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];
     __bf16* s_op = (__bf16*)s_dyn;  // [stage][xh, xl, wh, wl][64][kRtLd]
@@ -460,7 +462,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
     const int nstep = (kp + 1) * (a.H / kRtK) / a.ksplit - s0;
     auto stage = [&](int st) {
         const int stc = s0 + min(st, nstep - 1);  // past the end: a repeat into a buffer that is not read
-        __bf16* dst = s_op + (st % kRtStages) * kRtStageHalfs;
+        __bf16* dst = s_op + (st % NST) * kRtStageHalfs;
 #pragma unroll
         for (int i = 0; i < kRtDma; ++i) {
             // the wave's 64 slots are contiguous in LDS: base = the first slot of the wave
@@ -475,12 +477,12 @@ __global__ __launch_bounds__(256) void k_router_mfma(RouterMfmaArgs a) {
     const int arow = (ms * 32 + (lane & 31)) * kRtLd + (lane >> 5) * 8;
     const int brow = (ns * 32 + (lane & 31)) * kRtLd + (lane >> 5) * 8;
     stage(0);
-    stage(1);
+    if (NST == 3) stage(1);
     for (int st = 0; st < nstep; ++st) {
-        __builtin_amdgcn_s_waitcnt(kRtDma);  // vmcnt(step st + 1's loads): step st's have landed
-        __syncthreads();                     // ... for every wave; buffer (st + 2) % 3 (read at st - 1) is free
-        stage(st + 2);
-        const __bf16* op = s_op + (st % kRtStages) * kRtStageHalfs;
+        __builtin_amdgcn_s_waitcnt(NST == 3 ? kRtDma : 0);  // step st's loads have landed
+        __syncthreads();                     // ... for every wave; the buffer read at st - 1 is free
+        stage(st + NST - 1);
+        const __bf16* op = s_op + (st % NST) * kRtStageHalfs;
         const __bf16* xh = op;
         const __bf16* xl = op + kRtTile * kRtLd;
         const __bf16* wh = op + 2 * kRtTile * kRtLd;
@@ -1923,11 +1925,21 @@ static hipError_t launch_route_tables(const LayerDesc& L, const Workspace& ws, c
         x_f16 = false;  // written by the preparation
         hipLaunchKernelGGL(k_router_prep, dim3((T + 3) / 4 + (L.E + 3) / 4), dim3(256), 0, stream, ma);
         if ((err = hipGetLastError()) != hipSuccess) return err;
-        const size_t lds = (size_t)kRtStages * kRtStageHalfs * 2;
-        if ((err = hipFuncSetAttribute((const void*)k_router_mfma, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds)) != hipSuccess)
+        // tiles that fill the CUs once: split in two on two-buffer workgroups, two per CU
+        int nst = 3;
+        if (ma.ksplit == 1 && !dbg.approx && !dbg.bound && ma.n_tiles <= L.n_cu && L.H / kRtK >= 8 &&
+            (size_t)2 * 2 * T * L.E * sizeof(double) <= (size_t)T * (L.K + L.S) * L.H * sizeof(float)) {
+            nst = 2;
+            ma.ksplit = 2;
+            ta.rsplit = 2;
+        }
+        const void* rk = nst == 2 ? (const void*)k_router_mfma<2> : (const void*)k_router_mfma<3>;
+        const size_t lds = (size_t)nst * kRtStageHalfs * 2;
+        if ((err = hipFuncSetAttribute(rk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
             return err;
-        hipLaunchKernelGGL(k_router_mfma, dim3(ma.n_tiles * ma.ksplit), dim3(256), lds, stream, ma);
+        void* rargs[] = {&ma};
+        if ((err = hipLaunchKernel(rk, dim3(ma.n_tiles * ma.ksplit), dim3(256), rargs, lds, stream)) != hipSuccess)
+            return err;
         if ((err = hipGetLastError()) != hipSuccess) return err;
         if ((err = launch_topk(topk_kernel<true, false>(L.E), ta, nullptr, stream)) != hipSuccess) return err;
         if (dbg.approx &&
