@@ -367,12 +367,13 @@ int qmoe_layer_create(const qmoe_tensor* w_router, const qmoe_tensor* w_exp_gate
         d.mfma_min_tokens = (int)std::max<int64_t>(128, std::min<int64_t>(4096, (t + 15) / 16 * 16));
     }
     // token count from which routing runs the batched bf16-MFMA router: its cost is
-    // nearly flat in T (~70 us from 256 to 1024 tokens at the 35B-A3B shape), the exact
-    // grouped router's grows with T * n_experts * n_embd; measured crossovers: about
-    // 544 tokens at the 35B-A3B shape, 620 at Gemma 4's (both fit this rule)
+    // nearly flat in T (its tiles split over more workgroups at small T), the exact
+    // grouped router's grows with T * n_experts * n_embd; measured crossovers (whole
+    // layer, same box): about 140 tokens at the 35B-A3B shape, about 270 at Gemma 4's;
+    // this rule puts them at 224 and 272
     {
-        const double t = 544.0 * std::sqrt(524288.0 / ((double)d.E * (double)d.H));
-        d.big_router_min_tokens = (int)std::max(256.0, std::min(1024.0, std::ceil(t / 16.0) * 16.0));
+        const double t = 216.0 * std::sqrt(524288.0 / ((double)d.E * (double)d.H));
+        d.big_router_min_tokens = (int)std::max(128.0, std::min(1024.0, std::ceil(t / 16.0) * 16.0));
     }
     if (const char* env = std::getenv("QMOE_MFMA_MIN_TOKENS")) {
         const long v = std::strtol(env, nullptr, 10);
