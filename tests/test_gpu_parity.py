@@ -693,6 +693,35 @@ def test_random_shapes(gpu, spec, T):
     assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= _mfma_min_tokens(spec), min_identical=1.0)
 
 
+def _random_prefill_cases(n=48, seed=12):
+    """Seeded prefill-size shapes for the per-expert lists, the top-k block sizes and the
+    split router tiles: 129 to 2048 tokens, up to 1024 experts, top_k up to 20, hidden up
+    to 4096 (sizes bounded so the oracle stays quick)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        H = int(rng.choice([256, 512, 1056, 2048, 2816, 4096]))
+        E = int(rng.choice([8, 16, 64, 128, 256, 512, 1024]))
+        K = int(min(E, rng.choice([1, 2, 4, 8, 8, 16, 17, 20])))
+        F = int(rng.choice([64, 128, 512]))
+        T = int(rng.choice([129, 160, 224, 300, 545, 777, 1024, 1500, 2048]))
+        shared = bool(rng.integers(2))
+        wtype = TYPE_Q4_0 if rng.integers(2) else TYPE_Q8_0
+        if T * K * F * H > 6e9 or T * E * H > 8e9:
+            continue
+        cases.append(pytest.param(LayerSpec(H, E, K, F, shared, wtype), T, id=f"H{H}-E{E}-k{K}-F{F}-s{int(shared)}-"
+                                  f"{'q4' if wtype == TYPE_Q4_0 else 'q8'}-T{T}"))
+    return cases
+
+
+@pytest.mark.parametrize("spec,T", _random_prefill_cases())
+def test_random_prefill_shapes(gpu, spec, T):
+    """Seeded prefill-size shapes against the oracle: routing and lists bit-exact, h quants
+    exact and outputs within MFMA_TOL on the MFMA path (bit-identical below it)."""
+    y, got, y_ref, d_ref, *_ = run_pair(spec, T, seed=800 + T)
+    assert_parity(y, got, y_ref, d_ref, spec, mfma=T >= _mfma_min_tokens(spec), min_identical=1.0)
+
+
 def _chain_cases(n=12, seed=77):
     rng = np.random.default_rng(seed)
     cases = []
