@@ -84,7 +84,8 @@ static_assert(2 * 64 * kHLd * 4 <= 2 * (size_t)kStageBytes, "an epilogue pass's 
 // g (n block terms summed by fma in f32) relative to max(|g|, rms of the
 // block's g) is at most 1.2e-6 over 0.5M emulated values at n = 64; it is
 // charged as kAccErr * sqrt(n) (3e-6 at n = 64).  The activation's slope is
-// below kActSlope (SiLU 1.10, GELU 1.13); the f32 SiLU (within 3.6e-7 (1 + |g|)
+// below kActSlope (SiLU 1.10, GELU 1.13; SiLU charges its local slope instead,
+// from sigma(g)); the f32 SiLU (within 3.6e-7 (1 + |g|)
 // relative) and the product (half an ulp) are within kActRel * (1 + |g|) * |h|
 // of the exact ones.
 constexpr float kAccErr = 3.75e-7f;
@@ -284,7 +285,7 @@ __device__ __forceinline__ void h_block(const F16Args& a, f32x4* pg, f32x4* pu, 
             // GeGLU: the table entries at fp16(g) and at the ends of g's error
             // range, loaded unconditionally (16-bit indices) so that no load waits
             // behind a branch
-            float av, tl = 0.0f, th = 0.0f, lo = 0.0f, hi = 0.0f, eg = 0.0f;
+            float av, tl = 0.0f, th = 0.0f, lo = 0.0f, hi = 0.0f, eg = 0.0f, sgm = 0.0f;
             uint32_t l16 = 0, h16 = 0;
             if (ACT == kActGeluTanh) {
                 eg = a.acc_err * fmaxf(ag, rg);
@@ -297,7 +298,8 @@ __device__ __forceinline__ void h_block(const F16Args& a, f32x4* pg, f32x4* pu, 
                 th = fp16_to_f32(a.gelu_tab[h16]);
                 av = gv <= -10.0f ? 0.0f : (gv >= 10.0f ? gv : tv);
             } else {
-                av = act_f32<ACT>(a.gelu_tab, gv);
+                sgm = __builtin_amdgcn_rcpf(1.0f + __expf(-gv));  // act_f32's SiLU, its sigma kept
+                av = gv * sgm;
             }
             const float h = av * uv;
             const float ah = __builtin_fabsf(h);
@@ -317,8 +319,12 @@ __device__ __forceinline__ void h_block(const F16Args& a, f32x4* pg, f32x4* pu, 
                 const float eav = lo >= 10.0f ? eg : (hi <= -10.0f ? 0.0f : (near ? __builtin_fabsf(th - tl) : wide));
                 eh = au * eav + __builtin_fabsf(av) * (a.acc_err * fmaxf(au, ru));
             } else {
-                // |u| kActSlope eg + |av| eu
-                eh = a.acc_err * __builtin_fmaf(kActSlope * au, fmaxf(ag, rg), __builtin_fabsf(av) * fmaxf(au, ru));
+                // |u| slope eg + |av| eu, the slope over g's error range from sigma(g):
+                // |silu'(g)| = |s + silu(g) (1 - s)|, plus 0.5 eg (|silu''| <= 0.5) and
+                // 1e-3 for the f32 sigma
+                const float egs = a.acc_err * fmaxf(ag, rg);
+                const float sl = __builtin_fabsf(__builtin_fmaf(av, 1.0f - sgm, sgm)) + __builtin_fmaf(0.5f, egs, 1e-3f);
+                eh = __builtin_fmaf(au * sl, egs, __builtin_fabsf(av) * (a.acc_err * fmaxf(au, ru)));
             }
             eh = __builtin_fmaf(kActRel, __builtin_fmaf(ag, ah, ah), eh);
             h4[k] = h;
