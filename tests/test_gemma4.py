@@ -213,7 +213,7 @@ def assert_parity(y, got, y_ref, d_ref, min_identical=0.999, mfma=False):
 @pytest.mark.gpu
 @pytest.mark.parametrize("wname,T", [("GEMMA4", 1), ("GEMMA4", 10), ("GEMMA4", 16), ("GEMMA4", 17),
                                      ("GEMMA4", 100), ("GEMMA4", 200), ("GEMMA4", 300), ("GEMMA4", 700),
-                                     ("GEMMA4_Q8", 10), ("GEMMA4_Q8", 256)])
+                                     ("GEMMA4", 4096), ("GEMMA4_Q8", 10), ("GEMMA4_Q8", 256)])
 def test_gemma4_layer_matches_oracle(gpu, wname, T):
     """Decode (T <= 16: fused routing + gate/up + down/combine), streaming
     (17..127) and MFMA (>= 128; batched router from 272 at this shape) paths, from the Gemma 4
